@@ -1,0 +1,66 @@
+// The shared tiled GEMM, as the other translation units launch it.
+#pragma once
+
+#include "internal.h"
+
+namespace afhip {
+
+// One batched GEMM launch: C[b][m][n] = epilogue(sum_k A[b][m][k] * B[b][n][k]).
+// A is row-major [M][K] (row stride lda); B is [N][K] (row stride ldb), the
+// k-contiguous layout every kernel here consumes.
+struct GemmArgs {
+  const void* a = nullptr;
+  const void* b = nullptr;
+  void* c = nullptr;
+  const void* residual = nullptr;
+  const float* scale = nullptr;
+  const float* bias = nullptr;
+  int M = 0, N = 0, K = 0;
+  int64_t lda = 0, ldb = 0, ldc = 0;
+  int64_t sa = 0, sb = 0, sc = 0;
+  int batch = 1;
+  uint32_t flags = 0;
+  int head_cols = 0;  // heads * head_dim, ATTENTION only
+  float q_scale = 1.0f;
+  // Outer-product-mean contraction epilogue: y /= (eps + count[i][j]) with
+  // i = (row0 + m) / c_outer, j = n / c_outer; stored at the [i][j][a][b] layout.
+  const float* opm_count = nullptr;
+  int opm_outer = 0;
+  int opm_length = 0;
+  int opm_row0 = 0;
+  float opm_eps = 0.0f;
+};
+
+// Epilogue flags private to the library (beyond the public AFHIP_EPILOGUE_*).
+// OPM_CONTRACT: y /= (eps + count[i][j]), stored at [i_local][j][a][b].
+// OPM_OUTPUT:   y += bias[col] / (eps + count[opm_row0 + row]) (bias scaled by
+//               the pair's 1/(eps + count), outer-product-mean.ts:462-479).
+constexpr uint32_t EPILOGUE_OPM_CONTRACT = 1u << 16;
+constexpr uint32_t EPILOGUE_OPM_OUTPUT = 1u << 17;
+
+struct GemmTypes {
+  int precision;  // AFHIP_PRECISION_*
+  int a_dtype;    // AFHIP_F32 | AFHIP_F16
+  int b_dtype;    // AFHIP_F32 | AFHIP_F16 | AFHIP_I8
+  int c_dtype;    // AFHIP_F32 | AFHIP_F16
+};
+
+// Runs one GEMM with the given variant (tile shape); the variant's
+// vectorized flag is ignored and derived from alignment.
+int run_gemm(const GemmArgs& args, const GemmTypes& types, const afhip_variant& variant, const char* label,
+             hipStream_t stream);
+
+// Heuristic tile choice for a problem of this size.
+afhip_variant heuristic_variant(int precision, int64_t M, int64_t N, int64_t K, int batch);
+
+// The variant plans of this shape should use (pinned, calibrated or heuristic).
+afhip_variant select_variant(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);
+
+// W[k][n] (src) -> W[n][k] (dst), with dtype conversion.
+int pack_transpose(const void* src, int src_dtype, int rows_k, int cols_n, int64_t ld_src, void* dst,
+                   int dst_dtype, int64_t ld_dst, hipStream_t stream);
+
+// Elementwise f32 -> dst dtype conversion (dst may be F32: plain copy).
+int convert_f32(const float* src, int64_t count, void* dst, int dst_dtype, hipStream_t stream);
+
+}  // namespace afhip

@@ -1,0 +1,420 @@
+// The shared tiled GEMM for gfx950, its plan API, weight packing and the
+// int8 dequantisation kernels.
+//
+// One workgroup of 256 lanes (four wave64s in a 2 x 2 arrangement) covers a
+// BM x BN output tile and walks K in steps of 32. Both operands are staged
+// k-contiguous in LDS, double-buffered, with the next step's 16-byte global
+// loads issued before the current step's MFMAs. f16 precision feeds
+// v_mfma_f32_32x32x16_f16 (operands rounded to f16, f32 accumulation); f32
+// precision feeds v_mfma_f32_32x32x2_f32 (exact f32 products). int8 weights
+// are widened to f16 on their way into LDS, which is exact for |q| <= 127,
+// and their per-column scale is applied to the f32 accumulator.
+//
+// Workgroups are numbered so that consecutive tiles land on one XCD: the
+// hardware deals workgroup ids round-robin over the eight XCDs, so tile
+// t = (id % 8) * per_xcd + id / 8 keeps a batch's tiles (which share
+// operands) inside one XCD's L2.
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "gemm_kernel.h"
+
+namespace afhip {
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, const char* label, hipStream_t stream) {
+  AFHIP_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0 && g.batch > 0, "GEMM dimensions must be positive (M=%d N=%d K=%d batch=%d)",
+                g.M, g.N, g.K, g.batch);
+  AFHIP_REQUIRE(g.a && g.b && g.c, "GEMM operand or output is NULL");
+  AFHIP_REQUIRE(valid_precision(t.precision), "unknown precision %d", t.precision);
+  AFHIP_REQUIRE(valid_float_dtype(t.a_dtype), "source dtype must be f32 or f16");
+  AFHIP_REQUIRE(valid_float_dtype(t.b_dtype) || t.b_dtype == AFHIP_I8, "weight dtype must be f32, f16 or i8");
+  AFHIP_REQUIRE(valid_float_dtype(t.c_dtype), "output dtype must be f32 or f16");
+  AFHIP_REQUIRE(!(t.b_dtype == AFHIP_I8 && t.precision == AFHIP_PRECISION_F32),
+                "int8 weights run with f16 precision (the widening to f16 is exact)");
+  AFHIP_REQUIRE(!(g.flags & AFHIP_EPILOGUE_SCALE) || g.scale, "SCALE epilogue without a scale vector");
+  AFHIP_REQUIRE(!(g.flags & AFHIP_EPILOGUE_BIAS) || g.bias, "BIAS epilogue without a bias vector");
+  AFHIP_REQUIRE(!(g.flags & AFHIP_EPILOGUE_RESIDUAL) || g.residual, "RESIDUAL epilogue without a residual");
+  AFHIP_REQUIRE(!(g.flags & AFHIP_EPILOGUE_ATTENTION) || (g.head_cols > 0 && g.N == 4 * g.head_cols),
+                "ATTENTION epilogue needs columns == 4 * heads * head_dim");
+  const int va = 16 / (int)dtype_size(t.a_dtype), vb = 16 / (int)dtype_size(t.b_dtype);
+  bool vec = g.K % va == 0 && g.K % vb == 0 && g.lda % va == 0 && g.ldb % vb == 0 && g.sa % va == 0 &&
+             g.sb % vb == 0 && aligned16(g.a) && aligned16(g.b);
+  if (t.precision == AFHIP_PRECISION_F16) {
+    AFHIP_REQUIRE(t.b_dtype != AFHIP_F32, "f16 precision takes f16 or int8 weights (prepare them first)");
+    if (t.a_dtype == AFHIP_F32) return gemm_dispatch_f16_a32(g, t, v, vec, label, stream);
+    return gemm_dispatch_f16_a16(g, t, v, vec, label, stream);
+  }
+  AFHIP_REQUIRE(t.a_dtype == AFHIP_F32 && t.b_dtype == AFHIP_F32, "f32 precision takes f32 operands");
+  return gemm_dispatch_f32(g, t, v, vec, label, stream);
+}
+
+afhip_variant heuristic_variant(int precision, int64_t M, int64_t N, int64_t /*K*/, int batch) {
+  afhip_variant v{};
+  v.precision = precision;
+  v.tile_inner = gemm_detail::kBK;
+  v.vectorized = 1;
+  v.source = 0;
+  // Prefer the largest tile that still gives every CU two workgroups.
+  const int64_t target = 2 * (int64_t)(device_cu_count() > 0 ? device_cu_count() : 256);
+  const int shapes[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
+  for (auto& s : shapes) {
+    int64_t tiles = ceil_div(M, s[0]) * ceil_div(N, s[1]) * batch;
+    v.tile_rows = s[0];
+    v.tile_columns = s[1];
+    if (tiles >= target) return v;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Packing and conversion kernels
+// ---------------------------------------------------------------------------
+
+namespace {
+
+template <typename TS, typename TD>
+__global__ void pack_transpose_kernel(const TS* __restrict__ src, int K, int N, int64_t ld_src, TD* __restrict__ dst,
+                                      int64_t ld_dst) {
+  __shared__ float tile[32][33];
+  int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int r = ty; r < 32; r += 8) {
+    int k = k0 + r, n = n0 + tx;
+    tile[r][tx] = (k < K && n < N) ? (float)src[(int64_t)k * ld_src + n] : 0.0f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    int n = n0 + r, k = k0 + tx;
+    if (n < N && k < K) dst[(int64_t)n * ld_dst + k] = (TD)tile[tx][r];
+  }
+}
+
+template <typename TD>
+__global__ void convert_kernel(const float* __restrict__ src, int64_t count, TD* __restrict__ dst) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < count; i += stride) dst[i] = (TD)src[i];
+}
+
+__global__ void dequant_channel_kernel(const int8_t* __restrict__ q, const float* __restrict__ scale, int K, int N,
+                                       float* __restrict__ out) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t total = (int64_t)K * N;
+  if (i >= total) return;
+  int n = (int)(i % N);
+  // One correctly rounded product; __fmul_rn keeps it from being contracted.
+  out[i] = __fmul_rn((float)q[i], scale[n]);
+}
+
+__global__ void dequant_block_kernel(const int8_t* __restrict__ codes, const uint16_t* __restrict__ scales, int block,
+                                     int64_t start, int64_t count, float* __restrict__ out) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  int64_t absolute = start + i;
+  __half_raw raw;
+  raw.x = scales[absolute / block];
+  float s = __half2float(__half(raw));
+  out[i] = __fmul_rn((float)codes[absolute], s);
+}
+
+template <typename TS>
+int pack_dispatch(const TS* src, int K, int N, int64_t ld_src, void* dst, int dst_dtype, int64_t ld_dst,
+                  hipStream_t s) {
+  dim3 grid((unsigned)ceil_div(N, 32), (unsigned)ceil_div(K, 32));
+  if (dst_dtype == AFHIP_F32)
+    return launch("pack_transpose", pack_transpose_kernel<TS, float>, grid, dim3(256), 0, s, src, K, N, ld_src,
+                  (float*)dst, ld_dst);
+  if (dst_dtype == AFHIP_F16)
+    return launch("pack_transpose", pack_transpose_kernel<TS, half_t>, grid, dim3(256), 0, s, src, K, N, ld_src,
+                  (half_t*)dst, ld_dst);
+  return launch("pack_transpose", pack_transpose_kernel<TS, int8_t>, grid, dim3(256), 0, s, src, K, N, ld_src,
+                (int8_t*)dst, ld_dst);
+}
+
+}  // namespace
+
+int pack_transpose(const void* src, int src_dtype, int K, int N, int64_t ld_src, void* dst, int dst_dtype,
+                   int64_t ld_dst, hipStream_t s) {
+  AFHIP_REQUIRE(src && dst && K > 0 && N > 0, "invalid weight pack arguments");
+  AFHIP_REQUIRE(src_dtype != AFHIP_I8 || dst_dtype == AFHIP_I8, "int8 weights pack to int8 only");
+  if (src_dtype == AFHIP_F32) return pack_dispatch((const float*)src, K, N, ld_src, dst, dst_dtype, ld_dst, s);
+  if (src_dtype == AFHIP_F16) return pack_dispatch((const half_t*)src, K, N, ld_src, dst, dst_dtype, ld_dst, s);
+  return pack_dispatch((const int8_t*)src, K, N, ld_src, dst, dst_dtype, ld_dst, s);
+}
+
+int convert_f32(const float* src, int64_t count, void* dst, int dst_dtype, hipStream_t s) {
+  if (count <= 0) return AFHIP_OK;
+  unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(count, 256), 65536);
+  if (dst_dtype == AFHIP_F32)
+    return launch("convert", convert_kernel<float>, dim3(blocks), dim3(256), 0, s, src, count, (float*)dst);
+  return launch("convert", convert_kernel<half_t>, dim3(blocks), dim3(256), 0, s, src, count, (half_t*)dst);
+}
+
+// ---------------------------------------------------------------------------
+// Selection: pinned > calibrated > heuristic
+// ---------------------------------------------------------------------------
+
+namespace {
+std::mutex g_select_mutex;
+bool g_pinned = false;
+afhip_variant g_pin{};
+std::map<std::string, afhip_variant> g_calibrated;
+
+int log2_bucket(int64_t v) {
+  int b = 0;
+  while (v > 1) { v >>= 1; b++; }
+  return b;
+}
+}  // namespace
+
+std::string device_key();
+
+std::string shape_class(const GemmTypes& t, int64_t M, int64_t N, int64_t K, int batch) {
+  char key[160];
+  snprintf(key, sizeof(key), "p%d.a%d.w%d.c%d.m%d.n%d.k%d.b%d", t.precision, t.a_dtype, t.b_dtype, t.c_dtype,
+           log2_bucket(M), log2_bucket(N), log2_bucket(K), log2_bucket(batch));
+  return key;
+}
+
+afhip_variant select_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K, int batch) {
+  std::lock_guard<std::mutex> lock(g_select_mutex);
+  if (g_pinned) {
+    afhip_variant v = g_pin;
+    v.precision = t.precision;
+    v.source = 2;
+    return v;
+  }
+  if (!g_calibrated.empty()) {
+    auto it = g_calibrated.find(device_key() + "|" + shape_class(t, M, N, K, batch));
+    if (it != g_calibrated.end()) return it->second;
+  }
+  return heuristic_variant(t.precision, M, N, K, batch);
+}
+
+void install_calibrated(const std::string& key, const afhip_variant& v) {
+  std::lock_guard<std::mutex> lock(g_select_mutex);
+  g_calibrated[key] = v;
+}
+
+std::map<std::string, afhip_variant> calibrated_snapshot() {
+  std::lock_guard<std::mutex> lock(g_select_mutex);
+  return g_calibrated;
+}
+
+void replace_calibrated(const std::map<std::string, afhip_variant>& m) {
+  std::lock_guard<std::mutex> lock(g_select_mutex);
+  g_calibrated = m;
+}
+
+bool valid_variant(const afhip_variant& v) {
+  return (v.tile_rows == 64 || v.tile_rows == 128) && (v.tile_columns == 64 || v.tile_columns == 128) &&
+         v.tile_inner == gemm_detail::kBK && valid_precision(v.precision);
+}
+
+void pin_variant(const afhip_variant* v) {
+  std::lock_guard<std::mutex> lock(g_select_mutex);
+  g_pinned = v != nullptr;
+  if (v) g_pin = *v;
+}
+
+}  // namespace afhip
+
+// ---------------------------------------------------------------------------
+// C ABI: plans
+// ---------------------------------------------------------------------------
+
+struct afhip_gemm_plan {
+  afhip_gemm_desc desc;
+  afhip::GemmTypes types;
+  afhip_variant variant;
+  int64_t lda, ldw, ldc;
+};
+
+using namespace afhip;
+
+extern "C" {
+
+int afhip_gemm_grid(int64_t rows, int64_t columns, int32_t tile_columns, int32_t tile_rows, uint32_t out_xy[2]) {
+  AFHIP_REQUIRE(out_xy != nullptr, "output is NULL");
+  AFHIP_REQUIRE(rows > 0 && columns > 0 && rows <= ((int64_t)1 << 53) && columns <= ((int64_t)1 << 53),
+                "GEMM dispatch dimensions must be positive safe integers");
+  AFHIP_REQUIRE(tile_columns > 0 && tile_rows > 0, "tile sizes must be positive");
+  const int64_t limit = 65535;
+  int64_t column_tiles = ceil_div(columns, tile_columns);
+  int64_t row_tiles = ceil_div(rows, tile_rows);
+  int64_t folds = ceil_div(row_tiles, limit);
+  int64_t x = column_tiles * folds, y = row_tiles < limit ? row_tiles : limit;
+  AFHIP_REQUIRE(x <= 0xffffffffll, "grid too large");
+  out_xy[0] = (uint32_t)x;
+  out_xy[1] = (uint32_t)y;
+  return AFHIP_OK;
+}
+
+static int validate_desc(const afhip_gemm_desc* d) {
+  AFHIP_REQUIRE(d != nullptr, "descriptor is NULL");
+  AFHIP_REQUIRE(d->rows > 0 && d->inner > 0 && d->columns > 0 && d->batch > 0,
+                "GEMM dimensions must be positive (rows=%d inner=%d columns=%d batch=%d)", d->rows, d->inner,
+                d->columns, d->batch);
+  AFHIP_REQUIRE(valid_precision(d->precision), "unknown precision %d", d->precision);
+  AFHIP_REQUIRE(valid_float_dtype(d->a_dtype), "a_dtype must be F32 or F16");
+  AFHIP_REQUIRE(valid_float_dtype(d->w_dtype) || d->w_dtype == AFHIP_I8, "w_dtype must be F32, F16 or I8");
+  AFHIP_REQUIRE(valid_float_dtype(d->out_dtype), "out_dtype must be F32 or F16");
+  AFHIP_REQUIRE(d->w_layout == AFHIP_WEIGHT_COLUMN_CONTIGUOUS || d->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS,
+                "unknown weight layout %d", d->w_layout);
+  AFHIP_REQUIRE((d->epilogue & ~31u) == 0, "unknown epilogue flags 0x%x", d->epilogue);
+  if (d->epilogue & AFHIP_EPILOGUE_ATTENTION)
+    AFHIP_REQUIRE(d->heads > 0 && d->head_dim > 0 && d->columns == 4 * d->heads * d->head_dim,
+                  "attention epilogue needs columns == 4 * heads * head_dim");
+  AFHIP_REQUIRE(!(d->w_dtype == AFHIP_I8 && d->precision == AFHIP_PRECISION_F32),
+                "int8 weights need f16 precision");
+  AFHIP_REQUIRE(!(d->precision == AFHIP_PRECISION_F32 && d->a_dtype != AFHIP_F32),
+                "f32 precision needs an f32 source");
+  AFHIP_REQUIRE(!(d->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS && d->w_dtype != AFHIP_I8 &&
+                  d->w_dtype != (d->precision == AFHIP_PRECISION_F16 ? AFHIP_F16 : AFHIP_F32)),
+                "k-contiguous weights must be given in the precision's dtype (f16 for f16, f32 for f32)");
+  int64_t lda = d->lda ? d->lda : d->inner;
+  int64_t ldw = d->ldw ? d->ldw : (d->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS ? d->inner : d->columns);
+  int64_t ldc = d->ldc ? d->ldc : d->columns;
+  AFHIP_REQUIRE(lda >= d->inner, "lda %lld < inner %d", (long long)lda, d->inner);
+  AFHIP_REQUIRE(ldw >= (d->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS ? d->inner : d->columns), "ldw too small");
+  AFHIP_REQUIRE(ldc >= d->columns, "ldc %lld < columns %d", (long long)ldc, d->columns);
+  if (d->batch > 1)
+    AFHIP_REQUIRE(d->batch_stride_a >= 0 && d->batch_stride_w >= 0 && d->batch_stride_c > 0,
+                  "batched GEMM needs batch strides");
+  return AFHIP_OK;
+}
+
+int afhip_gemm_plan_create(const afhip_gemm_desc* desc, afhip_gemm_plan** out) {
+  if (int s = validate_desc(desc)) return s;
+  AFHIP_REQUIRE(out != nullptr, "output pointer is NULL");
+  auto* p = new (std::nothrow) afhip_gemm_plan;
+  if (!p) return set_error(AFHIP_ERR_OUT_OF_MEMORY, "plan allocation failed");
+  p->desc = *desc;
+  p->types = {desc->precision, desc->a_dtype, desc->w_dtype, desc->out_dtype};
+  p->lda = desc->lda ? desc->lda : desc->inner;
+  p->ldw = desc->ldw ? desc->ldw : (desc->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS ? desc->inner : desc->columns);
+  p->ldc = desc->ldc ? desc->ldc : desc->columns;
+  p->variant = select_variant(p->types, desc->rows, desc->columns, desc->inner, desc->batch);
+  *out = p;
+  return AFHIP_OK;
+}
+
+int afhip_gemm_plan_destroy(afhip_gemm_plan* plan) {
+  delete plan;
+  return AFHIP_OK;
+}
+
+// The weight dtype the kernels read for a precision: f16 (or int8) under f16
+// arithmetic, f32 under f32 arithmetic.
+static int kernel_w_dtype(const afhip_gemm_desc& d) {
+  if (d.precision == AFHIP_PRECISION_F16) return d.w_dtype == AFHIP_I8 ? AFHIP_I8 : AFHIP_F16;
+  return AFHIP_F32;
+}
+
+// Only a column-contiguous weight is rewritten per run (transposed, and
+// converted to the kernel's dtype on the way); a k-contiguous one must
+// already be in that dtype, which plan creation checks.
+static bool needs_weight_workspace(const afhip_gemm_desc& d) {
+  return d.w_layout == AFHIP_WEIGHT_COLUMN_CONTIGUOUS;
+}
+
+int afhip_gemm_workspace_size(const afhip_gemm_plan* plan, size_t* bytes) {
+  AFHIP_REQUIRE(plan && bytes, "NULL plan or output");
+  const auto& d = plan->desc;
+  if (needs_weight_workspace(d)) {
+    size_t one = (size_t)d.inner * d.columns * dtype_size(kernel_w_dtype(d));
+    size_t n = d.batch_stride_w == 0 ? 1 : (size_t)d.batch;
+    *bytes = round_up((int64_t)(one * n), 256);
+  } else {
+    *bytes = 0;
+  }
+  return AFHIP_OK;
+}
+
+int afhip_gemm_run(const afhip_gemm_plan* plan, const void* a, const void* w, const float* scale, const float* bias,
+                   const void* residual, void* c, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int s = require_open()) return s;
+  AFHIP_REQUIRE(plan != nullptr, "plan is NULL");
+  const auto& d = plan->desc;
+  hipStream_t st = (hipStream_t)stream;
+  GemmArgs g;
+  g.a = a;
+  g.b = w;
+  g.c = c;
+  g.residual = residual;
+  g.scale = scale;
+  g.bias = bias;
+  g.M = d.rows;
+  g.N = d.columns;
+  g.K = d.inner;
+  g.lda = plan->lda;
+  g.ldb = plan->ldw;
+  g.ldc = plan->ldc;
+  g.sa = d.batch_stride_a;
+  g.sb = d.batch_stride_w;
+  g.sc = d.batch_stride_c;
+  g.batch = d.batch;
+  g.flags = d.epilogue;
+  if (d.epilogue & AFHIP_EPILOGUE_ATTENTION) {
+    g.head_cols = d.heads * d.head_dim;
+    g.q_scale = (float)(1.0 / std::sqrt((double)d.head_dim));
+  }
+  GemmTypes types = plan->types;
+  if (needs_weight_workspace(d)) {
+    size_t need = 0;
+    afhip_gemm_workspace_size(plan, &need);
+    AFHIP_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+                  "these weights need a %zu-byte workspace to be laid out for the kernel", need);
+    AFHIP_REQUIRE(w != nullptr, "weight is NULL");
+    const int kd = kernel_w_dtype(d);
+    int nb = d.batch_stride_w == 0 ? 1 : d.batch;
+    size_t es = dtype_size(d.w_dtype), kes = dtype_size(kd);
+    for (int b = 0; b < nb; b++) {
+      const char* src = (const char*)w + (size_t)b * d.batch_stride_w * es;
+      char* dst = (char*)workspace + (size_t)b * d.inner * d.columns * kes;
+      if (int s = pack_transpose(src, d.w_dtype, d.inner, d.columns, plan->ldw, dst, kd, d.inner, st)) return s;
+    }
+    g.b = workspace;
+    g.ldb = d.inner;
+    g.sb = d.batch_stride_w == 0 ? 0 : (int64_t)d.inner * d.columns;
+    types.b_dtype = kd;
+  }
+  return run_gemm(g, types, plan->variant, "gemm", st);
+}
+
+int afhip_pack_weight(const void* src, int32_t src_dtype, int32_t rows_k, int32_t columns_n, void* dst,
+                      int32_t dst_dtype, void* stream) {
+  if (int s = require_open()) return s;
+  return pack_transpose(src, src_dtype, rows_k, columns_n, columns_n, dst, dst_dtype, rows_k, (hipStream_t)stream);
+}
+
+int afhip_dequant_q8_channel(const int8_t* q, const float* scale, int32_t rows_k, int32_t columns_n, float* out,
+                             void* stream) {
+  if (int s = require_open()) return s;
+  AFHIP_REQUIRE(q && scale && out && rows_k > 0 && columns_n > 0, "invalid dequantisation arguments");
+  int64_t total = (int64_t)rows_k * columns_n;
+  return launch("dequant_q8_channel", dequant_channel_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
+                (hipStream_t)stream, q, scale, rows_k, columns_n, out);
+}
+
+int afhip_dequant_q8_block(const int8_t* codes, const uint16_t* scales_f16, int32_t block, int64_t start, int64_t count,
+                           float* out, void* stream) {
+  if (int s = require_open()) return s;
+  AFHIP_REQUIRE(codes && scales_f16 && out, "NULL argument");
+  AFHIP_REQUIRE(block > 0, "int8 tensor has an invalid block size");
+  AFHIP_REQUIRE(start >= 0 && count >= 0, "tensor range is out of bounds");
+  if (count == 0) return AFHIP_OK;
+  return launch("dequant_q8_block", dequant_block_kernel, dim3((unsigned)ceil_div(count, 256)), dim3(256), 0,
+                (hipStream_t)stream, codes, scales_f16, block, start, count, out);
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+// Internal definitions shared by the afhip translation units (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/afhip.h"
+
+namespace afhip {
+
+// ---------------------------------------------------------------------------
+// Errors: every entry point funnels failures through set_error and returns a
+// status; no exception leaves the library.
+// ---------------------------------------------------------------------------
+int set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_status(hipError_t err, const char* what);
+
+#define AFHIP_CHECK_HIP(expr)                                   \
+  do {                                                          \
+    hipError_t err__ = (expr);                                  \
+    if (err__ != hipSuccess) return ::afhip::hip_status(err__, #expr); \
+  } while (0)
+
+#define AFHIP_REQUIRE(cond, ...)                                          \
+  do {                                                                    \
+    if (!(cond)) return ::afhip::set_error(AFHIP_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+bool is_open();
+int require_open();
+int device_cu_count();
+
+// ---------------------------------------------------------------------------
+// Kernel timing: launches go through launch_timed so a label can be
+// bracketed by hipEvents when timing is enabled.
+// ---------------------------------------------------------------------------
+bool timing_enabled();
+void timing_begin(const char* label, hipStream_t stream);
+void timing_end(const char* label, hipStream_t stream);
+
+// Raises a kernel's dynamic LDS ceiling to `bytes` (gfx950 grants up to
+// 160 KiB a workgroup); once per kernel and size.
+int allow_lds(const void* kernel, size_t bytes);
+
+template <typename Kernel, typename... Args>
+int launch(const char* label, Kernel kernel, dim3 grid, dim3 block, size_t shared, hipStream_t stream,
+           Args... args) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return AFHIP_OK;
+  const bool timed = timing_enabled();
+  if (timed) timing_begin(label, stream);
+  hipLaunchKernelGGL(kernel, grid, block, shared, stream, args...);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return hip_status(err, label);
+  if (timed) timing_end(label, stream);
+  return AFHIP_OK;
+}
+
+inline size_t dtype_size(int dtype) { return dtype == AFHIP_F32 ? 4 : dtype == AFHIP_F16 ? 2 : 1; }
+inline bool valid_float_dtype(int d) { return d == AFHIP_F32 || d == AFHIP_F16; }
+inline bool valid_precision(int p) { return p == AFHIP_PRECISION_F32 || p == AFHIP_PRECISION_F16; }
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// ---------------------------------------------------------------------------
+// Device-side vocabulary
+// ---------------------------------------------------------------------------
+typedef _Float16 half_t;
+typedef half_t half8 __attribute__((ext_vector_type(8)));
+typedef half_t half4 __attribute__((ext_vector_type(4)));
+typedef half_t half2v __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// The MFMA tile every kernel here is written against: 32 x 32 output per
+// wave64 instruction. Lane l owns output column (l % 32) and rows
+//   8 * (v / 4) + 4 * (l / 32) + (v % 4),  v = 0..15.
+// f16: A fragment = A[l % 32][8*(l/32) .. +8), B fragment = B[8*(l/32) .. +8][l % 32] (K = 16).
+// f32: A fragment = A[l % 32][l / 32],         B fragment = B[l / 32][l % 32]          (K = 2).
+__device__ __forceinline__ int mfma_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
+
+__device__ __forceinline__ floatx16 mfma_f16(half8 a, half8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx16 mfma_f32(float a, float b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+template <typename T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }
+
+}  // namespace afhip

@@ -1,0 +1,405 @@
+// Outer-product mean for gfx950.
+//
+// The reference (src/evoformer/outer-product-mean.ts:549-646) runs normalize,
+// project, pair-count, then per residue block a contraction and an output
+// projection. Here:
+//
+//  1. opm_project: LayerNorm of 64 MSA rows in LDS and both projections on
+//     MFMA, mask*(x + b). Rows are visited residue-major (row r = i*S + s
+//     reads MSA row (s, i)), so each output channel (i, a) receives a run of
+//     consecutive sequences: left and right are stored [L*c_o][S], the
+//     contraction axis contiguous, which is the k-contiguous operand layout
+//     the shared GEMM stages with 16-byte loads.
+//  2. opm_pair_count: count[i][j] = sum_s mask[s][i] mask[s][j] (:317-332).
+//  3. per residue block, the contraction through the shared GEMM,
+//     outer[i][j][a][b] = sum_s left[s][i][a] right[s][j][b] / (eps + count),
+//     divided in its epilogue as the reference's contraction does
+//     (:350-417), then the output projection through the shared GEMM with
+//     the bias scaled by the same 1/(eps + count) (:433-481).
+#include <algorithm>
+#include <cmath>
+
+#include "gemm.h"
+
+namespace afhip {
+
+namespace {
+
+constexpr int kRows = 64;
+
+struct OpmWeights {
+  size_t ln_scale, ln_offset, w_lr, b_lr, w_out, b_out, total;
+  int cmp;  // c_m padded to 32
+  int cop;  // 2 * c_outer padded to 64 (projection columns)
+  int czp;  // c_z padded to 32 (output rows of W_out^T)
+};
+
+OpmWeights opm_layout(const afhip_opm_desc& d) {
+  OpmWeights w{};
+  size_t es = d.precision == AFHIP_PRECISION_F16 ? 2 : 4;
+  w.cmp = (int)round_up(d.c_m, 32);
+  w.cop = (int)round_up(2 * d.c_outer, 64);
+  w.czp = (int)round_up(d.c_z, 32);
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    size_t here = at;
+    at = round_up((int64_t)(at + bytes), 256);
+    return here;
+  };
+  w.ln_scale = take(4 * (size_t)d.c_m);
+  w.ln_offset = take(4 * (size_t)d.c_m);
+  w.w_lr = take(es * (size_t)w.cop * w.cmp);
+  w.b_lr = take(4 * (size_t)w.cop);
+  w.w_out = take(es * (size_t)w.czp * d.c_outer * d.c_outer);
+  w.b_out = take(4 * (size_t)w.czp);
+  w.total = at;
+  return w;
+}
+
+struct OpmWorkspace {
+  size_t left, right, outer, count, total;
+  int64_t sp;  // sequence stride of left/right rows
+  int row_block;
+};
+
+OpmWorkspace opm_workspace(const afhip_opm_desc& d) {
+  OpmWorkspace w{};
+  size_t es = d.precision == AFHIP_PRECISION_F16 ? 2 : 4;
+  w.sp = round_up(d.sequences, 8);
+  w.row_block = d.row_block > 0 ? std::min(d.row_block, d.length) : d.length;
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    size_t here = at;
+    at = round_up((int64_t)(at + bytes), 256);
+    return here;
+  };
+  const size_t rows = (size_t)d.length * d.c_outer;
+  w.left = take(es * rows * w.sp);
+  w.right = take(es * rows * w.sp);
+  w.outer = take(es * (size_t)w.row_block * d.length * d.c_outer * d.c_outer);
+  w.count = take(4 * (size_t)d.length * d.length);
+  w.total = at;
+  return w;
+}
+
+struct ProjectArgs {
+  const void* msa;
+  const float* mask;
+  const float* ln_scale;
+  const float* ln_offset;
+  const void* w_lr;  // [cop][cmp]: rows [0, co) left, [co, 2co) right
+  const float* b_lr;
+  void* left;
+  void* right;
+  int64_t sp;
+  int S, L, cm, co, cmp, cop;
+  float eps;
+};
+
+template <typename MT, bool F16MATH>
+__global__ __launch_bounds__(256) void opm_project_kernel(ProjectArgs a) {
+  using CT = typename std::conditional<F16MATH, half_t, float>::type;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int xpitch = kRows + 1;
+  float* xs = reinterpret_cast<float*>(smem);
+  size_t off = round_up((int64_t)a.cmp * xpitch * 4, 16);
+  CT* an = reinterpret_cast<CT*>(smem + off);
+  const int apitch = a.cmp + 8;
+  if (F16MATH) off += round_up((int64_t)kRows * apitch * 2, 16);
+  CT* stage = reinterpret_cast<CT*>(smem + off);
+  constexpr int spitch = kRows + 8;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rows = a.S * a.L;
+  const int r0 = blockIdx.x * kRows;
+  const MT* msa = reinterpret_cast<const MT*>(a.msa);
+
+  for (int idx = tid; idx < kRows * a.cmp; idx += 256) {
+    const int i = idx / a.cmp, c = idx - i * a.cmp;
+    const int r = r0 + i;
+    float v = 0.0f;
+    if (r < rows && c < a.cm) {
+      const int res = r / a.S, s = r - res * a.S;
+      v = (float)msa[((int64_t)s * a.L + res) * a.cm + c];
+    }
+    xs[c * xpitch + i] = v;
+  }
+  __syncthreads();
+  {
+    const int q = tid >> 2, part = tid & 3;
+    float sum = 0.0f;
+    for (int c = part; c < a.cm; c += 4) sum += xs[c * xpitch + q];
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    const float mean = sum / (float)a.cm;
+    float var = 0.0f;
+    for (int c = part; c < a.cm; c += 4) {
+      float d = xs[c * xpitch + q] - mean;
+      var += d * d;
+    }
+    var += __shfl_xor(var, 1);
+    var += __shfl_xor(var, 2);
+    const float rstd = 1.0f / sqrtf(var / (float)a.cm + a.eps);
+    for (int c = part; c < a.cmp; c += 4) {
+      float v = c < a.cm ? (xs[c * xpitch + q] - mean) * rstd * a.ln_scale[c] + a.ln_offset[c] : 0.0f;
+      if (F16MATH) an[q * apitch + c] = (CT)v;
+      else xs[c * xpitch + q] = v;
+    }
+  }
+  __syncthreads();
+
+  const CT* W = reinterpret_cast<const CT*>(a.w_lr);
+  const int rw = 32 * (wave & 1);
+  for (int n0 = 0; n0 < a.cop; n0 += 64) {
+    const int nc = n0 + 32 * (wave >> 1);
+    floatx16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+    const int n = nc + (lane & 31);
+    if constexpr (F16MATH) {
+      for (int k = 0; k < a.cmp; k += 16) {
+        const int kk = k + 8 * (lane >> 5);
+        half8 af = *reinterpret_cast<const half8*>(an + (rw + (lane & 31)) * apitch + kk);
+        half8 bf = *reinterpret_cast<const half8*>(W + (size_t)n * a.cmp + kk);
+        acc = mfma_f16(af, bf, acc);
+      }
+    } else {
+      for (int k = 0; k < a.cmp; k += 2) {
+        const int kk = k + (lane >> 5);
+        acc = mfma_f32(xs[kk * xpitch + rw + (lane & 31)], W[(size_t)n * a.cmp + kk], acc);
+      }
+    }
+    const float bias = a.b_lr[n];
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int i = rw + mfma_row(v, lane);
+      const int r = r0 + i;
+      float val = 0.0f;
+      if (r < rows) {
+        const int res = r / a.S, s = r - res * a.S;
+        val = a.mask[(int64_t)s * a.L + res] * (acc[v] + bias);
+      }
+      stage[(n - n0) * spitch + i] = (CT)val;
+    }
+    __syncthreads();
+    // Channel (res, o) of left or right receives this tile's run of sequences.
+    for (int idx = tid; idx < 64 * kRows; idx += 256) {
+      const int nl = idx / kRows, i = idx - nl * kRows;
+      const int col = n0 + nl, r = r0 + i;
+      if (col >= 2 * a.co || r >= rows) continue;
+      const int res = r / a.S, s = r - res * a.S;
+      const bool is_left = col < a.co;
+      const int o = is_left ? col : col - a.co;
+      CT* dst = reinterpret_cast<CT*>(is_left ? a.left : a.right);
+      dst[((int64_t)res * a.co + o) * a.sp + s] = stage[nl * spitch + i];
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void opm_pair_count_kernel(const float* __restrict__ mask, int S, int L, float* __restrict__ count) {
+  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)L * L) return;
+  const int i = (int)(idx / L), j = (int)(idx % L);
+  float c = 0.0f;
+  for (int s = 0; s < S; s++) c += mask[(int64_t)s * L + i] * mask[(int64_t)s * L + j];
+  count[idx] = c;
+}
+
+template <typename CT>
+__global__ void opm_prepare_kernel(const float* __restrict__ packed, int cm, int co, int cz, int cmp, int cop, int czp,
+                                   CT* __restrict__ w_lr, float* __restrict__ b_lr, CT* __restrict__ w_out,
+                                   float* __restrict__ b_out, float* __restrict__ ln_s, float* __restrict__ ln_o) {
+  const float* ln_scale = packed;
+  const float* ln_offset = ln_scale + cm;
+  const float* left_w = ln_offset + cm;
+  const float* left_b = left_w + (size_t)cm * co;
+  const float* right_w = left_b + co;
+  const float* right_b = right_w + (size_t)cm * co;
+  const float* out_w = right_b + co;
+  const float* out_b = out_w + (size_t)co * co * cz;
+  const int64_t n_lr = (int64_t)cop * cmp, n_out = (int64_t)czp * co * co;
+  const int64_t total = n_lr + n_out + cop + czp + 2 * cm;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    if (i < n_lr) {  // [cop][cmp] <- left/right [cm][co] transposed
+      const int n = (int)(i / cmp), k = (int)(i % cmp);
+      float v = 0.0f;
+      if (k < cm && n < co) v = left_w[(size_t)k * co + n];
+      else if (k < cm && n < 2 * co) v = right_w[(size_t)k * co + (n - co)];
+      w_lr[i] = (CT)v;
+    } else if (i < n_lr + n_out) {  // [czp][co*co] <- out [co*co][cz] transposed
+      const int64_t j = i - n_lr;
+      const int n = (int)(j / (co * co)), k = (int)(j % (co * co));
+      w_out[j] = (CT)(n < cz ? out_w[(size_t)k * cz + n] : 0.0f);
+    } else if (i < n_lr + n_out + cop) {
+      const int n = (int)(i - n_lr - n_out);
+      b_lr[n] = n < co ? left_b[n] : (n < 2 * co ? right_b[n - co] : 0.0f);
+    } else if (i < n_lr + n_out + cop + czp) {
+      const int n = (int)(i - n_lr - n_out - cop);
+      b_out[n] = n < cz ? out_b[n] : 0.0f;
+    } else {
+      const int c = (int)(i - n_lr - n_out - cop - czp);
+      if (c < cm) ln_s[c] = ln_scale[c];
+      else ln_o[c - cm] = ln_offset[c - cm];
+    }
+  }
+}
+
+int validate(const afhip_opm_desc* d) {
+  AFHIP_REQUIRE(d != nullptr, "descriptor is NULL");
+  AFHIP_REQUIRE(d->sequences > 0 && d->length > 0 && d->c_m > 0 && d->c_outer > 0 && d->c_z > 0,
+                "outer product mean dimensions must be positive safe integers");
+  AFHIP_REQUIRE((int64_t)d->sequences * d->length <= (int64_t)1 << 30, "alignment too large");
+  AFHIP_REQUIRE(d->c_m <= 512, "c_m %d exceeds 512", d->c_m);
+  AFHIP_REQUIRE(valid_precision(d->precision), "unknown precision %d", d->precision);
+  AFHIP_REQUIRE(valid_float_dtype(d->msa_dtype) && valid_float_dtype(d->out_dtype), "dtypes must be f32 or f16");
+  AFHIP_REQUIRE(d->row_block >= 0, "rowBlockResidues must be non-negative");
+  AFHIP_REQUIRE(d->layer_norm_epsilon > 0 && d->normalization_epsilon >= 0, "epsilons must be positive");
+  return AFHIP_OK;
+}
+
+template <typename MT, bool F16MATH>
+int launch_project(const ProjectArgs& pa, size_t shared, hipStream_t s) {
+  if (int st = allow_lds((const void*)opm_project_kernel<MT, F16MATH>, shared)) return st;
+  return launch("opm.project", opm_project_kernel<MT, F16MATH>, dim3((unsigned)ceil_div((int64_t)pa.S * pa.L, kRows)),
+                dim3(256), shared, s, pa);
+}
+
+}  // namespace
+
+}  // namespace afhip
+
+using namespace afhip;
+
+extern "C" {
+
+int afhip_opm_weights_size(const afhip_opm_desc* desc, size_t* bytes) {
+  if (int s = validate(desc)) return s;
+  AFHIP_REQUIRE(bytes != nullptr, "output is NULL");
+  *bytes = opm_layout(*desc).total;
+  return AFHIP_OK;
+}
+
+int afhip_opm_workspace_size(const afhip_opm_desc* desc, size_t* bytes) {
+  if (int s = validate(desc)) return s;
+  AFHIP_REQUIRE(bytes != nullptr, "output is NULL");
+  *bytes = opm_workspace(*desc).total;
+  return AFHIP_OK;
+}
+
+int afhip_opm_prepare_weights(const afhip_opm_desc* desc, const float* packed, void* prepared, void* stream) {
+  if (int s = require_open()) return s;
+  if (int s = validate(desc)) return s;
+  AFHIP_REQUIRE(packed && prepared, "NULL weights");
+  const auto& d = *desc;
+  const OpmWeights w = opm_layout(d);
+  char* base = (char*)prepared;
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid(1024), block(256);
+  float* ln_s = (float*)(base + w.ln_scale);
+  float* ln_o = (float*)(base + w.ln_offset);
+  if (d.precision == AFHIP_PRECISION_F16) {
+    if (int s = launch("opm.prepare", opm_prepare_kernel<half_t>, grid, block, 0, st, packed, d.c_m, d.c_outer, d.c_z,
+                       w.cmp, w.cop, w.czp, (half_t*)(base + w.w_lr), (float*)(base + w.b_lr),
+                       (half_t*)(base + w.w_out), (float*)(base + w.b_out), ln_s, ln_o))
+      return s;
+  } else {
+    if (int s = launch("opm.prepare", opm_prepare_kernel<float>, grid, block, 0, st, packed, d.c_m, d.c_outer, d.c_z,
+                       w.cmp, w.cop, w.czp, (float*)(base + w.w_lr), (float*)(base + w.b_lr),
+                       (float*)(base + w.w_out), (float*)(base + w.b_out), ln_s, ln_o))
+      return s;
+  }
+  return AFHIP_OK;
+}
+
+int afhip_opm_run(const afhip_opm_desc* desc, const void* activations, const float* mask, const void* prepared,
+                  void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int s = require_open()) return s;
+  if (int s = validate(desc)) return s;
+  AFHIP_REQUIRE(activations && mask && prepared && out, "NULL tensor");
+  const auto& d = *desc;
+  const OpmWeights w = opm_layout(d);
+  const OpmWorkspace ws = opm_workspace(d);
+  AFHIP_REQUIRE(workspace != nullptr && workspace_bytes >= ws.total, "workspace of %zu bytes is smaller than %zu",
+                workspace_bytes, ws.total);
+  hipStream_t st = (hipStream_t)stream;
+  const bool f16 = d.precision == AFHIP_PRECISION_F16;
+  const char* wb = (const char*)prepared;
+  char* wsb = (char*)workspace;
+  const int S = d.sequences, L = d.length, co = d.c_outer;
+
+  ProjectArgs pa{};
+  pa.msa = activations;
+  pa.mask = mask;
+  pa.ln_scale = (const float*)(wb + w.ln_scale);
+  pa.ln_offset = (const float*)(wb + w.ln_offset);
+  pa.w_lr = wb + w.w_lr;
+  pa.b_lr = (const float*)(wb + w.b_lr);
+  pa.left = wsb + ws.left;
+  pa.right = wsb + ws.right;
+  pa.sp = ws.sp;
+  pa.S = S;
+  pa.L = L;
+  pa.cm = d.c_m;
+  pa.co = co;
+  pa.cmp = w.cmp;
+  pa.cop = w.cop;
+  pa.eps = d.layer_norm_epsilon;
+  size_t psh = round_up((int64_t)w.cmp * (kRows + 1) * 4, 16) +
+               (f16 ? round_up((int64_t)kRows * (w.cmp + 8) * 2, 16) : 0) + (size_t)64 * (kRows + 8) * (f16 ? 2 : 4);
+  int s;
+  if (f16) s = d.msa_dtype == AFHIP_F32 ? launch_project<float, true>(pa, psh, st) : launch_project<half_t, true>(pa, psh, st);
+  else s = d.msa_dtype == AFHIP_F32 ? launch_project<float, false>(pa, psh, st) : launch_project<half_t, false>(pa, psh, st);
+  if (s) return s;
+
+  float* count = (float*)(wsb + ws.count);
+  if ((s = launch("opm.pair_count", opm_pair_count_kernel, dim3((unsigned)ceil_div((int64_t)L * L, 256)), dim3(256), 0,
+                  st, mask, S, L, count)))
+    return s;
+
+  const int ct = f16 ? AFHIP_F16 : AFHIP_F32;
+  const size_t es = f16 ? 2 : 4;
+  for (int i0 = 0; i0 < L; i0 += ws.row_block) {
+    const int cnt = std::min(ws.row_block, L - i0);
+    GemmArgs g;
+    g.a = wsb + ws.left + es * (size_t)i0 * co * ws.sp;
+    g.b = wsb + ws.right;
+    g.c = wsb + ws.outer;
+    g.M = cnt * co;
+    g.N = L * co;
+    g.K = S;
+    g.lda = ws.sp;
+    g.ldb = ws.sp;
+    g.ldc = L * co;
+    g.flags = EPILOGUE_OPM_CONTRACT;
+    g.opm_count = count;
+    g.opm_outer = co;
+    g.opm_length = L;
+    g.opm_row0 = i0;
+    g.opm_eps = d.normalization_epsilon;
+    GemmTypes t1{d.precision, ct, ct, ct};
+    if ((s = run_gemm(g, t1, select_variant(t1, g.M, g.N, g.K, 1), "opm.contract", st))) return s;
+
+    GemmArgs h;
+    h.a = wsb + ws.outer;
+    h.b = wb + w.w_out;
+    h.c = (char*)out + dtype_size(d.out_dtype) * (size_t)i0 * L * d.c_z;
+    h.residual = h.c;
+    h.bias = (const float*)(wb + w.b_out);
+    h.M = cnt * L;
+    h.N = d.c_z;
+    h.K = co * co;
+    h.lda = co * co;
+    h.ldb = co * co;
+    h.ldc = d.c_z;
+    h.flags = EPILOGUE_OPM_OUTPUT | (d.residual ? AFHIP_EPILOGUE_RESIDUAL : 0u);
+    h.opm_count = count;
+    h.opm_row0 = i0 * L;
+    h.opm_eps = d.normalization_epsilon;
+    GemmTypes t2{d.precision, ct, ct, d.out_dtype};
+    if ((s = run_gemm(h, t2, select_variant(t2, h.M, h.N, h.K, 1), "opm.output", st))) return s;
+  }
+  return AFHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,320 @@
+/*
+ * afhip — MI355X (gfx950) kernels for alphafold2-webgpu's matrix-multiplication
+ * hot path, behind a C ABI.
+ *
+ * Conventions
+ *  - Every entry point returns an int status (AFHIP_OK or a negative code) and
+ *    never lets a C++ exception cross the boundary. The message of the last
+ *    failure on the calling thread is afhip_last_error().
+ *  - Tensor arguments are device pointers (HBM). A caller without its own
+ *    allocator uses afhip_buffer_*; a caller with one (PyTorch, a HIP
+ *    execution layer) passes its own pointers.
+ *  - `stream` is a hipStream_t passed as void*; NULL is the null stream.
+ *    Launches are asynchronous on that stream.
+ *  - Weights are prepared once by the *_prepare_weights entry points into the
+ *    layout and precision the kernels read (the counterpart of the reference's
+ *    packWeights), then passed to every run.
+ *  - Workspaces are caller-owned; *_workspace_size says how many bytes.
+ *
+ * Reference interfaces replaced are cited as file:line of the
+ * alphafold2-webgpu checkout.
+ */
+#ifndef AFHIP_H
+#define AFHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AFHIP_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define AFHIP_API __attribute__((visibility("default")))
+#else
+#define AFHIP_API
+#endif
+
+/* Status codes. The error vocabulary of the reference: RangeError for shapes
+ * and limits (src/triangle/types.ts:42-52, src/runtime/gemm.ts:372-374) maps
+ * to AFHIP_ERR_INVALID_ARGUMENT; "WebGPU validation failed"
+ * (src/triangle/webgpu.ts:191-192) maps to AFHIP_ERR_HIP. */
+#define AFHIP_OK 0
+#define AFHIP_ERR_INVALID_ARGUMENT (-1)
+#define AFHIP_ERR_OUT_OF_MEMORY (-2)
+#define AFHIP_ERR_HIP (-3)
+#define AFHIP_ERR_UNSUPPORTED (-4)
+#define AFHIP_ERR_NOT_OPEN (-5)
+
+/* Element types. */
+#define AFHIP_F32 0
+#define AFHIP_F16 1
+#define AFHIP_I8 2
+
+/* Arithmetic of a kernel's products and accumulator.
+ * F32: f32 operands, f32 products and sums (MFMA f32).
+ * F16: operands rounded to f16, f32 accumulation (MFMA f16); the reference's
+ *      "matrix" precision with an f16 unit (src/runtime/gemm.ts:150-206).
+ * Pure f16 accumulation is never offered, as SHIPPABLE_GEMM_PRECISIONS
+ * (src/runtime/gemm-selection.ts:160-162) excludes it. */
+#define AFHIP_PRECISION_F32 0
+#define AFHIP_PRECISION_F16 1
+
+/* ---------------------------------------------------------------------- */
+/* Context, errors, device report                                          */
+/* ---------------------------------------------------------------------- */
+
+/* Thread-local message of the last failure; never NULL. */
+AFHIP_API const char* afhip_last_error(void);
+AFHIP_API int afhip_abi_version(void);
+
+/* Selects the device for this process. Replaces request_device
+ * (native/wgpu-backend/src/device.rs:205-255) / requestAlphaFoldDevice
+ * (src/runtime/device.ts:375-467); one context per process, as the wgpu
+ * backend keeps one (device.rs:130-131). */
+AFHIP_API int afhip_open(int device_ordinal);
+AFHIP_API int afhip_close(void);
+
+/* JSON: name, gfx arch, CU count, clocks, LDS, HBM bytes. Replaces the
+ * adapter report of native/wgpu-backend/src/report.rs:61. */
+AFHIP_API int afhip_device_report(char* json, size_t capacity);
+
+/* ---------------------------------------------------------------------- */
+/* Buffers (native/wgpu-backend/src/lib.rs create_buffer, write_buffer,   */
+/* map_buffer, destroy_buffer)                                            */
+/* ---------------------------------------------------------------------- */
+
+AFHIP_API int afhip_buffer_create(size_t bytes, void** out);
+AFHIP_API int afhip_buffer_destroy(void* buffer);
+AFHIP_API int afhip_buffer_write(void* buffer, size_t offset, const void* source, size_t bytes);
+AFHIP_API int afhip_buffer_read(const void* buffer, size_t offset, void* destination, size_t bytes);
+AFHIP_API int afhip_synchronize(void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* GEMM plan and dispatch                                                 */
+/* ---------------------------------------------------------------------- */
+
+/* Epilogue flags, applied in this order to the f32 accumulator:
+ *   SCALE      y *= scale[column]            (mixed-q8 per-channel scale)
+ *   BIAS       y += bias[column]
+ *   ATTENTION  columns [0,heads*head_dim) are q: y *= 1/sqrt(head_dim);
+ *              columns [3*heads*head_dim, 4*heads*head_dim) are the gate:
+ *              y = sigmoid(y); src/evoformer/attention.ts:555-563
+ *   RELU       y = max(y, 0)                  src/evoformer/transition.ts:126
+ *   RESIDUAL   y += residual[row][column]     (may alias the output) */
+#define AFHIP_EPILOGUE_SCALE 1u
+#define AFHIP_EPILOGUE_BIAS 2u
+#define AFHIP_EPILOGUE_ATTENTION 4u
+#define AFHIP_EPILOGUE_RELU 8u
+#define AFHIP_EPILOGUE_RESIDUAL 16u
+
+/* Weight layouts. The reference's weightContiguous (gemm.ts:292-314):
+ * COLUMN is W[k][n] (weights[k*N+n], the linear's layout); K is W[n][k]
+ * (the triangle's [out][in]). */
+#define AFHIP_WEIGHT_COLUMN_CONTIGUOUS 0
+#define AFHIP_WEIGHT_K_CONTIGUOUS 1
+
+/* The plan a caller describes; the counterpart of TiledGemmShader
+ * (src/runtime/gemm.ts:230-339) with its WGSL fragments replaced by an
+ * enumerated description. C[b][m][n] = epilogue(sum_k A[b][m][k] W[b][k][n]).
+ * A is row-major [m][k] with row stride lda. */
+typedef struct afhip_gemm_desc {
+  int32_t rows;          /* M */
+  int32_t inner;         /* K */
+  int32_t columns;       /* N */
+  int32_t batch;         /* >= 1 */
+  int32_t precision;     /* AFHIP_PRECISION_* */
+  int32_t a_dtype;       /* AFHIP_F32 | AFHIP_F16 */
+  int32_t w_dtype;       /* AFHIP_F32 | AFHIP_F16 | AFHIP_I8 */
+  int32_t w_layout;      /* AFHIP_WEIGHT_* */
+  int32_t out_dtype;     /* AFHIP_F32 | AFHIP_F16 */
+  uint32_t epilogue;     /* AFHIP_EPILOGUE_* */
+  int32_t heads;         /* ATTENTION only */
+  int32_t head_dim;      /* ATTENTION only */
+  int64_t lda, ldw, ldc; /* leading dimensions in elements; 0 = packed */
+  int64_t batch_stride_a, batch_stride_w, batch_stride_c; /* elements */
+} afhip_gemm_desc;
+
+typedef struct afhip_gemm_plan afhip_gemm_plan;
+
+/* Validates the description and chooses a kernel (afhip_gemm_select). */
+AFHIP_API int afhip_gemm_plan_create(const afhip_gemm_desc* desc, afhip_gemm_plan** out);
+AFHIP_API int afhip_gemm_plan_destroy(afhip_gemm_plan* plan);
+/* Bytes of device workspace a run needs (a W transpose for the
+ * column-contiguous layout; 0 otherwise). */
+AFHIP_API int afhip_gemm_workspace_size(const afhip_gemm_plan* plan, size_t* bytes);
+/* scale: f32 [N] (SCALE); bias: f32 [N] (BIAS); residual: [M][ldc] of the
+ * output dtype (RESIDUAL). Unused pointers may be NULL. */
+AFHIP_API int afhip_gemm_run(const afhip_gemm_plan* plan, const void* a, const void* w, const float* scale,
+                   const float* bias, const void* residual, void* c, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* gemmGrid (src/runtime/gemm.ts:368-379): the reference's workgroup grid
+ * for an M x N output, row tiles past 65,535 folded into x. Host logic kept
+ * for callers that still size WebGPU-style grids. */
+AFHIP_API int afhip_gemm_grid(int64_t rows, int64_t columns, int32_t tile_columns, int32_t tile_rows,
+                    uint32_t out_xy[2]);
+
+/* The variant the library runs a description with: the counterpart of
+ * GemmVariant (src/runtime/gemm.ts:150-206). */
+typedef struct afhip_variant {
+  int32_t precision;   /* AFHIP_PRECISION_* */
+  int32_t tile_rows;   /* 64 | 128 */
+  int32_t tile_columns;/* 64 | 128 */
+  int32_t tile_inner;  /* 32 */
+  int32_t vectorized;  /* 16-byte operand loads */
+  int32_t source;      /* 0 heuristic, 1 calibrated, 2 pinned */
+} afhip_variant;
+
+/* Shape-driven selection: the calibrated answer for this description's
+ * shape class if one is held, else the heuristic. Replaces gemmVariant()
+ * and gemmVariantCandidates (gemm-selection.ts:234-272). */
+AFHIP_API int afhip_gemm_select(const afhip_gemm_desc* desc, afhip_variant* out);
+/* Measures every candidate tile for the description's shape class on the
+ * open device (correctness check first, then interleaved timing, as
+ * measureGemmVariants does, gemm-selection.ts:471-531), installs and
+ * returns the winner. Replaces calibrateGemmVariant (:560-660). */
+AFHIP_API int afhip_gemm_calibrate(const afhip_gemm_desc* desc, afhip_variant* out);
+/* Pins a variant for every plan created afterwards (NULL unpins); the
+ * counterpart of forceGemmVariant (gemm-selection.ts:122-125). */
+AFHIP_API int afhip_gemm_force_variant(const afhip_variant* variant);
+/* Calibration document (JSON, keyed by device, driver and shape class);
+ * the counterpart of readCalibration/writeCalibration
+ * (src/runtime/calibration-store.ts:119-131). A document that fails
+ * validation is ignored, as isGemmVariant rejects one (gemm-selection.ts:543-558). */
+AFHIP_API int afhip_calibration_load(const char* path);
+AFHIP_API int afhip_calibration_save(const char* path);
+
+/* Weight preparation for GEMM plans: W[k][n] -> W[n][k] (and f32 -> f16 when
+ * dst_dtype is F16). Element types of src and dst given explicitly. */
+AFHIP_API int afhip_pack_weight(const void* src, int32_t src_dtype, int32_t rows_k, int32_t columns_n,
+                      void* dst, int32_t dst_dtype, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Quantised weights                                                       */
+/* ---------------------------------------------------------------------- */
+
+/* Per-output-channel int8: w[k][n] = f32(q[k][n]) * scale[n] (one rounded
+ * product, bit-exact against the closed form). */
+AFHIP_API int afhip_dequant_q8_channel(const int8_t* q, const float* scale, int32_t rows_k, int32_t columns_n,
+                             float* out, void* stream);
+/* The reference bundle's mixed-q8 format: flat blocks of `block` codes, one
+ * f16 scale each; decodes values [start, start+count). Replaces the int8
+ * branch of readTensorRange (src/reference/dtype.ts:66-99). */
+AFHIP_API int afhip_dequant_q8_block(const int8_t* codes, const uint16_t* scales_f16, int32_t block, int64_t start,
+                           int64_t count, float* out, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Triangle multiplication                                                 */
+/* ---------------------------------------------------------------------- */
+
+#define AFHIP_TRIANGLE_OUTGOING 0
+#define AFHIP_TRIANGLE_INCOMING 1
+
+/* Replaces TriangleMultiplication{Outgoing,Incoming}Gpu.run
+ * (src/triangle/webgpu.ts:56-214) and encodeTriangleMultiplication
+ * (src/evoformer/block.ts:1497-1671). */
+typedef struct afhip_triangle_desc {
+  int32_t length;     /* L */
+  int32_t c_z;
+  int32_t c_hidden;
+  int32_t direction;  /* AFHIP_TRIANGLE_* */
+  int32_t precision;  /* AFHIP_PRECISION_* */
+  int32_t pair_dtype; /* z: AFHIP_F32 | AFHIP_F16 */
+  int32_t out_dtype;  /* AFHIP_F32 | AFHIP_F16 */
+  int32_t block_rows; /* output residue rows per block; 0 = all (TriangleGpuOptions.blockRows) */
+  int32_t residual;   /* out += result (the block encoder's residualOutput) */
+  float epsilon;      /* LayerNorm epsilon, 1e-5 by default */
+} afhip_triangle_desc;
+
+/* Bytes of the prepared weight buffer and of the workspace. */
+AFHIP_API int afhip_triangle_weights_size(const afhip_triangle_desc* desc, size_t* bytes);
+AFHIP_API int afhip_triangle_workspace_size(const afhip_triangle_desc* desc, size_t* bytes);
+/* packed: the sixteen f32 tensors in the order of src/triangle/weights.ts:4-10
+ * (ORDER), weights [out][in], as packWeights lays them out (weights.ts:20-34). */
+AFHIP_API int afhip_triangle_prepare_weights(const afhip_triangle_desc* desc, const float* packed, void* prepared,
+                                   void* stream);
+/* z [L][L][c_z]; mask [L][L] f32; out [L][L][c_z]. */
+AFHIP_API int afhip_triangle_run(const afhip_triangle_desc* desc, const void* z, const float* mask,
+                       const void* prepared, void* out, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Outer-product mean                                                      */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces OuterProductMeanGpu.run (src/evoformer/outer-product-mean.ts:549-646)
+ * and encodeOuterProductMean (src/evoformer/block.ts:1115-1246). */
+typedef struct afhip_opm_desc {
+  int32_t sequences;  /* S */
+  int32_t length;     /* L */
+  int32_t c_m;
+  int32_t c_outer;
+  int32_t c_z;
+  int32_t precision;  /* AFHIP_PRECISION_* */
+  int32_t msa_dtype;  /* activations: AFHIP_F32 | AFHIP_F16 */
+  int32_t out_dtype;  /* AFHIP_F32 | AFHIP_F16 */
+  int32_t row_block;  /* residues per contraction block; 0 = all (rowBlockResidues) */
+  int32_t residual;   /* out += result */
+  float layer_norm_epsilon;    /* 1e-5 */
+  float normalization_epsilon; /* 1e-3 */
+} afhip_opm_desc;
+
+AFHIP_API int afhip_opm_weights_size(const afhip_opm_desc* desc, size_t* bytes);
+AFHIP_API int afhip_opm_workspace_size(const afhip_opm_desc* desc, size_t* bytes);
+/* packed: f32 tensors in the order of packOuterProductMeanWeights
+ * (outer-product-mean.ts:64-79): layerNormScale [c_m], layerNormOffset [c_m],
+ * leftWeight [c_m][c_outer], leftBias, rightWeight [c_m][c_outer],
+ * rightBias, outputWeight [c_outer*c_outer][c_z], outputBias [c_z]. */
+AFHIP_API int afhip_opm_prepare_weights(const afhip_opm_desc* desc, const float* packed, void* prepared, void* stream);
+/* activations [S][L][c_m]; mask [S][L] f32; out [L][L][c_z]. */
+AFHIP_API int afhip_opm_run(const afhip_opm_desc* desc, const void* activations, const float* mask, const void* prepared,
+                  void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Transition                                                              */
+/* ---------------------------------------------------------------------- */
+
+/* Replaces TransitionGpu.run (src/evoformer/transition.ts:264-361):
+ * LayerNorm, linear channels->hidden + bias + ReLU, linear hidden->channels + bias. */
+typedef struct afhip_transition_desc {
+  int64_t rows;
+  int32_t channels;
+  int32_t hidden;
+  int32_t precision;  /* AFHIP_PRECISION_* */
+  int32_t in_dtype;   /* AFHIP_F32 | AFHIP_F16 */
+  int32_t out_dtype;  /* AFHIP_F32 | AFHIP_F16 */
+  int32_t residual;   /* out += result */
+  float epsilon;
+} afhip_transition_desc;
+
+AFHIP_API int afhip_transition_weights_size(const afhip_transition_desc* desc, size_t* bytes);
+AFHIP_API int afhip_transition_workspace_size(const afhip_transition_desc* desc, size_t* bytes);
+/* packed: f32 in the order of packTransitionWeights (transition.ts:157-177):
+ * layerNormScale [C], layerNormOffset [C], firstWeight [C][H], firstBias [H],
+ * secondWeight [H][C], secondBias [C]. */
+AFHIP_API int afhip_transition_prepare_weights(const afhip_transition_desc* desc, const float* packed, void* prepared,
+                                     void* stream);
+AFHIP_API int afhip_transition_run(const afhip_transition_desc* desc, const void* activations, const void* prepared,
+                         void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Kernel timing                                                           */
+/* ---------------------------------------------------------------------- */
+
+/* When enabled, every kernel the library launches is bracketed by hipEvents
+ * on its own stream and its duration accumulated under its label; the
+ * counterpart of WebGpuExecution's timestamp profile
+ * (src/runtime/execution.ts:329-345, :482-513). Reading synchronises the
+ * recorded events. JSON: {"label": {"count": n, "total_ms": t}, ...}. */
+AFHIP_API int afhip_timing_enable(int enable);
+AFHIP_API int afhip_timing_reset(void);
+AFHIP_API int afhip_timing_report(char* json, size_t capacity);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AFHIP_H */

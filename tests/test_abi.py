@@ -1,0 +1,108 @@
+"""The C ABI on the CPU: the library loads, exports every symbol
+include/afhip.h declares, and its host-only logic (the reference's gemmGrid,
+the selection record, validation) behaves without a GPU."""
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "afhip.h")).read()
+    return sorted(set(re.findall(r"AFHIP_API\s+(?:const\s+char\*|int)\s+(afhip_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_surface():
+    names = declared_symbols()
+    assert len(names) >= 38
+    for needed in ("afhip_gemm_run", "afhip_triangle_run", "afhip_opm_run", "afhip_transition_run",
+                   "afhip_gemm_calibrate", "afhip_dequant_q8_channel"):
+        assert needed in names
+
+
+def test_library_exports_every_declared_symbol():
+    from afhip import _lib
+
+    lib = _lib.library()
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert missing == []
+    assert set(declared_symbols()) <= set(_lib.SIGNATURES)
+
+
+def test_abi_version_and_not_open_errors():
+    import ctypes
+
+    from afhip import _lib
+
+    lib = _lib.library()
+    assert lib.afhip_abi_version() == 1
+    size = ctypes.c_size_t()
+    # A call that needs the device reports NOT_OPEN rather than touching HIP.
+    assert lib.afhip_buffer_create(16, ctypes.byref(ctypes.c_void_p())) == _lib.ERR_NOT_OPEN
+    assert "afhip_open" in _lib.last_error()
+    desc = _lib.TriangleDesc(384, 128, 128, 0, 1, 1, 0, 0, 0, 1e-5)
+    assert lib.afhip_triangle_workspace_size(ctypes.byref(desc), ctypes.byref(size)) == _lib.OK
+    # a, b (f16, channel-major) and the contracted block: 3 x 128 x 147456 x 2 bytes
+    assert size.value >= 3 * 128 * 147456 * 2
+
+
+def test_gemm_grid_matches_reference():
+    # test/gemm-selection.test.ts:239-262 and test/gemm.test.ts:57-61
+    from afhip import _lib, gemm
+
+    assert gemm.gemm_grid(64, 128) == (1, 1)
+    assert gemm.gemm_grid(65, 129) == (2, 2)
+    assert gemm.gemm_grid(65_535 * 64, 256) == (2, 65_535)
+    assert gemm.gemm_grid(256, 128) == (1, 4)
+    assert gemm.gemm_grid(256, 128, 128, 128) == (1, 2)
+    rows = 65_536 * 64
+    x, y = gemm.gemm_grid(rows, 128)
+    assert x <= 65_535 and y <= 65_535 and x * y >= rows // 64
+    for bad in [(0, 1), (1, 0), (-3, 4)]:
+        with pytest.raises(_lib.RangeError):
+            gemm.gemm_grid(*bad)
+
+
+def test_descriptor_validation_is_host_side():
+    import ctypes
+
+    from afhip import _lib
+
+    lib = _lib.library()
+    size = ctypes.c_size_t()
+    bad = _lib.TriangleDesc(0, 128, 128, 0, 1, 1, 0, 0, 0, 1e-5)
+    assert lib.afhip_triangle_workspace_size(ctypes.byref(bad), ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+    assert "positive" in _lib.last_error()
+    bad = _lib.TriangleDesc(8, 128, 128, 2, 1, 1, 0, 0, 0, 1e-5)
+    assert lib.afhip_triangle_workspace_size(ctypes.byref(bad), ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+    bad = _lib.TriangleDesc(8, 128, 128, 0, 1, 1, 0, 0, 0, -1.0)
+    assert lib.afhip_triangle_workspace_size(ctypes.byref(bad), ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+    opm = _lib.OpmDesc(512, 256, 256, 32, 128, 1, 1, 0, 0, 0, 1e-5, 1e-3)
+    assert lib.afhip_opm_workspace_size(ctypes.byref(opm), ctypes.byref(size)) == _lib.OK
+    tr = _lib.TransitionDesc(0, 128, 512, 1, 1, 0, 0, 1e-5)
+    assert lib.afhip_transition_workspace_size(ctypes.byref(tr), ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+
+
+def test_variant_selection_without_device():
+    from afhip import gemm
+
+    v = gemm.select_variant(131072, 256, 1024, precision="f16", a_dtype="f16", w_dtype="i8", out_dtype="f16")
+    assert v.tile_rows in (64, 128) and v.tile_columns in (64, 128) and v.source == "heuristic"
+    assert v.name.startswith("mfma-f16-")
+
+
+def test_calibration_document_round_trip(tmp_path):
+    from afhip import gemm
+
+    path = tmp_path / "calibration.json"
+    gemm.calibration_save(str(path))
+    text = path.read_text()
+    assert '"schema": 1' in text
+    # A corrupted document is ignored, not trusted (gemm-selection.ts:543-558).
+    path.write_text('{"schema": 1, "entries": {"x|y": {"precision": 1, "tile_rows": 96, '
+                    '"tile_columns": 128, "tile_inner": 32}}}')
+    gemm.calibration_load(str(path))
+    path.write_text("not json at all")
+    gemm.calibration_load(str(path))

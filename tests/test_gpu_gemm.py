@@ -1,0 +1,188 @@
+"""GEMM parity on the GPU: libafhip against the CPU oracle.
+
+Tolerances are the reference's: max|d|/max|ref| <= 1e-5 for the f32 path
+the per-variant bounds of
+test/gemm-half-precision.gpu.test.ts:35-41 for ragged shapes, 1e-2 for the
+f16 and mixed-q8 paths, and bit-exact for dequantised int8 weights.
+"""
+import numpy as np
+import pytest
+
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    from afhip import device
+
+    device.open_device(0)
+    return torch.device("cuda", 0)
+
+
+def rel_max(actual, expected):
+    a = np.asarray(actual, np.float64).reshape(-1)
+    e = np.asarray(expected, np.float64).reshape(-1)
+    return float(np.abs(a - e).max() / max(np.abs(e).max(), 1e-30))
+
+
+def to_dev(x, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def test_config1_pair_transition_linear_f32(dev):
+    # X [4096x128] ~N(0,1), W [128x512] ~N(0,1/128),
+    # bias ~N(0,0.02), ReLU; seed 0xAF2000 + 0.
+    from afhip import gemm
+
+    seed = 0xAF2000
+    x = ref.normal(seed, (4096, 128))
+    w = ref.normal(seed + 1, (128, 512), 1 / 128)
+    b = ref.normal(seed + 2, (512,), 0.02)
+    expect = ref.linear(x, w, b, relu=True)
+    out = gemm.linear(to_dev(x, dev), to_dev(w, dev), to_dev(b, dev), relu=True, precision="f32")
+    assert rel_max(out.cpu().numpy(), expect) <= 1e-5
+
+
+@pytest.mark.parametrize("inner", [256, 1024])
+@pytest.mark.parametrize("precision,tol", [("f32", 1e-4), ("f16", 5e-3)])
+def test_ragged_projection_matches_f64(dev, inner, precision, tol):
+    # test/gemm-half-precision.gpu.test.ts:206-261: rows 81, columns 132.
+    from afhip import gemm
+
+    a = ref.lcg_values(1, 81 * inner).reshape(81, inner)
+    w = ref.lcg_values(2, inner * 132).reshape(inner, 132)
+    b = ref.lcg_values(3, 132)
+    expect = ref.gemm_f64(a, w, b)
+    out = gemm.linear(to_dev(a, dev), to_dev(w, dev), to_dev(b, dev), precision=precision)
+    assert rel_max(out.cpu().numpy(), expect) <= tol
+
+
+@pytest.mark.parametrize("m,k,n", [(130, 96, 132), (1, 8, 1), (64, 32, 64), (257, 40, 31)])
+@pytest.mark.parametrize("precision", ["f32", "f16"])
+def test_odd_shapes(dev, m, k, n, precision):
+    from afhip import gemm
+
+    a = ref.normal(m * 7 + k, (m, k))
+    w = ref.normal(n * 3 + k, (k, n), 1 / k)
+    expect = ref.gemm_f64(a, w)
+    out = gemm.linear(to_dev(a, dev), to_dev(w, dev), precision=precision)
+    assert rel_max(out.cpu().numpy(), expect) <= (1e-5 if precision == "f32" else 5e-3)
+
+
+def test_every_tile_variant_agrees(dev):
+    from afhip import gemm
+
+    a = ref.normal(5, (300, 256))
+    w = ref.normal(6, (256, 200), 1 / 256)
+    expect = ref.gemm_f64(a, w)
+    for tr, tc in [(64, 64), (64, 128), (128, 64), (128, 128)]:
+        gemm.force_variant(gemm.GemmVariant("f32", tr, tc, source="pinned"))
+        try:
+            out = gemm.linear(to_dev(a, dev), to_dev(w, dev), precision="f32")
+        finally:
+            gemm.force_variant(None)
+        assert rel_max(out.cpu().numpy(), expect) <= 1e-5, (tr, tc)
+
+
+def test_relu_residual_epilogue(dev):
+    from afhip import gemm
+
+    a = ref.normal(11, (96, 64))
+    w = ref.normal(12, (64, 80), 1 / 64)
+    b = ref.normal(13, (80,), 0.02)
+    r = ref.normal(14, (96, 80))
+    expect = ref.linear(a, w, b, relu=True, residual=r)
+    out = gemm.linear(to_dev(a, dev), to_dev(w, dev), to_dev(b, dev), relu=True, residual=to_dev(r, dev))
+    assert rel_max(out.cpu().numpy(), expect) <= 1e-5
+
+
+def test_batched_k_contiguous(dev):
+    import torch
+
+    from afhip import gemm
+
+    B, M, N, K = 5, 70, 90, 48
+    a = ref.normal(21, (B, M, K))
+    w = ref.normal(22, (B, N, K), 1 / K)  # [n][k]
+    plan = gemm.TiledGemm(M, K, N, precision="f32", w_layout="k", batch=B, batch_stride_a=M * K,
+                          batch_stride_w=N * K, batch_stride_c=M * N)
+    out = plan.run(to_dev(a, dev), to_dev(w, dev)).cpu().numpy()
+    expect = np.einsum("bmk,bnk->bmn", a.astype(np.float64), w.astype(np.float64))
+    assert rel_max(out, expect) <= 1e-5
+    assert torch.cuda.is_available()
+
+
+def test_q8_channel_dequant_bit_exact(dev):
+    from afhip import gemm
+
+    q = ref.uniform_i8(0xAF2001, (256, 1024))
+    s = ref.uniform(0xAF2002, (1024,), 1e-3, 1e-2)
+    out = gemm.dequant_q8_channel(to_dev(q, dev), to_dev(s, dev)).cpu().numpy()
+    assert np.array_equal(out.view(np.uint32), ref.q8_channel_decode(q, s).view(np.uint32))
+
+
+def test_q8_block_dequant_known_answer_and_bit_exact(dev):
+    from afhip import gemm
+
+    codes = np.array([1, -2, 3, -4, 5], np.int8)
+    scales = np.array([0x3800, 0x4000], np.uint16)
+    out = gemm.dequant_q8_block(to_dev(codes, dev), to_dev(scales.view(np.int16), dev), 4).cpu().numpy()
+    assert list(out) == [0.5, -1, 1.5, -2, 10]
+    w = ref.normal(3, (4096,), 0.02)
+    c, s = ref.q8_block_encode(w, 64)
+    got = gemm.dequant_q8_block(to_dev(c, dev), to_dev(s.view(np.int16), dev), 64, 100, 3000).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.q8_block_decode(c, s, 64, 100, 3000).view(np.uint32))
+
+
+def _config2_inputs(rows):
+    seed = 0xAF2001
+    x = ref.round_f16(ref.normal(seed, (rows, 256)))
+    q = ref.uniform_i8(seed + 1, (256, 1024))
+    s = ref.uniform(seed + 2, (1024,), 1e-3, 1e-2)
+    return x, q, s
+
+
+@pytest.mark.parametrize("rows", [4096, 131072])
+def test_config2_mixed_q8_attention_projection(dev, rows):
+    # BASELINE config 2 (M = 512 * 256 = 131,072 at full size): f16 X, int8 W
+    # with per-column f32 scales, f32 accumulation, f16 q/k/v/gate.
+    from afhip import gemm
+
+    x, q, s = _config2_inputs(rows)
+    xd = to_dev(x.astype(np.float16), dev)
+    outs = gemm.attention_project(xd, to_dev(q, dev), heads=8, head_dim=32, scale=to_dev(s, dev))
+    check = np.arange(0, rows, max(1, rows // 2048))
+    wq = ref.q8_channel_decode(q, s)
+    expect = ref.attention_project(x[check], wq, None, heads=8, head_dim=32)
+    for got, exp in zip(outs, expect):
+        g = got.float().cpu().numpy()[check]
+        err = np.abs(g - exp)
+        assert np.all(err <= 1e-2 * np.maximum(1.0, np.abs(exp))), float(err.max())
+
+
+def test_attention_gate_bias_and_f32_path(dev):
+    from afhip import gemm
+
+    x = ref.normal(41, (100, 64))
+    w = ref.normal(42, (64, 4 * 2 * 8), 1 / 64)
+    gb = ref.normal(43, (16,), 0.02)
+    outs = gemm.attention_project(to_dev(x, dev), to_dev(w, dev), heads=2, head_dim=8, gate_bias=to_dev(gb, dev),
+                                  out_dtype="f32")
+    expect = ref.attention_project(x, w, gb, heads=2, head_dim=8)
+    for got, exp in zip(outs, expect):
+        assert rel_max(got.cpu().numpy(), exp) <= 1e-5
+
+
+def test_invalid_plan_raises_range_error(dev):
+    from afhip import _lib, gemm
+
+    with pytest.raises(_lib.RangeError):
+        gemm.TiledGemm(0, 4, 4)
+    with pytest.raises(_lib.RangeError):
+        gemm.TiledGemm(4, 4, 4, precision="f32", w_dtype="i8")

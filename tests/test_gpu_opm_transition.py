@@ -1,0 +1,116 @@
+"""Outer-product mean and transition parity on the GPU.
+
+OPM: test/outer-product-mean-reference.gpu.test.ts:103-130 (9 sequences x 8
+residues x 12 channels, c_o 32, c_z 16, every third mask entry zero, residue
+blocks of 3) at mean < 2e-5 / max < 2e-4; residue blocking bit-identical
+(test/evoformer-outer-product-mean.gpu.test.ts:78-81); f16 within 1e-2.
+Transition: the f32 path within 1e-5 of the largest value.
+"""
+import numpy as np
+import pytest
+
+from oracle import ref
+from test_oracle import opm_test_case
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    from afhip import device
+
+    device.open_device(0)
+    return torch.device("cuda", 0)
+
+
+def opm_input(act, mask, w, row_block=None):
+    S, L, cm = act.shape
+    return {"activations": act, "mask": mask, "sequences": S, "length": L, "cM": cm,
+            "cOuter": w["leftBias"].shape[0], "cZ": w["outputBias"].shape[0], "weights": w,
+            "layerNormEpsilon": 1e-5, "normalizationEpsilon": 1e-3, "rowBlockResidues": row_block}
+
+
+def test_opm_reference_case(dev):
+    from afhip import opm
+
+    act, mask, w = opm_test_case()
+    expect = ref.opm(act, mask, w)
+    out = opm.OuterProductMeanGpu().run(opm_input(act, mask, w, 3))["output"]
+    m = ref.error_metrics(out, expect)
+    assert m["meanAbsoluteError"] < 2e-5 and m["maxAbsoluteError"] < 2e-4
+
+
+def test_opm_blocking_bit_identical(dev):
+    from afhip import opm
+
+    act, mask, w = opm_test_case()
+    whole = opm.OuterProductMeanGpu().run(opm_input(act, mask, w))["output"]
+    for rb in (3, 1, 5):
+        blocked = opm.OuterProductMeanGpu().run(opm_input(act, mask, w, rb))["output"]
+        assert np.array_equal(whole.view(np.uint32), blocked.view(np.uint32)), rb
+
+
+@pytest.mark.parametrize("S,L,cm,co,cz", [(64, 24, 256, 32, 128), (33, 17, 40, 8, 12)])
+def test_opm_synthetic(dev, S, L, cm, co, cz):
+    from afhip import opm
+
+    act = ref.normal(S + L, (S, L, cm))
+    mask = (ref.uniform(S * L, (S, L), 0, 1) > 0.1).astype(np.float32)
+    w = {"layerNormScale": ref.normal(1, (cm,), 0.01, 1.0), "layerNormOffset": ref.normal(2, (cm,), 0.01),
+         "leftWeight": ref.normal(3, (cm, co), 1 / cm), "leftBias": ref.normal(4, (co,), 0.02),
+         "rightWeight": ref.normal(5, (cm, co), 1 / cm), "rightBias": ref.normal(6, (co,), 0.02),
+         "outputWeight": ref.normal(7, (co * co, cz), 1 / (co * co)), "outputBias": ref.normal(8, (cz,), 0.02)}
+    expect = ref.opm(act, mask, w)
+    scale = max(1.0, float(np.abs(expect).max()))
+    out = opm.OuterProductMeanGpu().run(opm_input(act, mask, w))["output"].reshape(expect.shape)
+    assert np.abs(out - expect).max() <= 1e-5 * scale
+    out16 = opm.OuterProductMeanGpu().run(opm_input(act, mask, w), {"precision": "f16"})["output"]
+    assert np.abs(out16.reshape(expect.shape) - expect).max() <= 1e-2 * scale
+
+
+def test_opm_all_masked_row_gives_bias_over_eps(dev):
+    from afhip import opm
+
+    act, mask, w = opm_test_case()
+    mask = mask.copy()
+    mask[:, 2] = 0  # residue 2 never aligned: count = 0 for its pairs
+    expect = ref.opm(act, mask, w)
+    out = opm.OuterProductMeanGpu().run(opm_input(act, mask, w))["output"].reshape(expect.shape)
+    assert np.allclose(out[2], w["outputBias"] / 1e-3, rtol=1e-5)
+    assert np.abs(out - expect).max() <= 1e-5 * np.abs(expect).max()
+
+
+def transition_case(rows, c, h, seed):
+    x = ref.normal(seed, (rows, c))
+    w = {"layerNormScale": ref.normal(seed + 1, (c,), 0.01, 1.0), "layerNormOffset": ref.normal(seed + 2, (c,), 0.01),
+         "firstWeight": ref.normal(seed + 3, (c, h), 1 / c), "firstBias": ref.normal(seed + 4, (h,), 0.02),
+         "secondWeight": ref.normal(seed + 5, (h, c), 1 / h), "secondBias": ref.normal(seed + 6, (c,), 0.02)}
+    return {"activations": x, "rows": rows, "channels": c, "hiddenChannels": h, "weights": w}
+
+
+@pytest.mark.parametrize("rows,c,h", [(4096, 128, 512), (77, 16, 64)])
+def test_transition(dev, rows, c, h):
+    from afhip import transition
+
+    inp = transition_case(rows, c, h, rows)
+    expect = ref.transition(inp["activations"], inp["weights"])
+    out = transition.TransitionGpu().run(inp)["output"].reshape(expect.shape)
+    assert np.abs(out - expect).max() <= 1e-5 * np.abs(expect).max()
+    out16 = transition.TransitionGpu().run(inp, {"precision": "f16"})["output"].reshape(expect.shape)
+    assert np.abs(out16 - expect).max() <= 1e-2 * max(1.0, np.abs(expect).max())
+
+
+def test_invalid_opm_and_transition_raise(dev):
+    from afhip import _lib, opm, transition
+
+    act, mask, w = opm_test_case()
+    bad = opm_input(act, mask, w)
+    bad["mask"] = mask.reshape(-1)[1:]
+    with pytest.raises(_lib.RangeError, match="mask has"):
+        opm.OuterProductMeanGpu().run(bad)
+    inp = transition_case(8, 4, 8, 1)
+    inp["rows"] = 0
+    with pytest.raises(_lib.RangeError):
+        transition.TransitionGpu().run(inp)
