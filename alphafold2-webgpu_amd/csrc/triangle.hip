@@ -22,6 +22,7 @@
 #include <cstring>
 
 #include "gemm.h"
+#include "triangle_fast.h"
 
 namespace afhip {
 
@@ -536,9 +537,31 @@ int afhip_triangle_run(const afhip_triangle_desc* desc, const void* z, const flo
   pa.chp = w.chp;
   pa.incoming = d.direction == AFHIP_TRIANGLE_INCOMING;
   pa.eps = d.epsilon;
-  size_t psh = round_up((int64_t)w.czp * (kRows + 1) * 4, 16) + (f16 ? round_up((int64_t)kRows * (w.czp + 8) * 2, 16) : 0) +
-               (size_t)64 * (kRows + 8) * (f16 ? 2 : 4);
-  int s = f16 ? dispatch_project<true>(d.pair_dtype, pa, psh, st) : dispatch_project<false>(d.pair_dtype, pa, psh, st);
+  // AlphaFold's widths in f16 take the persistent kernels of
+  // triangle_fast.hip; every other shape and the f32 path take the tiles below.
+  const bool fast = triangle_fast_eligible(d) && (reinterpret_cast<uintptr_t>(z) & 15) == 0;
+  int s;
+  if (fast) {
+    FastProjectArgs fa{};
+    fa.z = z;
+    fa.mask = mask;
+    fa.ln_w = pa.ln_w;
+    fa.ln_b = pa.ln_b;
+    fa.w_proj = (const half_t*)pa.w_proj;
+    fa.b_proj = pa.b_proj;
+    fa.out_a = (half_t*)pa.out_a;
+    fa.out_b = (half_t*)pa.out_b;
+    fa.cstride = ws.cstride;
+    fa.L = L;
+    fa.P = P;
+    fa.incoming = pa.incoming;
+    fa.eps = d.epsilon;
+    s = launch_triangle_project_f16(fa, d.pair_dtype, st);
+  } else {
+    size_t psh = round_up((int64_t)w.czp * (kRows + 1) * 4, 16) +
+                 (f16 ? round_up((int64_t)kRows * (w.czp + 8) * 2, 16) : 0) + (size_t)64 * (kRows + 8) * (f16 ? 2 : 4);
+    s = f16 ? dispatch_project<true>(d.pair_dtype, pa, psh, st) : dispatch_project<false>(d.pair_dtype, pa, psh, st);
+  }
   if (s) return s;
 
   // Row operand and column operand of the contraction (see the file comment).
@@ -588,8 +611,29 @@ int afhip_triangle_run(const afhip_triangle_desc* desc, const void* z, const flo
     oa.chp = w.chp;
     oa.residual = d.residual;
     oa.eps = d.epsilon;
-    s = f16 ? dispatch_output<true>(d.pair_dtype, d.out_dtype, oa, osh, st)
-            : dispatch_output<false>(d.pair_dtype, d.out_dtype, oa, osh, st);
+    if (fast) {
+      FastOutputArgs fo{};
+      fo.contracted = (const half_t*)oa.contracted;
+      fo.bstride = oa.bstride;
+      fo.z = z;
+      fo.ln_in_w = oa.ln_in_w;
+      fo.ln_in_b = oa.ln_in_b;
+      fo.ln_out_w = oa.ln_out_w;
+      fo.ln_out_b = oa.ln_out_b;
+      fo.w_z = (const half_t*)oa.w_z;
+      fo.b_z = oa.b_z;
+      fo.w_g = (const half_t*)oa.w_g;
+      fo.b_g = oa.b_g;
+      fo.out = out;
+      fo.pair0 = oa.pair0;
+      fo.pairs = oa.pairs;
+      fo.residual = oa.residual;
+      fo.eps = d.epsilon;
+      s = launch_triangle_output_f16(fo, d.pair_dtype, d.out_dtype, st);
+    } else {
+      s = f16 ? dispatch_output<true>(d.pair_dtype, d.out_dtype, oa, osh, st)
+              : dispatch_output<false>(d.pair_dtype, d.out_dtype, oa, osh, st);
+    }
     if (s) return s;
   }
   return AFHIP_OK;
