@@ -416,12 +416,14 @@ int validate(const afhip_triangle_desc* d) {
 
 template <typename ZT, bool F16MATH>
 int launch_project(const ProjectArgs& pa, size_t shared, hipStream_t s) {
+  if (int st = allow_lds((const void*)tri_project_kernel<ZT, F16MATH>, shared)) return st;
   return launch("triangle.project", tri_project_kernel<ZT, F16MATH>, dim3((unsigned)ceil_div(pa.P, kRows)),
                 dim3(256), shared, s, pa);
 }
 
 template <typename ZT, typename OT, bool F16MATH>
 int launch_output(const OutputArgs& oa, size_t shared, hipStream_t s) {
+  if (int st = allow_lds((const void*)tri_output_kernel<ZT, OT, F16MATH>, shared)) return st;
   return launch("triangle.output", tri_output_kernel<ZT, OT, F16MATH>, dim3((unsigned)ceil_div(oa.pairs, kRows)),
                 dim3(256), shared, s, oa);
 }
