@@ -31,6 +31,9 @@ EPILOGUE_RESIDUAL = 16
 WEIGHT_COLUMN_CONTIGUOUS = 0
 WEIGHT_K_CONTIGUOUS = 1
 
+KERNEL_REGISTER_STAGED = 0
+KERNEL_LDS_DMA = 1
+
 TRIANGLE_OUTGOING = 0
 TRIANGLE_INCOMING = 1
 
@@ -63,6 +66,7 @@ class Variant(ctypes.Structure):
     _fields_ = [
         ("precision", ctypes.c_int32), ("tile_rows", ctypes.c_int32), ("tile_columns", ctypes.c_int32),
         ("tile_inner", ctypes.c_int32), ("vectorized", ctypes.c_int32), ("source", ctypes.c_int32),
+        ("kernel", ctypes.c_int32),
     ]
 
 

@@ -21,6 +21,8 @@ GEMM_TILE_COLUMNS = 128
 
 _DTYPE_CODES = {"f32": _lib.F32, "f16": _lib.F16, "i8": _lib.I8}
 _PRECISION_CODES = {"f32": _lib.PRECISION_F32, "f16": _lib.PRECISION_F16}
+_KERNEL_CODES = {"register": _lib.KERNEL_REGISTER_STAGED, "lds_dma": _lib.KERNEL_LDS_DMA}
+_KERNEL_NAMES = {v: k for k, v in _KERNEL_CODES.items()}
 
 
 def gemm_grid(rows: int, columns: int, tile_columns: int = GEMM_TILE_COLUMNS,
@@ -37,27 +39,32 @@ def gemm_grid(rows: int, columns: int, tile_columns: int = GEMM_TILE_COLUMNS,
 
 @dataclass(frozen=True)
 class GemmVariant:
-    """The kernel a shape runs with (GemmVariant, gemm.ts:150-206): arithmetic
-    and output tile. `source` says whether it came from the heuristic, a
-    calibration or a pin."""
+    """The kernel a shape runs with (GemmVariant, gemm.ts:150-206): arithmetic,
+    kernel family and output tile. `kernel` is "register" (operands staged
+    through VGPRs; any dtype) or "lds_dma" (f16 operands loaded straight into
+    LDS, several k-steps in flight). `source` says whether it came from the
+    heuristic, a calibration or a pin."""
 
     precision: str
     tile_rows: int
     tile_columns: int
     tile_inner: int = 32
     source: str = "heuristic"
+    kernel: str = "register"
 
     @staticmethod
     def _from_c(v: _lib.Variant) -> "GemmVariant":
         return GemmVariant("f16" if v.precision == _lib.PRECISION_F16 else "f32", v.tile_rows, v.tile_columns,
-                           v.tile_inner, ("heuristic", "calibrated", "pinned")[v.source])
+                           v.tile_inner, ("heuristic", "calibrated", "pinned")[v.source],
+                           _KERNEL_NAMES[v.kernel])
 
     def _to_c(self) -> _lib.Variant:
-        return _lib.Variant(_PRECISION_CODES[self.precision], self.tile_rows, self.tile_columns, self.tile_inner, 1, 2)
+        return _lib.Variant(_PRECISION_CODES[self.precision], self.tile_rows, self.tile_columns, self.tile_inner, 1, 2,
+                            _KERNEL_CODES[self.kernel])
 
     @property
     def name(self) -> str:
-        return f"mfma-{self.precision}-{self.tile_rows}x{self.tile_columns}k{self.tile_inner}"
+        return f"mfma-{self.kernel}-{self.precision}-{self.tile_rows}x{self.tile_columns}k{self.tile_inner}"
 
 
 def _torch_dtype(code: str):

@@ -50,8 +50,14 @@ struct GemmTypes {
 int run_gemm(const GemmArgs& args, const GemmTypes& types, const afhip_variant& variant, const char* label,
              hipStream_t stream);
 
-// Heuristic tile choice for a problem of this size.
-afhip_variant heuristic_variant(int precision, int64_t M, int64_t N, int64_t K, int batch);
+// Heuristic kernel and tile choice for a problem of these types and size.
+afhip_variant heuristic_variant(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);
+
+// The LDS_DMA kernel family (gemm_dma.hip): f16 operands, B k-contiguous.
+bool dma_tile_supported(int tile_m, int tile_n);
+bool dma_eligible(const GemmArgs& args, const GemmTypes& types);
+void dma_heuristic_tile(int64_t M, int64_t N, int64_t batch, int* tile_m, int* tile_n);
+int run_gemm_dma(const GemmArgs& args, int c_dtype, int tile_m, int tile_n, const char* label, hipStream_t stream);
 
 // The variant plans of this shape should use (pinned, calibrated or heuristic).
 afhip_variant select_variant(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);

@@ -45,6 +45,15 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
   AFHIP_REQUIRE(!(g.flags & AFHIP_EPILOGUE_RESIDUAL) || g.residual, "RESIDUAL epilogue without a residual");
   AFHIP_REQUIRE(!(g.flags & AFHIP_EPILOGUE_ATTENTION) || (g.head_cols > 0 && g.N == 4 * g.head_cols),
                 "ATTENTION epilogue needs columns == 4 * heads * head_dim");
+  if (v.kernel == AFHIP_KERNEL_LDS_DMA) {
+    if (dma_eligible(g, t) && dma_tile_supported(v.tile_rows, v.tile_columns))
+      return run_gemm_dma(g, t.c_dtype, v.tile_rows, v.tile_columns, label, stream);
+    // Operands the LDS_DMA family cannot take (alignment, K % 8, dtypes) run
+    // on the register-staged kernel with its heuristic tile.
+    afhip_variant r = heuristic_variant(GemmTypes{t.precision, AFHIP_F32, AFHIP_F32, t.c_dtype}, g.M, g.N, g.K, g.batch);
+    return run_gemm(g, t, r, label, stream);
+  }
+  AFHIP_REQUIRE(v.kernel == AFHIP_KERNEL_REGISTER_STAGED, "unknown kernel family %d", v.kernel);
   const int va = 16 / (int)dtype_size(t.a_dtype), vb = 16 / (int)dtype_size(t.b_dtype);
   bool vec = g.K % va == 0 && g.K % vb == 0 && g.lda % va == 0 && g.ldb % vb == 0 && g.sa % va == 0 &&
              g.sb % vb == 0 && aligned16(g.a) && aligned16(g.b);
@@ -57,12 +66,18 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
   return gemm_dispatch_f32(g, t, v, vec, label, stream);
 }
 
-afhip_variant heuristic_variant(int precision, int64_t M, int64_t N, int64_t /*K*/, int batch) {
+afhip_variant heuristic_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t /*K*/, int batch) {
   afhip_variant v{};
-  v.precision = precision;
+  v.precision = t.precision;
   v.tile_inner = gemm_detail::kBK;
   v.vectorized = 1;
   v.source = 0;
+  if (t.precision == AFHIP_PRECISION_F16 && t.a_dtype == AFHIP_F16 && t.b_dtype == AFHIP_F16) {
+    v.kernel = AFHIP_KERNEL_LDS_DMA;
+    dma_heuristic_tile(M, N, batch, &v.tile_rows, &v.tile_columns);
+    return v;
+  }
+  v.kernel = AFHIP_KERNEL_REGISTER_STAGED;
   // Prefer the largest tile that still gives every CU two workgroups.
   const int64_t target = 2 * (int64_t)(device_cu_count() > 0 ? device_cu_count() : 256);
   const int shapes[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
@@ -191,13 +206,14 @@ afhip_variant select_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K
     afhip_variant v = g_pin;
     v.precision = t.precision;
     v.source = 2;
-    return v;
+    // A pinned LDS_DMA tile only applies where that family runs.
+    if (v.kernel != AFHIP_KERNEL_LDS_DMA || (t.a_dtype == AFHIP_F16 && t.b_dtype == AFHIP_F16)) return v;
   }
   if (!g_calibrated.empty()) {
     auto it = g_calibrated.find(device_key() + "|" + shape_class(t, M, N, K, batch));
     if (it != g_calibrated.end()) return it->second;
   }
-  return heuristic_variant(t.precision, M, N, K, batch);
+  return heuristic_variant(t, M, N, K, batch);
 }
 
 void install_calibrated(const std::string& key, const afhip_variant& v) {
@@ -216,8 +232,11 @@ void replace_calibrated(const std::map<std::string, afhip_variant>& m) {
 }
 
 bool valid_variant(const afhip_variant& v) {
-  return (v.tile_rows == 64 || v.tile_rows == 128) && (v.tile_columns == 64 || v.tile_columns == 128) &&
-         v.tile_inner == gemm_detail::kBK && valid_precision(v.precision);
+  if (v.tile_inner != gemm_detail::kBK || !valid_precision(v.precision)) return false;
+  if (v.kernel == AFHIP_KERNEL_LDS_DMA)
+    return v.precision == AFHIP_PRECISION_F16 && dma_tile_supported(v.tile_rows, v.tile_columns);
+  return v.kernel == AFHIP_KERNEL_REGISTER_STAGED && (v.tile_rows == 64 || v.tile_rows == 128) &&
+         (v.tile_columns == 64 || v.tile_columns == 128);
 }
 
 void pin_variant(const afhip_variant* v) {
@@ -303,7 +322,11 @@ int afhip_gemm_plan_create(const afhip_gemm_desc* desc, afhip_gemm_plan** out) {
   p->lda = desc->lda ? desc->lda : desc->inner;
   p->ldw = desc->ldw ? desc->ldw : (desc->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS ? desc->inner : desc->columns);
   p->ldc = desc->ldc ? desc->ldc : desc->columns;
-  p->variant = select_variant(p->types, desc->rows, desc->columns, desc->inner, desc->batch);
+  // Selected with the weight dtype the kernels will read (a column-contiguous
+  // f32 weight is converted on its way into the workspace).
+  GemmTypes kt = p->types;
+  if (desc->precision == AFHIP_PRECISION_F16 && desc->w_dtype != AFHIP_I8) kt.b_dtype = AFHIP_F16;
+  p->variant = select_variant(kt, desc->rows, desc->columns, desc->inner, desc->batch);
   *out = p;
   return AFHIP_OK;
 }

@@ -1,0 +1,277 @@
+// The LDS_DMA GEMM kernel family for gfx950: C[b] = epilogue(A[b] B[b]^T)
+// with A [M][K] and B [N][K] f16 (k-contiguous), f32 accumulation.
+//
+// It carries the triangle multiplication's O(L^3) contraction (per hidden
+// channel b, out[b][i][j] = sum_k R[b][i][k] C[b][j][k]; the reference
+// dispatches it once per channel along z, src/triangle/shaders.ts:452-496),
+// the outer-product-mean contraction and the f16 projections.
+//
+// Design:
+//  - One workgroup of four wave64s owns a BM x BN output tile (2 x 2 waves,
+//    each (BM/2) x (BN/2) in 32 x 32 v_mfma_f32_32x32x16_f16 tiles) and walks
+//    K in steps of 32 halves.
+//  - Operands travel global -> LDS without passing through VGPRs
+//    (buffer_load_dwordx4 ... lds). A k-step stage is (BM + BN) rows of
+//    64 bytes; each wave-level load instruction fills 16 rows (1 KiB of LDS,
+//    lane l -> row l/4, 16-byte slot l%4). STAGES stages are in flight, so the
+//    loads for step k + STAGES - 1 are issued while step k computes, and one
+//    barrier per k-step both publishes a stage and retires the one to refill.
+//  - Bank conflicts: a row's four 16-byte chunks are stored XOR-swizzled,
+//    slot = chunk ^ ((row >> 2) & 3), so the 16 rows a 16-lane group of an
+//    MFMA fragment read cover all 16 bank groups of a 256-byte line. The
+//    swizzle is applied by choosing which global chunk each lane loads.
+//  - Ragged edges cost nothing: every load goes through a buffer resource
+//    bounded to the tile's valid rows, and chunks past K get an offset beyond
+//    the resource, so the hardware returns zeros for both.
+//  - Tiles are numbered so that consecutive tiles (one batch's tiles, which
+//    share operand panels) run on one XCD: workgroup ids are dealt round-robin
+//    over the eight XCDs, so tile t = (id % 8) * per_xcd + id / 8.
+//  - The epilogue is the register-staged kernel's (gemm_kernel.h), so both
+//    families give the same epilogue arithmetic.
+#include <algorithm>
+
+#include "gemm_kernel.h"
+
+namespace afhip {
+
+typedef int int32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+
+// buffer_load_dword{,x3,x4} ... lds: each lane's `size` bytes from
+// rsrc + voffset land in LDS at M0 (= lds) + 16 * lane (for size 16).
+__device__ void buffer_load_lds(int32x4_t rsrc, lds_u32* lds, int size, int voffset, int soffset, int offset,
+                                int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+namespace {
+
+constexpr int kBK = 32;        // halves per k-step
+constexpr int kRowBytes = 64;  // one row of a k-step stage
+constexpr int kThreads = 256;
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+// Raw buffer resource (stride 0): loads at byte offsets >= `bytes` return 0.
+__device__ __forceinline__ int32x4_t make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  int32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
+
+template <int BM, int BN, int STAGES, typename TC>
+__global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::KernelArgs ka) {
+  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int ROWS = BM + BN;
+  constexpr int STAGE_BYTES = ROWS * kRowBytes;
+  constexpr int LOADS = ROWS / 16;  // wave-level load instructions per stage
+  constexpr int LPW = LOADS / 4;    // per wave
+  static_assert(BM % 64 == 0 && BN % 64 == 0 && LOADS % 4 == 0, "tile shape");
+  static_assert((STAGES - 2) * LPW < 64, "vmcnt holds at most 63 outstanding loads");
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+
+  const GemmArgs& g = ka.g;
+  const int id = blockIdx.x;
+  const int t = (id & 7) * ka.per_xcd + (id >> 3);
+  if (t >= ka.total_tiles) return;
+  const int per_batch = ka.tiles_m * ka.tiles_n;
+  const int bt = t / per_batch;
+  const int rt = t - bt * per_batch;
+  const int m0 = (rt / ka.tiles_n) * BM;
+  const int n0 = (rt % ka.tiles_n) * BN;
+
+  const int lane = threadIdx.x & 63;
+  // Wave-uniform by construction; readfirstlane lets the compiler keep the
+  // buffer resource choice below in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = (wave >> 1) * WTM;
+  const int wn = (wave & 1) * WTN;
+
+  const half_t* A = reinterpret_cast<const half_t*>(g.a) + (int64_t)bt * g.sa + (int64_t)m0 * g.lda;
+  const half_t* B = reinterpret_cast<const half_t*>(g.b) + (int64_t)bt * g.sb + (int64_t)n0 * g.ldb;
+  const int rows_a = min(BM, g.M - m0);
+  const int rows_b = min(BN, g.N - n0);
+  const int32x4_t ra = make_rsrc(A, (uint32_t)((int64_t)rows_a * g.lda * 2));
+  const int32x4_t rb = make_rsrc(B, (uint32_t)((int64_t)rows_b * g.ldb * 2));
+
+  // This lane's part of each of the wave's load instructions: instruction
+  // q = wave + 4 i fills stage rows [16 q, 16 q + 16); the lane fills slot
+  // lane % 4 of row 16 q + lane / 4 with global chunk slot ^ swizzle(row).
+  uint32_t base_off[LPW];
+  int chunk_k[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; i++) {
+    const int q = wave + 4 * i;
+    const int row = 16 * q + (lane >> 2);
+    const int chunk = (lane & 3) ^ swizzle(row);
+    chunk_k[i] = 8 * chunk;
+    if (16 * q < BM) base_off[i] = (uint32_t)((int64_t)row * g.lda * 2 + 16 * chunk);
+    else base_off[i] = (uint32_t)((int64_t)(row - BM) * g.ldb * 2 + 16 * chunk);
+  }
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+
+  auto issue = [&](int ks, int stage) {
+    const int k0 = ks * kBK;
+#pragma unroll
+    for (int i = 0; i < LPW; i++) {
+      const int q = wave + 4 * i;
+      const uint32_t off = k0 + chunk_k[i] < g.K ? base_off[i] + 2u * k0 : kOutOfRange;
+      lds_u32* dst = reinterpret_cast<lds_u32*>((uintptr_t)(lds0 + stage * STAGE_BYTES + q * 1024));
+      buffer_load_lds(16 * q < BM ? ra : rb, dst, 16, (int)off, 0, 0, 0);
+    }
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
+
+  const int nk = (g.K + kBK - 1) / kBK;
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; s++)
+    if (s < nk) issue(s, s);
+
+  const int frag_row = lane & 31;
+  for (int ks = 0; ks < nk; ks++) {
+    // Stage ks is complete once at most the later stages' loads are pending;
+    // the barrier then publishes it and retires stage ks - 1 for refilling.
+    if (ks + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * LPW>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (ks + STAGES - 1 < nk) issue(ks + STAGES - 1, (ks + STAGES - 1) % STAGES);
+    const unsigned char* st = smem + (ks % STAGES) * STAGE_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      const int chunk = 2 * kk + (lane >> 5);
+      half8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int row = wm + 32 * i + frag_row;
+        af[i] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int row = BM + wn + 32 * j + frag_row;
+        bf[j] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = mfma_f16(af[i], bf[j], acc[i][j]);
+    }
+    asm volatile("" ::: "memory");
+  }
+
+  if (g.flags == 0) {
+    // Plain store straight from the accumulators (the contraction's case).
+    TC* C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int col = n0 + wn + 32 * j + (lane & 31);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int row = m0 + wm + 32 * i + mfma_row(v, lane);
+          if (row < g.M && col < g.N) C[(int64_t)row * g.ldc + col] = (TC)acc[i][j][v];
+        }
+      }
+    return;
+  }
+  // Any other epilogue: each wave passes its 32 x 32 tiles through a private
+  // LDS square and applies the epilogue in a rolled loop, so the code stays
+  // small and the accumulators never need dynamic indexing.
+  __builtin_amdgcn_s_barrier();  // every wave is done reading the stages
+  asm volatile("" ::: "memory");
+  float* sq = reinterpret_cast<float*>(smem) + wave * (32 * 33);
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+#pragma unroll
+      for (int v = 0; v < 16; v++) sq[mfma_row(v, lane) * 33 + (lane & 31)] = acc[i][j][v];
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the square is written
+      __builtin_amdgcn_wave_barrier();
+      const int col = n0 + wn + 32 * j + (lane & 31);
+#pragma unroll 1
+      for (int e = 0; e < 16; e++) {
+        const int r = e + 16 * (lane >> 5);
+        const int row = m0 + wm + 32 * i + r;
+        const float y = sq[r * 33 + (lane & 31)];
+        if (row < g.M && col < g.N) gemm_detail::epilogue_store<TC>(g, bt, row, col, y);
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next tile overwrites
+      __builtin_amdgcn_wave_barrier();
+    }
+}
+
+template <int BM, int BN, int STAGES, typename TC>
+int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
+  gemm_detail::KernelArgs ka;
+  ka.g = g;
+  ka.tiles_m = (int)ceil_div(g.M, BM);
+  ka.tiles_n = (int)ceil_div(g.N, BN);
+  const int64_t total = (int64_t)ka.tiles_m * ka.tiles_n * g.batch;
+  if (total > ((int64_t)1 << 30)) return set_error(AFHIP_ERR_INVALID_ARGUMENT, "GEMM has too many tiles");
+  ka.total_tiles = (int)total;
+  ka.per_xcd = (int)ceil_div(total, 8);
+  const size_t shared = (size_t)STAGES * (BM + BN) * kRowBytes;
+  auto kernel = gemm_dma_kernel<BM, BN, STAGES, TC>;
+  if (int st = allow_lds((const void*)kernel, shared)) return st;
+  return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(kThreads), shared, s, ka);
+}
+
+template <typename TC> int launch_typed(const GemmArgs& g, int tm, int tn, const char* label, hipStream_t s) {
+  if (tm == 192 && tn == 192) return launch_tile<192, 192, 3, TC>(g, label, s);
+  if (tm == 128 && tn == 128) return launch_tile<128, 128, 4, TC>(g, label, s);
+  if (tm == 128 && tn == 256) return launch_tile<128, 256, 3, TC>(g, label, s);
+  return set_error(AFHIP_ERR_INVALID_ARGUMENT, "unsupported LDS_DMA tile %dx%d", tm, tn);
+}
+
+}  // namespace
+
+bool dma_tile_supported(int tm, int tn) {
+  return (tm == 192 && tn == 192) || (tm == 128 && tn == 128) || (tm == 128 && tn == 256);
+}
+
+bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (t.precision != AFHIP_PRECISION_F16 || t.a_dtype != AFHIP_F16 || t.b_dtype != AFHIP_F16) return false;
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return false;
+  if (!al16(g.a) || !al16(g.b)) return false;
+  if (g.K % 8 || g.lda % 8 || g.ldb % 8 || g.sa % 8 || g.sb % 8) return false;
+  if (g.lda < g.K || g.ldb < g.K) return false;
+  // Byte offsets within a 256-row panel stay below the out-of-range marker.
+  return (int64_t)256 * std::max(g.lda, g.ldb) * 2 < (int64_t)kOutOfRange;
+}
+
+void dma_heuristic_tile(int64_t M, int64_t N, int64_t batch, int* tm, int* tn) {
+  // 192 x 192 tiles when both edges are multiples of 192 (L = 384, 576, ...)
+  // and there are enough of them for two per CU; otherwise 128 x 128, which
+  // keeps ragged-edge waste low and the tile count high.
+  const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  if (M % 192 == 0 && N % 192 == 0 && (M / 192) * (N / 192) * batch >= 2 * cus) {
+    *tm = *tn = 192;
+    return;
+  }
+  *tm = *tn = 128;
+}
+
+int run_gemm_dma(const GemmArgs& g, int c_dtype, int tm, int tn, const char* label, hipStream_t s) {
+  if (c_dtype == AFHIP_F16) return launch_typed<half_t>(g, tm, tn, label, s);
+  return launch_typed<float>(g, tm, tn, label, s);
+}
+
+}  // namespace afhip

@@ -130,18 +130,27 @@ struct Events {
   }
 };
 
-std::vector<afhip_variant> candidates(int precision) {
+// The candidate set for a shape class (gemmVariantCandidates,
+// gemm-selection.ts:234-272): every register-staged tile, plus the LDS_DMA
+// tiles where its operand contract holds.
+std::vector<afhip_variant> candidates(int precision, bool dma) {
   std::vector<afhip_variant> out;
-  const int shapes[4][2] = {{64, 64}, {64, 128}, {128, 64}, {128, 128}};
-  for (auto& s : shapes) {
+  auto add = [&](int kernel, int rows, int cols) {
     afhip_variant v{};
     v.precision = precision;
-    v.tile_rows = s[0];
-    v.tile_columns = s[1];
+    v.tile_rows = rows;
+    v.tile_columns = cols;
     v.tile_inner = 32;
     v.vectorized = 1;
     v.source = 1;
+    v.kernel = kernel;
     out.push_back(v);
+  };
+  const int shapes[4][2] = {{64, 64}, {64, 128}, {128, 64}, {128, 128}};
+  for (auto& s : shapes) add(AFHIP_KERNEL_REGISTER_STAGED, s[0], s[1]);
+  if (dma) {
+    const int dshapes[3][2] = {{128, 128}, {192, 192}, {128, 256}};
+    for (auto& s : dshapes) add(AFHIP_KERNEL_LDS_DMA, s[0], s[1]);
   }
   return out;
 }
@@ -227,7 +236,7 @@ int afhip_gemm_calibrate(const afhip_gemm_desc* d, afhip_variant* out) {
   double scale = 0.0;
   for (float v : expect) scale = std::max(scale, (double)std::fabs(v));
 
-  std::vector<afhip_variant> cands = candidates(t.precision);
+  std::vector<afhip_variant> cands = candidates(t.precision, dma_eligible(g, t));
   std::vector<afhip_variant> usable;
   std::vector<char> host((size_t)cm * N * ec);
   for (auto& v : cands) {
@@ -243,7 +252,7 @@ int afhip_gemm_calibrate(const afhip_gemm_desc* d, afhip_variant* out) {
     if (rel <= kCheckTolerance) usable.push_back(v);
   }
   if (usable.empty()) {
-    *out = heuristic_variant(t.precision, M, N, K, B);
+    *out = heuristic_variant(t, M, N, K, B);
     return set_error(AFHIP_ERR_HIP, "no GEMM candidate reproduced the reference; keeping the heuristic");
   }
 
@@ -297,7 +306,7 @@ int afhip_calibration_save(const char* path) {
   for (auto& kv : m) {
     f << (first ? "\n  " : ",\n  ") << "\"" << kv.first << "\": {\"precision\": " << kv.second.precision
       << ", \"tile_rows\": " << kv.second.tile_rows << ", \"tile_columns\": " << kv.second.tile_columns
-      << ", \"tile_inner\": " << kv.second.tile_inner << "}";
+      << ", \"tile_inner\": " << kv.second.tile_inner << ", \"kernel\": " << kv.second.kernel << "}";
     first = false;
   }
   f << "\n}}\n";
@@ -330,6 +339,7 @@ int afhip_calibration_load(const char* path) {
     v.vectorized = 1;
     v.source = 1;
     // A remembered answer is validated, not trusted (gemm-selection.ts:543-558).
+    if (!read_int(obj, "kernel", v.kernel)) v.kernel = AFHIP_KERNEL_REGISTER_STAGED;
     if (read_int(obj, "precision", v.precision) && read_int(obj, "tile_rows", v.tile_rows) &&
         read_int(obj, "tile_columns", v.tile_columns) && read_int(obj, "tile_inner", v.tile_inner) &&
         valid_variant(v))

@@ -161,12 +161,23 @@ AFHIP_API int afhip_gemm_grid(int64_t rows, int64_t columns, int32_t tile_column
  * GemmVariant (src/runtime/gemm.ts:150-206). */
 typedef struct afhip_variant {
   int32_t precision;   /* AFHIP_PRECISION_* */
-  int32_t tile_rows;   /* 64 | 128 */
-  int32_t tile_columns;/* 64 | 128 */
+  int32_t tile_rows;   /* REGISTER_STAGED: 64 | 128; LDS_DMA: 128 | 192 */
+  int32_t tile_columns;/* REGISTER_STAGED: 64 | 128; LDS_DMA: 128 | 192 | 256 */
   int32_t tile_inner;  /* 32 */
   int32_t vectorized;  /* 16-byte operand loads */
   int32_t source;      /* 0 heuristic, 1 calibrated, 2 pinned */
+  int32_t kernel;      /* AFHIP_KERNEL_* */
 } afhip_variant;
+
+/* Kernel families a variant can name.
+ * REGISTER_STAGED: operands pass through VGPRs into double-buffered LDS; any
+ *   operand dtype (f32, f16, int8 weights), tiles 64 or 128 on each side.
+ * LDS_DMA: operands go global -> LDS directly (buffer loads into LDS), several
+ *   k-steps in flight; f16 operands, K a multiple of 8; tiles 128x128,
+ *   192x192 or 128x256. The counterpart of the reference's matrix kernel with
+ *   deeper k-staging (src/runtime/gemm.ts:470-479). */
+#define AFHIP_KERNEL_REGISTER_STAGED 0
+#define AFHIP_KERNEL_LDS_DMA 1
 
 /* Shape-driven selection: the calibrated answer for this description's
  * shape class if one is held, else the heuristic. Replaces gemmVariant()

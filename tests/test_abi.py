@@ -90,7 +90,14 @@ def test_variant_selection_without_device():
 
     v = gemm.select_variant(131072, 256, 1024, precision="f16", a_dtype="f16", w_dtype="i8", out_dtype="f16")
     assert v.tile_rows in (64, 128) and v.tile_columns in (64, 128) and v.source == "heuristic"
-    assert v.name.startswith("mfma-f16-")
+    assert v.kernel == "register" and v.name.startswith("mfma-register-f16-")
+    # f16 operands on both sides take the LDS_DMA family; the triangle
+    # contraction at L = 384 (128 channels) tiles 192 x 192, two per CU.
+    v = gemm.select_variant(384, 384, 384, precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f16",
+                            batch=128)
+    assert (v.kernel, v.tile_rows, v.tile_columns) == ("lds_dma", 192, 192)
+    v = gemm.select_variant(81, 256, 132, precision="f16", a_dtype="f16", w_dtype="f16")
+    assert (v.kernel, v.tile_rows, v.tile_columns) == ("lds_dma", 128, 128)
 
 
 def test_calibration_document_round_trip(tmp_path):

@@ -90,6 +90,66 @@ def test_every_tile_variant_agrees(dev):
         assert rel_max(out.cpu().numpy(), expect) <= 1e-5, (tr, tc)
 
 
+LDS_DMA_TILES = [(128, 128), (192, 192), (128, 256)]
+
+
+def _batched_f16_plan(gemm, B, M, N, K, out_dtype, lda=0):
+    lda = lda or K
+    return gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
+                          out_dtype=out_dtype, batch=B, lda=lda, batch_stride_a=M * lda, batch_stride_w=N * K,
+                          batch_stride_c=M * N)
+
+
+@pytest.mark.parametrize("out_dtype", ["f16", "f32"])
+@pytest.mark.parametrize("shape", [(3, 200, 136, 104, 0), (2, 64, 448, 40, 56), (1, 385, 193, 392, 0)])
+def test_lds_dma_tiles_match_register_kernel_bitwise(dev, out_dtype, shape):
+    # Both kernel families walk K in the same 32-deep steps of two 16-deep
+    # MFMAs, so they accumulate in one order: every tile gives the register-
+    # staged kernel's result bit for bit, ragged M, N and K tails included.
+    from afhip import gemm
+
+    B, M, N, K, lda = shape
+    lda = lda or K
+    a = ref.round_f16(ref.normal(31 + M, (B, M, lda)))
+    w = ref.round_f16(ref.normal(32 + N, (B, N, K), 1 / K))
+    ad, wd = to_dev(a, dev).half(), to_dev(w, dev).half()
+    results = {}
+    for kernel, tiles in (("register", [(128, 128)]), ("lds_dma", LDS_DMA_TILES)):
+        for tr, tc in tiles:
+            gemm.force_variant(gemm.GemmVariant("f16", tr, tc, source="pinned", kernel=kernel))
+            try:
+                plan = _batched_f16_plan(gemm, B, M, N, K, out_dtype, lda)
+                assert plan.variant().kernel == kernel
+                results[(kernel, tr, tc)] = plan.run(ad, wd).float().cpu().numpy()
+            finally:
+                gemm.force_variant(None)
+    base = results[("register", 128, 128)]
+    expect = np.einsum("bmk,bnk->bmn", a[:, :, :K].astype(np.float64), w.astype(np.float64))
+    assert rel_max(base, expect) <= 2e-3
+    for key, got in results.items():
+        assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), key
+
+
+def test_config3_contraction_full_size(dev):
+    # BASELINE config 3's contraction: 128 channels of a 384 x 384 x 384
+    # f16 product with f32 accumulation and f16 output, against torch's f32
+    # batched product of the same f16 values.
+    import torch
+
+    from afhip import gemm
+
+    C, L = 128, 384
+    g = torch.Generator(device="cpu").manual_seed(0xAF2002)
+    a = torch.randn(C, L, L, generator=g).half().to(dev)
+    b = torch.randn(C, L, L, generator=g).half().to(dev)
+    plan = _batched_f16_plan(gemm, C, L, L, L, "f16")
+    assert plan.variant().kernel == "lds_dma"
+    out = plan.run(a, b).float()
+    expect = torch.bmm(a.float(), b.float().transpose(1, 2).contiguous())
+    err = (out - expect).abs().max().item() / expect.abs().max().item()
+    assert err <= 2e-3, err
+
+
 def test_relu_residual_epilogue(dev):
     from afhip import gemm
 
