@@ -30,39 +30,16 @@
 //    families give the same epilogue arithmetic.
 #include <algorithm>
 
+#include "dma.h"
 #include "gemm_kernel.h"
 
 namespace afhip {
-
-typedef int int32x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) uint32_t lds_u32;
-
-// buffer_load_dword{,x3,x4} ... lds: each lane's `size` bytes from
-// rsrc + voffset land in LDS at M0 (= lds) + 16 * lane (for size 16).
-__device__ void buffer_load_lds(int32x4_t rsrc, lds_u32* lds, int size, int voffset, int soffset, int offset,
-                                int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
 
 namespace {
 
 constexpr int kBK = 32;        // halves per k-step
 constexpr int kRowBytes = 64;  // one row of a k-step stage
 constexpr int kThreads = 256;
-constexpr uint32_t kOutOfRange = 0x80000000u;
-
-// Raw buffer resource (stride 0): loads at byte offsets >= `bytes` return 0.
-__device__ __forceinline__ int32x4_t make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  int32x4_t r;
-  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
-  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
-  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
-  r[3] = 0x00020000;
-  return r;
-}
-
-template <int N> __device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
 
@@ -124,8 +101,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
     for (int i = 0; i < LPW; i++) {
       const int q = wave + 4 * i;
       const uint32_t off = k0 + chunk_k[i] < g.K ? base_off[i] + 2u * k0 : kOutOfRange;
-      lds_u32* dst = reinterpret_cast<lds_u32*>((uintptr_t)(lds0 + stage * STAGE_BYTES + q * 1024));
-      buffer_load_lds(16 * q < BM ? ra : rb, dst, 16, (int)off, 0, 0, 0);
+      dma16(16 * q < BM ? ra : rb, lds0 + stage * STAGE_BYTES + q * 1024, off);
     }
   };
 
@@ -148,8 +124,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
     // the barrier then publishes it and retires stage ks - 1 for refilling.
     if (ks + STAGES - 2 < nk) wait_vmcnt<(STAGES - 2) * LPW>();
     else wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    block_barrier<false>();  // this loop writes no LDS itself
     if (ks + STAGES - 1 < nk) issue(ks + STAGES - 1, (ks + STAGES - 1) % STAGES);
     const unsigned char* st = smem + (ks % STAGES) * STAGE_BYTES;
 #pragma unroll
@@ -193,8 +168,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
   // Any other epilogue: each wave passes its 32 x 32 tiles through a private
   // LDS square and applies the epilogue in a rolled loop, so the code stays
   // small and the accumulators never need dynamic indexing.
-  __builtin_amdgcn_s_barrier();  // every wave is done reading the stages
-  asm volatile("" ::: "memory");
+  block_barrier<false>();  // every wave is done reading the stages
   float* sq = reinterpret_cast<float*>(smem) + wave * (32 * 33);
 #pragma unroll
   for (int i = 0; i < TM; i++)

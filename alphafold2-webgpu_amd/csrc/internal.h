@@ -89,7 +89,16 @@ __device__ __forceinline__ floatx16 mfma_f32(float a, float b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// Hardware transcendentals (v_exp_f32, v_rcp_f32, v_rsq_f32; 1 ulp each):
+// a correctly rounded division or square root expands to a dozen
+// instructions, which in the per-element gates and LayerNorms costs more
+// than the MFMA work around them.
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_rsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
+// 1 / (1 + e^-x) = 1 / (1 + 2^(-x log2 e)); an infinite 2^(...) gives 0.
+__device__ __forceinline__ float sigmoidf_(float x) {
+  return fast_rcp(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
 template <typename T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
 template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }

@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void opm_project_kernel(ProjectArgs a) {
     }
     var += __shfl_xor(var, 1);
     var += __shfl_xor(var, 2);
-    const float rstd = 1.0f / sqrtf(var / (float)a.cm + a.eps);
+    const float rstd = fast_rsqrt(var / (float)a.cm + a.eps);
     for (int c = part; c < a.cmp; c += 4) {
       float v = c < a.cm ? (xs[c * xpitch + q] - mean) * rstd * a.ln_scale[c] + a.ln_offset[c] : 0.0f;
       if (F16MATH) an[q * apitch + c] = (CT)v;

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const IT* __restrict__ 
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  const float rstd = 1.0f / sqrtf(v / (float)C + eps);
+  const float rstd = fast_rsqrt(v / (float)C + eps);
   for (int c = lane; c < C; c += 64) y[row * C + c] = (CT)(((float)xr[c] - mean) * rstd * scale[c] + offset[c]);
 }
 

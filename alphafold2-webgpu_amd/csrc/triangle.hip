@@ -111,7 +111,7 @@ __device__ __forceinline__ void column_stats(const float* xs, int pitch, int cha
   }
   v += __shfl_xor(v, 1);
   v += __shfl_xor(v, 2);
-  rstd = 1.0f / sqrtf(v / (float)channels + eps);
+  rstd = fast_rsqrt(v / (float)channels + eps);
 }
 
 template <typename T> __device__ __forceinline__ float ldf(const T* p) { return (float)*p; }

@@ -60,13 +60,31 @@ def cpu_baseline() -> dict:
             "ms_per_step_extrapolated": full / (flops / seconds) * 1e3}
 
 
+def copy_probe(mib: int) -> None:
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_each_way": n * 4, "launches": 10}))
+
+
 def main() -> None:
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                        help="only run a plain device-to-device copy of MIB MiB 10 times (the known-size kernel "
+                             "rocprof's FETCH_SIZE / WRITE_SIZE readings are scaled by) and exit")
     args = parser.parse_args()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the path runs on one device and bench.py "
                                    "--gpus N>1 is not supported (see DESIGN.md for how it would shard)"}))

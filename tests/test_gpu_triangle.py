@@ -100,7 +100,7 @@ def test_f16_within_1e2(dev, name, direction):
 
 
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
-@pytest.mark.parametrize("length,cz,ch", [(64, 128, 128), (37, 16, 24), (96, 128, 128)])
+@pytest.mark.parametrize("length,cz,ch", [(64, 128, 128), (37, 16, 24), (96, 128, 128), (100, 128, 128)])
 def test_synthetic_against_oracle(dev, direction, length, cz, ch):
     inp = ref.deterministic_triangle_input(length, cz, ch, seed=length + cz)
     expect = ref.triangle(direction, inp["z"], inp["mask"], inp["weights"], inp["epsilon"])
