@@ -1,0 +1,757 @@
+// afhip.node: a thin Node-API addon over libafhip's C ABI (include/afhip.h),
+// the HIP counterpart of the reference's native/wgpu-backend addon.
+//
+// Conventions, as the wgpu addon keeps them (native/wgpu-backend/src/lib.rs,
+// device.rs):
+//  - device memory is referred to by u32 handles from a registry owned by the
+//    addon (lib.rs:24-730 hands out u32 handles for every wgpu object);
+//    explicit destroy calls free them (lib.rs:706-730);
+//  - host data crosses as TypedArrays, copied in and out;
+//  - every call is synchronous on the JS thread;
+//  - failures become JS exceptions: RangeError for invalid arguments (the
+//    reference's RangeError, src/triangle/types.ts:42-52), Error otherwise,
+//    with libafhip's message.
+// The operator entry points (triangleRun, opmRun, transitionRun) upload,
+// run and read back in one call, as TriangleMultiplicationGpu.run does
+// (src/triangle/webgpu.ts:56-201), and report the elapsed wall time from
+// the first upload through the readback, as that method does (:189-196).
+#include <node_api.h>
+
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/afhip.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Error plumbing
+// ---------------------------------------------------------------------------
+
+struct JsError {
+  bool range;
+  std::string message;
+};
+
+void throw_js(napi_env env, const JsError& e) {
+  if (e.range) napi_throw_range_error(env, nullptr, e.message.c_str());
+  else napi_throw_error(env, nullptr, e.message.c_str());
+}
+
+// Status of a libafhip call -> exception (returns false when thrown).
+bool check(napi_env env, int status, const char* what) {
+  if (status == AFHIP_OK) return true;
+  std::string msg = std::string(what) + ": " + afhip_last_error();
+  throw_js(env, {status == AFHIP_ERR_INVALID_ARGUMENT, msg});
+  return false;
+}
+
+#define NAPI_OK(expr)                                          \
+  do {                                                         \
+    if ((expr) != napi_ok) {                                   \
+      napi_throw_error(env, nullptr, "Node-API call failed: " #expr); \
+      return nullptr;                                          \
+    }                                                          \
+  } while (0)
+
+struct Args {
+  size_t argc = 8;
+  napi_value argv[8];
+  napi_value self;
+};
+
+bool get_args(napi_env env, napi_callback_info info, Args& a, size_t need) {
+  if (napi_get_cb_info(env, info, &a.argc, a.argv, &a.self, nullptr) != napi_ok) return false;
+  if (a.argc < need) {
+    napi_throw_type_error(env, nullptr, "too few arguments");
+    return false;
+  }
+  return true;
+}
+
+bool get_int64(napi_env env, napi_value v, int64_t* out) {
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok) return false;
+  if (t == napi_bigint) {
+    bool lossless;
+    return napi_get_value_bigint_int64(env, v, out, &lossless) == napi_ok;
+  }
+  double d;
+  if (t != napi_number || napi_get_value_double(env, v, &d) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "expected a number");
+    return false;
+  }
+  *out = (int64_t)d;
+  return true;
+}
+
+bool get_string(napi_env env, napi_value v, std::string* out) {
+  size_t len = 0;
+  if (napi_get_value_string_utf8(env, v, nullptr, 0, &len) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "expected a string");
+    return false;
+  }
+  std::vector<char> buf(len + 1);
+  napi_get_value_string_utf8(env, v, buf.data(), buf.size(), &len);
+  out->assign(buf.data(), len);
+  return true;
+}
+
+// Integer-valued property of a descriptor object (missing -> fallback).
+bool prop_int(napi_env env, napi_value obj, const char* name, int64_t fallback, int64_t* out) {
+  bool has = false;
+  napi_has_named_property(env, obj, name, &has);
+  if (!has) {
+    *out = fallback;
+    return true;
+  }
+  napi_value v;
+  napi_get_named_property(env, obj, name, &v);
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_undefined) {
+    *out = fallback;
+    return true;
+  }
+  return get_int64(env, v, out);
+}
+
+bool prop_double(napi_env env, napi_value obj, const char* name, double fallback, double* out) {
+  bool has = false;
+  napi_has_named_property(env, obj, name, &has);
+  if (!has) {
+    *out = fallback;
+    return true;
+  }
+  napi_value v;
+  napi_get_named_property(env, obj, name, &v);
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_undefined) {
+    *out = fallback;
+    return true;
+  }
+  if (napi_get_value_double(env, v, out) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "expected a number");
+    return false;
+  }
+  return true;
+}
+
+struct HostView {
+  void* data = nullptr;
+  size_t bytes = 0;
+  napi_typedarray_type type = napi_uint8_array;
+};
+
+bool get_view(napi_env env, napi_value v, HostView* out) {
+  bool is_typed = false;
+  napi_is_typedarray(env, v, &is_typed);
+  if (!is_typed) {
+    napi_throw_type_error(env, nullptr, "expected a TypedArray");
+    return false;
+  }
+  size_t length = 0, offset = 0;
+  napi_value ab;
+  if (napi_get_typedarray_info(env, v, &out->type, &length, &out->data, &ab, &offset) != napi_ok) return false;
+  size_t es = 1;
+  switch (out->type) {
+    case napi_int16_array: case napi_uint16_array: es = 2; break;
+    case napi_int32_array: case napi_uint32_array: case napi_float32_array: es = 4; break;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: es = 8; break;
+    default: es = 1;
+  }
+  out->bytes = length * es;
+  return true;
+}
+
+napi_value make_float32(napi_env env, const std::vector<float>& v) {
+  napi_value ab, arr;
+  void* data = nullptr;
+  if (napi_create_arraybuffer(env, v.size() * 4, &data, &ab) != napi_ok) return nullptr;
+  if (!v.empty()) std::memcpy(data, v.data(), v.size() * 4);
+  if (napi_create_typedarray(env, napi_float32_array, v.size(), ab, 0, &arr) != napi_ok) return nullptr;
+  return arr;
+}
+
+napi_value make_number(napi_env env, double d) {
+  napi_value v;
+  napi_create_double(env, d, &v);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Device-memory registry (u32 handles), the wgpu addon's Registry
+// (native/wgpu-backend/src/device.rs:60-95) for HIP buffers and plans.
+// ---------------------------------------------------------------------------
+
+struct Registry {
+  uint32_t next = 1;
+  std::map<uint32_t, std::pair<void*, size_t>> buffers;
+  std::map<uint32_t, afhip_gemm_plan*> plans;
+};
+Registry g_reg;
+
+// RAII device allocation for the operator entry points.
+struct DeviceBuf {
+  void* p = nullptr;
+  ~DeviceBuf() {
+    if (p) afhip_buffer_destroy(p);
+  }
+  int alloc(size_t bytes) { return afhip_buffer_create(bytes ? bytes : 1, &p); }
+};
+
+double now_ms() {
+  using namespace std::chrono;
+  return duration<double, std::milli>(steady_clock::now().time_since_epoch()).count();
+}
+
+// ---------------------------------------------------------------------------
+// Context
+// ---------------------------------------------------------------------------
+
+napi_value Open(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 0)) return nullptr;
+  int64_t ordinal = 0;
+  if (a.argc > 0 && !get_int64(env, a.argv[0], &ordinal)) return nullptr;
+  if (!check(env, afhip_open((int)ordinal), "open")) return nullptr;
+  return nullptr;
+}
+
+napi_value Close(napi_env env, napi_callback_info) {
+  for (auto& kv : g_reg.buffers) afhip_buffer_destroy(kv.second.first);
+  for (auto& kv : g_reg.plans) afhip_gemm_plan_destroy(kv.second);
+  g_reg.buffers.clear();
+  g_reg.plans.clear();
+  if (!check(env, afhip_close(), "close")) return nullptr;
+  return nullptr;
+}
+
+napi_value AbiVersion(napi_env env, napi_callback_info) { return make_number(env, afhip_abi_version()); }
+
+napi_value DeviceReport(napi_env env, napi_callback_info) {
+  std::vector<char> buf(4096);
+  if (!check(env, afhip_device_report(buf.data(), buf.size()), "deviceReport")) return nullptr;
+  napi_value s;
+  NAPI_OK(napi_create_string_utf8(env, buf.data(), NAPI_AUTO_LENGTH, &s));
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// Buffers
+// ---------------------------------------------------------------------------
+
+napi_value BufferCreate(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  int64_t bytes;
+  if (!get_int64(env, a.argv[0], &bytes)) return nullptr;
+  if (bytes <= 0) {
+    throw_js(env, {true, "buffer size must be positive"});
+    return nullptr;
+  }
+  void* p = nullptr;
+  if (!check(env, afhip_buffer_create((size_t)bytes, &p), "bufferCreate")) return nullptr;
+  const uint32_t h = g_reg.next++;
+  g_reg.buffers[h] = {p, (size_t)bytes};
+  return make_number(env, h);
+}
+
+bool lookup_buffer(napi_env env, napi_value v, void** p, size_t* bytes) {
+  int64_t h;
+  if (!get_int64(env, v, &h)) return false;
+  auto it = g_reg.buffers.find((uint32_t)h);
+  if (it == g_reg.buffers.end()) {
+    throw_js(env, {true, "unknown buffer handle " + std::to_string(h)});
+    return false;
+  }
+  *p = it->second.first;
+  if (bytes) *bytes = it->second.second;
+  return true;
+}
+
+napi_value BufferDestroy(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  int64_t h;
+  if (!get_int64(env, a.argv[0], &h)) return nullptr;
+  auto it = g_reg.buffers.find((uint32_t)h);
+  if (it == g_reg.buffers.end()) return nullptr;
+  afhip_buffer_destroy(it->second.first);
+  g_reg.buffers.erase(it);
+  return nullptr;
+}
+
+napi_value BufferWrite(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  void* p;
+  size_t cap;
+  int64_t offset;
+  HostView src;
+  if (!lookup_buffer(env, a.argv[0], &p, &cap) || !get_int64(env, a.argv[1], &offset) || !get_view(env, a.argv[2], &src))
+    return nullptr;
+  if (offset < 0 || (size_t)offset + src.bytes > cap) {
+    throw_js(env, {true, "write past the end of the buffer"});
+    return nullptr;
+  }
+  if (!check(env, afhip_buffer_write(p, (size_t)offset, src.data, src.bytes), "bufferWrite")) return nullptr;
+  return nullptr;
+}
+
+napi_value BufferRead(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  void* p;
+  size_t cap;
+  int64_t offset;
+  HostView dst;
+  if (!lookup_buffer(env, a.argv[0], &p, &cap) || !get_int64(env, a.argv[1], &offset) || !get_view(env, a.argv[2], &dst))
+    return nullptr;
+  if (offset < 0 || (size_t)offset + dst.bytes > cap) {
+    throw_js(env, {true, "read past the end of the buffer"});
+    return nullptr;
+  }
+  if (!check(env, afhip_buffer_read(p, (size_t)offset, dst.data, dst.bytes), "bufferRead")) return nullptr;
+  return nullptr;
+}
+
+napi_value Synchronize(napi_env env, napi_callback_info) {
+  if (!check(env, afhip_synchronize(nullptr), "synchronize")) return nullptr;
+  return nullptr;
+}
+
+// ---------------------------------------------------------------------------
+// GEMM plan surface
+// ---------------------------------------------------------------------------
+
+bool read_gemm_desc(napi_env env, napi_value o, afhip_gemm_desc* d) {
+  std::memset(d, 0, sizeof(*d));
+  int64_t v;
+#define FIELD(name, js, fallback)                                   \
+  if (!prop_int(env, o, js, fallback, &v)) return false;            \
+  d->name = (decltype(d->name))v;
+  FIELD(rows, "rows", 0)
+  FIELD(inner, "inner", 0)
+  FIELD(columns, "columns", 0)
+  FIELD(batch, "batch", 1)
+  FIELD(precision, "precision", AFHIP_PRECISION_F32)
+  FIELD(a_dtype, "aDtype", AFHIP_F32)
+  FIELD(w_dtype, "wDtype", AFHIP_F32)
+  FIELD(w_layout, "wLayout", AFHIP_WEIGHT_COLUMN_CONTIGUOUS)
+  FIELD(out_dtype, "outDtype", AFHIP_F32)
+  FIELD(epilogue, "epilogue", 0)
+  FIELD(heads, "heads", 0)
+  FIELD(head_dim, "headDim", 0)
+  FIELD(lda, "lda", 0)
+  FIELD(ldw, "ldw", 0)
+  FIELD(ldc, "ldc", 0)
+  FIELD(batch_stride_a, "batchStrideA", 0)
+  FIELD(batch_stride_w, "batchStrideW", 0)
+  FIELD(batch_stride_c, "batchStrideC", 0)
+#undef FIELD
+  return true;
+}
+
+napi_value variant_object(napi_env env, const afhip_variant& v) {
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "precision", make_number(env, v.precision));
+  napi_set_named_property(env, o, "tileRows", make_number(env, v.tile_rows));
+  napi_set_named_property(env, o, "tileColumns", make_number(env, v.tile_columns));
+  napi_set_named_property(env, o, "tileInner", make_number(env, v.tile_inner));
+  napi_set_named_property(env, o, "source", make_number(env, v.source));
+  napi_set_named_property(env, o, "kernel", make_number(env, v.kernel));
+  return o;
+}
+
+napi_value GemmGrid(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  int64_t rows, cols, tc = 128, tr = 64;
+  if (!get_int64(env, a.argv[0], &rows) || !get_int64(env, a.argv[1], &cols)) return nullptr;
+  if (a.argc > 2 && !get_int64(env, a.argv[2], &tc)) return nullptr;
+  if (a.argc > 3 && !get_int64(env, a.argv[3], &tr)) return nullptr;
+  uint32_t xy[2];
+  if (!check(env, afhip_gemm_grid(rows, cols, (int32_t)tc, (int32_t)tr, xy), "gemmGrid")) return nullptr;
+  napi_value arr;
+  napi_create_array_with_length(env, 2, &arr);
+  napi_set_element(env, arr, 0, make_number(env, xy[0]));
+  napi_set_element(env, arr, 1, make_number(env, xy[1]));
+  return arr;
+}
+
+napi_value GemmSelect(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  afhip_gemm_desc d;
+  if (!read_gemm_desc(env, a.argv[0], &d)) return nullptr;
+  afhip_variant v;
+  if (!check(env, afhip_gemm_select(&d, &v), "gemmSelect")) return nullptr;
+  return variant_object(env, v);
+}
+
+napi_value GemmCalibrate(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  afhip_gemm_desc d;
+  if (!read_gemm_desc(env, a.argv[0], &d)) return nullptr;
+  afhip_variant v;
+  if (!check(env, afhip_gemm_calibrate(&d, &v), "gemmCalibrate")) return nullptr;
+  return variant_object(env, v);
+}
+
+napi_value GemmForceVariant(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 0)) return nullptr;
+  napi_valuetype t = napi_undefined;
+  if (a.argc > 0) napi_typeof(env, a.argv[0], &t);
+  if (t == napi_undefined || t == napi_null) {
+    if (!check(env, afhip_gemm_force_variant(nullptr), "gemmForceVariant")) return nullptr;
+    return nullptr;
+  }
+  afhip_variant v{};
+  int64_t x;
+  if (!prop_int(env, a.argv[0], "precision", AFHIP_PRECISION_F16, &x)) return nullptr;
+  v.precision = (int32_t)x;
+  if (!prop_int(env, a.argv[0], "tileRows", 128, &x)) return nullptr;
+  v.tile_rows = (int32_t)x;
+  if (!prop_int(env, a.argv[0], "tileColumns", 128, &x)) return nullptr;
+  v.tile_columns = (int32_t)x;
+  if (!prop_int(env, a.argv[0], "tileInner", 32, &x)) return nullptr;
+  v.tile_inner = (int32_t)x;
+  if (!prop_int(env, a.argv[0], "kernel", AFHIP_KERNEL_REGISTER_STAGED, &x)) return nullptr;
+  v.kernel = (int32_t)x;
+  v.vectorized = 1;
+  v.source = 2;
+  if (!check(env, afhip_gemm_force_variant(&v), "gemmForceVariant")) return nullptr;
+  return nullptr;
+}
+
+napi_value CalibrationLoad(napi_env env, napi_callback_info info) {
+  Args a;
+  std::string path;
+  if (!get_args(env, info, a, 1) || !get_string(env, a.argv[0], &path)) return nullptr;
+  if (!check(env, afhip_calibration_load(path.c_str()), "calibrationLoad")) return nullptr;
+  return nullptr;
+}
+
+napi_value CalibrationSave(napi_env env, napi_callback_info info) {
+  Args a;
+  std::string path;
+  if (!get_args(env, info, a, 1) || !get_string(env, a.argv[0], &path)) return nullptr;
+  if (!check(env, afhip_calibration_save(path.c_str()), "calibrationSave")) return nullptr;
+  return nullptr;
+}
+
+napi_value GemmPlanCreate(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  afhip_gemm_desc d;
+  if (!read_gemm_desc(env, a.argv[0], &d)) return nullptr;
+  afhip_gemm_plan* plan = nullptr;
+  if (!check(env, afhip_gemm_plan_create(&d, &plan), "gemmPlanCreate")) return nullptr;
+  const uint32_t h = g_reg.next++;
+  g_reg.plans[h] = plan;
+  return make_number(env, h);
+}
+
+napi_value GemmPlanDestroy(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  int64_t h;
+  if (!get_int64(env, a.argv[0], &h)) return nullptr;
+  auto it = g_reg.plans.find((uint32_t)h);
+  if (it != g_reg.plans.end()) {
+    afhip_gemm_plan_destroy(it->second);
+    g_reg.plans.erase(it);
+  }
+  return nullptr;
+}
+
+napi_value GemmWorkspaceSize(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  int64_t h;
+  if (!get_int64(env, a.argv[0], &h)) return nullptr;
+  auto it = g_reg.plans.find((uint32_t)h);
+  if (it == g_reg.plans.end()) {
+    throw_js(env, {true, "unknown plan handle"});
+    return nullptr;
+  }
+  size_t bytes = 0;
+  if (!check(env, afhip_gemm_workspace_size(it->second, &bytes), "gemmWorkspaceSize")) return nullptr;
+  return make_number(env, (double)bytes);
+}
+
+// gemmRun(plan, {a, w, scale?, bias?, residual?, c, workspace?}) with buffer handles.
+napi_value GemmRun(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  int64_t h;
+  if (!get_int64(env, a.argv[0], &h)) return nullptr;
+  auto it = g_reg.plans.find((uint32_t)h);
+  if (it == g_reg.plans.end()) {
+    throw_js(env, {true, "unknown plan handle"});
+    return nullptr;
+  }
+  const char* names[7] = {"a", "w", "scale", "bias", "residual", "c", "workspace"};
+  void* ptrs[7] = {};
+  size_t sizes[7] = {};
+  for (int i = 0; i < 7; i++) {
+    bool has = false;
+    napi_has_named_property(env, a.argv[1], names[i], &has);
+    if (!has) continue;
+    napi_value v;
+    napi_get_named_property(env, a.argv[1], names[i], &v);
+    napi_valuetype t;
+    napi_typeof(env, v, &t);
+    if (t == napi_undefined || t == napi_null) continue;
+    if (!lookup_buffer(env, v, &ptrs[i], &sizes[i])) return nullptr;
+  }
+  if (!check(env,
+             afhip_gemm_run(it->second, ptrs[0], ptrs[1], (const float*)ptrs[2], (const float*)ptrs[3], ptrs[4],
+                            ptrs[5], ptrs[6], sizes[6], nullptr),
+             "gemmRun"))
+    return nullptr;
+  return nullptr;
+}
+
+// ---------------------------------------------------------------------------
+// Operators with host arrays (upload, prepare, run, read back)
+// ---------------------------------------------------------------------------
+
+napi_value result_object(napi_env env, const std::vector<float>& out, double ms, size_t peak) {
+  napi_value o, mem;
+  napi_create_object(env, &o);
+  napi_value arr = make_float32(env, out);
+  if (!arr) return nullptr;
+  napi_set_named_property(env, o, "output", arr);
+  napi_set_named_property(env, o, "elapsedMilliseconds", make_number(env, ms));
+  napi_create_object(env, &mem);
+  napi_set_named_property(env, mem, "peakBytes", make_number(env, (double)peak));
+  napi_set_named_property(env, o, "memory", mem);
+  return o;
+}
+
+// triangleRun(desc, z: Float32Array | Uint16Array (f16 bits), mask: Float32Array, packed: Float32Array)
+napi_value TriangleRun(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 4)) return nullptr;
+  afhip_triangle_desc d{};
+  int64_t v;
+  double eps;
+  napi_value o = a.argv[0];
+  if (!prop_int(env, o, "length", 0, &v)) return nullptr;
+  d.length = (int32_t)v;
+  if (!prop_int(env, o, "cZ", 0, &v)) return nullptr;
+  d.c_z = (int32_t)v;
+  if (!prop_int(env, o, "cHidden", 0, &v)) return nullptr;
+  d.c_hidden = (int32_t)v;
+  if (!prop_int(env, o, "direction", AFHIP_TRIANGLE_OUTGOING, &v)) return nullptr;
+  d.direction = (int32_t)v;
+  if (!prop_int(env, o, "precision", AFHIP_PRECISION_F32, &v)) return nullptr;
+  d.precision = (int32_t)v;
+  if (!prop_int(env, o, "blockRows", 0, &v)) return nullptr;
+  d.block_rows = (int32_t)v;
+  if (!prop_double(env, o, "epsilon", 1e-5, &eps)) return nullptr;
+  d.epsilon = (float)eps;
+  d.out_dtype = AFHIP_F32;
+  d.residual = 0;
+  HostView z, mask, packed;
+  if (!get_view(env, a.argv[1], &z) || !get_view(env, a.argv[2], &mask) || !get_view(env, a.argv[3], &packed))
+    return nullptr;
+  d.pair_dtype = z.type == napi_uint16_array ? AFHIP_F16 : AFHIP_F32;
+  size_t wbytes = 0, wsbytes = 0;
+  if (!check(env, afhip_triangle_weights_size(&d, &wbytes), "triangle") ||
+      !check(env, afhip_triangle_workspace_size(&d, &wsbytes), "triangle"))
+    return nullptr;
+  const size_t pairs = (size_t)d.length * d.length;
+  const size_t zbytes = pairs * d.c_z * (d.pair_dtype == AFHIP_F16 ? 2 : 4);
+  if (z.bytes != zbytes || mask.bytes != pairs * 4) {
+    throw_js(env, {true, "z or mask does not match the descriptor's shape"});
+    return nullptr;
+  }
+  const double t0 = now_ms();
+  DeviceBuf dz, dm, dp, dw, dws, dout;
+  if (!check(env, dz.alloc(zbytes), "triangle") || !check(env, dm.alloc(mask.bytes), "triangle") ||
+      !check(env, dp.alloc(packed.bytes), "triangle") || !check(env, dw.alloc(wbytes), "triangle") ||
+      !check(env, dws.alloc(wsbytes), "triangle") || !check(env, dout.alloc(pairs * d.c_z * 4), "triangle"))
+    return nullptr;
+  if (!check(env, afhip_buffer_write(dz.p, 0, z.data, zbytes), "triangle") ||
+      !check(env, afhip_buffer_write(dm.p, 0, mask.data, mask.bytes), "triangle") ||
+      !check(env, afhip_buffer_write(dp.p, 0, packed.data, packed.bytes), "triangle") ||
+      !check(env, afhip_triangle_prepare_weights(&d, (const float*)dp.p, dw.p, nullptr), "triangle") ||
+      !check(env, afhip_triangle_run(&d, dz.p, (const float*)dm.p, dw.p, dout.p, dws.p, wsbytes, nullptr),
+             "triangle"))
+    return nullptr;
+  std::vector<float> out(pairs * d.c_z);
+  if (!check(env, afhip_buffer_read(dout.p, 0, out.data(), out.size() * 4), "triangle")) return nullptr;
+  const double ms = now_ms() - t0;
+  const size_t peak = zbytes + mask.bytes + packed.bytes + wbytes + wsbytes + out.size() * 4;
+  return result_object(env, out, ms, peak);
+}
+
+// opmRun(desc, activations: Float32Array, mask: Float32Array, packed: Float32Array)
+napi_value OpmRun(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 4)) return nullptr;
+  afhip_opm_desc d{};
+  int64_t v;
+  double e1, e2;
+  napi_value o = a.argv[0];
+  if (!prop_int(env, o, "sequences", 0, &v)) return nullptr;
+  d.sequences = (int32_t)v;
+  if (!prop_int(env, o, "length", 0, &v)) return nullptr;
+  d.length = (int32_t)v;
+  if (!prop_int(env, o, "cM", 0, &v)) return nullptr;
+  d.c_m = (int32_t)v;
+  if (!prop_int(env, o, "cOuter", 0, &v)) return nullptr;
+  d.c_outer = (int32_t)v;
+  if (!prop_int(env, o, "cZ", 0, &v)) return nullptr;
+  d.c_z = (int32_t)v;
+  if (!prop_int(env, o, "precision", AFHIP_PRECISION_F32, &v)) return nullptr;
+  d.precision = (int32_t)v;
+  if (!prop_int(env, o, "rowBlockResidues", 0, &v)) return nullptr;
+  d.row_block = (int32_t)v;
+  if (!prop_double(env, o, "layerNormEpsilon", 1e-5, &e1) || !prop_double(env, o, "normalizationEpsilon", 1e-3, &e2))
+    return nullptr;
+  d.layer_norm_epsilon = (float)e1;
+  d.normalization_epsilon = (float)e2;
+  d.msa_dtype = AFHIP_F32;
+  d.out_dtype = AFHIP_F32;
+  HostView act, mask, packed;
+  if (!get_view(env, a.argv[1], &act) || !get_view(env, a.argv[2], &mask) || !get_view(env, a.argv[3], &packed))
+    return nullptr;
+  size_t wbytes = 0, wsbytes = 0;
+  if (!check(env, afhip_opm_weights_size(&d, &wbytes), "outerProductMean") ||
+      !check(env, afhip_opm_workspace_size(&d, &wsbytes), "outerProductMean"))
+    return nullptr;
+  const size_t rows = (size_t)d.sequences * d.length;
+  if (act.bytes != rows * d.c_m * 4 || mask.bytes != rows * 4) {
+    throw_js(env, {true, "activations or mask do not match the descriptor's shape"});
+    return nullptr;
+  }
+  const size_t obytes = (size_t)d.length * d.length * d.c_z * 4;
+  const double t0 = now_ms();
+  DeviceBuf da, dm, dp, dw, dws, dout;
+  if (!check(env, da.alloc(act.bytes), "outerProductMean") || !check(env, dm.alloc(mask.bytes), "outerProductMean") ||
+      !check(env, dp.alloc(packed.bytes), "outerProductMean") || !check(env, dw.alloc(wbytes), "outerProductMean") ||
+      !check(env, dws.alloc(wsbytes), "outerProductMean") || !check(env, dout.alloc(obytes), "outerProductMean"))
+    return nullptr;
+  if (!check(env, afhip_buffer_write(da.p, 0, act.data, act.bytes), "outerProductMean") ||
+      !check(env, afhip_buffer_write(dm.p, 0, mask.data, mask.bytes), "outerProductMean") ||
+      !check(env, afhip_buffer_write(dp.p, 0, packed.data, packed.bytes), "outerProductMean") ||
+      !check(env, afhip_opm_prepare_weights(&d, (const float*)dp.p, dw.p, nullptr), "outerProductMean") ||
+      !check(env, afhip_opm_run(&d, da.p, (const float*)dm.p, dw.p, dout.p, dws.p, wsbytes, nullptr),
+             "outerProductMean"))
+    return nullptr;
+  std::vector<float> out(obytes / 4);
+  if (!check(env, afhip_buffer_read(dout.p, 0, out.data(), obytes), "outerProductMean")) return nullptr;
+  const double ms = now_ms() - t0;
+  return result_object(env, out, ms, act.bytes + mask.bytes + packed.bytes + wbytes + wsbytes + obytes);
+}
+
+// transitionRun(desc, activations: Float32Array, packed: Float32Array)
+napi_value TransitionRun(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  afhip_transition_desc d{};
+  int64_t v;
+  double eps;
+  napi_value o = a.argv[0];
+  if (!prop_int(env, o, "rows", 0, &v)) return nullptr;
+  d.rows = v;
+  if (!prop_int(env, o, "channels", 0, &v)) return nullptr;
+  d.channels = (int32_t)v;
+  if (!prop_int(env, o, "hidden", 0, &v)) return nullptr;
+  d.hidden = (int32_t)v;
+  if (!prop_int(env, o, "precision", AFHIP_PRECISION_F32, &v)) return nullptr;
+  d.precision = (int32_t)v;
+  if (!prop_double(env, o, "epsilon", 1e-5, &eps)) return nullptr;
+  d.epsilon = (float)eps;
+  d.in_dtype = AFHIP_F32;
+  d.out_dtype = AFHIP_F32;
+  HostView act, packed;
+  if (!get_view(env, a.argv[1], &act) || !get_view(env, a.argv[2], &packed)) return nullptr;
+  size_t wbytes = 0, wsbytes = 0;
+  if (!check(env, afhip_transition_weights_size(&d, &wbytes), "transition") ||
+      !check(env, afhip_transition_workspace_size(&d, &wsbytes), "transition"))
+    return nullptr;
+  if (act.bytes != (size_t)d.rows * d.channels * 4) {
+    throw_js(env, {true, "activations do not match the descriptor's shape"});
+    return nullptr;
+  }
+  const double t0 = now_ms();
+  DeviceBuf da, dp, dw, dws, dout;
+  if (!check(env, da.alloc(act.bytes), "transition") || !check(env, dp.alloc(packed.bytes), "transition") ||
+      !check(env, dw.alloc(wbytes), "transition") || !check(env, dws.alloc(wsbytes), "transition") ||
+      !check(env, dout.alloc(act.bytes), "transition"))
+    return nullptr;
+  if (!check(env, afhip_buffer_write(da.p, 0, act.data, act.bytes), "transition") ||
+      !check(env, afhip_buffer_write(dp.p, 0, packed.data, packed.bytes), "transition") ||
+      !check(env, afhip_transition_prepare_weights(&d, (const float*)dp.p, dw.p, nullptr), "transition") ||
+      !check(env, afhip_transition_run(&d, da.p, dw.p, dout.p, dws.p, wsbytes, nullptr), "transition"))
+    return nullptr;
+  std::vector<float> out(act.bytes / 4);
+  if (!check(env, afhip_buffer_read(dout.p, 0, out.data(), act.bytes), "transition")) return nullptr;
+  const double ms = now_ms() - t0;
+  return result_object(env, out, ms, act.bytes * 2 + packed.bytes + wbytes + wsbytes);
+}
+
+// ---------------------------------------------------------------------------
+// Kernel timing (WebGpuExecution's timestamp profile, execution.ts:329-345)
+// ---------------------------------------------------------------------------
+
+napi_value TimingEnable(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  bool on = false;
+  napi_get_value_bool(env, a.argv[0], &on);
+  if (!check(env, afhip_timing_enable(on ? 1 : 0), "timingEnable")) return nullptr;
+  return nullptr;
+}
+
+napi_value TimingReset(napi_env env, napi_callback_info) {
+  if (!check(env, afhip_timing_reset(), "timingReset")) return nullptr;
+  return nullptr;
+}
+
+napi_value TimingReport(napi_env env, napi_callback_info) {
+  std::vector<char> buf(1 << 16);
+  if (!check(env, afhip_timing_report(buf.data(), buf.size()), "timingReport")) return nullptr;
+  napi_value s;
+  NAPI_OK(napi_create_string_utf8(env, buf.data(), NAPI_AUTO_LENGTH, &s));
+  return s;
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+  const struct {
+    const char* name;
+    napi_callback cb;
+  } fns[] = {
+      {"open", Open}, {"close", Close}, {"abiVersion", AbiVersion}, {"deviceReport", DeviceReport},
+      {"bufferCreate", BufferCreate}, {"bufferDestroy", BufferDestroy}, {"bufferWrite", BufferWrite},
+      {"bufferRead", BufferRead}, {"synchronize", Synchronize}, {"gemmGrid", GemmGrid}, {"gemmSelect", GemmSelect},
+      {"gemmCalibrate", GemmCalibrate}, {"gemmForceVariant", GemmForceVariant}, {"calibrationLoad", CalibrationLoad},
+      {"calibrationSave", CalibrationSave}, {"gemmPlanCreate", GemmPlanCreate}, {"gemmPlanDestroy", GemmPlanDestroy},
+      {"gemmWorkspaceSize", GemmWorkspaceSize}, {"gemmRun", GemmRun}, {"triangleRun", TriangleRun},
+      {"opmRun", OpmRun}, {"transitionRun", TransitionRun}, {"timingEnable", TimingEnable},
+      {"timingReset", TimingReset}, {"timingReport", TimingReport},
+  };
+  for (const auto& f : fns) {
+    napi_value fn;
+    if (napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn) != napi_ok) return nullptr;
+    if (napi_set_named_property(env, exports, f.name, fn) != napi_ok) return nullptr;
+  }
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)

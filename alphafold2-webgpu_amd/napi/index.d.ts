@@ -1,0 +1,152 @@
+// Types of the afhip Node-API shim (index.js), matching the reference's
+// operator signatures so TypeScript callers swap the class and nothing else:
+// src/triangle/webgpu.ts:9-23, src/triangle/types.ts:9-52,
+// src/evoformer/outer-product-mean.ts:21-40, src/evoformer/transition.ts:18-31.
+
+export interface MemorySnapshot {
+  peakBytes: number;
+}
+
+export interface OperatorResult {
+  output: Float32Array;
+  elapsedMilliseconds: number;
+  memory: MemorySnapshot;
+}
+
+export type Precision = "f32" | "f16";
+
+export interface TriangleMultiplicationWeights {
+  layerNormInWeight: Float32Array;
+  layerNormInBias: Float32Array;
+  linearAPWeight: Float32Array;
+  linearAPBias: Float32Array;
+  linearAGWeight: Float32Array;
+  linearAGBias: Float32Array;
+  linearBPWeight: Float32Array;
+  linearBPBias: Float32Array;
+  linearBGWeight: Float32Array;
+  linearBGBias: Float32Array;
+  layerNormOutWeight: Float32Array;
+  layerNormOutBias: Float32Array;
+  linearZWeight: Float32Array;
+  linearZBias: Float32Array;
+  linearGWeight: Float32Array;
+  linearGBias: Float32Array;
+}
+
+export interface TriangleMultiplicationInput {
+  shape: readonly [length: number, cZ: number, cHidden: number];
+  /** [L][L][cZ] f32, or f16 bit patterns as a Uint16Array */
+  z: Float32Array | Uint16Array;
+  mask: Float32Array;
+  weights: TriangleMultiplicationWeights;
+  epsilon?: number;
+}
+
+export interface TriangleGpuOptions {
+  precision?: Precision;
+  blockRows?: number;
+}
+
+export declare class TriangleMultiplicationOutgoingGpu {
+  run(input: TriangleMultiplicationInput, options?: TriangleGpuOptions): OperatorResult;
+}
+
+export declare class TriangleMultiplicationIncomingGpu {
+  run(input: TriangleMultiplicationInput, options?: TriangleGpuOptions): OperatorResult;
+}
+
+export interface OuterProductMeanWeights {
+  layerNormScale: Float32Array;
+  layerNormOffset: Float32Array;
+  leftWeight: Float32Array;
+  leftBias: Float32Array;
+  rightWeight: Float32Array;
+  rightBias: Float32Array;
+  outputWeight: Float32Array;
+  outputBias: Float32Array;
+}
+
+export interface OuterProductMeanInput {
+  shape: readonly [sequences: number, length: number, cM: number, cOuter: number, cZ: number];
+  activations: Float32Array;
+  mask: Float32Array;
+  weights: OuterProductMeanWeights;
+  layerNormEpsilon?: number;
+  normalizationEpsilon?: number;
+}
+
+export declare class OuterProductMeanGpu {
+  run(input: OuterProductMeanInput, options?: { precision?: Precision; rowBlockResidues?: number }): OperatorResult;
+}
+
+export interface TransitionWeights {
+  layerNormScale: Float32Array;
+  layerNormOffset: Float32Array;
+  firstWeight: Float32Array;
+  firstBias: Float32Array;
+  secondWeight: Float32Array;
+  secondBias: Float32Array;
+}
+
+export interface TransitionInput {
+  shape: readonly [rows: number, channels: number, hidden: number];
+  activations: Float32Array;
+  weights: TransitionWeights;
+  epsilon?: number;
+}
+
+export declare class TransitionGpu {
+  run(input: TransitionInput, options?: { precision?: Precision }): OperatorResult;
+}
+
+/** The GEMM plan description (include/afhip.h afhip_gemm_desc). */
+export interface GemmDesc {
+  rows: number;
+  inner: number;
+  columns: number;
+  batch?: number;
+  precision?: number;
+  aDtype?: number;
+  wDtype?: number;
+  wLayout?: number;
+  outDtype?: number;
+  epilogue?: number;
+  heads?: number;
+  headDim?: number;
+  lda?: number;
+  ldw?: number;
+  ldc?: number;
+  batchStrideA?: number;
+  batchStrideW?: number;
+  batchStrideC?: number;
+}
+
+/** GemmVariant (src/runtime/gemm.ts:150-206) as the library reports it. */
+export interface GemmVariant {
+  precision: number;
+  tileRows: number;
+  tileColumns: number;
+  tileInner: number;
+  source: number;
+  kernel: number;
+}
+
+export declare function requestHipDevice(ordinal?: number): { report: Record<string, unknown> };
+export declare function gemmGrid(rows: number, columns: number, tileColumns?: number, tileRows?: number): [number, number];
+export declare function gemmSelect(desc: GemmDesc): GemmVariant;
+export declare function calibrateGemmVariant(desc: GemmDesc): GemmVariant;
+export declare function forceGemmVariant(variant?: Partial<GemmVariant> | null): void;
+export declare function calibrationLoad(file: string): void;
+export declare function calibrationSave(file: string): void;
+export declare function validateTriangleInput(input: TriangleMultiplicationInput): void;
+export declare function packTriangleWeights(weights: TriangleMultiplicationWeights): Float32Array;
+export declare function errorMetrics(
+  actual: ArrayLike<number>,
+  expected: ArrayLike<number>,
+): { meanAbsoluteError: number; maxAbsoluteError: number; rootMeanSquareError: number };
+export declare const TRIANGLE_ORDER: readonly string[];
+export declare const DTYPE: { f32: 0; f16: 1; i8: 2 };
+export declare const PRECISION: { f32: 0; f16: 1 };
+export declare const KERNEL: { register: 0; lds_dma: 1 };
+export declare const EPILOGUE: { scale: 1; bias: 2; attention: 4; relu: 8; residual: 16 };

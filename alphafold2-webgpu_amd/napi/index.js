@@ -1,0 +1,228 @@
+"use strict";
+// The TypeScript host's view of afhip.node: classes with the reference's
+// operator signatures, so a caller swaps the class and nothing else.
+//
+//   TriangleMultiplication{Outgoing,Incoming}Gpu(device).run(input, options)
+//     src/triangle/webgpu.ts:9-23, :56-214
+//   OuterProductMeanGpu(device).run(input, options)
+//     src/evoformer/outer-product-mean.ts:21-40, :549-646
+//   TransitionGpu(device).run(input, options)
+//     src/evoformer/transition.ts:18-31, :264-361
+//   gemmGrid, the GEMM variant selection and its persisted calibration
+//     src/runtime/gemm.ts:213-228, :368-379; src/runtime/gemm-selection.ts:122-125, :560-660
+//
+// Inputs are the reference's (Float32Array tensors, weights by name, shape
+// tuples); results are {output: Float32Array, elapsedMilliseconds, memory}.
+// The loader follows src/runtime/wgpu/backend.ts:80-99: require the addon
+// lazily and say how to build it when it is missing.
+//
+// Written for any Node with Node-API 8 (no ?? or ?. syntax).
+
+var path = require("path");
+
+var native = null;
+function addon() {
+  if (native) return native;
+  var file = path.join(__dirname, "afhip.node");
+  try {
+    native = require(file);
+  } catch (err) {
+    var e = new Error("afhip.node is not built (" + file + "): run `make -C alphafold2-webgpu_amd napi`; " +
+      "there is no fallback (" + err.message + ")");
+    e.cause = err;
+    throw e;
+  }
+  return native;
+}
+
+var F32 = 0, F16 = 1, I8 = 2;
+var PRECISION = { f32: 0, f16: 1 };
+var KERNEL = { register: 0, lds_dma: 1 };
+var EPILOGUE = { scale: 1, bias: 2, attention: 4, relu: 8, residual: 16 };
+
+var opened = false;
+function requestHipDevice(ordinal) {
+  // The counterpart of requestAlphaFoldDevice (src/runtime/device.ts:375-467):
+  // one context per process.
+  if (!opened) {
+    addon().open(ordinal === undefined ? 0 : ordinal);
+    opened = true;
+  }
+  return { report: JSON.parse(addon().deviceReport()) };
+}
+
+function positiveInteger(name, value) {
+  if (typeof value !== "number" || !Number.isSafeInteger(value) || value <= 0) {
+    throw new RangeError(name + " must be a positive safe integer; received " + value);
+  }
+}
+
+function expectLength(name, value, length) {
+  if (!value || value.length !== length) {
+    throw new RangeError(name + " has " + (value ? value.length : 0) + " values; expected " + length);
+  }
+}
+
+var TRIANGLE_ORDER = [
+  "layerNormInWeight", "layerNormInBias",
+  "linearAPWeight", "linearAPBias", "linearAGWeight", "linearAGBias",
+  "linearBPWeight", "linearBPBias", "linearBGWeight", "linearBGBias",
+  "layerNormOutWeight", "layerNormOutBias",
+  "linearZWeight", "linearZBias", "linearGWeight", "linearGBias",
+];
+
+function triangleWeightSizes(cZ, cHidden) {
+  return {
+    layerNormInWeight: cZ, layerNormInBias: cZ,
+    linearAPWeight: cHidden * cZ, linearAPBias: cHidden, linearAGWeight: cHidden * cZ, linearAGBias: cHidden,
+    linearBPWeight: cHidden * cZ, linearBPBias: cHidden, linearBGWeight: cHidden * cZ, linearBGBias: cHidden,
+    layerNormOutWeight: cHidden, layerNormOutBias: cHidden,
+    linearZWeight: cZ * cHidden, linearZBias: cZ, linearGWeight: cZ * cZ, linearGBias: cZ,
+  };
+}
+
+// validateTriangleInput (src/triangle/types.ts:54-89).
+function validateTriangleInput(input) {
+  var shape = input.shape;
+  positiveInteger("length", shape[0]);
+  positiveInteger("cZ", shape[1]);
+  positiveInteger("cHidden", shape[2]);
+  var pairs = shape[0] * shape[0];
+  expectLength("z", input.z, pairs * shape[1]);
+  expectLength("mask", input.mask, pairs);
+  var sizes = triangleWeightSizes(shape[1], shape[2]);
+  TRIANGLE_ORDER.forEach(function (name) { expectLength(name, input.weights[name], sizes[name]); });
+  if (input.epsilon !== undefined && !(input.epsilon > 0 && isFinite(input.epsilon))) {
+    throw new RangeError("epsilon must be finite and positive; received " + input.epsilon);
+  }
+}
+
+// packWeights (src/triangle/weights.ts:20-34): f32, ORDER, [out][in].
+function packTriangleWeights(weights) {
+  var total = 0;
+  TRIANGLE_ORDER.forEach(function (n) { total += weights[n].length; });
+  var out = new Float32Array(total);
+  var at = 0;
+  TRIANGLE_ORDER.forEach(function (n) { out.set(weights[n], at); at += weights[n].length; });
+  return out;
+}
+
+function TriangleMultiplicationGpu(direction) {
+  this.direction = direction;
+}
+TriangleMultiplicationGpu.prototype.run = function (input, options) {
+  options = options || {};
+  validateTriangleInput(input);
+  var precision = options.precision === undefined ? "f32" : options.precision;
+  if (!(precision in PRECISION)) throw new RangeError("unknown precision " + precision);
+  requestHipDevice();
+  return addon().triangleRun({
+    length: input.shape[0], cZ: input.shape[1], cHidden: input.shape[2],
+    direction: this.direction === "incoming" ? 1 : 0,
+    precision: PRECISION[precision],
+    blockRows: options.blockRows === undefined ? 0 : options.blockRows,
+    epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
+  }, input.z, input.mask, packTriangleWeights(input.weights));
+};
+
+function TriangleMultiplicationOutgoingGpu() { TriangleMultiplicationGpu.call(this, "outgoing"); }
+TriangleMultiplicationOutgoingGpu.prototype = Object.create(TriangleMultiplicationGpu.prototype);
+function TriangleMultiplicationIncomingGpu() { TriangleMultiplicationGpu.call(this, "incoming"); }
+TriangleMultiplicationIncomingGpu.prototype = Object.create(TriangleMultiplicationGpu.prototype);
+
+var OPM_ORDER = ["layerNormScale", "layerNormOffset", "leftWeight", "leftBias", "rightWeight", "rightBias",
+  "outputWeight", "outputBias"];
+
+function packOrdered(weights, order) {
+  var total = 0;
+  order.forEach(function (n) { total += weights[n].length; });
+  var out = new Float32Array(total);
+  var at = 0;
+  order.forEach(function (n) { out.set(weights[n], at); at += weights[n].length; });
+  return out;
+}
+
+// OuterProductMeanGpu.run (src/evoformer/outer-product-mean.ts:549-646).
+// input: {shape: [sequences, length, cM, cOuter, cZ], activations, mask, weights}
+function OuterProductMeanGpu() {}
+OuterProductMeanGpu.prototype.run = function (input, options) {
+  options = options || {};
+  var s = input.shape;
+  s.forEach(function (v, i) { positiveInteger(["sequences", "length", "cM", "cOuter", "cZ"][i], v); });
+  expectLength("activations", input.activations, s[0] * s[1] * s[2]);
+  expectLength("mask", input.mask, s[0] * s[1]);
+  var precision = options.precision === undefined ? "f32" : options.precision;
+  requestHipDevice();
+  return addon().opmRun({
+    sequences: s[0], length: s[1], cM: s[2], cOuter: s[3], cZ: s[4], precision: PRECISION[precision],
+    rowBlockResidues: options.rowBlockResidues === undefined ? 0 : options.rowBlockResidues,
+    layerNormEpsilon: input.layerNormEpsilon === undefined ? 1e-5 : input.layerNormEpsilon,
+    normalizationEpsilon: input.normalizationEpsilon === undefined ? 1e-3 : input.normalizationEpsilon,
+  }, input.activations, input.mask, packOrdered(input.weights, OPM_ORDER));
+};
+
+var TRANSITION_ORDER = ["layerNormScale", "layerNormOffset", "firstWeight", "firstBias", "secondWeight",
+  "secondBias"];
+
+// TransitionGpu.run (src/evoformer/transition.ts:264-361).
+// input: {shape: [rows, channels, hidden], activations, weights}
+function TransitionGpu() {}
+TransitionGpu.prototype.run = function (input, options) {
+  options = options || {};
+  var s = input.shape;
+  positiveInteger("rows", s[0]);
+  positiveInteger("channels", s[1]);
+  positiveInteger("hidden", s[2]);
+  expectLength("activations", input.activations, s[0] * s[1]);
+  var precision = options.precision === undefined ? "f32" : options.precision;
+  requestHipDevice();
+  return addon().transitionRun({
+    rows: s[0], channels: s[1], hidden: s[2], precision: PRECISION[precision],
+    epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
+  }, input.activations, packOrdered(input.weights, TRANSITION_ORDER));
+};
+
+// gemmGrid (src/runtime/gemm.ts:368-379).
+function gemmGrid(rows, columns, tileColumns, tileRows) {
+  return addon().gemmGrid(rows, columns, tileColumns === undefined ? 128 : tileColumns,
+    tileRows === undefined ? 64 : tileRows);
+}
+
+// errorMetrics (src/triangle/types.ts:91-110).
+function errorMetrics(actual, expected) {
+  if (actual.length !== expected.length || actual.length === 0) {
+    throw new RangeError("error metrics require equally sized, non-empty arrays");
+  }
+  var sum = 0, max = 0, sq = 0;
+  for (var i = 0; i < actual.length; i++) {
+    var d = Math.abs(actual[i] - expected[i]);
+    sum += d;
+    sq += d * d;
+    if (d > max) max = d;
+  }
+  return { meanAbsoluteError: sum / actual.length, maxAbsoluteError: max,
+    rootMeanSquareError: Math.sqrt(sq / actual.length) };
+}
+
+module.exports = {
+  addon: addon,
+  requestHipDevice: requestHipDevice,
+  TriangleMultiplicationOutgoingGpu: TriangleMultiplicationOutgoingGpu,
+  TriangleMultiplicationIncomingGpu: TriangleMultiplicationIncomingGpu,
+  OuterProductMeanGpu: OuterProductMeanGpu,
+  TransitionGpu: TransitionGpu,
+  validateTriangleInput: validateTriangleInput,
+  packTriangleWeights: packTriangleWeights,
+  errorMetrics: errorMetrics,
+  gemmGrid: gemmGrid,
+  gemmSelect: function (desc) { return addon().gemmSelect(desc); },
+  calibrateGemmVariant: function (desc) { requestHipDevice(); return addon().gemmCalibrate(desc); },
+  forceGemmVariant: function (variant) { addon().gemmForceVariant(variant === undefined ? null : variant); },
+  calibrationLoad: function (file) { addon().calibrationLoad(file); },
+  calibrationSave: function (file) { addon().calibrationSave(file); },
+  TRIANGLE_ORDER: TRIANGLE_ORDER,
+  DTYPE: { f32: F32, f16: F16, i8: I8 },
+  PRECISION: PRECISION,
+  KERNEL: KERNEL,
+  EPILOGUE: EPILOGUE,
+};

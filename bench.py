@@ -1,23 +1,30 @@
 """Benchmark of the hot path on one MI355X.
 
-A step is the pair stack's two triangle multiplications (outgoing, then
-incoming) at N_res = 384, c_z = c_hidden = 128: z f16
-~N(0,1), projection weights ~N(0, 1/128), f16 operands with f32
-accumulation, f32 output. Inputs are generated once on the host (splitmix64 +
-Box-Muller, seed 0xAF2000 + 2), rounded to f16 and resident in HBM before
-the timed region.
+Headline: a step is the pair stack's two triangle
+multiplications (outgoing, then incoming) at N_res = 384,
+c_z = c_hidden = 128: z f16 ~N(0,1), projection weights ~N(0, 1/128), f16
+operands with f32 accumulation, f32 output. Inputs are generated once on the
+host (splitmix64 + Box-Muller, seed 0xAF2000 + config index, N(mu, v) read
+as variance v), rounded to f16 and resident in HBM before the timed region.
 
-Prints one JSON line. `value` is the step's algorithmic TFLOP/s (2*M*K*N
-per GEMM, LayerNorm and sigmoid not counted, as src/runtime/kernel-cost.ts:71
-counts). `roofline` is the dominant kernel (the channel-batched contraction)
-measured with hipEvents on its own stream inside this run. `cpu_baseline`
-is the CPU oracle (oracle/afref.c, one thread) on a bounded sample.
+Prints one JSON line. `value` is the step's algorithmic TFLOP/s (2*M*K*N per
+GEMM; LayerNorm and sigmoid not counted, as src/runtime/kernel-cost.ts:71
+counts); `triangle_ms` is the per-operation time the metric quotes.
+`kernels` holds each triangle kernel's roofline, measured with hipEvents on
+the stream it is launched on (afhip_timing_*) during the same run;
+`roofline` is the dominant one (largest average duration). `traffic` is the
+HBM bytes per launch from rocprofv3's FETCH_SIZE and WRITE_SIZE counters,
+scaled against a plain copy, as recorded in
+profiles/triangle_l384_hbm_traffic.md. `configs` measures BASELINE's other
+configurations the same way. `cpu_baseline` is the CPU oracle
+(oracle/afref.c, one thread) on a bounded sample.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -27,8 +34,11 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Evoformer GEMM TFLOP/s (% MFMA peak); triangle-mult ms @N_res=384"
 PEAK_F16_TFLOPS = 2500.0   # MI355X dense f16 MFMA, published
+PEAK_F32_TFLOPS = 157.3    # MI355X fp32, published
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, published
 L, CZ, CH = 384, 128, 128
+SEED = 0xAF2000
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "triangle_l384_hbm_traffic.md")
 
 
 def triangle_flops(length: int, cz: int, ch: int) -> dict:
@@ -39,6 +49,41 @@ def triangle_flops(length: int, cz: int, ch: int) -> dict:
         "output": 2 * pairs * ch * cz,
         "gate": 2 * pairs * cz * cz,
     }
+
+
+def triangle_bytes(length: int, cz: int, ch: int, pair_bytes: int = 2, out_bytes: int = 4) -> dict:
+    """Algorithmic HBM bytes per launch of each f16-path kernel."""
+    pairs = length * length
+    return {
+        "triangle.project": pairs * cz * pair_bytes + pairs * 4 + 2 * ch * pairs * 2,
+        "triangle.contract": 2 * ch * pairs * 2 + ch * pairs * 2,
+        "triangle.output": ch * pairs * 2 + pairs * cz * pair_bytes + pairs * cz * out_bytes,
+    }
+
+
+def recorded_traffic() -> dict:
+    """traffic_bytes lines of the committed rocprof summary, if present."""
+    try:
+        text = open(TRAFFIC_FILE, encoding="utf-8").read()
+    except OSError:
+        return {}
+    return {m.group(1): int(m.group(2)) for m in re.finditer(r"traffic_bytes (\S+) (\d+)", text)}
+
+
+def triangle_weights(seed: int, cz: int, ch: int) -> dict:
+    from oracle import ref
+
+    weights = {}
+    shapes = ref.triangle_weight_shapes(cz, ch)
+    for i, name in enumerate(ref.TRIANGLE_ORDER):
+        shape = shapes[name]
+        if name.startswith("layerNorm"):
+            weights[name] = ref.normal(seed + 100 + i, shape, 0.01, 1.0 if name.endswith("Weight") else 0.0)
+        elif name.endswith("Bias"):
+            weights[name] = ref.normal(seed + 100 + i, shape, 0.02)
+        else:
+            weights[name] = ref.normal(seed + 100 + i, shape, 1.0 / shape[1])
+    return weights
 
 
 def cpu_baseline() -> dict:
@@ -56,7 +101,8 @@ def cpu_baseline() -> dict:
     full = 2 * sum(triangle_flops(L, CZ, CH).values())
     return {"value": flops / seconds / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"one outgoing triangle multiplication at L={length}, c_z=c_h={CH} "
-                      f"({seconds:.2f} s); a full step would take {full / (flops / seconds):.0f} s",
+                      f"({seconds:.2f} s, oracle/afref.c single-threaded -O2); a full step at L={L} "
+                      f"would take {full / (flops / seconds):.0f} s",
             "ms_per_step_extrapolated": full / (flops / seconds) * 1e3}
 
 
@@ -72,12 +118,153 @@ def copy_probe(mib: int) -> None:
     print(json.dumps({"copy_probe_bytes_each_way": n * 4, "launches": 10}))
 
 
+def timed(fn, steps: int, warmup: int):
+    """(ms per call by wall clock around synchronised loops, per-kernel
+    average ms from the library's hipEvents)."""
+    import torch
+
+    from afhip import device
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - start) * 1e3 / steps
+    device.timing_reset()
+    device.timing_enable(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    report = device.timing_report()
+    device.timing_enable(False)
+    return ms, {k: v["total_ms"] / v["count"] for k, v in report.items()}
+
+
+def rate(kernel: str, ms: float, *, flops: float | None = None, nbytes: float | None = None,
+         peak_tflops: float = PEAK_F16_TFLOPS, traffic=None) -> dict:
+    if flops is not None:
+        achieved = flops / (ms * 1e-3) / 1e12
+        out = {"kernel": kernel, "bound": "mfma", "achieved": round(achieved, 2), "peak": peak_tflops,
+               "unit": "TFLOP/s", "frac": round(achieved / peak_tflops, 4)}
+    else:
+        achieved = nbytes / (ms * 1e-3) / 1e9
+        out = {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+               "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    out["traffic"] = traffic
+    out["avg_ms"] = round(ms, 5)
+    return out
+
+
+def measure_configs(steps: int, warmup: int) -> dict:
+    """BASELINE configs 1, 2, 4 and 5, each with synthetic inputs of the
+    stated shape and distribution."""
+    import numpy as np
+    import torch
+
+    from afhip import device, gemm, opm, transition, triangle
+    from oracle import ref
+
+    dev = device.device()
+    out = {}
+
+    # Config 1: pair-transition first linear, f32, 4096x128x512, bias, ReLU.
+    s = SEED
+    x = torch.from_numpy(ref.normal(s, (4096, 128))).to(dev)
+    w = torch.from_numpy(np.ascontiguousarray(ref.normal(s + 1, (128, 512), 1 / 128).T)).to(dev)  # [N][K]
+    b = torch.from_numpy(ref.normal(s + 2, (512,), 0.02)).to(dev)
+    plan = gemm.TiledGemm(4096, 128, 512, precision="f32", w_layout="k", epilogue=("bias", "relu"))
+    y = plan.run(x, w, bias=b)
+    ms, k = timed(lambda: plan.run(x, w, bias=b, out=y), steps * 5, warmup)
+    kms = k.get("gemm", ms)
+    out["1_pair_transition_linear_f32"] = {
+        "ms": round(kms, 5), "wall_ms": round(ms, 5), "variant": plan.variant().name,
+        "roofline": rate("gemm", kms, flops=2 * 4096 * 128 * 512, peak_tflops=PEAK_F32_TFLOPS)}
+    del x, w, b, y, plan
+
+    # Config 2: fused QKV+gate projection, mixed-q8: X f16 [131072x256],
+    # W int8 [256x1024] (per-column f32 scales), f32 accumulate, f16 out.
+    s = SEED + 1
+    rows = 512 * 256
+    x = torch.from_numpy(ref.round_f16(ref.normal(s, (rows, 256)))).half().to(dev)
+    q = torch.from_numpy(np.ascontiguousarray(ref.uniform_i8(s + 1, (256, 1024)).T)).to(dev)  # [N][K] int8
+    scale = torch.from_numpy(ref.uniform(s + 2, (1024,), 1e-3, 1e-2)).to(dev)
+    plan = gemm.TiledGemm(rows, 256, 1024, precision="f16", a_dtype="f16", w_dtype="i8", w_layout="k",
+                          out_dtype="f16", epilogue=("scale", "attention"), heads=8, head_dim=32)
+    y = plan.run(x, q, scale=scale)
+    ms, k = timed(lambda: plan.run(x, q, scale=scale, out=y), steps, warmup)
+    kms = k.get("gemm", ms)
+    nbytes = 2 * rows * 256 + 256 * 1024 + 4 * 1024 + 2 * rows * 1024
+    out["2_qkv_gate_projection_q8"] = {
+        "ms": round(kms, 5), "wall_ms": round(ms, 5), "variant": plan.variant().name,
+        "tflops": round(2 * rows * 256 * 1024 / (kms * 1e-3) / 1e12, 2),
+        "roofline": rate("gemm", kms, nbytes=nbytes)}
+    del x, q, scale, y, plan
+
+    # Config 4: outer-product mean, N_seq=512, N_res=256, c_m=256 -> 32+32 -> 128, f16.
+    s = SEED + 3
+    S4, L4, CM, CO, CZ4 = 512, 256, 256, 32, 128
+    act = torch.from_numpy(ref.round_f16(ref.normal(s, (S4, L4, CM)))).half().to(dev)
+    mask = torch.ones((S4, L4), dtype=torch.float32, device=dev)
+    wts = {"layerNormScale": ref.normal(s + 1, (CM,), 0.01, 1.0), "layerNormOffset": ref.normal(s + 2, (CM,), 0.01),
+           "leftWeight": ref.normal(s + 3, (CM, CO), 1 / CM), "leftBias": ref.normal(s + 4, (CO,), 0.02),
+           "rightWeight": ref.normal(s + 5, (CM, CO), 1 / CM), "rightBias": ref.normal(s + 6, (CO,), 0.02),
+           "outputWeight": ref.normal(s + 7, (CO * CO, CZ4), 1 / (CO * CO)), "outputBias": ref.normal(s + 8, (CZ4,), 0.02)}
+    op = opm.OuterProductMean(S4, L4, CM, CO, CZ4, precision="f16", msa_dtype="f16", out_dtype="f32")
+    op.prepare(wts)
+    y = op(act, mask)
+    ms, k = timed(lambda: op(act, mask, out=y), steps, warmup)
+    flops4 = {"opm.project": 2 * S4 * L4 * CM * 2 * CO, "opm.contract": 2 * (L4 * CO) ** 2 * S4,
+              "opm.output": 2 * L4 * L4 * CO * CO * CZ4}
+    out["4_outer_product_mean"] = {
+        "ms": round(ms, 5), "tflops": round(sum(flops4.values()) / (ms * 1e-3) / 1e12, 2),
+        "kernel_ms": {kk: round(v, 5) for kk, v in k.items()},
+        "kernels": {kk: rate(kk, k[kk], flops=f) for kk, f in flops4.items() if kk in k}}
+    del act, mask, op, y
+
+    # Config 5: long-complex pair stack at N_res=1024: triangle incoming
+    # (128 batched 1024^3 contractions) + pair transition 128->512->128 over
+    # 1,048,576 rows, f16 activations, f32 accumulation.
+    s = SEED + 4
+    L5 = 1024
+    z = torch.from_numpy(ref.round_f16(ref.normal(s, (L5, L5, CZ)))).half().to(dev)
+    mask = torch.ones((L5, L5), dtype=torch.float32, device=dev)
+    tri = triangle.TriangleMultiplication(L5, CZ, CH, direction="incoming", precision="f16", pair_dtype="f16",
+                                          out_dtype="f16")
+    tri.prepare(triangle_weights(s, CZ, CH))
+    zo = tri(z, mask)
+    ms, k = timed(lambda: tri(z, mask, out=zo), max(3, steps // 4), 1)
+    f5 = triangle_flops(L5, CZ, CH)
+    entry = {"triangle_incoming_ms": round(ms, 4),
+             "triangle_tflops": round((f5["project"] + f5["contract"] + f5["output"] + f5["gate"]) / (ms * 1e-3) / 1e12, 2),
+             "triangle_kernel_ms": {kk: round(v, 5) for kk, v in k.items()}}
+    if "triangle.contract" in k:
+        entry["contract"] = rate("triangle.contract", k["triangle.contract"], flops=f5["contract"])
+    rows5 = L5 * L5
+    tw = {"layerNormScale": ref.normal(s + 20, (CZ,), 0.01, 1.0), "layerNormOffset": ref.normal(s + 21, (CZ,), 0.01),
+          "firstWeight": ref.normal(s + 22, (CZ, 4 * CZ), 1 / CZ), "firstBias": ref.normal(s + 23, (4 * CZ,), 0.02),
+          "secondWeight": ref.normal(s + 24, (4 * CZ, CZ), 1 / (4 * CZ)), "secondBias": ref.normal(s + 25, (CZ,), 0.02)}
+    trans = transition.Transition(rows5, CZ, 4 * CZ, precision="f16", in_dtype="f16", out_dtype="f16")
+    trans.prepare(tw)
+    zf = z.reshape(rows5, CZ)
+    to = trans(zf)
+    ms_t, k_t = timed(lambda: trans(zf, out=to), max(3, steps // 4), 1)
+    ft = 2 * 2 * rows5 * CZ * 4 * CZ
+    entry.update({"transition_ms": round(ms_t, 4), "transition_tflops": round(ft / (ms_t * 1e-3) / 1e12, 2),
+                  "transition_kernel_ms": {kk: round(v, 5) for kk, v in k_t.items()}})
+    out["5_long_complex_pair_stack_l1024"] = entry
+    return out
+
+
 def main() -> None:
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--headline-only", action="store_true", help="skip BASELINE configs 1, 2, 4 and 5")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                         help="only run a plain device-to-device copy of MIB MiB 10 times (the known-size kernel "
                              "rocprof's FETCH_SIZE / WRITE_SIZE readings are scaled by) and exit")
@@ -98,20 +285,10 @@ def main() -> None:
 
     device.open_device(0)
     dev = device.device()
-    seed = 0xAF2000 + 2
+    seed = SEED + 2
     z = ref.round_f16(ref.normal(seed, (L, L, CZ)))
     mask = np.ones((L, L), np.float32)
-    weights = {}
-    shapes = ref.triangle_weight_shapes(CZ, CH)
-    for i, name in enumerate(ref.TRIANGLE_ORDER):
-        shape = shapes[name]
-        if name.startswith("layerNorm"):
-            center = 1.0 if name.endswith("Weight") else 0.0
-            weights[name] = ref.normal(seed + 100 + i, shape, 0.01, center)
-        elif name.endswith("Bias"):
-            weights[name] = ref.normal(seed + 100 + i, shape, 0.02)
-        else:
-            weights[name] = ref.normal(seed + 100 + i, shape, 1.0 / shape[1])
+    weights = triangle_weights(seed, CZ, CH)
     zd = torch.from_numpy(z).half().to(dev)
     md = torch.from_numpy(mask).to(dev)
     ops = []
@@ -125,30 +302,23 @@ def main() -> None:
         for op, out in ops:
             op(zd, md, out=out)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    start = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - start) * 1e3 / args.steps
-
-    # Per-kernel durations: hipEvents bracket every launch on its own stream.
-    device.timing_reset()
-    device.timing_enable(True)
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    timings = device.timing_report()
-    device.timing_enable(False)
-    per_kernel = {k: v["total_ms"] / v["count"] for k, v in timings.items()}
+    ms_per_step, per_kernel = timed(step, args.steps, args.warmup)
 
     flops = triangle_flops(L, CZ, CH)
     step_flops = 2 * sum(flops.values())
     value = step_flops / (ms_per_step * 1e-3) / 1e12
-    contract_ms = per_kernel.get("triangle.contract", float("nan"))
-    achieved = flops["contract"] / (contract_ms * 1e-3) / 1e12
+    traffic = recorded_traffic()
+    nbytes = triangle_bytes(L, CZ, CH)
+    kernels = {}
+    for name in ("triangle.project", "triangle.contract", "triangle.output"):
+        if name not in per_kernel:
+            continue
+        if name == "triangle.contract":
+            kernels[name] = rate(name, per_kernel[name], flops=flops["contract"], traffic=traffic.get(name))
+        else:
+            kernels[name] = rate(name, per_kernel[name], nbytes=nbytes[name], traffic=traffic.get(name))
+        kernels[name]["algorithmic"] = flops["contract"] if name == "triangle.contract" else nbytes[name]
+    dominant = max(kernels, key=lambda n: kernels[n]["avg_ms"])
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -165,12 +335,15 @@ def main() -> None:
         "config": {"workload": "triangle multiplication outgoing + incoming, N_res=384, c_z=c_hidden=128, "
                                "f16 in, f32 accumulate, f32 out (BASELINE config 3)",
                    "n_res": L, "c_z": CZ, "c_hidden": CH, "parallelism": "none (1 GPU)"},
-        "roofline": {"kernel": "triangle.contract", "bound": "mfma", "achieved": round(achieved, 2),
-                     "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_F16_TFLOPS, 4),
-                     "traffic": None, "avg_ms": round(contract_ms, 5)},
-        "kernel_ms": {k: round(v, 5) for k, v in per_kernel.items()},
         "triangle_ms": round(ms_per_step / 2, 4),
+        "roofline": kernels[dominant],
+        "kernels": kernels,
+        "kernel_ms": {k: round(v, 5) for k, v in per_kernel.items()},
     }
+    if not args.headline_only:
+        del ops, zd, md
+        torch.cuda.empty_cache()
+        result["configs"] = measure_configs(args.steps, args.warmup)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result))

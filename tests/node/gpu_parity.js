@@ -1,0 +1,70 @@
+"use strict";
+// GPU parity through the Node-API addon, as the reference's own GPU tests
+// run it (test/triangle-multiplication-outgoing.gpu.test.ts:30-91,
+// test/evoformer-triangle-incoming.gpu.test.ts:42-106).
+var assert = require("assert");
+var path = require("path");
+var afhip = require("../../alphafold2-webgpu_amd/napi/index.js");
+var loadTriangleBundle = require("./fixtures.js").loadTriangleBundle;
+
+var golden = path.join(__dirname, "..", "golden");
+var report = { node: process.versions.node, cases: [] };
+afhip.requestHipDevice(0);
+
+function transposePairs(data, L, C) {
+  var out = new Float32Array(data.length);
+  for (var i = 0; i < L; i++)
+    for (var j = 0; j < L; j++)
+      for (var c = 0; c < C; c++) out[(j * L + i) * C + c] = data[(i * L + j) * C + c];
+  return out;
+}
+
+["openfold-triangle-small", "alphafold-short-9"].forEach(function (name) {
+  var b = loadTriangleBundle(path.join(golden, name, "manifest.json"));
+  var L = b.input.shape[0], C = b.input.shape[1];
+  var out = new afhip.TriangleMultiplicationOutgoingGpu().run(b.input, { precision: "f32" });
+  var m32 = afhip.errorMetrics(out.output, b.expected);
+  assert.ok(m32.meanAbsoluteError < 1e-5 && m32.maxAbsoluteError < 1e-4, name + " f32 " + JSON.stringify(m32));
+  assert.ok(out.elapsedMilliseconds > 0 && out.memory.peakBytes > 0);
+  var out16 = new afhip.TriangleMultiplicationOutgoingGpu().run(b.input, { precision: "f16" });
+  var m16 = afhip.errorMetrics(out16.output, b.expected);
+  assert.ok(m16.meanAbsoluteError < 1e-3 && m16.maxAbsoluteError < 1e-2, name + " f16 " + JSON.stringify(m16));
+  var blocked = new afhip.TriangleMultiplicationOutgoingGpu().run(b.input, { precision: "f32", blockRows: 2 });
+  assert.deepStrictEqual(Buffer.from(blocked.output.buffer), Buffer.from(out.output.buffer), name + " blocking");
+  // incoming(z) = T(outgoing(T(z))): the reference's kjc,kic->ijc (src/triangle/shaders.ts:452-495).
+  var t = { shape: b.input.shape, epsilon: b.input.epsilon, weights: b.input.weights,
+    z: transposePairs(b.input.z, L, C), mask: transposePairs(b.input.mask, L, 1) };
+  var incoming = new afhip.TriangleMultiplicationIncomingGpu().run(b.input, { precision: "f32" }).output;
+  var via = transposePairs(new afhip.TriangleMultiplicationOutgoingGpu().run(t, { precision: "f32" }).output, L, C);
+  var mi = afhip.errorMetrics(incoming, via);
+  assert.ok(mi.maxAbsoluteError <= 1e-6, name + " incoming " + JSON.stringify(mi));
+  report.cases.push({ fixture: name, f32: m32, f16: m16, incomingVsTransposed: mi });
+});
+
+// Outer-product mean: the reference test's small case and closed form for an
+// all-ones mask with zero projections (count = S, rank-one outer product).
+(function () {
+  var S = 7, L = 5, cM = 6, cO = 4, cZ = 3;
+  function fill(n, f) { var a = new Float32Array(n); for (var i = 0; i < n; i++) a[i] = f(i); return a; }
+  var lb = fill(cO, function (i) { return 0.1 * (i + 1); });
+  var rb = fill(cO, function (i) { return -0.2 * (i + 1); });
+  var wo = fill(cO * cO * cZ, function (i) { return Math.sin(i + 1) * 0.3; });
+  var bo = fill(cZ, function (i) { return 0.05 * i; });
+  var input = { shape: [S, L, cM, cO, cZ], activations: fill(S * L * cM, function (i) { return Math.cos(i); }),
+    mask: fill(S * L, function () { return 1; }),
+    weights: { layerNormScale: fill(cM, function () { return 1; }), layerNormOffset: fill(cM, function () { return 0; }),
+      leftWeight: fill(cM * cO, function () { return 0; }), leftBias: lb,
+      rightWeight: fill(cM * cO, function () { return 0; }), rightBias: rb, outputWeight: wo, outputBias: bo } };
+  var out = new afhip.OuterProductMeanGpu().run(input, { precision: "f32" }).output;
+  var worst = 0;
+  for (var z = 0; z < cZ; z++) {
+    var e = bo[z];
+    for (var a = 0; a < cO; a++) for (var c = 0; c < cO; c++) e += S * lb[a] * rb[c] * wo[(a * cO + c) * cZ + z];
+    e /= 1e-3 + S;
+    for (var p = 0; p < L * L; p++) worst = Math.max(worst, Math.abs(out[p * cZ + z] - e) / Math.max(1, Math.abs(e)));
+  }
+  assert.ok(worst < 1e-5, "opm closed form " + worst);
+  report.cases.push({ opmClosedFormMaxRelative: worst });
+})();
+
+console.log(JSON.stringify(report));
