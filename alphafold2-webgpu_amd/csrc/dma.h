@@ -29,17 +29,21 @@ typedef int int32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
-// 16 bytes per lane into LDS [lds, lds + 1024). `lds` must be wave-uniform.
-// The s_nop covers the one wait state between writing M0 and its use.
+// 16 bytes per lane into LDS [lds, lds + 1024). `lds` must be wave-uniform;
+// readfirstlane puts it in a scalar register even where the compiler cannot
+// prove that. The s_nop covers the one wait state between writing M0 and
+// its use.
 __device__ __forceinline__ void dma16(int32x4_t rsrc, uint32_t lds, uint32_t voffset) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voffset),
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset),
                "s"(rsrc)
                : "memory");
 }
 
 // 4 bytes per lane into LDS [lds, lds + 256).
 __device__ __forceinline__ void dma4(int32x4_t rsrc, uint32_t lds, uint32_t voffset) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voffset),
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset),
                "s"(rsrc)
                : "memory");
 }

@@ -29,10 +29,13 @@ namespace afhip {
 namespace {
 
 constexpr int kRows = 64;  // pair rows per workgroup in the projection kernels
+constexpr int kC = 128;    // the fast path's c_z = c_hidden
 
 struct TriWeights {
   // Offsets in bytes into the prepared buffer.
-  size_t ln_in_w, ln_in_b, w_proj, b_proj, ln_out_w, ln_out_b, w_z, b_z, w_g, b_g, total;
+  size_t ln_in_w, ln_in_b, w_proj, b_proj, ln_out_w, ln_out_b, w_z, b_z, w_g, b_g;
+  size_t fold_w, fold_b;  // the f16 fast path's folded weights (0 when not eligible)
+  size_t total;
   int czp, chp, czo;  // padded input width (multiple of 32), padded hidden, padded output rows
 };
 
@@ -58,6 +61,10 @@ TriWeights tri_layout(const afhip_triangle_desc& d) {
   w.b_z = take(4 * (size_t)w.czo);
   w.w_g = take(es * (size_t)w.czo * w.czp);
   w.b_g = take(4 * (size_t)w.czo);
+  if (triangle_fast_eligible(d)) {
+    w.fold_w = take(2 * (size_t)kFoldMatrices * d.c_z * d.c_z);
+    w.fold_b = take(4 * (size_t)kFoldMatrices * d.c_z);
+  }
   w.total = at;
   return w;
 }
@@ -371,6 +378,37 @@ __global__ __launch_bounds__(256) void tri_output_kernel(OutputArgs a) {
 // Weight preparation: f32 [out][in] tensors -> padded CT matrices
 // ---------------------------------------------------------------------------
 
+// The fast path's weights with the LayerNorm affines folded in, so its
+// kernels normalise to x_hat = (x - mean) / sigma and nothing more:
+//   W' = s W diag(gamma),  b' = s (b + W beta),
+// gamma, beta the LayerNorm feeding the matrix and s = -log2(e) for the two
+// gates (their sigmoid then reads 1 / (1 + 2^acc)). Matrices, in order:
+// AP, AG, BP, BG (LayerNorm-in), Z (LayerNorm-out), G (LayerNorm-in), all
+// [out][in]; every product and the bias sum are taken in double and rounded
+// once (weights to f16, biases to f32).
+struct FoldSources {
+  const float* w[kFoldMatrices];
+  const float* b[kFoldMatrices];
+  const float* gamma[kFoldMatrices];
+  const float* beta[kFoldMatrices];
+  float scale[kFoldMatrices];
+};
+
+__global__ void fold_weights_kernel(FoldSources src, int n_out, int n_in, half_t* __restrict__ w_out,
+                                    float* __restrict__ b_out) {
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= kFoldMatrices * n_out) return;
+  const int m = id / n_out, n = id - m * n_out;
+  const double s = src.scale[m];
+  const float* w = src.w[m] + (size_t)n * n_in;
+  double bias = src.b[m][n];
+  for (int k = 0; k < n_in; k++) {
+    bias += (double)w[k] * (double)src.beta[m][k];
+    w_out[((size_t)m * n_out + n) * n_in + k] = (half_t)(s * (double)w[k] * (double)src.gamma[m][k]);
+  }
+  b_out[(size_t)m * n_out + n] = (float)(s * bias);
+}
+
 template <typename CT>
 __global__ void pad_matrix_kernel(const float* __restrict__ src, int rows, int cols, CT* __restrict__ dst,
                                   int prow, int pcol) {
@@ -501,6 +539,24 @@ int afhip_triangle_prepare_weights(const afhip_triangle_desc* desc, const float*
   if ((s = pad_vector(packed + o[13], cz, base + w.b_z, w.czo, st))) return s;
   if ((s = mat(14, cz, cz, w.w_g, w.czo, w.czp))) return s;
   if ((s = pad_vector(packed + o[15], cz, base + w.b_g, w.czo, st))) return s;
+  if (triangle_fast_eligible(d)) {
+    // ORDER indices: LN-in 0/1, AP 2/3, AG 4/5, BP 6/7, BG 8/9, LN-out 10/11, Z 12/13, G 14/15.
+    const int wi[kFoldMatrices] = {2, 4, 6, 8, 12, 14};
+    const int gi[kFoldMatrices] = {0, 0, 0, 0, 10, 0};
+    const float kNegLog2e = -1.4426950408889634f;
+    const float sc[kFoldMatrices] = {1.0f, kNegLog2e, 1.0f, kNegLog2e, 1.0f, kNegLog2e};
+    FoldSources fs{};
+    for (int m = 0; m < kFoldMatrices; m++) {
+      fs.w[m] = packed + o[wi[m]];
+      fs.b[m] = packed + o[wi[m] + 1];
+      fs.gamma[m] = packed + o[gi[m]];
+      fs.beta[m] = packed + o[gi[m] + 1];
+      fs.scale[m] = sc[m];
+    }
+    if ((s = launch("tri_prepare", fold_weights_kernel, dim3((unsigned)ceil_div(kFoldMatrices * cz, 128)), dim3(128),
+                    0, st, fs, cz, cz, (half_t*)(base + w.fold_w), (float*)(base + w.fold_b))))
+      return s;
+  }
   return AFHIP_OK;
 }
 
@@ -547,10 +603,8 @@ int afhip_triangle_run(const afhip_triangle_desc* desc, const void* z, const flo
     FastProjectArgs fa{};
     fa.z = z;
     fa.mask = mask;
-    fa.ln_w = pa.ln_w;
-    fa.ln_b = pa.ln_b;
-    fa.w_proj = (const half_t*)pa.w_proj;
-    fa.b_proj = pa.b_proj;
+    fa.w_proj = (const half_t*)(wb + w.fold_w);
+    fa.b_proj = (const float*)(wb + w.fold_b);
     fa.out_a = (half_t*)pa.out_a;
     fa.out_b = (half_t*)pa.out_b;
     fa.cstride = ws.cstride;
@@ -618,14 +672,10 @@ int afhip_triangle_run(const afhip_triangle_desc* desc, const void* z, const flo
       fo.contracted = (const half_t*)oa.contracted;
       fo.bstride = oa.bstride;
       fo.z = z;
-      fo.ln_in_w = oa.ln_in_w;
-      fo.ln_in_b = oa.ln_in_b;
-      fo.ln_out_w = oa.ln_out_w;
-      fo.ln_out_b = oa.ln_out_b;
-      fo.w_z = (const half_t*)oa.w_z;
-      fo.b_z = oa.b_z;
-      fo.w_g = (const half_t*)oa.w_g;
-      fo.b_g = oa.b_g;
+      fo.w_z = (const half_t*)(wb + w.fold_w) + (size_t)4 * kC * kC;
+      fo.b_z = (const float*)(wb + w.fold_b) + 4 * kC;
+      fo.w_g = (const half_t*)(wb + w.fold_w) + (size_t)5 * kC * kC;
+      fo.b_g = (const float*)(wb + w.fold_b) + 5 * kC;
       fo.out = out;
       fo.pair0 = oa.pair0;
       fo.pairs = oa.pairs;

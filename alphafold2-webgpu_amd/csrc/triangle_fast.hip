@@ -4,27 +4,35 @@
 // Both are persistent (one 512-lane workgroup per CU walking 64-pair tiles)
 // and split their eight waves by role:
 //  - waves 0-3 issue the tile loads, straight into a ring of LDS stages
-//    (buffer_load ... lds), STAGES - 1 tiles ahead of the tile being
-//    computed. They issue no other vector-memory instruction, so the
-//    s_waitcnt vmcnt that says "this tile has landed" is exact.
+//    (buffer_load ... lds) several tiles ahead. They issue no other
+//    vector-memory instruction, so the s_waitcnt vmcnt that says "this tile
+//    has landed" is exact.
 //  - waves 4-7 write the finished tile back from an LDS staging area with
 //    16-byte stores that cover whole 128-byte lines.
-//  - all eight compute: LayerNorm out of the stage into an f16 operand tile,
-//    then MFMA with weights held in VGPRs for the whole kernel
+//  - all eight compute, with the weights held in VGPRs for the whole kernel
 //    (2 x 8 half8 fragments = 64 VGPRs per wave).
+//
+// The weights come folded (fold_weights_kernel, triangle.hip): the
+// LayerNorm affines live inside W and b, so normalising is one FMA per
+// element (x_hat = x rstd - mean rstd), the biases seed the accumulators,
+// and the gates' rows carry -log2(e), so sigmoid(g) = 1 / (1 + 2^acc).
 //
 // tri_project: wave w projects operand (w >> 2) (a or b), channels
 // [32 (w & 3), +32), projection and gate together. The MFMA is issued as
-// W (A operand) x zn^T (B operand), so each accumulator is channel-major and
-// a = mask (p + bp) sigmoid(g + bg) drops into the [channel][pair] staging
-// that becomes the contraction's channel-major operand rows.
+// zn (A operand) x W^T (B operand): a lane's accumulator column is one
+// channel and its rows come in runs of four consecutive pairs, so
+// a = mask p sigmoid(g) goes into the [channel][pair] staging (the
+// contraction's channel-major operand rows) as 8-byte writes. The loop is
+// software-pipelined: tile t's MFMAs and tile t+1's LayerNorm are one
+// straight-line block (two zn buffers), so the matrix and vector pipes
+// overlap, with two barriers per tile.
 //
 // tri_output: the contraction tile arrives channel-major; its LayerNorm over
 // the 128 hidden channels is computed as per-wave partial statistics (each
 // wave owns 16 channels of every pair) merged with Chan's formula, so no
 // transpose is needed. z's LayerNorm, linearZ and linearG follow, and
-// out = (p + bz) sigmoid(g + bg) (+ out when accumulating) is written along
-// the pair's 128 channels.
+// out = p sigmoid(g) (+ out when accumulating) is written along the pair's
+// 128 channels.
 #include <algorithm>
 
 #include "dma.h"
@@ -64,19 +72,30 @@ template <> __device__ __forceinline__ void read8<float>(const unsigned char* p,
   }
 }
 
-// LayerNorm of a 128-channel row held by 16 consecutive lanes (8 channels
-// each): two-pass mean and biased variance in f32, eps inside the root, as
-// the reference's statistics kernels compute them (src/triangle/shaders.ts:
-// 242-281); the normalised f16 values go to dst (8 halves).
-__device__ __forceinline__ void layer_norm16(const float* x, const float* w, const float* b, float eps,
-                                             half_t* dst) {
+template <int CTRL> __device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over a row of 16 lanes, every lane receiving it: DPP quad permutes,
+// then the half-row and row mirrors, each fused into a v_add_f32_dpp (no LDS
+// traffic, unlike a ds_bpermute shuffle).
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror: lane i <-> 7 - i
+  x += dpp<0x140>(x);  // row_mirror: lane i <-> 15 - i
+  return x;
+}
+
+// x_hat of a 128-channel row held by 16 consecutive lanes (8 channels each):
+// two-pass mean and biased variance in f32, eps inside the root, as the
+// reference's statistics kernels compute them (src/triangle/shaders.ts:
+// 242-281); the affine is folded into the weights. 8 halves to dst.
+__device__ __forceinline__ void normalize16(const float* x, float eps, half_t* dst) {
   float s = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; e++) s += x[e];
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  s += __shfl_xor(s, 4);
-  s += __shfl_xor(s, 8);
+  s = row_sum16(s);
   const float mean = s * (1.0f / kC);
   float v = 0.0f;
 #pragma unroll
@@ -84,19 +103,20 @@ __device__ __forceinline__ void layer_norm16(const float* x, const float* w, con
     const float d = x[e] - mean;
     v += d * d;
   }
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
+  v = row_sum16(v);
   const float rstd = fast_rsqrt(v * (1.0f / kC) + eps);
+  const float shift = -mean * rstd;
   half8 h;
 #pragma unroll
-  for (int e = 0; e < 8; e++) h[e] = (half_t)((x[e] - mean) * rstd * w[e] + b[e]);
+  for (int e = 0; e < 8; e++) h[e] = (half_t)fmaf(x[e], rstd, shift);
   *reinterpret_cast<half8*>(dst) = h;
 }
 
-// Loader-wave wait: stage `it` has landed once at most the loads issued
-// after it (`later` instructions) are outstanding.
+// sigmoid of the gate whose accumulator holds -(g) log2(e).
+__device__ __forceinline__ float gate_of(float acc) { return fast_rcp(1.0f + __builtin_amdgcn_exp2f(acc)); }
+
+// Loader-wave wait: a tile has landed once at most the loads issued after
+// it (LATER instructions, when all were issued) are outstanding.
 template <int LATER> __device__ __forceinline__ void wait_stage(bool later_issued) {
   if (later_issued) wait_vmcnt<LATER>();
   else wait_vmcnt<0>();
@@ -115,32 +135,32 @@ template <typename ZT> struct ProjectLayout {
   static constexpr int LPW = ZLOADS / kLoaderWaves;   // per loader wave (wave 0 adds the mask)
   static constexpr int ROWS_PER_LOAD = 1024 / ZROW;
   static constexpr int LANES_PER_ROW = 64 / ROWS_PER_LOAD;
-  static constexpr int ZN = STAGES * STAGE;
-  static constexpr int OUT = ZN + kTile * kPitch * 2;
-  static constexpr int PARAMS = OUT + 2 * kC * kOutPitch * 2;
-  static constexpr int BYTES = PARAMS + 6 * kC * 4;
+  static constexpr int ZN = STAGES * STAGE;                 // two x_hat tiles
+  static constexpr int MASK = ZN + 2 * kTile * kPitch * 2;  // two tiles' masks
+  static constexpr int OUT = MASK + 2 * kTile * 4;          // [256 channels][64 pairs] staging
+  static constexpr int BYTES = OUT + 2 * kC * kOutPitch * 2;
 };
 
 template <typename ZT>
 __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjectArgs a, int ntiles) {
   using Lay = ProjectLayout<ZT>;
+  constexpr int S = Lay::STAGES;
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
-  half_t* zn = reinterpret_cast<half_t*>(smem + Lay::ZN);
-  half_t* ost = reinterpret_cast<half_t*>(smem + Lay::OUT);
-  float* ln = reinterpret_cast<float*>(smem + Lay::PARAMS);  // w [128], b [128]
-  float* bias = ln + 2 * kC;                                  // ap, ag, bp, bg [128] each
+  half_t* const zn_base = reinterpret_cast<half_t*>(smem + Lay::ZN);
+  float* const mask_base = reinterpret_cast<float*>(smem + Lay::MASK);
+  half_t* const ost = reinterpret_cast<half_t*>(smem + Lay::OUT);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int o = wave >> 2;         // 0: a (left), 1: b (right)
   const int hb = 32 * (wave & 3);  // channel block
   const int G = gridDim.x;
+  const int t0 = blockIdx.x;
 
-  for (int i = tid; i < 2 * kC; i += kThreads) ln[i] = i < kC ? a.ln_w[i] : a.ln_b[i - kC];
-  for (int i = tid; i < 4 * kC; i += kThreads) bias[i] = a.b_proj[i];
-
-  // Weight fragments: W[n][k] with n = hb + lane % 32, k = 16 s + 8 (lane / 32).
-  const half_t* wp = a.w_proj + (size_t)(2 * o) * kC * kC + (size_t)(hb + (lane & 31)) * kC + 8 * (lane >> 5);
+  // Weight fragments (the B operand): W[n][k] with n = hb + lane % 32,
+  // k = 16 s + 8 (lane / 32); the biases of this lane's channel.
+  const int ch = hb + (lane & 31);
+  const half_t* wp = a.w_proj + (size_t)(2 * o) * kC * kC + (size_t)ch * kC + 8 * (lane >> 5);
   const half_t* wg = wp + (size_t)kC * kC;
   half8 fp[8], fg[8];
 #pragma unroll
@@ -148,6 +168,8 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
     fp[s] = *reinterpret_cast<const half8*>(wp + 16 * s);
     fg[s] = *reinterpret_cast<const half8*>(wg + 16 * s);
   }
+  const float bp = a.b_proj[(2 * o) * kC + ch];
+  const float bg = a.b_proj[(2 * o + 1) * kC + ch];
   wait_vmcnt<0>();  // weights in hand before the tile loads queue up behind them
 
   const int32x4_t rz = make_rsrc(a.z, (uint32_t)((int64_t)a.P * Lay::ZROW));
@@ -171,27 +193,20 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       dma4(rm, base + Lay::ZBYTES, off);
     }
   };
-
-  int tile = blockIdx.x;
-  if (wave < kLoaderWaves) {
-#pragma unroll
-    for (int s = 0; s < Lay::STAGES - 1; s++)
-      if (tile + s * G < ntiles) issue(tile + s * G, s);
-  }
-  const float* bp = bias + (2 * o) * kC;
-  const float* bg = bias + (2 * o + 1) * kC;
-
-  for (int it = 0; tile < ntiles; it++, tile += G) {
-    const int stage = it % Lay::STAGES;
-    if (wave < kLoaderWaves) {
-      const bool later = tile + (Lay::STAGES - 2) * G < ntiles;
-      if (wave == 0) wait_stage<(Lay::STAGES - 2) * (Lay::LPW + 1)>(later);
-      else wait_stage<(Lay::STAGES - 2) * Lay::LPW>(later);
+  // Loader waves: the tile issued `later_tiles` tiles before the newest has
+  // landed (when all of those were issued; otherwise wait for everything).
+  auto wait_tile = [&](bool later_issued, bool all_stages_later) {
+    if (all_stages_later) {
+      if (wave == 0) wait_stage<(S - 1) * (Lay::LPW + 1)>(later_issued);
+      else wait_stage<(S - 1) * Lay::LPW>(later_issued);
+    } else {
+      if (wave == 0) wait_stage<(S - 2) * (Lay::LPW + 1)>(later_issued);
+      else wait_stage<(S - 2) * Lay::LPW>(later_issued);
     }
-    block_barrier();  // B1: stage `it` is complete; stage it - 1 and zn are free
-    if (wave < kLoaderWaves && tile + (Lay::STAGES - 1) * G < ntiles)
-      issue(tile + (Lay::STAGES - 1) * G, (it + Lay::STAGES - 1) % Lay::STAGES);
-
+  };
+  // x_hat of the tile in `stage` into zn; the tile's mask into mdst (the
+  // stage is refilled before the tile's epilogue runs).
+  auto layer_norm_tile = [&](int stage, half_t* zn, float* mdst) {
     const unsigned char* st = smem + stage * Lay::STAGE;
 #pragma unroll
     for (int pass = 0; pass < 2; pass++) {
@@ -199,33 +214,78 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       const int c0 = (tid & 15) * 8;
       float x[8];
       read8<ZT>(st + row * Lay::ZROW + c0 * (int)sizeof(ZT), x);
-      layer_norm16(x, ln + c0, ln + kC + c0, a.eps, zn + row * kPitch + c0);
+      normalize16(x, a.eps, zn + row * kPitch + c0);
     }
-    block_barrier();  // B2: zn is complete
+    // Every wave copies the same 64 values (no branch, so this stays in the
+    // straight-line block the MFMAs are scheduled with).
+    mdst[lane] = reinterpret_cast<const float*>(st + Lay::ZBYTES)[lane];
+  };
 
-    const float* mk = reinterpret_cast<const float*>(st + Lay::ZBYTES);
+  if (t0 >= ntiles) return;
+  if (wave < kLoaderWaves) {
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++) {
-      floatx16 accp, accg;
+    for (int s = 0; s < S; s++)
+      if (t0 + s * G < ntiles) issue(t0 + s * G, s);
+    wait_tile(t0 + (S - 1) * G < ntiles, true);
+  }
+  block_barrier();  // the first tile has landed
+  layer_norm_tile(0, zn_base, mask_base);
+
+  for (int it = 0, tile = t0; tile < ntiles; it++, tile += G) {
+    // Tiles it + 2 .. it + S - 1 may still be in flight; tile it + 1 must be in.
+    if (wave < kLoaderWaves) wait_tile(tile + (S - 1) * G < ntiles, false);
+    block_barrier();  // B1: zn[it % 2] complete, the next tile landed, staging free
+    if (wave < kLoaderWaves && tile + S * G < ntiles) issue(tile + S * G, it % S);
+
+    const half_t* zn = zn_base + (it & 1) * kTile * kPitch;
+    const float* mk = mask_base + (it & 1) * kTile;
+    half_t* orow = ost + (o * kC + ch) * kOutPitch;
+    floatx16 accp[2], accg[2];
 #pragma unroll
-      for (int v = 0; v < 16; v++) accp[v] = accg[v] = 0.0f;
+    for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        accp[sub][v] = bp;
+        accg[sub][v] = bg;
+      }
+    auto mfma_sub = [&](int sub) {
       const half_t* zrow = zn + (sub * 32 + (lane & 31)) * kPitch + 8 * (lane >> 5);
 #pragma unroll
       for (int s = 0; s < 8; s++) {
         const half8 zf = *reinterpret_cast<const half8*>(zrow + 16 * s);
-        accp = mfma_f16(fp[s], zf, accp);
-        accg = mfma_f16(fg[s], zf, accg);
+        accp[sub] = mfma_f16(zf, fp[s], accp[sub]);
+        accg[sub] = mfma_f16(zf, fg[s], accg[sub]);
       }
-      const int p = sub * 32 + (lane & 31);
-      const float m = mk[p];
+    };
+    auto epilogue_sub = [&](int sub) {
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int c = hb + mfma_row(v, lane);
-        const float val = m * (accp[v] + bp[c]) * sigmoidf_(accg[v] + bg[c]);
-        ost[(o * kC + c) * kOutPitch + p] = (half_t)val;
+      for (int g4 = 0; g4 < 4; g4++) {
+        // rows 4 g4 .. 4 g4 + 3 of the accumulator: pairs p0 .. p0 + 3
+        const int p0 = sub * 32 + 8 * g4 + 4 * (lane >> 5);
+        const floatx4 m4 = *reinterpret_cast<const floatx4*>(mk + p0);
+        half4 h;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          h[e] = (half_t)(m4[e] * accp[sub][4 * g4 + e] * gate_of(accg[sub][4 * g4 + e]));
+        *reinterpret_cast<half4*>(orow + p0) = h;
       }
+    };
+    // Sub-tile 0's MFMAs beside the next tile's LayerNorm (a tile past the
+    // end normalises whatever the stage holds, into a buffer nobody reads),
+    // sub-tile 1's beside sub-tile 0's gates; the scheduling groups below ask
+    // the compiler to interleave each MFMA with vector work instead of
+    // issuing them back to back.
+    mfma_sub(0);
+    layer_norm_tile((it + 1) % S, zn_base + ((it + 1) & 1) * kTile * kPitch, mask_base + ((it + 1) & 1) * kTile);
+    mfma_sub(1);
+    epilogue_sub(0);
+    epilogue_sub(1);
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // then five VALU
     }
-    block_barrier();  // B3: the staged tile is complete
+    block_barrier();  // B2: the staged tile and zn[(it + 1) % 2] are complete
 
     if (wave >= kLoaderWaves) {
       // 256 channel rows x 64 pairs: eight 16-byte chunks per row. Pairs past
@@ -253,20 +313,23 @@ template <typename ZT, typename OT> struct OutputLayout {
   static constexpr int ZROW = kC * (int)sizeof(ZT);
   static constexpr int XBYTES = kC * kTile * 2;      // contraction tile, [128 channels][64 pairs] f16
   static constexpr int ZBYTES = kTile * ZROW;
-  static constexpr int STAGE = XBYTES + ZBYTES;
+  static constexpr int RAW_STAGE = XBYTES + ZBYTES;
   static constexpr int STAGES = sizeof(ZT) == 2 ? 3 : 2;
   static constexpr int XLOADS = XBYTES / 1024;       // 8 channel rows per load
   static constexpr int ZLOADS = ZBYTES / 1024;
   static constexpr int LPW = (XLOADS + ZLOADS) / kLoaderWaves;
   static constexpr int ZROWS_PER_LOAD = 1024 / ZROW;
   static constexpr int ZLANES_PER_ROW = 64 / ZROWS_PER_LOAD;
-  static constexpr int OROW = kC * (int)sizeof(OT);  // staged output row (the stage it aliases is dead by then)
-  static_assert(kTile * OROW <= STAGE, "output staging fits in a stage");
+  static constexpr int OROW = kC * (int)sizeof(OT);  // bytes of one output row
+  // The output tile is staged in the stage it came from (dead by then), rows
+  // padded by 16 bytes so the 32 pair rows one store instruction covers
+  // fall in different bank groups.
+  static constexpr int OPITCH = OROW + 16;
+  static constexpr int STAGE = RAW_STAGE > kTile * OPITCH ? RAW_STAGE : kTile * OPITCH;
   static constexpr int HN = STAGES * STAGE;
   static constexpr int GN = HN + kTile * kPitch * 2;
   static constexpr int PART = GN + kTile * kPitch * 2;   // [8 waves][64 pairs] x (mean, m2)
-  static constexpr int PARAMS = PART + 8 * kTile * 2 * 4;
-  static constexpr int BYTES = PARAMS + 6 * kC * 4;
+  static constexpr int BYTES = PART + 8 * kTile * 2 * 4;
 };
 
 template <typename ZT, typename OT>
@@ -276,21 +339,14 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
   half_t* hn = reinterpret_cast<half_t*>(smem + Lay::HN);
   half_t* gn = reinterpret_cast<half_t*>(smem + Lay::GN);
   float2* part = reinterpret_cast<float2*>(smem + Lay::PART);
-  float* ln = reinterpret_cast<float*>(smem + Lay::PARAMS);  // out w, out b, in w, in b, bz, bg
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nt = 32 * (wave & 3), rh = 32 * (wave >> 2);
   const int G = gridDim.x;
-  for (int i = tid; i < kC; i += kThreads) {
-    ln[i] = a.ln_out_w[i];
-    ln[kC + i] = a.ln_out_b[i];
-    ln[2 * kC + i] = a.ln_in_w[i];
-    ln[3 * kC + i] = a.ln_in_b[i];
-    ln[4 * kC + i] = a.b_z[i];
-    ln[5 * kC + i] = a.b_g[i];
-  }
 
+  // Weight fragments (the A operand): W[n][k] with n = nt + lane % 32; the
+  // biases of this lane's accumulator rows n = nt + mfma_row(v).
   const half_t* wz = a.w_z + (size_t)(nt + (lane & 31)) * kC + 8 * (lane >> 5);
   const half_t* wgp = a.w_g + (size_t)(nt + (lane & 31)) * kC + 8 * (lane >> 5);
   half8 fz[8], fg[8];
@@ -298,6 +354,12 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
   for (int s = 0; s < 8; s++) {
     fz[s] = *reinterpret_cast<const half8*>(wz + 16 * s);
     fg[s] = *reinterpret_cast<const half8*>(wgp + 16 * s);
+  }
+  float bzv[16], bgv[16];
+#pragma unroll
+  for (int v = 0; v < 16; v++) {
+    bzv[v] = a.b_z[nt + mfma_row(v, lane)];
+    bgv[v] = a.b_g[nt + mfma_row(v, lane)];
   }
   wait_vmcnt<0>();  // weights in hand before the tile loads queue up behind them
 
@@ -363,14 +425,14 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
       }
       part[wave * kTile + lane] = make_float2(mean, m2);
     }
-    // z's LayerNorm, rows of 16 lanes.
+    // z's x_hat, rows of 16 lanes.
 #pragma unroll
     for (int pass = 0; pass < 2; pass++) {
       const int row = pass * 32 + (tid >> 4);
       const int c0 = (tid & 15) * 8;
       float x[8];
       read8<ZT>(st + Lay::XBYTES + row * Lay::ZROW + c0 * (int)sizeof(ZT), x);
-      layer_norm16(x, ln + 2 * kC + c0, ln + 3 * kC + c0, a.eps, gn + row * kPitch + c0);
+      normalize16(x, a.eps, gn + row * kPitch + c0);
     }
     block_barrier();  // B2: partial statistics and gn complete
     {
@@ -387,12 +449,12 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
         m2 += pw.y + 16.0f * d * d;
       }
       const float rstd = fast_rsqrt(m2 * (1.0f / kC) + a.eps);
+      const float shift = -mean * rstd;
       half8 h0, h1;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        const int c = 16 * wave + e;
-        h0[e] = (half_t)((xh[e] - mean) * rstd * ln[c] + ln[kC + c]);
-        h1[e] = (half_t)((xh[e + 8] - mean) * rstd * ln[c + 8] + ln[kC + c + 8]);
+        h0[e] = (half_t)fmaf(xh[e], rstd, shift);
+        h1[e] = (half_t)fmaf(xh[e + 8], rstd, shift);
       }
       half_t* dst = hn + lane * kPitch + 16 * wave;
       reinterpret_cast<half8*>(dst)[0] = h0;
@@ -400,24 +462,38 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
     }
     block_barrier();  // B3: hn complete; the stage is dead and becomes the output staging
 
+    // W (A operand) x x_hat^T (B operand): the accumulator's column is the
+    // pair rh + lane % 32 and its rows come in runs of four consecutive
+    // output channels, staged as one 4-element write each.
     floatx16 accz, accg;
 #pragma unroll
-    for (int v = 0; v < 16; v++) accz[v] = accg[v] = 0.0f;
+    for (int v = 0; v < 16; v++) {
+      accz[v] = bzv[v];
+      accg[v] = bgv[v];
+    }
     const half_t* hrow = hn + (rh + (lane & 31)) * kPitch + 8 * (lane >> 5);
     const half_t* grow = gn + (rh + (lane & 31)) * kPitch + 8 * (lane >> 5);
 #pragma unroll
     for (int s = 0; s < 8; s++) {
-      accz = mfma_f16(*reinterpret_cast<const half8*>(hrow + 16 * s), fz[s], accz);
-      accg = mfma_f16(*reinterpret_cast<const half8*>(grow + 16 * s), fg[s], accg);
+      accz = mfma_f16(fz[s], *reinterpret_cast<const half8*>(hrow + 16 * s), accz);
+      accg = mfma_f16(fg[s], *reinterpret_cast<const half8*>(grow + 16 * s), accg);
     }
     {
-      const int n = nt + (lane & 31);
-      const float bzn = ln[4 * kC + n], bgn = ln[5 * kC + n];
-      OT* ost = reinterpret_cast<OT*>(st);
+      unsigned char* orow = st + (rh + (lane & 31)) * Lay::OPITCH;
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int q = rh + mfma_row(v, lane);
-        ost[q * kC + n] = (OT)((accz[v] + bzn) * sigmoidf_(accg[v] + bgn));
+      for (int g4 = 0; g4 < 4; g4++) {
+        const int n0 = nt + 8 * g4 + 4 * (lane >> 5);
+        OT y[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[e] = (OT)(accz[4 * g4 + e] * gate_of(accg[4 * g4 + e]));
+        if constexpr (sizeof(OT) == 4) {
+          *reinterpret_cast<floatx4*>(orow + n0 * 4) = floatx4{(float)y[0], (float)y[1], (float)y[2], (float)y[3]};
+        } else {
+          half4 h;
+#pragma unroll
+          for (int e = 0; e < 4; e++) h[e] = (half_t)y[e];
+          *reinterpret_cast<half4*>(orow + n0 * 2) = h;
+        }
       }
     }
     block_barrier();  // B4: the output tile is staged
@@ -433,7 +509,7 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
         const int idx = t4 + 256 * k;
         const int q = idx / CHUNKS, chunk = idx % CHUNKS;
         if (q0 + q >= a.pairs) continue;
-        uint4 v = *reinterpret_cast<const uint4*>(st + q * Lay::OROW + chunk * 16);
+        uint4 v = *reinterpret_cast<const uint4*>(st + q * Lay::OPITCH + chunk * 16);
         unsigned char* dst =
             reinterpret_cast<unsigned char*>(a.out) + ((size_t)a.pair0 + q0 + q) * Lay::OROW + chunk * 16;
         if (a.residual) {
