@@ -33,6 +33,7 @@ WEIGHT_K_CONTIGUOUS = 1
 
 KERNEL_REGISTER_STAGED = 0
 KERNEL_LDS_DMA = 1
+KERNEL_STREAM = 2
 
 TRIANGLE_OUTGOING = 0
 TRIANGLE_INCOMING = 1

@@ -21,7 +21,8 @@ GEMM_TILE_COLUMNS = 128
 
 _DTYPE_CODES = {"f32": _lib.F32, "f16": _lib.F16, "i8": _lib.I8}
 _PRECISION_CODES = {"f32": _lib.PRECISION_F32, "f16": _lib.PRECISION_F16}
-_KERNEL_CODES = {"register": _lib.KERNEL_REGISTER_STAGED, "lds_dma": _lib.KERNEL_LDS_DMA}
+_KERNEL_CODES = {"register": _lib.KERNEL_REGISTER_STAGED, "lds_dma": _lib.KERNEL_LDS_DMA,
+                 "stream": _lib.KERNEL_STREAM}
 _KERNEL_NAMES = {v: k for k, v in _KERNEL_CODES.items()}
 
 
@@ -43,7 +44,9 @@ class GemmVariant:
     kernel family and output tile. `kernel` is "register" (operands staged
     through VGPRs; any dtype) or "lds_dma" (f16 operands loaded straight into
     LDS, several k-steps in flight). `source` says whether it came from the
-    heuristic, a calibration or a pin."""
+    heuristic, a calibration or a pin. "stream" keeps the weight in registers
+    and streams 64-row activation tiles past it (tall f16-output projections
+    with K of 64, 128 or 256)."""
 
     precision: str
     tile_rows: int
@@ -105,6 +108,7 @@ class TiledGemm:
         handle = ctypes.c_void_p()
         _lib.call("afhip_gemm_plan_create", ctypes.byref(self.desc), ctypes.byref(handle))
         self._plan = handle
+        self._destroy = _lib._lib.afhip_gemm_plan_destroy
         size = ctypes.c_size_t()
         _lib.call("afhip_gemm_workspace_size", self._plan, ctypes.byref(size))
         self.workspace_bytes = size.value
@@ -113,9 +117,12 @@ class TiledGemm:
         self.shape = (batch, rows, columns)
 
     def __del__(self):
+        # The destroy entry point is held by the object itself: at interpreter
+        # exit the module globals may already be gone.
         plan = getattr(self, "_plan", None)
-        if plan is not None and plan.value and _lib._lib is not None:
-            _lib._lib.afhip_gemm_plan_destroy(plan)
+        destroy = getattr(self, "_destroy", None)
+        if plan is not None and plan.value and destroy is not None:
+            destroy(plan)
             self._plan = None
 
     def variant(self) -> GemmVariant:

@@ -40,6 +40,19 @@ __device__ __forceinline__ void dma16(int32x4_t rsrc, uint32_t lds, uint32_t vof
                : "memory");
 }
 
+// dma16 when `enable` (wave-uniform) is nonzero. The test and the skip are
+// inside the statement, so a caller's straight-line code stays one basic
+// block the compiler can schedule MFMAs and VALU work across.
+__device__ __forceinline__ void dma16_if(int32x4_t rsrc, uint32_t lds, uint32_t voffset, int enable) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  const int on = __builtin_amdgcn_readfirstlane(enable);
+  asm volatile(
+      "s_cmp_eq_u32 %3, 0\n\ts_cbranch_scc1 1f\n\ts_mov_b32 m0, %0\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n1:" ::"s"(m0),
+      "v"(voffset), "s"(rsrc), "s"(on)
+      : "memory", "scc");
+}
+
 // 4 bytes per lane into LDS [lds, lds + 256).
 __device__ __forceinline__ void dma4(int32x4_t rsrc, uint32_t lds, uint32_t voffset) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);

@@ -59,6 +59,12 @@ bool dma_eligible(const GemmArgs& args, const GemmTypes& types);
 void dma_heuristic_tile(int64_t M, int64_t N, int64_t batch, int* tile_m, int* tile_n);
 int run_gemm_dma(const GemmArgs& args, int c_dtype, int tile_m, int tile_n, const char* label, hipStream_t stream);
 
+// The STREAM kernel (gemm_stream.hip): f16 activations and output, f16 or
+// int8 weights held in registers, K in {64, 128, 256}, N % 64 == 0.
+bool stream_shape_ok(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);
+bool stream_eligible(const GemmArgs& args, const GemmTypes& types);
+int run_gemm_stream(const GemmArgs& args, const GemmTypes& types, const char* label, hipStream_t stream);
+
 // The variant plans of this shape should use (pinned, calibrated or heuristic).
 afhip_variant select_variant(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);
 

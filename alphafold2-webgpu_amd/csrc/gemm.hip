@@ -30,6 +30,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
+static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int batch);
+
 int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, const char* label, hipStream_t stream) {
   AFHIP_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0 && g.batch > 0, "GEMM dimensions must be positive (M=%d N=%d K=%d batch=%d)",
                 g.M, g.N, g.K, g.batch);
@@ -45,6 +47,12 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
   AFHIP_REQUIRE(!(g.flags & AFHIP_EPILOGUE_RESIDUAL) || g.residual, "RESIDUAL epilogue without a residual");
   AFHIP_REQUIRE(!(g.flags & AFHIP_EPILOGUE_ATTENTION) || (g.head_cols > 0 && g.N == 4 * g.head_cols),
                 "ATTENTION epilogue needs columns == 4 * heads * head_dim");
+  if (v.kernel == AFHIP_KERNEL_STREAM) {
+    if (stream_eligible(g, t)) return run_gemm_stream(g, t, label, stream);
+    // Operands STREAM cannot take run on the family the tile heuristic picks
+    // for them without it.
+    return run_gemm(g, t, tile_variant(t, g.M, g.N, g.batch), label, stream);
+  }
   if (v.kernel == AFHIP_KERNEL_LDS_DMA) {
     if (dma_eligible(g, t) && dma_tile_supported(v.tile_rows, v.tile_columns))
       return run_gemm_dma(g, t.c_dtype, v.tile_rows, v.tile_columns, label, stream);
@@ -66,7 +74,8 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
   return gemm_dispatch_f32(g, t, v, vec, label, stream);
 }
 
-afhip_variant heuristic_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t /*K*/, int batch) {
+// The heuristic among the tiled families (LDS_DMA, REGISTER_STAGED).
+static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int batch) {
   afhip_variant v{};
   v.precision = t.precision;
   v.tile_inner = gemm_detail::kBK;
@@ -88,6 +97,23 @@ afhip_variant heuristic_variant(const GemmTypes& t, int64_t M, int64_t N, int64_
     if (tiles >= target) return v;
   }
   return v;
+}
+
+// Weight-stationary streaming for tall, bandwidth-bound projections (many
+// rows against a short K and at least 448 columns, so a slice's eight waves
+// are mostly busy); the tiled families otherwise.
+afhip_variant heuristic_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K, int batch) {
+  if (stream_shape_ok(t, M, N, K, batch) && M >= 4096 && N >= 448) {
+    afhip_variant v{};
+    v.precision = t.precision;
+    v.tile_rows = 64;
+    v.tile_columns = 512;
+    v.tile_inner = gemm_detail::kBK;
+    v.vectorized = 1;
+    v.kernel = AFHIP_KERNEL_STREAM;
+    return v;
+  }
+  return tile_variant(t, M, N, batch);
 }
 
 // ---------------------------------------------------------------------------
@@ -206,8 +232,12 @@ afhip_variant select_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K
     afhip_variant v = g_pin;
     v.precision = t.precision;
     v.source = 2;
-    // A pinned LDS_DMA tile only applies where that family runs.
-    if (v.kernel != AFHIP_KERNEL_LDS_DMA || (t.a_dtype == AFHIP_F16 && t.b_dtype == AFHIP_F16)) return v;
+    // A pinned LDS_DMA or STREAM variant only applies where that family runs.
+    if (v.kernel == AFHIP_KERNEL_STREAM) {
+      if (stream_shape_ok(t, M, N, K, batch)) return v;
+    } else if (v.kernel != AFHIP_KERNEL_LDS_DMA || (t.a_dtype == AFHIP_F16 && t.b_dtype == AFHIP_F16)) {
+      return v;
+    }
   }
   if (!g_calibrated.empty()) {
     auto it = g_calibrated.find(device_key() + "|" + shape_class(t, M, N, K, batch));
@@ -235,6 +265,8 @@ bool valid_variant(const afhip_variant& v) {
   if (v.tile_inner != gemm_detail::kBK || !valid_precision(v.precision)) return false;
   if (v.kernel == AFHIP_KERNEL_LDS_DMA)
     return v.precision == AFHIP_PRECISION_F16 && dma_tile_supported(v.tile_rows, v.tile_columns);
+  if (v.kernel == AFHIP_KERNEL_STREAM)
+    return v.precision == AFHIP_PRECISION_F16 && v.tile_rows == 64 && v.tile_columns == 512;
   return v.kernel == AFHIP_KERNEL_REGISTER_STAGED && (v.tile_rows == 64 || v.tile_rows == 128) &&
          (v.tile_columns == 64 || v.tile_columns == 128);
 }

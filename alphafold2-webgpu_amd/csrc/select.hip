@@ -133,7 +133,7 @@ struct Events {
 // The candidate set for a shape class (gemmVariantCandidates,
 // gemm-selection.ts:234-272): every register-staged tile, plus the LDS_DMA
 // tiles where its operand contract holds.
-std::vector<afhip_variant> candidates(int precision, bool dma) {
+std::vector<afhip_variant> candidates(int precision, bool dma, bool stream) {
   std::vector<afhip_variant> out;
   auto add = [&](int kernel, int rows, int cols) {
     afhip_variant v{};
@@ -152,6 +152,7 @@ std::vector<afhip_variant> candidates(int precision, bool dma) {
     const int dshapes[3][2] = {{128, 128}, {192, 192}, {128, 256}};
     for (auto& s : dshapes) add(AFHIP_KERNEL_LDS_DMA, s[0], s[1]);
   }
+  if (stream) add(AFHIP_KERNEL_STREAM, 64, 512);
   return out;
 }
 
@@ -236,7 +237,7 @@ int afhip_gemm_calibrate(const afhip_gemm_desc* d, afhip_variant* out) {
   double scale = 0.0;
   for (float v : expect) scale = std::max(scale, (double)std::fabs(v));
 
-  std::vector<afhip_variant> cands = candidates(t.precision, dma_eligible(g, t));
+  std::vector<afhip_variant> cands = candidates(t.precision, dma_eligible(g, t), stream_eligible(g, t));
   std::vector<afhip_variant> usable;
   std::vector<char> host((size_t)cm * N * ec);
   for (auto& v : cands) {

@@ -148,5 +148,5 @@ export declare function errorMetrics(
 export declare const TRIANGLE_ORDER: readonly string[];
 export declare const DTYPE: { f32: 0; f16: 1; i8: 2 };
 export declare const PRECISION: { f32: 0; f16: 1 };
-export declare const KERNEL: { register: 0; lds_dma: 1 };
+export declare const KERNEL: { register: 0; lds_dma: 1; stream: 2 };
 export declare const EPILOGUE: { scale: 1; bias: 2; attention: 4; relu: 8; residual: 16 };

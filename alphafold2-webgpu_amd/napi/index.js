@@ -37,7 +37,7 @@ function addon() {
 
 var F32 = 0, F16 = 1, I8 = 2;
 var PRECISION = { f32: 0, f16: 1 };
-var KERNEL = { register: 0, lds_dma: 1 };
+var KERNEL = { register: 0, lds_dma: 1, stream: 2 };
 var EPILOGUE = { scale: 1, bias: 2, attention: 4, relu: 8, residual: 16 };
 
 var opened = false;

@@ -161,8 +161,8 @@ AFHIP_API int afhip_gemm_grid(int64_t rows, int64_t columns, int32_t tile_column
  * GemmVariant (src/runtime/gemm.ts:150-206). */
 typedef struct afhip_variant {
   int32_t precision;   /* AFHIP_PRECISION_* */
-  int32_t tile_rows;   /* REGISTER_STAGED: 64 | 128; LDS_DMA: 128 | 192 */
-  int32_t tile_columns;/* REGISTER_STAGED: 64 | 128; LDS_DMA: 128 | 192 | 256 */
+  int32_t tile_rows;   /* REGISTER_STAGED: 64 | 128; LDS_DMA: 128 | 192; STREAM: 64 */
+  int32_t tile_columns;/* REGISTER_STAGED: 64 | 128; LDS_DMA: 128 | 192 | 256; STREAM: 512 */
   int32_t tile_inner;  /* 32 */
   int32_t vectorized;  /* 16-byte operand loads */
   int32_t source;      /* 0 heuristic, 1 calibrated, 2 pinned */
@@ -175,9 +175,17 @@ typedef struct afhip_variant {
  * LDS_DMA: operands go global -> LDS directly (buffer loads into LDS), several
  *   k-steps in flight; f16 operands, K a multiple of 8; tiles 128x128,
  *   192x192 or 128x256. The counterpart of the reference's matrix kernel with
- *   deeper k-staging (src/runtime/gemm.ts:470-479). */
+ *   deeper k-staging (src/runtime/gemm.ts:470-479).
+ * STREAM: weight-stationary: the weight stays in registers and 64-row tiles of
+ *   the activations stream past it, each byte read and written once; f16
+ *   activations and output, f16 or int8 weights, K of 64, 128 or 256, columns
+ *   a multiple of 64, no batch, SCALE/BIAS/ATTENTION/RELU epilogues (BIAS up
+ *   to K = 128); other operands run on a tiled family instead. The
+ *   counterpart of the reference's mixed-q8 projection kernels
+ *   (src/runtime/gemm.ts:150-206) for the bandwidth-bound projections. */
 #define AFHIP_KERNEL_REGISTER_STAGED 0
 #define AFHIP_KERNEL_LDS_DMA 1
+#define AFHIP_KERNEL_STREAM 2
 
 /* Shape-driven selection: the calibrated answer for this description's
  * shape class if one is held, else the heuristic. Replaces gemmVariant()

@@ -88,7 +88,13 @@ def test_descriptor_validation_is_host_side():
 def test_variant_selection_without_device():
     from afhip import gemm
 
+    # BASELINE config 2 (tall, K = 256, int8 weights, f16 out) streams past
+    # register-resident weights; with an f32 output it stays on the register-
+    # staged kernel.
     v = gemm.select_variant(131072, 256, 1024, precision="f16", a_dtype="f16", w_dtype="i8", out_dtype="f16")
+    assert (v.kernel, v.tile_rows, v.tile_columns, v.source) == ("stream", 64, 512, "heuristic")
+    assert v.name == "mfma-stream-f16-64x512k32"
+    v = gemm.select_variant(131072, 256, 1024, precision="f16", a_dtype="f16", w_dtype="i8", out_dtype="f32")
     assert v.tile_rows in (64, 128) and v.tile_columns in (64, 128) and v.source == "heuristic"
     assert v.kernel == "register" and v.name.startswith("mfma-register-f16-")
     # f16 operands on both sides take the LDS_DMA family; the triangle

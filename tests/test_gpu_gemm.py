@@ -130,6 +130,62 @@ def test_lds_dma_tiles_match_register_kernel_bitwise(dev, out_dtype, shape):
         assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), key
 
 
+@pytest.mark.parametrize("shape", [
+    # rows, K, N, weight dtype, epilogue, lda
+    (5000, 256, 1024, "i8", ("scale", "attention"), 0),  # config 2's shape, ragged last tile
+    (777, 128, 512, "f16", ("bias", "relu"), 0),
+    (4096, 64, 576, "i8", ("scale",), 0),                # a second slice with one wave's columns
+    (300, 128, 512, "f16", (), 136),                     # strided rows
+])
+def test_stream_matches_register_kernel_bitwise(dev, shape):
+    # The STREAM kernel accumulates K in the same ascending 16-deep MFMA steps
+    # as the register-staged kernel and applies the epilogue in the same order,
+    # so its f16 output is the register kernel's bit for bit.
+    import torch
+
+    from afhip import gemm
+
+    M, K, N, wd, epi, lda = shape
+    lda = lda or K
+    a = ref.round_f16(ref.normal(61 + M, (M, lda)))
+    if wd == "i8":
+        w = ref.uniform_i8(62 + N, (N, K))
+        wt = to_dev(w, dev)
+    else:
+        w = ref.round_f16(ref.normal(62 + N, (N, K), 1 / K))
+        wt = to_dev(w, dev).half()
+    scale = to_dev(ref.uniform(63, (N,), 1e-3, 1e-2), dev) if "scale" in epi else None
+    bias = to_dev(ref.normal(64, (N,), 0.5), dev) if "bias" in epi else None
+    heads = dict(heads=N // 128, head_dim=32) if "attention" in epi else {}
+    ad = to_dev(a, dev).half()
+    results = {}
+    for kernel, tr, tc in (("register", 128, 128), ("stream", 64, 512)):
+        gemm.force_variant(gemm.GemmVariant("f16", tr, tc, source="pinned", kernel=kernel))
+        try:
+            plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype=wd, w_layout="k", out_dtype="f16",
+                                  epilogue=epi, lda=lda, **heads)
+            assert plan.variant().kernel == kernel
+            results[kernel] = plan.run(ad, wt, scale=scale, bias=bias)
+            torch.cuda.synchronize()
+            results[kernel] = results[kernel].cpu().numpy()
+        finally:
+            gemm.force_variant(None)
+    assert np.array_equal(results["stream"].view(np.uint16), results["register"].view(np.uint16))
+    acc = a[:, :K].astype(np.float64) @ w.astype(np.float64).T
+    if scale is not None:
+        acc = acc * scale.cpu().numpy()
+    if bias is not None:
+        acc = acc + bias.cpu().numpy()
+    if "attention" in epi:
+        hd = N // 4
+        acc[:, :hd] /= np.sqrt(32.0)
+        acc[:, 3 * hd:] = 1 / (1 + np.exp(-acc[:, 3 * hd:]))
+    if "relu" in epi:
+        acc = np.maximum(acc, 0)
+    err = np.abs(results["stream"].astype(np.float64) - acc)
+    assert np.all(err <= 1e-2 * np.maximum(1.0, np.abs(acc))), float(err.max())
+
+
 def test_config3_contraction_full_size(dev):
     # BASELINE config 3's contraction: 128 channels of a 384 x 384 x 384
     # f16 product with f32 accumulation and f16 output, against torch's f32
