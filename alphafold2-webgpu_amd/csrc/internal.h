@@ -89,6 +89,34 @@ __device__ __forceinline__ floatx16 mfma_f32(float a, float b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+template <int CTRL> __device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over a row of 16 lanes, every lane receiving it: DPP quad permutes,
+// then the half-row and row mirrors, each fused into a v_add_f32_dpp (no LDS
+// traffic, unlike a ds_bpermute shuffle).
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror: lane i <-> 7 - i
+  x += dpp<0x140>(x);  // row_mirror: lane i <-> 15 - i
+  return x;
+}
+
+// Sum over each aligned group of N lanes (N = 8, 16 or 32), every lane of the
+// group receiving it: the 16-lane steps are DPP, the step across the two rows
+// of a 32-lane group a swizzle.
+template <int N> __device__ __forceinline__ float lane_sum(float x) {
+  static_assert(N == 8 || N == 16 || N == 32, "lane group");
+  x += dpp<0xB1>(x);
+  x += dpp<0x4E>(x);
+  x += dpp<0x141>(x);
+  if constexpr (N >= 16) x += dpp<0x140>(x);
+  if constexpr (N == 32) x += __shfl_xor(x, 16);
+  return x;
+}
+
 // Hardware transcendentals (v_exp_f32, v_rcp_f32, v_rsq_f32; 1 ulp each):
 // a correctly rounded division or square root expands to a dozen
 // instructions, which in the per-element gates and LayerNorms costs more

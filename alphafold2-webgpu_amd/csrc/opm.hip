@@ -10,7 +10,14 @@
 //     consecutive sequences: left and right are stored [L*c_o][S], the
 //     contraction axis contiguous, which is the k-contiguous operand layout
 //     the shared GEMM stages with 16-byte loads.
-//  2. opm_pair_count: count[i][j] = sum_s mask[s][i] mask[s][j] (:317-332).
+//     Under f16 arithmetic with c_outer = 32 and c_m of 64, 128 or 256 (the
+//     MSA and extra-MSA stacks) a persistent kernel does the same per tile
+//     of 64 sequences of one residue: 16-byte row loads one tile ahead,
+//     LayerNorm statistics across the lanes holding a row, the projection
+//     weights resident in VGPRs, and 128-byte channel-major stores.
+//  2. pair count: count[i][j] = sum_s mask[s][i] mask[s][j] (:317-332), as an
+//     f32 GEMM of the transposed mask with itself (exact for 0/1 masks, whose
+//     partial sums are small integers).
 //  3. per residue block, the contraction through the shared GEMM,
 //     outer[i][j][a][b] = sum_s left[s][i][a] right[s][j][b] / (eps + count),
 //     divided in its epilogue as the reference's contraction does
@@ -57,7 +64,7 @@ OpmWeights opm_layout(const afhip_opm_desc& d) {
 }
 
 struct OpmWorkspace {
-  size_t left, right, outer, count, total;
+  size_t left, right, outer, count, mask_t, total;
   int64_t sp;  // sequence stride of left/right rows
   int row_block;
 };
@@ -78,6 +85,7 @@ OpmWorkspace opm_workspace(const afhip_opm_desc& d) {
   w.right = take(es * rows * w.sp);
   w.outer = take(es * (size_t)w.row_block * d.length * d.c_outer * d.c_outer);
   w.count = take(4 * (size_t)d.length * d.length);
+  w.mask_t = take(4 * (size_t)d.length * w.sp);
   w.total = at;
   return w;
 }
@@ -197,13 +205,198 @@ __global__ __launch_bounds__(256) void opm_project_kernel(ProjectArgs a) {
   }
 }
 
-__global__ void opm_pair_count_kernel(const float* __restrict__ mask, int S, int L, float* __restrict__ count) {
-  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)L * L) return;
-  const int i = (int)(idx / L), j = (int)(idx % L);
-  float c = 0.0f;
-  for (int s = 0; s < S; s++) c += mask[(int64_t)s * L + i] * mask[(int64_t)s * L + j];
-  count[idx] = c;
+// mask [S][L] -> mask_t [L][sp] (sequence axis contiguous, zero padded), the
+// k-contiguous operand layout of the pair-count GEMM. 32 x 32 tiles through LDS.
+__global__ __launch_bounds__(256) void opm_mask_transpose_kernel(const float* __restrict__ mask, int S, int L, int sp,
+                                                                 float* __restrict__ mask_t) {
+  __shared__ float tile[32][33];
+  const int s0 = blockIdx.x * 32, i0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int r = ty; r < 32; r += 8) {
+    const int s = s0 + r, i = i0 + tx;
+    tile[r][tx] = s < S && i < L ? mask[(int64_t)s * L + i] : 0.0f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int i = i0 + r, s = s0 + tx;
+    if (i < L && s < sp) mask_t[(int64_t)i * sp + s] = tile[tx][r];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fast projection: f16 arithmetic, c_outer = 32, c_m = CM in {64, 128, 256}.
+// ---------------------------------------------------------------------------
+constexpr int kFastRows = 64;  // sequences per tile, all of one residue
+constexpr int kFastThreads = 256;
+
+template <int CM> struct FastLayout {
+  static constexpr int APITCH = CM + 8;                 // x_hat row, halves (16-byte shifted rows)
+  static constexpr int SPITCH = kFastRows + 8;          // staging row (one channel), halves
+  static constexpr int XHAT = 0;
+  static constexpr int STG = XHAT + kFastRows * APITCH * 2;
+  static constexpr int MASK = STG + 64 * SPITCH * 2;
+  static constexpr int BYTES = MASK + kFastRows * 4;
+};
+
+template <typename MT> struct RowChunk;  // 8 consecutive channels of one row
+template <> struct RowChunk<half_t> {
+  uint4 v;
+  __device__ void load(const half_t* p) { v = *reinterpret_cast<const uint4*>(p); }
+  __device__ void zero() { v = make_uint4(0, 0, 0, 0); }
+  __device__ void get(float* x) const {
+    const half8 h = __builtin_bit_cast(half8, v);
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = (float)h[e];
+  }
+};
+template <> struct RowChunk<float> {
+  float4 a, b;
+  __device__ void load(const float* p) {
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+  }
+  __device__ void zero() { a = b = make_float4(0.f, 0.f, 0.f, 0.f); }
+  __device__ void get(float* x) const {
+    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+  }
+};
+
+// Persistent: workgroup g walks tiles g, g + grid, ... (tile t = residue
+// t / tiles_per_res, sequences [64 (t % tiles_per_res), +64)). Each wave
+// holds 16 rows of the next tile in VGPRs while the current one computes:
+// LPR = CM / 8 lanes per row, 8 channels per lane. The projection is
+// x_hat [64 x CM] (A operand, from LDS) times W^T (B operand, VGPRs): wave w
+// computes rows 32 (w & 1) and output columns 32 (w >> 1) (left, then right).
+template <int CM, typename MT>
+__global__ __launch_bounds__(kFastThreads, 2) void opm_project_fast_kernel(ProjectArgs a, int ntiles,
+                                                                          int tiles_per_res) {
+  using Lay = FastLayout<CM>;
+  constexpr int LPR = CM / 8;             // lanes per row
+  constexpr int RPL = 64 / LPR;           // rows per wave-level load
+  constexpr int LOADS = 16 / RPL;         // loads per wave per tile
+  constexpr int KS = CM / 16;             // MFMA k-steps
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  half_t* const xhat = reinterpret_cast<half_t*>(smem + Lay::XHAT);
+  half_t* const stg = reinterpret_cast<half_t*>(smem + Lay::STG);
+  float* const mbuf = reinterpret_cast<float*>(smem + Lay::MASK);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c0 = 8 * (lane % LPR);  // this lane's channels in a row
+  const MT* msa = reinterpret_cast<const MT*>(a.msa);
+
+  float gam[8], bet[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    gam[e] = a.ln_scale[c0 + e];
+    bet[e] = a.ln_offset[c0 + e];
+  }
+  // W [cop][cmp] rows n = 32 (wave >> 1) + lane % 32: the B fragment of k-step kk.
+  const int n = 32 * (wave >> 1) + (lane & 31);
+  const half_t* W = reinterpret_cast<const half_t*>(a.w_lr) + (size_t)n * a.cmp + 8 * (lane >> 5);
+  half8 wf[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; kk++) wf[kk] = *reinterpret_cast<const half8*>(W + 16 * kk);
+  const float bias = a.b_lr[n];
+
+  RowChunk<MT> raw[LOADS];
+  float mval = 0.0f;
+  auto fetch = [&](int t) {
+    const int res = t / tiles_per_res, s0 = (t - res * tiles_per_res) * kFastRows;
+#pragma unroll
+    for (int j = 0; j < LOADS; j++) {
+      const int s = s0 + 16 * wave + RPL * j + lane / LPR;
+      if (s < a.S) raw[j].load(msa + ((int64_t)s * a.L + res) * CM + c0);
+      else raw[j].zero();
+    }
+    if (tid < kFastRows) mval = s0 + tid < a.S ? a.mask[(int64_t)(s0 + tid) * a.L + res] : 0.0f;
+  };
+
+  int t = blockIdx.x;
+  if (t >= ntiles) return;
+  fetch(t);
+  for (; t < ntiles; t += gridDim.x) {
+    const int res = t / tiles_per_res, s0 = (t - res * tiles_per_res) * kFastRows;
+    // LayerNorm: two-pass mean and biased variance in f32, eps inside the
+    // root (outer-product-mean.ts:221-261), the affine applied per channel.
+#pragma unroll
+    for (int j = 0; j < LOADS; j++) {
+      float x[8];
+      raw[j].get(x);
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) sum += x[e];
+      const float mean = lane_sum<LPR>(sum) / (float)CM;
+      float var = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float d = x[e] - mean;
+        var += d * d;
+      }
+      const float rstd = fast_rsqrt(lane_sum<LPR>(var) / (float)CM + a.eps);
+      half8 h;
+#pragma unroll
+      for (int e = 0; e < 8; e++) h[e] = (half_t)((x[e] - mean) * rstd * gam[e] + bet[e]);
+      const int row = 16 * wave + RPL * j + lane / LPR;
+      *reinterpret_cast<half8*>(xhat + row * Lay::APITCH + c0) = h;
+    }
+    if (tid < kFastRows) mbuf[tid] = mval;
+    if (t + (int)gridDim.x < ntiles) fetch(t + gridDim.x);  // lands while this tile computes
+    __syncthreads();
+
+    floatx16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+    const half_t* arow = xhat + (32 * (wave & 1) + (lane & 31)) * Lay::APITCH + 8 * (lane >> 5);
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) acc = mfma_f16(*reinterpret_cast<const half8*>(arow + 16 * kk), wf[kk], acc);
+    // Lane holds column n and rows 32 (w & 1) + 8 g4 + 4 (lane / 32) + e:
+    // mask * (x W + b), four consecutive sequences per 8-byte staging write.
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++) {
+      const int r = 32 * (wave & 1) + 8 * g4 + 4 * (lane >> 5);
+      const floatx4 m4 = *reinterpret_cast<const floatx4*>(mbuf + r);
+      half4 h;
+#pragma unroll
+      for (int e = 0; e < 4; e++) h[e] = (half_t)(m4[e] * (acc[4 * g4 + e] + bias));
+      *reinterpret_cast<half4*>(stg + n * Lay::SPITCH + r) = h;
+    }
+    __syncthreads();
+    // 64 channel rows of 128 bytes: wave w writes rows 16 w .. 16 w + 15,
+    // eight lanes per row; sequences past sp (the padded row length) are
+    // skipped, those in [S, sp) are zeros.
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int ch = 16 * wave + 8 * j + (lane >> 3), chunk = lane & 7;
+      const int sq = s0 + 8 * chunk;
+      if (sq < a.sp) {
+        const uint4 v = *reinterpret_cast<const uint4*>(stg + ch * Lay::SPITCH + 8 * chunk);
+        half_t* dst = reinterpret_cast<half_t*>(ch < 32 ? a.left : a.right);
+        *reinterpret_cast<uint4*>(dst + ((int64_t)res * 32 + (ch & 31)) * a.sp + sq) = v;
+      }
+    }
+  }
+}
+
+bool project_fast_ok(const afhip_opm_desc& d) {
+  return d.precision == AFHIP_PRECISION_F16 && d.c_outer == 32 && (d.c_m == 64 || d.c_m == 128 || d.c_m == 256);
+}
+
+template <int CM, typename MT> int launch_fast(const ProjectArgs& pa, hipStream_t s) {
+  auto k = opm_project_fast_kernel<CM, MT>;
+  constexpr size_t bytes = FastLayout<CM>::BYTES;
+  if (int st = allow_lds((const void*)k, bytes)) return st;
+  const int tiles_per_res = (int)ceil_div(pa.S, kFastRows);
+  const int ntiles = tiles_per_res * pa.L;
+  const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const int grid = std::min(ntiles, 2 * cus);
+  return launch("opm.project", k, dim3((unsigned)grid), dim3(kFastThreads), bytes, s, pa, ntiles, tiles_per_res);
+}
+
+template <typename MT> int launch_fast_cm(const ProjectArgs& pa, hipStream_t s) {
+  if (pa.cm == 64) return launch_fast<64, MT>(pa, s);
+  if (pa.cm == 128) return launch_fast<128, MT>(pa, s);
+  return launch_fast<256, MT>(pa, s);
 }
 
 template <typename CT>
@@ -348,14 +541,33 @@ int afhip_opm_run(const afhip_opm_desc* desc, const void* activations, const flo
   size_t psh = round_up((int64_t)w.cmp * (kRows + 1) * 4, 16) +
                (f16 ? round_up((int64_t)kRows * (w.cmp + 8) * 2, 16) : 0) + (size_t)64 * (kRows + 8) * (f16 ? 2 : 4);
   int s;
-  if (f16) s = d.msa_dtype == AFHIP_F32 ? launch_project<float, true>(pa, psh, st) : launch_project<half_t, true>(pa, psh, st);
-  else s = d.msa_dtype == AFHIP_F32 ? launch_project<float, false>(pa, psh, st) : launch_project<half_t, false>(pa, psh, st);
+  if (project_fast_ok(d) && (reinterpret_cast<uintptr_t>(activations) & 15) == 0)
+    s = d.msa_dtype == AFHIP_F32 ? launch_fast_cm<float>(pa, st) : launch_fast_cm<half_t>(pa, st);
+  else if (f16)
+    s = d.msa_dtype == AFHIP_F32 ? launch_project<float, true>(pa, psh, st) : launch_project<half_t, true>(pa, psh, st);
+  else
+    s = d.msa_dtype == AFHIP_F32 ? launch_project<float, false>(pa, psh, st) : launch_project<half_t, false>(pa, psh, st);
   if (s) return s;
 
   float* count = (float*)(wsb + ws.count);
-  if ((s = launch("opm.pair_count", opm_pair_count_kernel, dim3((unsigned)ceil_div((int64_t)L * L, 256)), dim3(256), 0,
-                  st, mask, S, L, count)))
+  float* mask_t = (float*)(wsb + ws.mask_t);
+  if ((s = launch("opm.mask_transpose", opm_mask_transpose_kernel,
+                  dim3((unsigned)ceil_div(ws.sp, 32), (unsigned)ceil_div(L, 32)), dim3(256), 0, st, mask, S, L,
+                  (int)ws.sp, mask_t)))
     return s;
+  {
+    GemmArgs g;
+    g.a = mask_t;
+    g.b = mask_t;
+    g.c = count;
+    g.M = L;
+    g.N = L;
+    g.K = (int)ws.sp;  // the zero padding adds nothing
+    g.lda = g.ldb = ws.sp;
+    g.ldc = L;
+    GemmTypes tc{AFHIP_PRECISION_F32, AFHIP_F32, AFHIP_F32, AFHIP_F32};
+    if ((s = run_gemm(g, tc, select_variant(tc, g.M, g.N, g.K, 1), "opm.pair_count", st))) return s;
+  }
 
   const int ct = f16 ? AFHIP_F16 : AFHIP_F32;
   const size_t es = f16 ? 2 : 4;

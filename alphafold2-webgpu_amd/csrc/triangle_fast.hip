@@ -72,21 +72,6 @@ template <> __device__ __forceinline__ void read8<float>(const unsigned char* p,
   }
 }
 
-template <int CTRL> __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
-}
-
-// Sum over a row of 16 lanes, every lane receiving it: DPP quad permutes,
-// then the half-row and row mirrors, each fused into a v_add_f32_dpp (no LDS
-// traffic, unlike a ds_bpermute shuffle).
-__device__ __forceinline__ float row_sum16(float x) {
-  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
-  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
-  x += dpp<0x141>(x);  // row_half_mirror: lane i <-> 7 - i
-  x += dpp<0x140>(x);  // row_mirror: lane i <-> 15 - i
-  return x;
-}
-
 // x_hat of a 128-channel row held by 16 consecutive lanes (8 channels each):
 // two-pass mean and biased variance in f32, eps inside the root, as the
 // reference's statistics kernels compute them (src/triangle/shaders.ts:

@@ -70,6 +70,33 @@ def test_opm_synthetic(dev, S, L, cm, co, cz):
     assert np.abs(out16.reshape(expect.shape) - expect).max() <= 1e-2 * scale
 
 
+@pytest.mark.parametrize("S,L,cm,msa_dtype", [(100, 9, 256, "f16"), (130, 5, 64, "f32"), (64, 7, 128, "f16")])
+def test_opm_f16_fast_projection(dev, S, L, cm, msa_dtype):
+    # The persistent f16 projection (c_outer 32, c_m 64/128/256): ragged
+    # sequence tiles, f16 and f32 MSA input, against the f64 oracle within the
+    # f16 tolerance.
+    import torch
+
+    from afhip import opm
+
+    co, cz = 32, 16
+    act = ref.normal(S * 3 + L, (S, L, cm))
+    if msa_dtype == "f16":
+        act = ref.round_f16(act)
+    mask = (ref.uniform(S + 7 * L, (S, L), 0, 1) > 0.2).astype(np.float32)
+    w = {"layerNormScale": ref.normal(11, (cm,), 0.1, 1.0), "layerNormOffset": ref.normal(12, (cm,), 0.1),
+         "leftWeight": ref.normal(13, (cm, co), 1 / cm), "leftBias": ref.normal(14, (co,), 0.02),
+         "rightWeight": ref.normal(15, (cm, co), 1 / cm), "rightBias": ref.normal(16, (co,), 0.02),
+         "outputWeight": ref.normal(17, (co * co, cz), 1 / (co * co)), "outputBias": ref.normal(18, (cz,), 0.02)}
+    expect = ref.opm(act, mask, w)
+    op = opm.OuterProductMean(S, L, cm, co, cz, precision="f16", msa_dtype=msa_dtype, out_dtype="f32")
+    op.prepare(w)
+    tdt = torch.float16 if msa_dtype == "f16" else torch.float32
+    out = op(torch.from_numpy(act).to(dev, tdt), torch.from_numpy(mask).to(dev)).cpu().numpy()
+    scale = max(1.0, float(np.abs(expect).max()))
+    assert np.abs(out - expect).max() <= 1e-2 * scale
+
+
 def test_opm_all_masked_row_gives_bias_over_eps(dev):
     from afhip import opm
 
