@@ -56,7 +56,7 @@ afhip_variant heuristic_variant(const GemmTypes& types, int64_t M, int64_t N, in
 // The LDS_DMA kernel family (gemm_dma.hip): f16 operands, B k-contiguous.
 bool dma_tile_supported(int tile_m, int tile_n);
 bool dma_eligible(const GemmArgs& args, const GemmTypes& types);
-void dma_heuristic_tile(int64_t M, int64_t N, int64_t batch, int* tile_m, int* tile_n);
+void dma_heuristic_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int* tile_m, int* tile_n);
 int run_gemm_dma(const GemmArgs& args, int c_dtype, int tile_m, int tile_n, const char* label, hipStream_t stream);
 
 // The STREAM kernel (gemm_stream.hip): f16 activations and output, f16 or

@@ -30,7 +30,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
-static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int batch);
+static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K, int batch);
 
 int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, const char* label, hipStream_t stream) {
   AFHIP_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0 && g.batch > 0, "GEMM dimensions must be positive (M=%d N=%d K=%d batch=%d)",
@@ -51,7 +51,7 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
     if (stream_eligible(g, t)) return run_gemm_stream(g, t, label, stream);
     // Operands STREAM cannot take run on the family the tile heuristic picks
     // for them without it.
-    return run_gemm(g, t, tile_variant(t, g.M, g.N, g.batch), label, stream);
+    return run_gemm(g, t, tile_variant(t, g.M, g.N, g.K, g.batch), label, stream);
   }
   if (v.kernel == AFHIP_KERNEL_LDS_DMA) {
     if (dma_eligible(g, t) && dma_tile_supported(v.tile_rows, v.tile_columns))
@@ -75,7 +75,7 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
 }
 
 // The heuristic among the tiled families (LDS_DMA, REGISTER_STAGED).
-static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int batch) {
+static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K, int batch) {
   afhip_variant v{};
   v.precision = t.precision;
   v.tile_inner = gemm_detail::kBK;
@@ -83,7 +83,7 @@ static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int 
   v.source = 0;
   if (t.precision == AFHIP_PRECISION_F16 && t.a_dtype == AFHIP_F16 && t.b_dtype == AFHIP_F16) {
     v.kernel = AFHIP_KERNEL_LDS_DMA;
-    dma_heuristic_tile(M, N, batch, &v.tile_rows, &v.tile_columns);
+    dma_heuristic_tile(M, N, K, batch, &v.tile_rows, &v.tile_columns);
     return v;
   }
   v.kernel = AFHIP_KERNEL_REGISTER_STAGED;
@@ -113,7 +113,7 @@ afhip_variant heuristic_variant(const GemmTypes& t, int64_t M, int64_t N, int64_
     v.kernel = AFHIP_KERNEL_STREAM;
     return v;
   }
-  return tile_variant(t, M, N, batch);
+  return tile_variant(t, M, N, K, batch);
 }
 
 // ---------------------------------------------------------------------------

@@ -141,28 +141,146 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
         const int row = BM + wn + 32 * j + frag_row;
         bf[j] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
       }
+      // Issued as B x A^T: the accumulator's rows are output columns, so a
+      // lane ends with four consecutive columns of one output row per group
+      // (the same products summed in the same k order as A x B^T).
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = mfma_f16(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < TN; j++) acc[i][j] = mfma_f16(bf[j], af[i], acc[i][j]);
     }
     asm volatile("" ::: "memory");
   }
 
-  if (g.flags == 0) {
-    // Plain store straight from the accumulators (the contraction's case).
-    TC* C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
+  if constexpr (sizeof(TC) == 2) {
+    if (g.flags == 0 && (g.ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(g.c) & 15) == 0 && (g.sc & 7) == 0) {
+      // Plain f16 store (the contraction's case), staged through the stage
+      // memory (BM x BN halves fit in it) so that every wave-level store
+      // writes whole 128-byte lines. Row r keeps 16-byte chunk c at slot
+      // c ^ (r & 7); a lane holds row wm + 32 i + lane % 32 and, per group g4,
+      // columns wn + 32 j + 8 g4 + 4 (lane / 32) + [0, 4): one 8-byte write.
+      static_assert(BM * BN * 2 <= STAGES * STAGE_BYTES, "the tile fits the stage memory");
+      constexpr int ROWB = BN * 2;
+      block_barrier<false>();  // every wave is done reading the stages
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+      for (int i = 0; i < TM; i++) {
+        const int r = wm + 32 * i + (lane & 31);
 #pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const int col = n0 + wn + 32 * j + (lane & 31);
+        for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-          const int row = m0 + wm + 32 * i + mfma_row(v, lane);
-          if (row < g.M && col < g.N) C[(int64_t)row * g.ldc + col] = (TC)acc[i][j][v];
+          for (int g4 = 0; g4 < 4; g4++) {
+            const int chunk = (wn + 32 * j + 8 * g4) >> 3;
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) h[e] = (half_t)acc[i][j][4 * g4 + e];
+            *reinterpret_cast<half4*>(smem + r * ROWB + 16 * (chunk ^ (r & 7)) + 8 * (lane >> 5)) = h;
+          }
+      }
+      block_barrier();
+      half_t* C = reinterpret_cast<half_t*>(g.c) + (int64_t)bt * g.sc;
+      constexpr int CPR = BN / 8;  // 16-byte chunks per row
+#pragma unroll 4
+      for (int idx = threadIdx.x; idx < BM * CPR; idx += kThreads) {
+        const int r = idx / CPR, c = idx - r * CPR;
+        const int row = m0 + r, col = n0 + 8 * c;
+        const uint4 v = *reinterpret_cast<const uint4*>(smem + r * ROWB + 16 * (c ^ (r & 7)));
+        if (row < g.M) {
+          half_t* dst = C + (int64_t)row * g.ldc + col;
+          if (col + 8 <= g.N) {
+            *reinterpret_cast<uint4*>(dst) = v;
+          } else {
+            const half8 h = __builtin_bit_cast(half8, v);
+            for (int e = 0; e < 8 && col + e < g.N; e++) dst[e] = h[e];
+          }
         }
       }
+      return;
+    }
+  }
+  if constexpr (sizeof(TC) == 2) {
+    if (g.flags == EPILOGUE_OPM_CONTRACT && g.opm_outer == 32 && (reinterpret_cast<uintptr_t>(g.c) & 15) == 0) {
+      // Outer-product-mean contraction with c_outer = 32: row = i_local * 32
+      // + a, col = j * 32 + b, so each 32 x 32 MFMA tile is one pair (i, j)
+      // and lands as the contiguous 2 KiB block outer[i_local][j][a][b],
+      // divided by (eps + count[i][j]) (one reciprocal per block). The tile
+      // is staged through the stage memory as in the plain case, then every
+      // wave-level store writes half a block (1 KiB of whole lines).
+      static_assert(BM * BN * 2 <= STAGES * STAGE_BYTES, "the tile fits the stage memory");
+      constexpr int ROWB = BN * 2;
+      block_barrier<false>();  // every wave is done reading the stages
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int r = wm + 32 * i + (lane & 31);
+        const int il = (m0 + wm + 32 * i) >> 5;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          const int jj = (n0 + wn + 32 * j) >> 5;
+          const float cnt = il < (g.M >> 5) && jj < g.opm_length
+                                ? g.opm_count[(int64_t)(g.opm_row0 + il) * g.opm_length + jj]
+                                : 0.0f;
+          const float rcp = 1.0f / (g.opm_eps + cnt);
+#pragma unroll
+          for (int g4 = 0; g4 < 4; g4++) {
+            const int chunk = (wn + 32 * j + 8 * g4) >> 3;
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) h[e] = (half_t)(acc[i][j][4 * g4 + e] * rcp);
+            *reinterpret_cast<half4*>(smem + r * ROWB + 16 * (chunk ^ (r & 7)) + 8 * (lane >> 5)) = h;
+          }
+        }
+      }
+      block_barrier();
+      half_t* C = reinterpret_cast<half_t*>(g.c);
+      constexpr int BLOCKS = (BM / 32) * (BN / 32);
+      // Half-block h of tile block q: rows a in [16 h, 16 h + 16), 4 lanes per
+      // 64-byte row.
+#pragma unroll 2
+      for (int idx = threadIdx.x >> 6; idx < 2 * BLOCKS; idx += kThreads / 64) {
+        const int q = idx >> 1, half = idx & 1;
+        const int bi = q / (BN / 32), bj = q - bi * (BN / 32);
+        const int a = 16 * half + (lane >> 2), c = lane & 3;  // 16-byte chunk c of the 64-byte row
+        const int il = (m0 >> 5) + bi, jj = (n0 >> 5) + bj;
+        const int r = 32 * bi + a, chunk = 4 * bj + c;
+        const uint4 v = *reinterpret_cast<const uint4*>(smem + r * ROWB + 16 * (chunk ^ (r & 7)));
+        if (32 * il < g.M && jj < g.opm_length)
+          *reinterpret_cast<uint4*>(C + (((int64_t)il * g.opm_length + jj) * 32 + a) * 32 + 8 * c) = v;
+      }
+      return;
+    }
+  }
+  if (g.flags == 0) {
+    // Plain store straight from the accumulators: lane holds row
+    // m0 + wm + 32 i + lane % 32 and, per group g4, columns
+    // n0 + wn + 32 j + 8 g4 + 4 (lane / 32) + [0, 4).
+    TC* C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
+    const bool vec4 = (g.ldc & 3) == 0 && ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TC) - 1)) == 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int row = m0 + wm + 32 * i + (lane & 31);
+      if (row >= g.M) continue;
+      TC* crow = C + (int64_t)row * g.ldc;
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+          const int col = n0 + wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+          if (vec4 && col + 3 < g.N) {
+            if constexpr (sizeof(TC) == 2) {
+              half4 h;
+#pragma unroll
+              for (int e = 0; e < 4; e++) h[e] = (half_t)acc[i][j][4 * g4 + e];
+              *reinterpret_cast<half4*>(crow + col) = h;
+            } else {
+              *reinterpret_cast<floatx4*>(crow + col) =
+                  floatx4{acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3]};
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              if (col + e < g.N) crow[col + e] = (TC)acc[i][j][4 * g4 + e];
+          }
+        }
+    }
     return;
   }
   // Any other epilogue: each wave passes its 32 x 32 tiles through a private
@@ -175,7 +293,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
 #pragma unroll
     for (int j = 0; j < TN; j++) {
 #pragma unroll
-      for (int v = 0; v < 16; v++) sq[mfma_row(v, lane) * 33 + (lane & 31)] = acc[i][j][v];
+      for (int v = 0; v < 16; v++) sq[(lane & 31) * 33 + mfma_row(v, lane)] = acc[i][j][v];
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the square is written
       __builtin_amdgcn_wave_barrier();
       const int col = n0 + wn + 32 * j + (lane & 31);
@@ -231,12 +349,23 @@ bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
   return (int64_t)256 * std::max(g.lda, g.ldb) * 2 < (int64_t)kOutOfRange;
 }
 
-void dma_heuristic_tile(int64_t M, int64_t N, int64_t batch, int* tm, int* tn) {
-  // 192 x 192 tiles when both edges are multiples of 192 (L = 384, 576, ...)
-  // and there are enough of them for two per CU; otherwise 128 x 128, which
-  // keeps ragged-edge waste low and the tile count high.
+void dma_heuristic_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int* tm, int* tn) {
+  // Measured on MI355X (triangle contractions at L = 384 and 1024, the
+  // outer-product-mean contraction and output, transition shapes):
+  //  - long K on large outputs: 128 x 256, the widest reuse per loaded byte;
+  //  - otherwise 192 x 192 when its ragged edges waste at most 1/20 of the
+  //    work and there are at least two tiles per CU;
+  //  - otherwise 128 x 128, which keeps ragged-edge waste low and the tile
+  //    count high.
   const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  if (M % 192 == 0 && N % 192 == 0 && (M / 192) * (N / 192) * batch >= 2 * cus) {
+  auto waste = [](int64_t x, int64_t t) { return (double)(ceil_div(x, t) * t - x) / (double)x; };
+  if (K >= 768 && M >= 1024 && N >= 1024 && waste(M, 128) <= 0.05 && waste(N, 256) <= 0.05 &&
+      ceil_div(M, 128) * ceil_div(N, 256) * batch >= 2 * cus) {
+    *tm = 128;
+    *tn = 256;
+    return;
+  }
+  if (waste(M, 192) <= 0.05 && waste(N, 192) <= 0.05 && ceil_div(M, 192) * ceil_div(N, 192) * batch >= 2 * cus) {
     *tm = *tn = 192;
     return;
   }
