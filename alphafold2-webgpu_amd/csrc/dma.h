@@ -40,6 +40,24 @@ __device__ __forceinline__ void dma16(int32x4_t rsrc, uint32_t lds, uint32_t vof
                : "memory");
 }
 
+// dma16 with a wave-uniform byte offset added to every lane's (soffset).
+__device__ __forceinline__ void dma16_so(int32x4_t rsrc, uint32_t lds, uint32_t voffset, uint32_t soffset) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soffset);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0), "v"(voffset),
+               "s"(rsrc), "s"(so)
+               : "memory");
+}
+
+// dma4 with a wave-uniform byte offset added to every lane's (soffset).
+__device__ __forceinline__ void dma4_so(int32x4_t rsrc, uint32_t lds, uint32_t voffset, uint32_t soffset) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soffset);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(m0), "v"(voffset),
+               "s"(rsrc), "s"(so)
+               : "memory");
+}
+
 // dma16 when `enable` (wave-uniform) is nonzero. The test and the skip are
 // inside the statement, so a caller's straight-line code stays one basic
 // block the compiler can schedule MFMAs and VALU work across.

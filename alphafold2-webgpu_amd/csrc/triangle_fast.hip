@@ -42,6 +42,8 @@ namespace afhip {
 
 namespace {
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kTile = 64;            // pairs per tile
 constexpr int kC = 128;              // c_z = c_hidden
 constexpr int kThreads = 512;
@@ -126,7 +128,7 @@ template <typename ZT> struct ProjectLayout {
   static constexpr int BYTES = OUT + 2 * kC * kOutPitch * 2;
 };
 
-template <typename ZT>
+template <typename ZT, bool INCOMING>
 __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjectArgs a, int ntiles) {
   using Lay = ProjectLayout<ZT>;
   constexpr int S = Lay::STAGES;
@@ -160,22 +162,54 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
   const int32x4_t rz = make_rsrc(a.z, (uint32_t)((int64_t)a.P * Lay::ZROW));
   const int32x4_t rm = make_rsrc(a.mask, (uint32_t)((int64_t)a.P * 4));
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
-  auto issue = [&](int tile, int stage) {  // loader waves only
+  // Load geometry: load i of a loader wave fills stage row
+  // row_i = (wave + 4 i) * ROWS_PER_LOAD + lane / LANES_PER_ROW, 16-byte chunk
+  // lane % LANES_PER_ROW; wave 0 also loads the tile's 64 mask values.
+  // Outgoing pairs are consecutive rows of z: the lane's offset within the
+  // tile is fixed and the tile's base rides in the instruction's scalar
+  // offset; rows past P fall past the resource (zeros). Incoming pairs are z
+  // transposed: row r of the tile stream is pair (r % L) * L + r / L, whose
+  // coordinates (r / L, r % L) each lane advances by G * 64 rows per issued
+  // tile instead of dividing.
+  constexpr int NL = Lay::LPW + 1;  // the loads, then the mask (wave 0)
+  uint32_t vofs[NL];
+  int ci[NL], ck[NL];  // incoming: r / L and r % L of the lane's next row
+  const int dq = (G * kTile) / a.L, dr = (G * kTile) % a.L;
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    const int row = i < Lay::LPW ? (wave + kLoaderWaves * i) * Lay::ROWS_PER_LOAD + lane / Lay::LANES_PER_ROW : lane;
+    const int chunk = i < Lay::LPW ? lane % Lay::LANES_PER_ROW : 0;
+    if constexpr (INCOMING) {
+      const int r = t0 * kTile + row;
+      ci[i] = r / a.L;
+      ck[i] = r - ci[i] * a.L;
+      vofs[i] = 16u * chunk;
+    } else {
+      vofs[i] = i < Lay::LPW ? (uint32_t)(row * Lay::ZROW + 16 * chunk) : (uint32_t)(4 * row);
+    }
+  }
+  auto issue = [&](int tile, int stage) {  // loader waves only, tiles t0, t0 + G, ... in order
     const uint32_t base = lds0 + stage * Lay::STAGE;
 #pragma unroll
-    for (int i = 0; i < Lay::LPW; i++) {
-      const int q = wave + kLoaderWaves * i;
-      const int row = q * Lay::ROWS_PER_LOAD + lane / Lay::LANES_PER_ROW;
-      const int chunk = lane % Lay::LANES_PER_ROW;
-      const int r = tile * kTile + row;
-      const uint32_t off =
-          r < a.P ? (uint32_t)pair_of(r, a.L, a.incoming) * Lay::ZROW + 16u * chunk : kOutOfRange;
-      dma16(rz, base + q * 1024, off);
-    }
-    if (wave == 0) {
-      const int r = tile * kTile + lane;
-      const uint32_t off = r < a.P ? (uint32_t)pair_of(r, a.L, a.incoming) * 4u : kOutOfRange;
-      dma4(rm, base + Lay::ZBYTES, off);
+    for (int i = 0; i < NL; i++) {
+      if (i == Lay::LPW && wave != 0) break;
+      const uint32_t lds = i < Lay::LPW ? base + (wave + kLoaderWaves * i) * 1024 : base + Lay::ZBYTES;
+      const uint32_t esz = i < Lay::LPW ? (uint32_t)Lay::ZROW : 4u;
+      if constexpr (INCOMING) {
+        const uint32_t off = ci[i] < a.L ? (uint32_t)(ck[i] * a.L + ci[i]) * esz + vofs[i] : kOutOfRange;
+        if (i < Lay::LPW) dma16(rz, lds, off);
+        else dma4(rm, lds, off);
+        ck[i] += dr;
+        ci[i] += dq;
+        if (ck[i] >= a.L) {
+          ck[i] -= a.L;
+          ci[i] += 1;
+        }
+      } else {
+        const uint32_t so = (uint32_t)tile * kTile * esz;
+        if (i < Lay::LPW) dma16_so(rz, lds, vofs[i], so);
+        else dma4_so(rm, lds, vofs[i], so);
+      }
     }
   };
   // Loader waves: the tile issued `later_tiles` tiles before the newest has
@@ -205,6 +239,15 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
     // straight-line block the MFMAs are scheduled with).
     mdst[lane] = reinterpret_cast<const float*>(st + Lay::ZBYTES)[lane];
   };
+
+  const int t4 = tid - kLoaderWaves * 64;
+  const int srow = t4 >> 3, schunk = t4 & 7;
+  uint32_t svof[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) svof[k] = (uint32_t)(((int64_t)(srow + 32 * k) * a.cstride + schunk * 8) * 2);
+  const int obytes = (int)((int64_t)kC * a.cstride * 2);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(a.out_a, 0, obytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(a.out_b, 0, obytes, 0x00020000);
 
   if (t0 >= ntiles) return;
   if (wave < kLoaderWaves) {
@@ -273,18 +316,15 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
     block_barrier();  // B2: the staged tile and zn[(it + 1) % 2] are complete
 
     if (wave >= kLoaderWaves) {
-      // 256 channel rows x 64 pairs: eight 16-byte chunks per row. Pairs past
-      // P land in the operand's padding (its rows are cstride >= 64 * ntiles
+      // 256 channel rows x 64 pairs: eight 16-byte chunks per row; store k
+      // writes row (t4 >> 3) + 32 k (a's rows, then b's). The lane's offsets
+      // are fixed, the tile's base rides in the scalar offset. Pairs past P
+      // land in the operand's padding (its rows are cstride >= 64 * ntiles
       // long), which the contraction never reads.
-      const int t4 = tid - kLoaderWaves * 64;
 #pragma unroll
       for (int k = 0; k < 8; k++) {
-        const int idx = t4 + 256 * k;
-        const int row = idx >> 3, chunk = idx & 7;
-        const uint4 v = *reinterpret_cast<const uint4*>(ost + row * kOutPitch + chunk * 8);
-        half_t* dst = (row < kC ? a.out_a : a.out_b) + (size_t)(row & (kC - 1)) * a.cstride +
-                      (size_t)tile * kTile + chunk * 8;
-        *reinterpret_cast<uint4*>(dst) = v;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ost + (srow + 32 * k) * kOutPitch + schunk * 8);
+        __builtin_amdgcn_raw_buffer_store_b128(v, k < 4 ? rsa : rsb, svof[k & 3], (uint32_t)tile * kTile * 2, 0);
       }
     }
   }
@@ -527,17 +567,20 @@ bool triangle_fast_eligible(const afhip_triangle_desc& d) {
   return P * kC * (d.pair_dtype == AFHIP_F32 ? 4 : 2) < (int64_t)kOutOfRange;
 }
 
-int launch_triangle_project_f16(const FastProjectArgs& a, int pair_dtype, hipStream_t s) {
+template <typename ZT, bool INCOMING> int launch_project(const FastProjectArgs& a, hipStream_t s) {
   const int tiles = (int)ceil_div(a.P, kTile);
-  const dim3 g(grid_for(tiles)), b(kThreads);
-  if (pair_dtype == AFHIP_F16) {
-    auto k = tri_project_f16_kernel<half_t>;
-    if (int st = prepare_lds(k, ProjectLayout<half_t>::BYTES)) return st;
-    return launch("triangle.project", k, g, b, ProjectLayout<half_t>::BYTES, s, a, tiles);
-  }
-  auto k = tri_project_f16_kernel<float>;
-  if (int st = prepare_lds(k, ProjectLayout<float>::BYTES)) return st;
-  return launch("triangle.project", k, g, b, ProjectLayout<float>::BYTES, s, a, tiles);
+  auto k = tri_project_f16_kernel<ZT, INCOMING>;
+  if (int st = prepare_lds(k, ProjectLayout<ZT>::BYTES)) return st;
+  return launch("triangle.project", k, dim3(grid_for(tiles)), dim3(kThreads), ProjectLayout<ZT>::BYTES, s, a, tiles);
+}
+
+int launch_triangle_project_f16(const FastProjectArgs& a, int pair_dtype, hipStream_t s) {
+  // Buffer offsets are 32-bit: the operands' 128 rows and z must stay below 2 GiB.
+  AFHIP_REQUIRE((int64_t)kC * a.cstride * 2 < ((int64_t)1 << 31) && (int64_t)a.P * kC * 4 < ((int64_t)1 << 31),
+                "triangle of %d pairs exceeds the projection kernel's 2 GiB operand bound", a.P);
+  if (pair_dtype == AFHIP_F16)
+    return a.incoming ? launch_project<half_t, true>(a, s) : launch_project<half_t, false>(a, s);
+  return a.incoming ? launch_project<float, true>(a, s) : launch_project<float, false>(a, s);
 }
 
 template <typename ZT, typename OT> int launch_output(const FastOutputArgs& a, hipStream_t s) {
