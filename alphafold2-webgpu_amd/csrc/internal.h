@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 
 #include <cstdint>
@@ -35,12 +36,15 @@ int require_open();
 int device_cu_count();
 
 // ---------------------------------------------------------------------------
-// Kernel timing: launches go through launch_timed so a label can be
-// bracketed by hipEvents when timing is enabled.
+// Kernel timing: when enabled, each launch carries a start and a stop event
+// on its own dispatch (hipExtLaunchKernelGGL), which time the kernel's
+// execution as a kernel trace does, without event packets of their own
+// between launches.
 // ---------------------------------------------------------------------------
 bool timing_enabled();
-void timing_begin(const char* label, hipStream_t stream);
-void timing_end(const char* label, hipStream_t stream);
+// Two fresh events for one launch labelled `label` (false: timing skipped).
+bool timing_events(hipEvent_t* start, hipEvent_t* stop);
+void timing_record(const char* label, hipEvent_t start, hipEvent_t stop);
 
 // Raises a kernel's dynamic LDS ceiling to `bytes` (gfx950 grants up to
 // 160 KiB a workgroup); once per kernel and size.
@@ -50,12 +54,17 @@ template <typename Kernel, typename... Args>
 int launch(const char* label, Kernel kernel, dim3 grid, dim3 block, size_t shared, hipStream_t stream,
            Args... args) {
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return AFHIP_OK;
-  const bool timed = timing_enabled();
-  if (timed) timing_begin(label, stream);
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (timing_enabled() && timing_events(&start, &stop)) {
+    hipExtLaunchKernelGGL(kernel, grid, block, shared, stream, start, stop, 0, args...);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return hip_status(err, label);
+    timing_record(label, start, stop);
+    return AFHIP_OK;
+  }
   hipLaunchKernelGGL(kernel, grid, block, shared, stream, args...);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return hip_status(err, label);
-  if (timed) timing_end(label, stream);
   return AFHIP_OK;
 }
 

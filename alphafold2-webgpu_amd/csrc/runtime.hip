@@ -22,7 +22,6 @@ struct TimingRecord {
 bool g_timing = false;
 std::vector<TimingRecord> g_pending;
 std::map<std::string, std::pair<long, double>> g_totals;
-std::map<std::string, hipEvent_t> g_open_start;
 }  // namespace
 
 int set_error(int status, const char* fmt, ...) {
@@ -63,22 +62,16 @@ int allow_lds(const void* kernel, size_t bytes) {
   return AFHIP_OK;
 }
 
-void timing_begin(const char* label, hipStream_t stream) {
-  hipEvent_t start;
-  if (hipEventCreate(&start) != hipSuccess) return;
-  (void)hipEventRecord(start, stream);
-  g_open_start[label] = start;
+bool timing_events(hipEvent_t* start, hipEvent_t* stop) {
+  if (hipEventCreate(start) != hipSuccess) return false;
+  if (hipEventCreate(stop) != hipSuccess) {
+    (void)hipEventDestroy(*start);
+    return false;
+  }
+  return true;
 }
 
-void timing_end(const char* label, hipStream_t stream) {
-  auto it = g_open_start.find(label);
-  if (it == g_open_start.end()) return;
-  hipEvent_t stop;
-  if (hipEventCreate(&stop) != hipSuccess) return;
-  (void)hipEventRecord(stop, stream);
-  g_pending.push_back({it->second, stop, label});
-  g_open_start.erase(it);
-}
+void timing_record(const char* label, hipEvent_t start, hipEvent_t stop) { g_pending.push_back({start, stop, label}); }
 
 static void timing_drain() {
   for (auto& r : g_pending) {

@@ -51,12 +51,6 @@ constexpr int kLoaderWaves = 4;
 constexpr int kPitch = kC + 8;       // halves: 272-byte operand rows, 16-byte aligned, conflict-free fragments
 constexpr int kOutPitch = kTile + 8; // halves: projection staging rows
 
-__device__ __forceinline__ int pair_of(int r, int L, bool incoming) {
-  if (!incoming) return r;
-  const int j = r / L;
-  return (r - j * L) * L + j;
-}
-
 // Eight consecutive channels of one row of a stage, as f32.
 template <typename T> __device__ __forceinline__ void read8(const unsigned char* p, float* x);
 template <> __device__ __forceinline__ void read8<half_t>(const unsigned char* p, float* x) {

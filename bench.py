@@ -38,7 +38,7 @@ PEAK_F32_TFLOPS = 157.3    # MI355X fp32, published
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, published
 L, CZ, CH = 384, 128, 128
 SEED = 0xAF2000
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "triangle_l384_hbm_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_triangle_l384_and_q8_projection.md")
 
 
 def triangle_flops(length: int, cz: int, ch: int) -> dict:
@@ -158,7 +158,7 @@ def rate(kernel: str, ms: float, *, flops: float | None = None, nbytes: float | 
     return out
 
 
-def measure_configs(steps: int, warmup: int) -> dict:
+def measure_configs(steps: int, warmup: int, which=(1, 2, 4, 5)) -> dict:
     """BASELINE configs 1, 2, 4 and 5, each with synthetic inputs of the
     stated shape and distribution."""
     import numpy as np
@@ -169,92 +169,97 @@ def measure_configs(steps: int, warmup: int) -> dict:
 
     dev = device.device()
     out = {}
-
-    # Config 1: pair-transition first linear, f32, 4096x128x512, bias, ReLU.
-    s = SEED
-    x = torch.from_numpy(ref.normal(s, (4096, 128))).to(dev)
-    w = torch.from_numpy(np.ascontiguousarray(ref.normal(s + 1, (128, 512), 1 / 128).T)).to(dev)  # [N][K]
-    b = torch.from_numpy(ref.normal(s + 2, (512,), 0.02)).to(dev)
-    plan = gemm.TiledGemm(4096, 128, 512, precision="f32", w_layout="k", epilogue=("bias", "relu"))
-    y = plan.run(x, w, bias=b)
-    ms, k = timed(lambda: plan.run(x, w, bias=b, out=y), steps * 5, warmup)
-    kms = k.get("gemm", ms)
-    out["1_pair_transition_linear_f32"] = {
-        "ms": round(kms, 5), "wall_ms": round(ms, 5), "variant": plan.variant().name,
-        "roofline": rate("gemm", kms, flops=2 * 4096 * 128 * 512, peak_tflops=PEAK_F32_TFLOPS)}
-    del x, w, b, y, plan
-
-    # Config 2: fused QKV+gate projection, mixed-q8: X f16 [131072x256],
-    # W int8 [256x1024] (per-column f32 scales), f32 accumulate, f16 out.
-    s = SEED + 1
-    rows = 512 * 256
-    x = torch.from_numpy(ref.round_f16(ref.normal(s, (rows, 256)))).half().to(dev)
-    q = torch.from_numpy(np.ascontiguousarray(ref.uniform_i8(s + 1, (256, 1024)).T)).to(dev)  # [N][K] int8
-    scale = torch.from_numpy(ref.uniform(s + 2, (1024,), 1e-3, 1e-2)).to(dev)
-    plan = gemm.TiledGemm(rows, 256, 1024, precision="f16", a_dtype="f16", w_dtype="i8", w_layout="k",
-                          out_dtype="f16", epilogue=("scale", "attention"), heads=8, head_dim=32)
-    y = plan.run(x, q, scale=scale)
-    ms, k = timed(lambda: plan.run(x, q, scale=scale, out=y), steps, warmup)
-    kms = k.get("gemm", ms)
-    nbytes = 2 * rows * 256 + 256 * 1024 + 4 * 1024 + 2 * rows * 1024
-    out["2_qkv_gate_projection_q8"] = {
-        "ms": round(kms, 5), "wall_ms": round(ms, 5), "variant": plan.variant().name,
-        "tflops": round(2 * rows * 256 * 1024 / (kms * 1e-3) / 1e12, 2),
-        "roofline": rate("gemm", kms, nbytes=nbytes)}
-    del x, q, scale, y, plan
-
-    # Config 4: outer-product mean, N_seq=512, N_res=256, c_m=256 -> 32+32 -> 128, f16.
-    s = SEED + 3
-    S4, L4, CM, CO, CZ4 = 512, 256, 256, 32, 128
-    act = torch.from_numpy(ref.round_f16(ref.normal(s, (S4, L4, CM)))).half().to(dev)
-    mask = torch.ones((S4, L4), dtype=torch.float32, device=dev)
-    wts = {"layerNormScale": ref.normal(s + 1, (CM,), 0.01, 1.0), "layerNormOffset": ref.normal(s + 2, (CM,), 0.01),
-           "leftWeight": ref.normal(s + 3, (CM, CO), 1 / CM), "leftBias": ref.normal(s + 4, (CO,), 0.02),
-           "rightWeight": ref.normal(s + 5, (CM, CO), 1 / CM), "rightBias": ref.normal(s + 6, (CO,), 0.02),
-           "outputWeight": ref.normal(s + 7, (CO * CO, CZ4), 1 / (CO * CO)), "outputBias": ref.normal(s + 8, (CZ4,), 0.02)}
-    op = opm.OuterProductMean(S4, L4, CM, CO, CZ4, precision="f16", msa_dtype="f16", out_dtype="f32")
-    op.prepare(wts)
-    y = op(act, mask)
-    ms, k = timed(lambda: op(act, mask, out=y), steps, warmup)
-    flops4 = {"opm.project": 2 * S4 * L4 * CM * 2 * CO, "opm.contract": 2 * (L4 * CO) ** 2 * S4,
-              "opm.output": 2 * L4 * L4 * CO * CO * CZ4}
-    out["4_outer_product_mean"] = {
-        "ms": round(ms, 5), "tflops": round(sum(flops4.values()) / (ms * 1e-3) / 1e12, 2),
-        "kernel_ms": {kk: round(v, 5) for kk, v in k.items()},
-        "kernels": {kk: rate(kk, k[kk], flops=f) for kk, f in flops4.items() if kk in k}}
-    del act, mask, op, y
-
-    # Config 5: long-complex pair stack at N_res=1024: triangle incoming
-    # (128 batched 1024^3 contractions) + pair transition 128->512->128 over
-    # 1,048,576 rows, f16 activations, f32 accumulation.
-    s = SEED + 4
-    L5 = 1024
-    z = torch.from_numpy(ref.round_f16(ref.normal(s, (L5, L5, CZ)))).half().to(dev)
-    mask = torch.ones((L5, L5), dtype=torch.float32, device=dev)
-    tri = triangle.TriangleMultiplication(L5, CZ, CH, direction="incoming", precision="f16", pair_dtype="f16",
-                                          out_dtype="f16")
-    tri.prepare(triangle_weights(s, CZ, CH))
-    zo = tri(z, mask)
-    ms, k = timed(lambda: tri(z, mask, out=zo), max(3, steps // 4), 1)
-    f5 = triangle_flops(L5, CZ, CH)
-    entry = {"triangle_incoming_ms": round(ms, 4),
-             "triangle_tflops": round((f5["project"] + f5["contract"] + f5["output"] + f5["gate"]) / (ms * 1e-3) / 1e12, 2),
-             "triangle_kernel_ms": {kk: round(v, 5) for kk, v in k.items()}}
-    if "triangle.contract" in k:
-        entry["contract"] = rate("triangle.contract", k["triangle.contract"], flops=f5["contract"])
-    rows5 = L5 * L5
-    tw = {"layerNormScale": ref.normal(s + 20, (CZ,), 0.01, 1.0), "layerNormOffset": ref.normal(s + 21, (CZ,), 0.01),
-          "firstWeight": ref.normal(s + 22, (CZ, 4 * CZ), 1 / CZ), "firstBias": ref.normal(s + 23, (4 * CZ,), 0.02),
-          "secondWeight": ref.normal(s + 24, (4 * CZ, CZ), 1 / (4 * CZ)), "secondBias": ref.normal(s + 25, (CZ,), 0.02)}
-    trans = transition.Transition(rows5, CZ, 4 * CZ, precision="f16", in_dtype="f16", out_dtype="f16")
-    trans.prepare(tw)
-    zf = z.reshape(rows5, CZ)
-    to = trans(zf)
-    ms_t, k_t = timed(lambda: trans(zf, out=to), max(3, steps // 4), 1)
-    ft = 2 * 2 * rows5 * CZ * 4 * CZ
-    entry.update({"transition_ms": round(ms_t, 4), "transition_tflops": round(ft / (ms_t * 1e-3) / 1e12, 2),
-                  "transition_kernel_ms": {kk: round(v, 5) for kk, v in k_t.items()}})
-    out["5_long_complex_pair_stack_l1024"] = entry
+    if 1 in which:
+        # Config 1: pair-transition first linear, f32, 4096x128x512, bias, ReLU.
+        s = SEED
+        x = torch.from_numpy(ref.normal(s, (4096, 128))).to(dev)
+        w = torch.from_numpy(np.ascontiguousarray(ref.normal(s + 1, (128, 512), 1 / 128).T)).to(dev)  # [N][K]
+        b = torch.from_numpy(ref.normal(s + 2, (512,), 0.02)).to(dev)
+        plan = gemm.TiledGemm(4096, 128, 512, precision="f32", w_layout="k", epilogue=("bias", "relu"))
+        y = plan.run(x, w, bias=b)
+        ms, k = timed(lambda: plan.run(x, w, bias=b, out=y), steps * 5, warmup)
+        kms = k.get("gemm", ms)
+        out["1_pair_transition_linear_f32"] = {
+            "ms": round(kms, 5), "wall_ms": round(ms, 5), "variant": plan.variant().name,
+            "roofline": rate("gemm", kms, flops=2 * 4096 * 128 * 512, peak_tflops=PEAK_F32_TFLOPS)}
+        del x, w, b, y, plan
+    if 2 in which:
+        # Config 2: fused QKV+gate projection, mixed-q8: X f16 [131072x256],
+        # W int8 [256x1024] (per-column f32 scales), f32 accumulate, f16 out.
+        s = SEED + 1
+        rows = 512 * 256
+        x = torch.from_numpy(ref.round_f16(ref.normal(s, (rows, 256)))).half().to(dev)
+        q = torch.from_numpy(np.ascontiguousarray(ref.uniform_i8(s + 1, (256, 1024)).T)).to(dev)  # [N][K] int8
+        scale = torch.from_numpy(ref.uniform(s + 2, (1024,), 1e-3, 1e-2)).to(dev)
+        plan = gemm.TiledGemm(rows, 256, 1024, precision="f16", a_dtype="f16", w_dtype="i8", w_layout="k",
+                              out_dtype="f16", epilogue=("scale", "attention"), heads=8, head_dim=32)
+        y = plan.run(x, q, scale=scale)
+        ms, k = timed(lambda: plan.run(x, q, scale=scale, out=y), steps, warmup)
+        kms = k.get("gemm", ms)
+        nbytes = 2 * rows * 256 + 256 * 1024 + 4 * 1024 + 2 * rows * 1024
+        out["2_qkv_gate_projection_q8"] = {
+            "ms": round(kms, 5), "wall_ms": round(ms, 5), "variant": plan.variant().name,
+            "tflops": round(2 * rows * 256 * 1024 / (kms * 1e-3) / 1e12, 2),
+            "roofline": rate("gemm", kms, nbytes=nbytes, traffic=recorded_traffic().get("config2.gemm"))}
+        del x, q, scale, y, plan
+    if 4 in which:
+        # Config 4: outer-product mean, N_seq=512, N_res=256, c_m=256 -> 32+32 -> 128, f16.
+        s = SEED + 3
+        S4, L4, CM, CO, CZ4 = 512, 256, 256, 32, 128
+        act = torch.from_numpy(ref.round_f16(ref.normal(s, (S4, L4, CM)))).half().to(dev)
+        mask = torch.ones((S4, L4), dtype=torch.float32, device=dev)
+        wts = {"layerNormScale": ref.normal(s + 1, (CM,), 0.01, 1.0), "layerNormOffset": ref.normal(s + 2, (CM,), 0.01),
+               "leftWeight": ref.normal(s + 3, (CM, CO), 1 / CM), "leftBias": ref.normal(s + 4, (CO,), 0.02),
+               "rightWeight": ref.normal(s + 5, (CM, CO), 1 / CM), "rightBias": ref.normal(s + 6, (CO,), 0.02),
+               "outputWeight": ref.normal(s + 7, (CO * CO, CZ4), 1 / (CO * CO)), "outputBias": ref.normal(s + 8, (CZ4,), 0.02)}
+        op = opm.OuterProductMean(S4, L4, CM, CO, CZ4, precision="f16", msa_dtype="f16", out_dtype="f32")
+        op.prepare(wts)
+        y = op(act, mask)
+        ms, k = timed(lambda: op(act, mask, out=y), steps, warmup)
+        flops4 = {"opm.project": 2 * S4 * L4 * CM * 2 * CO, "opm.contract": 2 * (L4 * CO) ** 2 * S4,
+                  "opm.output": 2 * L4 * L4 * CO * CO * CZ4}
+        out["4_outer_product_mean"] = {
+            "ms": round(ms, 5), "tflops": round(sum(flops4.values()) / (ms * 1e-3) / 1e12, 2),
+            "kernel_ms": {kk: round(v, 5) for kk, v in k.items()},
+            "kernels": {kk: rate(kk, k[kk], flops=f) for kk, f in flops4.items() if kk in k and kk != "opm.project"}}
+        # The projection is bandwidth-bound: it reads m f16 and the mask and
+        # writes left and right f16 ([L*c_o][S] each).
+        if "opm.project" in k:
+            out["4_outer_product_mean"]["kernels"]["opm.project"] = rate(
+                "opm.project", k["opm.project"], nbytes=2 * S4 * L4 * CM + 4 * S4 * L4 + 2 * 2 * L4 * CO * S4)
+        del act, mask, op, y
+    if 5 in which:
+        # Config 5: long-complex pair stack at N_res=1024: triangle incoming
+        # (128 batched 1024^3 contractions) + pair transition 128->512->128 over
+        # 1,048,576 rows, f16 activations, f32 accumulation.
+        s = SEED + 4
+        L5 = 1024
+        z = torch.from_numpy(ref.round_f16(ref.normal(s, (L5, L5, CZ)))).half().to(dev)
+        mask = torch.ones((L5, L5), dtype=torch.float32, device=dev)
+        tri = triangle.TriangleMultiplication(L5, CZ, CH, direction="incoming", precision="f16", pair_dtype="f16",
+                                              out_dtype="f16")
+        tri.prepare(triangle_weights(s, CZ, CH))
+        zo = tri(z, mask)
+        ms, k = timed(lambda: tri(z, mask, out=zo), max(3, steps // 4), 1)
+        f5 = triangle_flops(L5, CZ, CH)
+        entry = {"triangle_incoming_ms": round(ms, 4),
+                 "triangle_tflops": round((f5["project"] + f5["contract"] + f5["output"] + f5["gate"]) / (ms * 1e-3) / 1e12, 2),
+                 "triangle_kernel_ms": {kk: round(v, 5) for kk, v in k.items()}}
+        if "triangle.contract" in k:
+            entry["contract"] = rate("triangle.contract", k["triangle.contract"], flops=f5["contract"])
+        rows5 = L5 * L5
+        tw = {"layerNormScale": ref.normal(s + 20, (CZ,), 0.01, 1.0), "layerNormOffset": ref.normal(s + 21, (CZ,), 0.01),
+              "firstWeight": ref.normal(s + 22, (CZ, 4 * CZ), 1 / CZ), "firstBias": ref.normal(s + 23, (4 * CZ,), 0.02),
+              "secondWeight": ref.normal(s + 24, (4 * CZ, CZ), 1 / (4 * CZ)), "secondBias": ref.normal(s + 25, (CZ,), 0.02)}
+        trans = transition.Transition(rows5, CZ, 4 * CZ, precision="f16", in_dtype="f16", out_dtype="f16")
+        trans.prepare(tw)
+        zf = z.reshape(rows5, CZ)
+        to = trans(zf)
+        ms_t, k_t = timed(lambda: trans(zf, out=to), max(3, steps // 4), 1)
+        ft = 2 * 2 * rows5 * CZ * 4 * CZ
+        entry.update({"transition_ms": round(ms_t, 4), "transition_tflops": round(ft / (ms_t * 1e-3) / 1e12, 2),
+                      "transition_kernel_ms": {kk: round(v, 5) for kk, v in k_t.items()}})
+        out["5_long_complex_pair_stack_l1024"] = entry
     return out
 
 
@@ -265,6 +270,8 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--headline-only", action="store_true", help="skip BASELINE configs 1, 2, 4 and 5")
+    parser.add_argument("--configs", default="1,2,4,5",
+                        help="comma-separated BASELINE configs to measure besides the headline (config 3)")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                         help="only run a plain device-to-device copy of MIB MiB 10 times (the known-size kernel "
                              "rocprof's FETCH_SIZE / WRITE_SIZE readings are scaled by) and exit")
@@ -340,10 +347,11 @@ def main() -> None:
         "kernels": kernels,
         "kernel_ms": {k: round(v, 5) for k, v in per_kernel.items()},
     }
-    if not args.headline_only:
+    which = tuple(int(c) for c in args.configs.split(",") if c.strip()) if not args.headline_only else ()
+    if which:
         del ops, zd, md
         torch.cuda.empty_cache()
-        result["configs"] = measure_configs(args.steps, args.warmup)
+        result["configs"] = measure_configs(args.steps, args.warmup, which)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result))
