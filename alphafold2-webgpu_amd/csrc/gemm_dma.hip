@@ -179,20 +179,26 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
       block_barrier();
       half_t* C = reinterpret_cast<half_t*>(g.c) + (int64_t)bt * g.sc;
       constexpr int CPR = BN / 8;  // 16-byte chunks per row
-#pragma unroll 4
-      for (int idx = threadIdx.x; idx < BM * CPR; idx += kThreads) {
-        const int r = idx / CPR, c = idx - r * CPR;
-        const int row = m0 + r, col = n0 + 8 * c;
-        const uint4 v = *reinterpret_cast<const uint4*>(smem + r * ROWB + 16 * (c ^ (r & 7)));
-        if (row < g.M) {
-          half_t* dst = C + (int64_t)row * g.ldc + col;
-          if (col + 8 <= g.N) {
-            *reinterpret_cast<uint4*>(dst) = v;
-          } else {
-            const half8 h = __builtin_bit_cast(half8, v);
-            for (int e = 0; e < 8 && col + e < g.N; e++) dst[e] = h[e];
+      static_assert((BM * CPR) % (2 * kThreads) == 0, "stores go in pairs");
+      for (int idx0 = threadIdx.x; idx0 < BM * CPR; idx0 += 2 * kThreads) {
+        u32x4 v[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+          const int idx = idx0 + k * kThreads;
+          const int r = idx / CPR, c = idx - r * CPR;
+          const int row = m0 + r, col = n0 + 8 * c;
+          v[k] = *reinterpret_cast<const u32x4*>(smem + r * ROWB + 16 * (c ^ (r & 7)));
+          if (row < g.M) {
+            half_t* dst = C + (int64_t)row * g.ldc + col;
+            if (col + 8 <= g.N) {
+              *reinterpret_cast<u32x4*>(dst) = v[k];
+            } else {
+              const half8 h = __builtin_bit_cast(half8, v[k]);
+              for (int e = 0; e < 8 && col + e < g.N; e++) dst[e] = h[e];
+            }
           }
         }
+        stores_read(v[0], v[1]);
       }
       return;
     }
@@ -234,16 +240,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
       constexpr int BLOCKS = (BM / 32) * (BN / 32);
       // Half-block h of tile block q: rows a in [16 h, 16 h + 16), 4 lanes per
       // 64-byte row.
-#pragma unroll 2
-      for (int idx = threadIdx.x >> 6; idx < 2 * BLOCKS; idx += kThreads / 64) {
-        const int q = idx >> 1, half = idx & 1;
-        const int bi = q / (BN / 32), bj = q - bi * (BN / 32);
-        const int a = 16 * half + (lane >> 2), c = lane & 3;  // 16-byte chunk c of the 64-byte row
-        const int il = (m0 >> 5) + bi, jj = (n0 >> 5) + bj;
-        const int r = 32 * bi + a, chunk = 4 * bj + c;
-        const uint4 v = *reinterpret_cast<const uint4*>(smem + r * ROWB + 16 * (chunk ^ (r & 7)));
-        if (32 * il < g.M && jj < g.opm_length)
-          *reinterpret_cast<uint4*>(C + (((int64_t)il * g.opm_length + jj) * 32 + a) * 32 + 8 * c) = v;
+      static_assert((2 * BLOCKS) % (2 * (kThreads / 64)) == 0, "stores go in pairs");
+      for (int idx0 = threadIdx.x >> 6; idx0 < 2 * BLOCKS; idx0 += 2 * (kThreads / 64)) {
+        u32x4 v[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+          const int idx = idx0 + k * (kThreads / 64);
+          const int q = idx >> 1, half = idx & 1;
+          const int bi = q / (BN / 32), bj = q - bi * (BN / 32);
+          const int a = 16 * half + (lane >> 2), c = lane & 3;  // 16-byte chunk c of the 64-byte row
+          const int il = (m0 >> 5) + bi, jj = (n0 >> 5) + bj;
+          const int r = 32 * bi + a, chunk = 4 * bj + c;
+          v[k] = *reinterpret_cast<const u32x4*>(smem + r * ROWB + 16 * (chunk ^ (r & 7)));
+          if (32 * il < g.M && jj < g.opm_length)
+            *reinterpret_cast<u32x4*>(C + (((int64_t)il * g.opm_length + jj) * 32 + a) * 32 + 8 * c) = v[k];
+        }
+        stores_read(v[0], v[1]);
       }
       return;
     }

@@ -55,7 +55,6 @@ constexpr int kBM = 32;             // rows per tile
 constexpr int kBN = 64 * kWaves;    // columns per slice
 constexpr int kStages = 3;
 
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 template <int K> struct StreamLayout {
   static constexpr int RB = 2 * K;                     // bytes of one activation row
@@ -233,9 +232,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_stream_kernel(StreamArgs g) 
   auto store_part = [&](__amdgpu_buffer_rsrc_t rc, int buf, int i, bool on) {
     const int c = lane & 31;
     const int r = 2 * ((wave - kLoaders) * kPer + i) + (lane >> 5);
-    const u32x4 v = *reinterpret_cast<const u32x4*>(ost + buf * Lay::OBUF + r * Lay::OROW + 16 * (c ^ (r & 7)));
+    u32x4 v = *reinterpret_cast<const u32x4*>(ost + buf * Lay::OBUF + r * Lay::OROW + 16 * (c ^ (r & 7)));
     const uint32_t off = on && scol < g.N ? (uint32_t)(r * g.ldc * 2 + 2 * scol) : kOutOfRange;
     __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
+    stores_read(v);
   };
 
   // The persistent loop, software-pipelined: tile t's MFMAs, tile t-1's

@@ -137,6 +137,22 @@ __device__ __forceinline__ float sigmoidf_(float x) {
   return fast_rcp(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
 
+// Vector-memory stores read their data VGPRs some time after they issue
+// (under heavy memory traffic, long after), counting in EXP_CNT until they
+// have; the compiler takes the data as read at issue and may hand the
+// registers to the next instruction. A store whose data registers can be
+// rewritten soon after (the next LDS read into the same registers, say) is
+// followed by stores_read(data...), which waits for EXP_CNT to drain and
+// keeps the registers live up to the wait.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void stores_read(u32x4& a) { asm volatile("s_waitcnt expcnt(0)" : "+v"(a)); }
+__device__ __forceinline__ void stores_read(u32x4& a, u32x4& b) {
+  asm volatile("s_waitcnt expcnt(0)" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void stores_read(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  asm volatile("s_waitcnt expcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+
 template <typename T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
 template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }
 

@@ -365,16 +365,18 @@ __global__ __launch_bounds__(kFastThreads, 2) void opm_project_fast_kernel(Proje
     // 64 channel rows of 128 bytes: wave w writes rows 16 w .. 16 w + 15,
     // eight lanes per row; sequences past sp (the padded row length) are
     // skipped, those in [S, sp) are zeros.
+    u32x4 v[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int ch = 16 * wave + 8 * j + (lane >> 3), chunk = lane & 7;
       const int sq = s0 + 8 * chunk;
+      v[j] = *reinterpret_cast<const u32x4*>(stg + ch * Lay::SPITCH + 8 * chunk);
       if (sq < a.sp) {
-        const uint4 v = *reinterpret_cast<const uint4*>(stg + ch * Lay::SPITCH + 8 * chunk);
         half_t* dst = reinterpret_cast<half_t*>(ch < 32 ? a.left : a.right);
-        *reinterpret_cast<uint4*>(dst + ((int64_t)res * 32 + (ch & 31)) * a.sp + sq) = v;
+        *reinterpret_cast<u32x4*>(dst + ((int64_t)res * 32 + (ch & 31)) * a.sp + sq) = v[j];
       }
     }
+    stores_read(v[0], v[1]);
   }
 }
 

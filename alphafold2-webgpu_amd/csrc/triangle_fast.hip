@@ -42,8 +42,6 @@ namespace afhip {
 
 namespace {
 
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-
 constexpr int kTile = 64;            // pairs per tile
 constexpr int kC = 128;              // c_z = c_hidden
 constexpr int kThreads = 512;
@@ -161,18 +159,20 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
   // lane % LANES_PER_ROW; wave 0 also loads the tile's 64 mask values.
   // Outgoing pairs are consecutive rows of z: the lane's offset within the
   // tile is fixed and the tile's base rides in the instruction's scalar
-  // offset; rows past P fall past the resource (zeros). Incoming pairs are z
+  // offset; rows past P read as zeros. Incoming pairs are z
   // transposed: row r of the tile stream is pair (r % L) * L + r / L, whose
   // coordinates (r / L, r % L) each lane advances by G * 64 rows per issued
   // tile instead of dividing.
   constexpr int NL = Lay::LPW + 1;  // the loads, then the mask (wave 0)
   uint32_t vofs[NL];
+  int vrow[NL];        // the tile row the lane fills
   int ci[NL], ck[NL];  // incoming: r / L and r % L of the lane's next row
   const int dq = (G * kTile) / a.L, dr = (G * kTile) % a.L;
 #pragma unroll
   for (int i = 0; i < NL; i++) {
     const int row = i < Lay::LPW ? (wave + kLoaderWaves * i) * Lay::ROWS_PER_LOAD + lane / Lay::LANES_PER_ROW : lane;
     const int chunk = i < Lay::LPW ? lane % Lay::LANES_PER_ROW : 0;
+    vrow[i] = row;
     if constexpr (INCOMING) {
       const int r = t0 * kTile + row;
       ci[i] = r / a.L;
@@ -200,9 +200,12 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
           ci[i] += 1;
         }
       } else {
+        // Rows past P take an out-of-range vector offset (the scalar offset
+        // alone is not range-checked on every generation).
         const uint32_t so = (uint32_t)tile * kTile * esz;
-        if (i < Lay::LPW) dma16_so(rz, lds, vofs[i], so);
-        else dma4_so(rm, lds, vofs[i], so);
+        const uint32_t off = vrow[i] < a.P - tile * kTile ? vofs[i] : kOutOfRange;
+        if (i < Lay::LPW) dma16_so(rz, lds, off, so);
+        else dma4_so(rm, lds, off, so);
       }
     }
   };
@@ -316,9 +319,14 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       // land in the operand's padding (its rows are cstride >= 64 * ntiles
       // long), which the contraction never reads.
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(ost + (srow + 32 * k) * kOutPitch + schunk * 8);
-        __builtin_amdgcn_raw_buffer_store_b128(v, k < 4 ? rsa : rsb, svof[k & 3], (uint32_t)tile * kTile * 2, 0);
+      for (int h = 0; h < 2; h++) {
+        u32x4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = *reinterpret_cast<const u32x4*>(ost + (srow + 32 * (4 * h + k)) * kOutPitch + schunk * 8);
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          __builtin_amdgcn_raw_buffer_store_b128(v[k], h == 0 ? rsa : rsb, svof[k], (uint32_t)tile * kTile * 2, 0);
+        stores_read(v[0], v[1], v[2], v[3]);
       }
     }
   }
@@ -523,23 +531,29 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
       constexpr int PER_LANE = kTile * CHUNKS / 256;
       const int t4 = tid - kLoaderWaves * 64;
       const int q0 = tile * kTile;
+      static_assert(PER_LANE % 4 == 0, "stores go in groups of four");
 #pragma unroll
-      for (int k = 0; k < PER_LANE; k++) {
-        const int idx = t4 + 256 * k;
-        const int q = idx / CHUNKS, chunk = idx % CHUNKS;
-        if (q0 + q >= a.pairs) continue;
-        uint4 v = *reinterpret_cast<const uint4*>(st + q * Lay::OPITCH + chunk * 16);
-        unsigned char* dst =
-            reinterpret_cast<unsigned char*>(a.out) + ((size_t)a.pair0 + q0 + q) * Lay::OROW + chunk * 16;
-        if (a.residual) {
-          const uint4 r = *reinterpret_cast<const uint4*>(dst);
-          constexpr int E = 16 / (int)sizeof(OT);
-          OT* vv = reinterpret_cast<OT*>(&v);
-          const OT* rr = reinterpret_cast<const OT*>(&r);
+      for (int k0 = 0; k0 < PER_LANE; k0 += 4) {
+        u32x4 v[4];
 #pragma unroll
-          for (int e = 0; e < E; e++) vv[e] = (OT)((float)vv[e] + (float)rr[e]);
+        for (int k = 0; k < 4; k++) {
+          const int idx = t4 + 256 * (k0 + k);
+          const int q = idx / CHUNKS, chunk = idx % CHUNKS;
+          v[k] = *reinterpret_cast<const u32x4*>(st + q * Lay::OPITCH + chunk * 16);
+          unsigned char* dst =
+              reinterpret_cast<unsigned char*>(a.out) + ((size_t)a.pair0 + q0 + q) * Lay::OROW + chunk * 16;
+          if (q0 + q >= a.pairs) continue;
+          if (a.residual) {
+            const u32x4 r = *reinterpret_cast<const u32x4*>(dst);
+            constexpr int E = 16 / (int)sizeof(OT);
+            OT* vv = reinterpret_cast<OT*>(&v[k]);
+            const OT* rr = reinterpret_cast<const OT*>(&r);
+#pragma unroll
+            for (int e = 0; e < E; e++) vv[e] = (OT)((float)vv[e] + (float)rr[e]);
+          }
+          *reinterpret_cast<u32x4*>(dst) = v[k];
         }
-        *reinterpret_cast<uint4*>(dst) = v;
+        stores_read(v[0], v[1], v[2], v[3]);
       }
     }
   }

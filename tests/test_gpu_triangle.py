@@ -129,6 +129,36 @@ def test_f16_pair_input_and_residual(dev):
     assert np.all(np.abs(got - expect) <= 1e-2 * np.maximum(1.0, np.abs(expect)))
 
 
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("length,shift", [(37, 0.0), (100, 6.0), (300, -3.0)])
+def test_f16_pair_input_against_oracle(dev, direction, length, shift):
+    """f16 z (the kernels that take z's rows into the MFMA as loaded, with
+    the LayerNorm mean subtracted in the accumulator): ragged last tiles
+    (37 * 37 pairs), several tiles a CU (300 * 300), and rows whose mean is
+    far from zero, where a lost mean correction would show at once. At
+    300 * 300 the expectation is the f32 path (itself held to the oracle at
+    1e-5 above), which the oracle would take ~20 s to produce."""
+    import torch
+
+    from afhip import triangle
+
+    cz = ch = 128
+    inp = ref.deterministic_triangle_input(length, cz, ch, seed=length + 7)
+    z16 = ref.round_f16(inp["z"] + np.float32(shift))
+    if length <= 128:
+        expect = ref.triangle(direction, z16, inp["mask"], inp["weights"])
+    else:
+        f32 = triangle.TriangleMultiplication(length, cz, ch, direction=direction, precision="f32")
+        f32.prepare(inp["weights"])
+        expect = f32(torch.from_numpy(z16).to(dev), torch.from_numpy(inp["mask"]).to(dev)).cpu().numpy()
+    op = triangle.TriangleMultiplication(length, cz, ch, direction=direction, precision="f16", pair_dtype="f16",
+                                         out_dtype="f32")
+    op.prepare(inp["weights"])
+    out = op(torch.from_numpy(z16).half().to(dev), torch.from_numpy(inp["mask"]).to(dev)).cpu().numpy()
+    err = np.abs(out.reshape(expect.shape) - expect)
+    assert np.all(err <= 1e-2 * np.maximum(1.0, np.abs(expect)))
+
+
 def test_invalid_input_raises_range_error(dev):
     from afhip import _lib
 
