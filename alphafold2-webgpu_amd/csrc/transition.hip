@@ -1,7 +1,9 @@
 // Transition for gfx950: LayerNorm, linear channels -> hidden + bias + ReLU,
 // linear hidden -> channels + bias (src/evoformer/transition.ts:179-234,
-// :264-361). The LayerNorm is one wave per row, writing the normalised rows
-// in the GEMM's operand dtype; both linears run through the shared GEMM.
+// :264-361). The LayerNorm writes the normalised rows in the GEMM's operand
+// dtype (rows spread over lane groups with 16-byte accesses for the f16 path
+// at 64, 128 or 256 channels, one wave per row otherwise); both linears run
+// through the shared GEMM.
 #include <algorithm>
 #include <cmath>
 
@@ -119,8 +121,95 @@ int validate(const afhip_transition_desc* d) {
   return AFHIP_OK;
 }
 
+// f16 output, C = 8 LANES channels (64, 128 or 256): LANES consecutive lanes
+// own a row, eight channels each (one 16-byte load of f16, two of f32), so
+// the whole row is in registers after one pass and its sums are DPP
+// reductions within the lane group; each lane carries four rows at a time to
+// keep loads in flight. The same two-pass statistics and the same
+// expression as layer_norm_kernel.
+template <typename IT, int LANES>
+__global__ __launch_bounds__(256) void layer_norm_rows_kernel(const IT* __restrict__ x, int64_t rows,
+                                                              const float* __restrict__ scale,
+                                                              const float* __restrict__ offset, float eps,
+                                                              half_t* __restrict__ y) {
+  constexpr int C = 8 * LANES;
+  constexpr int RPW = 64 / LANES;  // rows a wave covers per load
+  constexpr int U = 4;             // rows in flight per lane
+  constexpr int LOADS = sizeof(IT) / 2;
+  const int lane = threadIdx.x & 63, sub = lane / LANES, part = lane % LANES;
+  float sc[8], of[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    sc[e] = scale[8 * part + e];
+    of[e] = offset[8 * part + e];
+  }
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t base = wave * RPW * U; base < rows; base += waves * RPW * U) {
+    u32x4 raw[U][LOADS];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t row = base + u * RPW + sub;
+#pragma unroll
+      for (int l = 0; l < LOADS; l++)
+        raw[u][l] = row < rows ? reinterpret_cast<const u32x4*>(x + row * C + 8 * part)[l] : u32x4{0u, 0u, 0u, 0u};
+    }
+    u32x4 out[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      float v[8];
+      if constexpr (sizeof(IT) == 2) {
+        const half8 h = __builtin_bit_cast(half8, raw[u][0]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (float)h[e];
+      } else {
+#pragma unroll
+        for (int l = 0; l < 2; l++) {
+          const floatx4 f = __builtin_bit_cast(floatx4, raw[u][l]);
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[4 * l + e] = f[e];
+        }
+      }
+      float s = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) s += v[e];
+      const float mean = lane_sum<LANES>(s) / (float)C;
+      float d2 = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float d = v[e] - mean;
+        d2 += d * d;
+      }
+      const float rstd = fast_rsqrt(lane_sum<LANES>(d2) / (float)C + eps);
+      half8 h;
+#pragma unroll
+      for (int e = 0; e < 8; e++) h[e] = (half_t)((v[e] - mean) * rstd * sc[e] + of[e]);
+      out[u] = __builtin_bit_cast(u32x4, h);
+      const int64_t row = base + u * RPW + sub;
+      if (row < rows) *reinterpret_cast<u32x4*>(y + row * C + 8 * part) = out[u];
+    }
+    stores_read(out[0], out[1], out[2], out[3]);
+  }
+}
+
 template <typename IT, typename CT>
 int launch_ln(const void* x, int64_t rows, int C, const float* s, const float* o, float eps, void* y, hipStream_t st) {
+  if constexpr (sizeof(CT) == 2) {
+    const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    if (aligned && (C == 64 || C == 128 || C == 256)) {
+      const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+      const int64_t rows_per_block = 4 * (64 / (C / 8)) * 4;  // four waves, four rows in flight per lane
+      const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(rows, rows_per_block), (int64_t)cus * 8);
+      if (C == 64)
+        return launch("transition.layer_norm", layer_norm_rows_kernel<IT, 8>, dim3(grid), dim3(256), 0, st,
+                      (const IT*)x, rows, s, o, eps, (half_t*)y);
+      if (C == 128)
+        return launch("transition.layer_norm", layer_norm_rows_kernel<IT, 16>, dim3(grid), dim3(256), 0, st,
+                      (const IT*)x, rows, s, o, eps, (half_t*)y);
+      return launch("transition.layer_norm", layer_norm_rows_kernel<IT, 32>, dim3(grid), dim3(256), 0, st,
+                    (const IT*)x, rows, s, o, eps, (half_t*)y);
+    }
+  }
   return launch("transition.layer_norm", layer_norm_kernel<IT, CT>, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, st,
                 (const IT*)x, rows, C, s, o, eps, (CT*)y);
 }

@@ -266,8 +266,10 @@ def measure_configs(steps: int, warmup: int, which=(1, 2, 4, 5)) -> dict:
 def main() -> None:
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=3)
+    # A headline step is ~0.2 ms: 100 steps keep the timed region short while
+    # averaging past the first steps' clock ramp.
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--headline-only", action="store_true", help="skip BASELINE configs 1, 2, 4 and 5")
     parser.add_argument("--configs", default="1,2,4,5",

@@ -129,6 +129,23 @@ def test_transition(dev, rows, c, h):
     assert np.abs(out16 - expect).max() <= 1e-2 * max(1.0, np.abs(expect).max())
 
 
+@pytest.mark.parametrize("rows,c", [(4099, 128), (1001, 64), (515, 256)])
+def test_transition_f16_rows(dev, rows, c):
+    """f16 activations in and out (the LayerNorm that spreads rows over lane
+    groups), with row counts that leave ragged last blocks."""
+    import torch
+
+    from afhip import transition
+
+    inp = transition_case(rows, c, 4 * c, rows + c)
+    x16 = ref.round_f16(inp["activations"])
+    expect = ref.transition(x16, inp["weights"])
+    op = transition.Transition(rows, c, 4 * c, precision="f16", in_dtype="f16", out_dtype="f16")
+    op.prepare(inp["weights"])
+    out = op(torch.from_numpy(x16).half().to(dev)).float().cpu().numpy()
+    assert np.abs(out - expect).max() <= 1e-2 * max(1.0, np.abs(expect).max())
+
+
 def test_invalid_opm_and_transition_raise(dev):
     from afhip import _lib, opm, transition
 
