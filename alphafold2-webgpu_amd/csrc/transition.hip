@@ -1,13 +1,16 @@
 // Transition for gfx950: LayerNorm, linear channels -> hidden + bias + ReLU,
 // linear hidden -> channels + bias (src/evoformer/transition.ts:179-234,
-// :264-361). The LayerNorm writes the normalised rows in the GEMM's operand
+// :264-361). At f16 precision with 128 channels and hidden 512 (the pair
+// transition) one fused kernel does all three steps (transition_fused.hip).
+// Otherwise the LayerNorm writes the normalised rows in the GEMM's operand
 // dtype (rows spread over lane groups with 16-byte accesses for the f16 path
-// at 64, 128 or 256 channels, one wave per row otherwise); both linears run
+// at 64, 128 or 256 channels, one wave per row otherwise) and both linears run
 // through the shared GEMM.
 #include <algorithm>
 #include <cmath>
 
 #include "gemm.h"
+#include "transition_fused.h"
 
 namespace afhip {
 
@@ -270,6 +273,21 @@ int afhip_transition_run(const afhip_transition_desc* desc, const void* activati
   const char* wb = (const char*)prepared;
   char* normalized = (char*)workspace_ptr + ws.normalized;
   char* hidden = (char*)workspace_ptr + ws.hidden;
+  if (transition_fused_eligible(d, activations, out)) {
+    FusedTransitionArgs f{};
+    f.x = activations;
+    f.out = out;
+    f.rows = d.rows;
+    f.residual = d.residual;
+    f.scale = (const float*)(wb + w.scale);
+    f.offset = (const float*)(wb + w.offset);
+    f.eps = d.epsilon;
+    f.w1 = (const half_t*)(wb + w.w1);
+    f.b1 = (const float*)(wb + w.b1);
+    f.w2 = (const half_t*)(wb + w.w2);
+    f.b2 = (const float*)(wb + w.b2);
+    return launch_transition_fused(f, d.in_dtype, d.out_dtype, st);
+  }
   const size_t ie = dtype_size(d.in_dtype), oe = dtype_size(d.out_dtype);
   for (int64_t r0 = 0; r0 < d.rows; r0 += ws.chunk) {
     const int64_t rows = std::min<int64_t>(ws.chunk, d.rows - r0);

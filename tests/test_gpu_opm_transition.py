@@ -146,6 +146,57 @@ def test_transition_f16_rows(dev, rows, c):
     assert np.abs(out - expect).max() <= 1e-2 * max(1.0, np.abs(expect).max())
 
 
+@pytest.mark.parametrize("rows,in_dt,out_dt,residual", [
+    (1, "f16", "f16", False), (31, "f32", "f32", False), (33, "f16", "f32", True), (4099, "f32", "f16", True),
+    (8191, "f16", "f16", True), (64, "f32", "f32", True)])
+def test_transition_fused_pair(dev, rows, in_dt, out_dt, residual):
+    """The pair transition at f16 precision, channels 128 and hidden 512, runs
+    as one fused kernel: every input/output dtype pair, the residual added
+    into the output, and row counts that leave a ragged last 32-row tile."""
+    import torch
+
+    from afhip import transition
+
+    c, h = 128, 512
+    inp = transition_case(rows, c, h, 7 * rows + 3)
+    x = inp["activations"] if in_dt == "f32" else ref.round_f16(inp["activations"])
+    base = ref.normal(rows + 11, (rows, c))
+    base = base if out_dt == "f32" else ref.round_f16(base)
+    expect = ref.transition(x, inp["weights"]) + (base if residual else 0.0)
+    op = transition.Transition(rows, c, h, precision="f16", in_dtype=in_dt, out_dtype=out_dt, residual=residual)
+    op.prepare(inp["weights"])
+    tdt = {"f32": torch.float32, "f16": torch.float16}
+    out = torch.from_numpy(base).to(tdt[out_dt]).to(dev)
+    op(torch.from_numpy(x).to(tdt[in_dt]).to(dev), out=out)
+    got = out.float().cpu().numpy()
+    assert np.abs(got - expect).max() <= 1e-2 * max(1.0, np.abs(expect).max())
+
+
+def test_transition_fused_in_place_full_size(dev):
+    """z += transition(z) in place over the 1024^2 rows of a long complex's
+    pair representation, against a float32 PyTorch restatement of the same
+    LayerNorm and linears on the device."""
+    import torch
+
+    from afhip import transition
+
+    rows, c, h = 1 << 20, 128, 512
+    inp = transition_case(64, c, h, 5)
+    w = {k: torch.from_numpy(np.asarray(v, np.float32)).to(dev) for k, v in inp["weights"].items()}
+    g = torch.Generator(device=dev).manual_seed(3)
+    z = torch.randn(rows, c, generator=g, device=dev).half()
+    zf = z.float()
+    y = torch.nn.functional.layer_norm(zf, (c,), w["layerNormScale"], w["layerNormOffset"], 1e-5)
+    y = torch.relu(y @ w["firstWeight"] + w["firstBias"]) @ w["secondWeight"] + w["secondBias"]
+    expect = zf + y
+    del y
+    op = transition.Transition(rows, c, h, precision="f16", in_dtype="f16", out_dtype="f16", residual=True)
+    op.prepare(inp["weights"])
+    op(z, out=z)
+    err = (z.float() - expect).abs().max().item()
+    assert err <= 1e-2 * max(1.0, expect.abs().max().item())
+
+
 def test_invalid_opm_and_transition_raise(dev):
     from afhip import _lib, opm, transition
 
