@@ -7,9 +7,10 @@
 // the outer-product-mean contraction and the f16 projections.
 //
 // Design:
-//  - One workgroup of four wave64s owns a BM x BN output tile (2 x 2 waves,
-//    each (BM/2) x (BN/2) in 32 x 32 v_mfma_f32_32x32x16_f16 tiles) and walks
-//    K in steps of 32 halves.
+//  - One workgroup of WM x WN wave64s owns a BM x BN output tile (each wave
+//    (BM/WM) x (BN/WN) in 32 x 32 v_mfma_f32_32x32x16_f16 tiles) and walks
+//    K in steps of 32 halves: 2 x 2 waves for the 128- and 192-row tiles, two
+//    of which share a CU; 2 x 4 waves, one workgroup a CU, for 256 x 256.
 //  - Operands travel global -> LDS without passing through VGPRs
 //    (buffer_load_dwordx4 ... lds). A k-step stage is (BM + BN) rows of
 //    64 bytes; each wave-level load instruction fills 16 rows (1 KiB of LDS,
@@ -26,6 +27,12 @@
 //  - Tiles are numbered so that consecutive tiles (one batch's tiles, which
 //    share operand panels) run on one XCD: workgroup ids are dealt round-robin
 //    over the eight XCDs, so tile t = (id % 8) * per_xcd + id / 8.
+//  - The 256 x 256 tile runs a pipelined schedule: each k-step's two
+//    16-deep halves are read into separate fragment registers, and the
+//    barrier that publishes stage k + 1 sits between the MFMAs of the first
+//    half and those of the second, so a wave waits at the barrier while its
+//    MFMAs still run and starts the next step with operands already in
+//    registers. Five stages keep the loads three steps ahead.
 //  - The epilogue is the register-staged kernel's (gemm_kernel.h), so both
 //    families give the same epilogue arithmetic.
 #include <algorithm>
@@ -39,20 +46,23 @@ namespace {
 
 constexpr int kBK = 32;        // halves per k-step
 constexpr int kRowBytes = 64;  // one row of a k-step stage
-constexpr int kThreads = 256;
 
 __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
 
-template <int BM, int BN, int STAGES, typename TC>
-__global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::KernelArgs ka) {
-  constexpr int WTM = BM / 2, WTN = BN / 2;
+template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC>
+__global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_kernel(gemm_detail::KernelArgs ka) {
+  constexpr int WAVES = WM * WN;
+  constexpr int kThreads = 64 * WAVES;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int ROWS = BM + BN;
   constexpr int STAGE_BYTES = ROWS * kRowBytes;
-  constexpr int LOADS = ROWS / 16;  // wave-level load instructions per stage
-  constexpr int LPW = LOADS / 4;    // per wave
-  static_assert(BM % 64 == 0 && BN % 64 == 0 && LOADS % 4 == 0, "tile shape");
+  constexpr int LOADS = ROWS / 16;    // wave-level load instructions per stage
+  constexpr int LPW = LOADS / WAVES;  // per wave
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0 && LOADS % WAVES == 0, "tile shape");
+  static_assert(BM % 16 == 0, "a load instruction fills rows of one operand");
   static_assert((STAGES - 2) * LPW < 64, "vmcnt holds at most 63 outstanding loads");
+  static_assert(!PIPE || STAGES >= 4, "the pipelined schedule keeps STAGES - 2 steps in flight");
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
 
   const GemmArgs& g = ka.g;
@@ -69,8 +79,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
   // Wave-uniform by construction; readfirstlane lets the compiler keep the
   // buffer resource choice below in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = (wave >> 1) * WTM;
-  const int wn = (wave & 1) * WTN;
+  const int wm = (wave / WN) * WTM;
+  const int wn = (wave % WN) * WTN;
 
   const half_t* A = reinterpret_cast<const half_t*>(g.a) + (int64_t)bt * g.sa + (int64_t)m0 * g.lda;
   const half_t* B = reinterpret_cast<const half_t*>(g.b) + (int64_t)bt * g.sb + (int64_t)n0 * g.ldb;
@@ -80,13 +90,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
   const int32x4_t rb = make_rsrc(B, (uint32_t)((int64_t)rows_b * g.ldb * 2));
 
   // This lane's part of each of the wave's load instructions: instruction
-  // q = wave + 4 i fills stage rows [16 q, 16 q + 16); the lane fills slot
+  // q = wave + WAVES i fills stage rows [16 q, 16 q + 16); the lane fills slot
   // lane % 4 of row 16 q + lane / 4 with global chunk slot ^ swizzle(row).
   uint32_t base_off[LPW];
   int chunk_k[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; i++) {
-    const int q = wave + 4 * i;
+    const int q = wave + WAVES * i;
     const int row = 16 * q + (lane >> 2);
     const int chunk = (lane & 3) ^ swizzle(row);
     chunk_k[i] = 8 * chunk;
@@ -99,7 +109,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
     const int k0 = ks * kBK;
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
-      const int q = wave + 4 * i;
+      const int q = wave + WAVES * i;
       const uint32_t off = k0 + chunk_k[i] < g.K ? base_off[i] + 2u * k0 : kOutOfRange;
       dma16(16 * q < BM ? ra : rb, lds0 + stage * STAGE_BYTES + q * 1024, off);
     }
@@ -119,6 +129,69 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
     if (s < nk) issue(s, s);
 
   const int frag_row = lane & 31;
+  // Fragments of half kk (16 halves of k) of a stage: chunk 2 kk + lane / 32.
+  auto read_frags = [&](const unsigned char* st, int kk, half8* af, half8* bf) {
+    const int chunk = 2 * kk + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int row = wm + 32 * i + frag_row;
+      af[i] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int row = BM + wn + 32 * j + frag_row;
+      bf[j] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
+    }
+  };
+  // Issued as B x A^T: the accumulator's rows are output columns, so a lane
+  // ends with four consecutive columns of one output row per group (the same
+  // products summed in the same k order as A x B^T).
+  auto mfmas = [&](const half8* af, const half8* bf) {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) acc[i][j] = mfma_f16(bf[j], af[i], acc[i][j]);
+  };
+  if constexpr (PIPE) {
+    // The rest of the prologue: stages nk .. STAGES - 2 are issued too (their
+    // offsets are all past K, so they load zeros without touching memory),
+    // and every step issues one stage, so each wait below counts a fixed
+    // number of loads and the loop body has no branches: a branch around a
+    // wait or a barrier would join paths with different LDS reads pending,
+    // and the compiler then waits for all of them before the next MFMA.
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; s++)
+      if (s >= nk) issue(s, s);
+    // Stage 0 has landed once at most stages 1 .. STAGES - 2 are pending.
+    wait_vmcnt<(STAGES - 2) * LPW>();
+    block_barrier<false>();
+    half8 a0[TM], b0[TN], a1[TM], b1[TN];
+    read_frags(smem, 0, a0, b0);
+    // sched_barrier(0) keeps the compiler from moving instructions across
+    // the phase boundaries: left free, it reuses one set of fragment
+    // registers for both halves (so a half's reads wait for the other half's
+    // MFMAs) and hoists MFMAs above the barrier.
+    for (int ks = 0; ks + 1 < nk; ks++) {
+      read_frags(smem + (ks % STAGES) * STAGE_BYTES, 1, a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      // Stage ks + 1 has landed once at most stages ks + 2 .. ks + STAGES - 2
+      // are pending; the barrier publishes it and retires stage ks - 1, whose
+      // fragments every wave consumed before this point.
+      wait_vmcnt<(STAGES - 3) * LPW>();
+      block_barrier<false>();
+      issue(ks + STAGES - 1, (ks + STAGES - 1) % STAGES);
+      read_frags(smem + ((ks + 1) % STAGES) * STAGE_BYTES, 0, a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    read_frags(smem + ((nk - 1) % STAGES) * STAGE_BYTES, 1, a1, b1);
+    mfmas(a0, b0);
+    mfmas(a1, b1);
+    wait_vmcnt<0>();  // the zero loads past K land before the stages are reused
+  } else
   for (int ks = 0; ks < nk; ks++) {
     // Stage ks is complete once at most the later stages' loads are pending;
     // the barrier then publishes it and retires stage ks - 1 for refilling.
@@ -129,25 +202,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
     const unsigned char* st = smem + (ks % STAGES) * STAGE_BYTES;
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) {
-      const int chunk = 2 * kk + (lane >> 5);
       half8 af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const int row = wm + 32 * i + frag_row;
-        af[i] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
-      }
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const int row = BM + wn + 32 * j + frag_row;
-        bf[j] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
-      }
-      // Issued as B x A^T: the accumulator's rows are output columns, so a
-      // lane ends with four consecutive columns of one output row per group
-      // (the same products summed in the same k order as A x B^T).
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = mfma_f16(bf[j], af[i], acc[i][j]);
+      read_frags(st, kk, af, bf);
+      mfmas(af, bf);
     }
     asm volatile("" ::: "memory");
   }
@@ -240,12 +297,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
       constexpr int BLOCKS = (BM / 32) * (BN / 32);
       // Half-block h of tile block q: rows a in [16 h, 16 h + 16), 4 lanes per
       // 64-byte row.
-      static_assert((2 * BLOCKS) % (2 * (kThreads / 64)) == 0, "stores go in pairs");
-      for (int idx0 = threadIdx.x >> 6; idx0 < 2 * BLOCKS; idx0 += 2 * (kThreads / 64)) {
+      static_assert((2 * BLOCKS) % (2 * WAVES) == 0, "stores go in pairs");
+      for (int idx0 = threadIdx.x >> 6; idx0 < 2 * BLOCKS; idx0 += 2 * WAVES) {
         u32x4 v[2];
 #pragma unroll
         for (int k = 0; k < 2; k++) {
-          const int idx = idx0 + k * (kThreads / 64);
+          const int idx = idx0 + k * WAVES;
           const int q = idx >> 1, half = idx & 1;
           const int bi = q / (BN / 32), bj = q - bi * (BN / 32);
           const int a = 16 * half + (lane >> 2), c = lane & 3;  // 16-byte chunk c of the 64-byte row
@@ -321,7 +378,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_dma_kernel(gemm_detail::Kern
     }
 }
 
-template <int BM, int BN, int STAGES, typename TC>
+template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC>
 int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   gemm_detail::KernelArgs ka;
   ka.g = g;
@@ -332,22 +389,23 @@ int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   ka.total_tiles = (int)total;
   ka.per_xcd = (int)ceil_div(total, 8);
   const size_t shared = (size_t)STAGES * (BM + BN) * kRowBytes;
-  auto kernel = gemm_dma_kernel<BM, BN, STAGES, TC>;
+  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC>;
   if (int st = allow_lds((const void*)kernel, shared)) return st;
-  return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(kThreads), shared, s, ka);
+  return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(64 * WM * WN), shared, s, ka);
 }
 
 template <typename TC> int launch_typed(const GemmArgs& g, int tm, int tn, const char* label, hipStream_t s) {
-  if (tm == 192 && tn == 192) return launch_tile<192, 192, 3, TC>(g, label, s);
-  if (tm == 128 && tn == 128) return launch_tile<128, 128, 4, TC>(g, label, s);
-  if (tm == 128 && tn == 256) return launch_tile<128, 256, 3, TC>(g, label, s);
+  if (tm == 192 && tn == 192) return launch_tile<192, 192, 3, 2, 2, false, TC>(g, label, s);
+  if (tm == 128 && tn == 128) return launch_tile<128, 128, 4, 2, 2, false, TC>(g, label, s);
+  if (tm == 128 && tn == 256) return launch_tile<128, 256, 3, 2, 2, false, TC>(g, label, s);
+  if (tm == 256 && tn == 256) return launch_tile<256, 256, 5, 2, 4, true, TC>(g, label, s);
   return set_error(AFHIP_ERR_INVALID_ARGUMENT, "unsupported LDS_DMA tile %dx%d", tm, tn);
 }
 
 }  // namespace
 
 bool dma_tile_supported(int tm, int tn) {
-  return (tm == 192 && tn == 192) || (tm == 128 && tn == 128) || (tm == 128 && tn == 256);
+  return (tm == 192 && tn == 192) || (tm == 128 && tn == 128) || (tm == 128 && tn == 256) || (tm == 256 && tn == 256);
 }
 
 bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
@@ -362,23 +420,33 @@ bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
 }
 
 void dma_heuristic_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int* tm, int* tn) {
-  // Measured on MI355X (triangle contractions at L = 384 and 1024, the
-  // outer-product-mean contraction and output, transition shapes):
-  //  - long K on large outputs: 128 x 256, the widest reuse per loaded byte;
-  //  - otherwise 192 x 192 when its ragged edges waste at most 1/20 of the
-  //    work and there are at least two tiles per CU;
-  //  - otherwise 128 x 128, which keeps ragged-edge waste low and the tile
-  //    count high.
+  // Measured on MI355X (kernel time; triangle contractions 128 x L^3, the
+  // outer-product-mean contraction and output):
+  //            128x128  192x192  128x256  256x256
+  //  L = 1024   394 us   373 us   340 us   335 us
+  //  L = 768    186      155      160      164
+  //  L = 512     52       55       48       49
+  //  L = 384     28       25       30       36
+  //  OPM 8192x8192x512       123 / 96 / 104 / 95;  OPM 65536x128x1024   28 / 37 / 36 / 34
+  // so: 256 x 256 for long K on large outputs; else 192 x 192 when its
+  // ragged edges waste at most 1/20 of the work and there are at least two
+  // tiles a CU; else 128 x 256 when K and the output are wide enough; else
+  // 128 x 128, which keeps ragged-edge waste low and the tile count high.
   const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
   auto waste = [](int64_t x, int64_t t) { return (double)(ceil_div(x, t) * t - x) / (double)x; };
-  if (K >= 768 && M >= 1024 && N >= 1024 && waste(M, 128) <= 0.05 && waste(N, 256) <= 0.05 &&
-      ceil_div(M, 128) * ceil_div(N, 256) * batch >= 2 * cus) {
-    *tm = 128;
-    *tn = 256;
+  if (K >= 1024 && M >= 1024 && N >= 1024 && waste(M, 256) <= 0.05 && waste(N, 256) <= 0.05 &&
+      ceil_div(M, 256) * ceil_div(N, 256) * batch >= cus) {
+    *tm = *tn = 256;
     return;
   }
   if (waste(M, 192) <= 0.05 && waste(N, 192) <= 0.05 && ceil_div(M, 192) * ceil_div(N, 192) * batch >= 2 * cus) {
     *tm = *tn = 192;
+    return;
+  }
+  if (K >= 512 && M >= 512 && N >= 512 && waste(M, 128) <= 0.05 && waste(N, 256) <= 0.05 &&
+      ceil_div(M, 128) * ceil_div(N, 256) * batch >= 2 * cus) {
+    *tm = 128;
+    *tn = 256;
     return;
   }
   *tm = *tn = 128;

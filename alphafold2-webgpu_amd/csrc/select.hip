@@ -149,7 +149,7 @@ std::vector<afhip_variant> candidates(int precision, bool dma, bool stream) {
   const int shapes[4][2] = {{64, 64}, {64, 128}, {128, 64}, {128, 128}};
   for (auto& s : shapes) add(AFHIP_KERNEL_REGISTER_STAGED, s[0], s[1]);
   if (dma) {
-    const int dshapes[3][2] = {{128, 128}, {192, 192}, {128, 256}};
+    const int dshapes[4][2] = {{128, 128}, {192, 192}, {128, 256}, {256, 256}};
     for (auto& s : dshapes) add(AFHIP_KERNEL_LDS_DMA, s[0], s[1]);
   }
   if (stream) add(AFHIP_KERNEL_STREAM, 64, 512);

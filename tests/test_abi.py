@@ -104,10 +104,14 @@ def test_variant_selection_without_device():
     assert (v.kernel, v.tile_rows, v.tile_columns) == ("lds_dma", 192, 192)
     v = gemm.select_variant(81, 256, 132, precision="f16", a_dtype="f16", w_dtype="f16")
     assert (v.kernel, v.tile_rows, v.tile_columns) == ("lds_dma", 128, 128)
-    # Long K on large outputs (the L = 1024 contraction) takes 128 x 256; the
-    # outer-product-mean contraction (8192 x 512 x 8192) 192 x 192 with its
-    # 0.8% ragged edge; its narrow output GEMM stays on 128 x 128.
+    # Long K on large outputs (the L = 1024 contraction) takes 256 x 256, the
+    # L = 512 one 128 x 256; the outer-product-mean contraction
+    # (8192 x 512 x 8192) 192 x 192 with its 0.8% ragged edge; its narrow
+    # output GEMM stays on 128 x 128.
     v = gemm.select_variant(1024, 1024, 1024, precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f16",
+                            batch=128)
+    assert (v.kernel, v.tile_rows, v.tile_columns) == ("lds_dma", 256, 256)
+    v = gemm.select_variant(512, 512, 512, precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f16",
                             batch=128)
     assert (v.kernel, v.tile_rows, v.tile_columns) == ("lds_dma", 128, 256)
     v = gemm.select_variant(8192, 512, 8192, precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f16")

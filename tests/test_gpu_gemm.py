@@ -90,7 +90,7 @@ def test_every_tile_variant_agrees(dev):
         assert rel_max(out.cpu().numpy(), expect) <= 1e-5, (tr, tc)
 
 
-LDS_DMA_TILES = [(128, 128), (192, 192), (128, 256)]
+LDS_DMA_TILES = [(128, 128), (192, 192), (128, 256), (256, 256)]
 
 
 def _batched_f16_plan(gemm, B, M, N, K, out_dtype, lda=0):
@@ -201,6 +201,31 @@ def test_config3_contraction_full_size(dev):
     plan = _batched_f16_plan(gemm, C, L, L, L, "f16")
     assert plan.variant().kernel == "lds_dma"
     out = plan.run(a, b).float()
+    expect = torch.bmm(a.float(), b.float().transpose(1, 2).contiguous())
+    err = (out - expect).abs().max().item() / expect.abs().max().item()
+    assert err <= 2e-3, err
+
+
+@pytest.mark.parametrize("tile", [(128, 256), (256, 256)])
+def test_config5_contraction_full_size(dev, tile):
+    # BASELINE config 5's contraction (128 channels of 1024 x 1024 x 1024)
+    # on the tiles chosen for long K, against torch's f32 batched product of
+    # the same f16 values.
+    import torch
+
+    from afhip import gemm
+
+    C, L = 128, 1024
+    g = torch.Generator(device="cpu").manual_seed(0xAF2005)
+    a = torch.randn(C, L, L, generator=g).half().to(dev)
+    b = torch.randn(C, L, L, generator=g).half().to(dev)
+    gemm.force_variant(gemm.GemmVariant("f16", tile[0], tile[1], source="pinned", kernel="lds_dma"))
+    try:
+        plan = _batched_f16_plan(gemm, C, L, L, L, "f16")
+        assert plan.variant().kernel == "lds_dma"
+        out = plan.run(a, b).float()
+    finally:
+        gemm.force_variant(None)
     expect = torch.bmm(a.float(), b.float().transpose(1, 2).contiguous())
     err = (out - expect).abs().max().item() / expect.abs().max().item()
     assert err <= 2e-3, err
