@@ -20,7 +20,9 @@
 // Loads: waves 0-3 bring x tiles into a ring of three LDS stages by DMA (and
 // issue no other vector-memory instruction, so their vmcnt waits are exact);
 // waves 4-7 write the finished tile of the previous iteration from one of two
-// staging buffers, with the residual read-modify-write there.
+// staging buffers, with the residual read-modify-write there. A tile's
+// LayerNorm runs during the previous tile's second linear, three barriers a
+// tile.
 #include <algorithm>
 
 #include "dma.h"
@@ -157,62 +159,78 @@ __global__ __launch_bounds__(kThreads, 1) void transition_fused_kernel(FusedTran
   half_t* const hid = reinterpret_cast<half_t*>(smem + Lay::HID);
   float* const part = reinterpret_cast<float*>(smem + Lay::PART);
 
+  // LayerNorm of the tile in stage slot `slot` into x_hat: two-pass mean and
+  // biased variance in f32, eps inside the root (transition.ts:179-234).
+  auto layer_norm = [&](int slot) {
+    const unsigned char* st = smem + slot * Lay::STAGE + lrow * Lay::XROW;
+    float x[8];
+    if constexpr (sizeof(IT) == 2) {
+      const half8 h = *reinterpret_cast<const half8*>(st + 16 * lpart);
+#pragma unroll
+      for (int e = 0; e < 8; e++) x[e] = (float)h[e];
+    } else {
+      const floatx4 f0 = reinterpret_cast<const floatx4*>(st + 32 * lpart)[0];
+      const floatx4 f1 = reinterpret_cast<const floatx4*>(st + 32 * lpart)[1];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        x[e] = f0[e];
+        x[e + 4] = f1[e];
+      }
+    }
+    float s1 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) s1 += x[e];
+    const float mean = row_sum16(s1) / (float)kC;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float d = x[e] - mean;
+      s2 += d * d;
+    }
+    const float rstd = fast_rsqrt(row_sum16(s2) / (float)kC + a.eps);
+    half8 h;
+#pragma unroll
+    for (int e = 0; e < 8; e++) h[e] = (half_t)((x[e] - mean) * rstd * sc[e] + of[e]);
+    *reinterpret_cast<half8*>(xhat + lrow * kXPitch + 8 * lpart) = h;
+  };
+
   if (t0 >= ntiles) return;
+  // Tile i of this workgroup (tile t0 + i G) goes to stage slot i % 3. Slots
+  // for tiles 0, 1, 2 are issued here; tile i + 3 is issued once tile i has
+  // been normalised.
   if (wave < kLoaders) {
 #pragma unroll
-    for (int s = 0; s < S - 1; s++)
+    for (int s = 0; s < S; s++)
       if (t0 + s * G < ntiles) issue(t0 + s * G, s);
+    // Tile 0 has landed once at most tiles 1 and 2 are outstanding.
+    if (t0 + 2 * G < ntiles) wait_vmcnt<2 * LPW>();
+    else if (t0 + G < ntiles) wait_vmcnt<LPW>();
+    else wait_vmcnt<0>();
   }
+  block_barrier();
+  layer_norm(0);
 
+  // Per tile i, three barriers:
+  //   A: x_hat(i) is complete, tile i + 1 has landed, staging(i - 1) is complete
+  //      -> loaders refill tile i's slot with tile i + 3, storers write tile
+  //         i - 1, everyone runs the first linear
+  //   B: hidden(i) is complete and x_hat is free
+  //      -> the second linear, with tile i + 1's LayerNorm in the same
+  //         straight-line block so its vector work issues under the MFMAs
+  //   C: the partial sums are complete -> waves 0-3 finish the tile into staging
   int it = 0, tile = t0;
   for (; tile < ntiles; it++, tile += G) {
     if (wave < kLoaders) {
-      // Tile it has landed once at most tile it + 1's loads are outstanding.
-      if (tile + G < ntiles) wait_vmcnt<LPW>();
+      // Tile it + 1 has landed once at most tile it + 2's loads are outstanding.
+      if (tile + 2 * G < ntiles) wait_vmcnt<LPW>();
       else wait_vmcnt<0>();
     }
-    block_barrier();  // B1: tile it landed; the previous tile's staging is complete
+    block_barrier();  // A
     if (wave < kLoaders) {
-      if (tile + 2 * G < ntiles) issue(tile + 2 * G, (it + 2) % S);
+      if (tile + 3 * G < ntiles) issue(tile + 3 * G, it % S);
     } else if (it > 0) {
       store_tile((it + 1) & 1, tile - G);
     }
-
-    // LayerNorm of the tile into x_hat: two-pass mean and biased variance in
-    // f32, eps inside the root (transition.ts:179-234).
-    {
-      const unsigned char* st = smem + (it % S) * Lay::STAGE + lrow * Lay::XROW;
-      float x[8];
-      if constexpr (sizeof(IT) == 2) {
-        const half8 h = *reinterpret_cast<const half8*>(st + 16 * lpart);
-#pragma unroll
-        for (int e = 0; e < 8; e++) x[e] = (float)h[e];
-      } else {
-        const floatx4 f0 = reinterpret_cast<const floatx4*>(st + 32 * lpart)[0];
-        const floatx4 f1 = reinterpret_cast<const floatx4*>(st + 32 * lpart)[1];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          x[e] = f0[e];
-          x[e + 4] = f1[e];
-        }
-      }
-      float s1 = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) s1 += x[e];
-      const float mean = row_sum16(s1) / (float)kC;
-      float s2 = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const float d = x[e] - mean;
-        s2 += d * d;
-      }
-      const float rstd = fast_rsqrt(row_sum16(s2) / (float)kC + a.eps);
-      half8 h;
-#pragma unroll
-      for (int e = 0; e < 8; e++) h[e] = (half_t)((x[e] - mean) * rstd * sc[e] + of[e]);
-      *reinterpret_cast<half8*>(xhat + lrow * kXPitch + 8 * lpart) = h;
-    }
-    block_barrier();  // B2: x_hat complete
 
     // First linear: hidden units 64 wave .. + 63 of the 32 rows.
     {
@@ -235,23 +253,25 @@ __global__ __launch_bounds__(kThreads, 1) void transition_fused_kernel(FusedTran
           *reinterpret_cast<half4*>(hid + col * kHPitch + 64 * wave + 32 * cb + 8 * g4 + 4 * hi) = h;
         }
     }
-    block_barrier();  // B3: hidden complete
+    block_barrier();  // B
 
-    // Second linear: outputs 32 cb2 .. + 31 over hidden half kh.
+    // Second linear: outputs 32 cb2 .. + 31 over hidden half kh; then the
+    // next tile's LayerNorm (past the last tile it normalises a stale slot,
+    // whose x_hat nothing reads).
     floatx16 acc2 = {};
 #pragma unroll
     for (int s = 0; s < 16; s++) {
       const half8 hf = *reinterpret_cast<const half8*>(hid + col * kHPitch + 256 * kh + 16 * s + 8 * hi);
       acc2 = mfma_f16(w2f[s], hf, acc2);
     }
-    if (kh == 0) {
-      acc2 = mfma_f16(w2f[16], ones, acc2);
-    } else {
+    acc2 = mfma_f16(w2f[16], ones, acc2);  // the bias; its fragment is zero on the waves of half 1
+    layer_norm((it + 1) % S);
+    if (kh != 0) {
       floatx4* pp = reinterpret_cast<floatx4*>(part + (cb2 * 64 + lane) * 16);
 #pragma unroll
       for (int q = 0; q < 4; q++) pp[q] = floatx4{acc2[4 * q], acc2[4 * q + 1], acc2[4 * q + 2], acc2[4 * q + 3]};
     }
-    block_barrier();  // B4: partial sums complete
+    block_barrier();  // C
     if (kh == 0) {
       const floatx4* pp = reinterpret_cast<const floatx4*>(part + (cb2 * 64 + lane) * 16);
       unsigned char* ob = smem + Lay::OUTB + (it & 1) * kRows * Lay::OPITCH + col * Lay::OPITCH;
