@@ -129,6 +129,7 @@ SIGNATURES = {
     "afhip_pack_weight": [_vp, _i32, _i32, _i32, _vp, _i32, _vp],
     "afhip_dequant_q8_channel": [_vp, _vp, _i32, _i32, _vp, _vp],
     "afhip_dequant_q8_block": [_vp, _vp, _i32, _i64, _i64, _vp, _vp],
+    "afhip_pack_weight_q8_block": [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp],
     "afhip_triangle_weights_size": [ctypes.POINTER(TriangleDesc), _szp],
     "afhip_triangle_workspace_size": [ctypes.POINTER(TriangleDesc), _szp],
     "afhip_triangle_prepare_weights": [ctypes.POINTER(TriangleDesc), _vp, _vp, _vp],

@@ -254,6 +254,30 @@ def dequant_q8_channel(q, scale):
     return out
 
 
+def pack_weight_q8_block(codes, scales_f16_bits, rows_k: int, columns_n: int, *, block: int = 64, start: int = 0,
+                         dtype: str = "f16"):
+    """The bundle's mixed-q8 weight [rows_k][columns_n] (flat from element
+    `start` of `codes`) decoded on the device straight into the packed GEMM
+    operand W[n][k] of `dtype` (readTensorRange's int8 branch,
+    src/reference/dtype.ts:66-99, without the f32 copy). Use it with a plan of
+    w_dtype `dtype` and w_layout "k"."""
+    import torch
+
+    if rows_k <= 0 or columns_n <= 0:
+        raise _lib.RangeError("weight dimensions must be positive")
+    if block <= 0:
+        raise _lib.RangeError("int8 tensor has an invalid block size")
+    if start < 0 or start + rows_k * columns_n > codes.numel():
+        raise _lib.RangeError("tensor range is out of bounds")
+    if (start + rows_k * columns_n - 1) // block >= scales_f16_bits.numel():
+        raise _lib.RangeError("int8 tensor has too few scales")
+    out = torch.empty((columns_n, rows_k), dtype=torch.float16 if dtype == "f16" else torch.float32,
+                      device=device())
+    _lib.call("afhip_pack_weight_q8_block", ptr(codes), ptr(scales_f16_bits), block, start, rows_k, columns_n,
+              ptr(out), _lib.F16 if dtype == "f16" else _lib.F32, stream_handle())
+    return out
+
+
 def dequant_q8_block(codes, scales_f16_bits, block: int = 64, start: int = 0, count: int | None = None):
     """readTensorRange's int8 branch (src/reference/dtype.ts:66-99) on the device."""
     import torch

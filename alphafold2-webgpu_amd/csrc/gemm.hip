@@ -167,6 +167,37 @@ __global__ void dequant_block_kernel(const int8_t* __restrict__ codes, const uin
   out[i] = __fmul_rn((float)codes[absolute], s);
 }
 
+// W[n][k] (k-contiguous, the GEMM's packed operand) from the reference
+// bundle's mixed-q8 tensor [K][N], stored flat from element `start` of the
+// bundle's int8 stream: w = f32(code[e]) * f32(scale_f16[e / block]),
+// e = start + k N + n (src/reference/dtype.ts:66-99), one correctly rounded
+// product as the host decode computes it, then converted to TD (round to
+// nearest even for f16). A 32 x 32 tile passes through LDS so that both the
+// code reads (along n) and the stores (along k) are contiguous.
+template <typename TD>
+__global__ void pack_q8_block_kernel(const int8_t* __restrict__ codes, const uint16_t* __restrict__ scales, int block,
+                                     int64_t start, int K, int N, TD* __restrict__ dst) {
+  __shared__ float tile[32][33];
+  const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int r = ty; r < 32; r += 8) {
+    const int k = k0 + r, n = n0 + tx;
+    float v = 0.0f;
+    if (k < K && n < N) {
+      const int64_t e = start + (int64_t)k * N + n;
+      __half_raw raw;
+      raw.x = scales[e / block];
+      v = __fmul_rn((float)codes[e], __half2float(__half(raw)));
+    }
+    tile[r][tx] = v;
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int n = n0 + r, k = k0 + tx;
+    if (n < N && k < K) dst[(int64_t)n * K + k] = (TD)tile[tx][r];
+  }
+}
+
 template <typename TS>
 int pack_dispatch(const TS* src, int K, int N, int64_t ld_src, void* dst, int dst_dtype, int64_t ld_dst,
                   hipStream_t s) {
@@ -470,6 +501,23 @@ int afhip_dequant_q8_block(const int8_t* codes, const uint16_t* scales_f16, int3
   if (count == 0) return AFHIP_OK;
   return launch("dequant_q8_block", dequant_block_kernel, dim3((unsigned)ceil_div(count, 256)), dim3(256), 0,
                 (hipStream_t)stream, codes, scales_f16, block, start, count, out);
+}
+
+int afhip_pack_weight_q8_block(const int8_t* codes, const uint16_t* scales_f16, int32_t block, int64_t start,
+                               int32_t rows_k, int32_t columns_n, void* dst, int32_t dst_dtype, void* stream) {
+  if (int s = require_open()) return s;
+  AFHIP_REQUIRE(codes && scales_f16 && dst, "NULL argument");
+  AFHIP_REQUIRE(block > 0, "int8 tensor has an invalid block size");
+  AFHIP_REQUIRE(start >= 0, "tensor range is out of bounds");
+  AFHIP_REQUIRE(rows_k > 0 && columns_n > 0, "weight dimensions must be positive");
+  AFHIP_REQUIRE(rows_k <= 65535 * 32, "weight has too many rows");
+  AFHIP_REQUIRE(dst_dtype == AFHIP_F32 || dst_dtype == AFHIP_F16, "packed q8 weights decode to f32 or f16");
+  const dim3 grid((unsigned)ceil_div(columns_n, 32), (unsigned)ceil_div(rows_k, 32));
+  if (dst_dtype == AFHIP_F32)
+    return launch("pack_q8_block", pack_q8_block_kernel<float>, grid, dim3(256), 0, (hipStream_t)stream, codes,
+                  scales_f16, block, start, rows_k, columns_n, (float*)dst);
+  return launch("pack_q8_block", pack_q8_block_kernel<half_t>, grid, dim3(256), 0, (hipStream_t)stream, codes,
+                scales_f16, block, start, rows_k, columns_n, (half_t*)dst);
 }
 
 }  // extern "C"

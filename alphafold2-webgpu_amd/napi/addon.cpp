@@ -18,6 +18,7 @@
 #include <node_api.h>
 
 #include <chrono>
+#include <climits>
 #include <cstdint>
 #include <cstring>
 #include <map>
@@ -522,6 +523,47 @@ napi_value GemmRun(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+// packWeightQ8Block(codes, scales, block, start, rowsK, columnsN, dst, dtype)
+// with buffer handles: the bundle's int8 codes and f16 scale bits in, the
+// packed GEMM operand W[n][k] of dtype (DTYPE.f32 or DTYPE.f16) out
+// (afhip_pack_weight_q8_block). The buffers' sizes bound every access.
+napi_value PackWeightQ8Block(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 8)) return nullptr;
+  void *codes, *scales, *dst;
+  size_t codes_bytes, scales_bytes, dst_bytes;
+  int64_t block, start, rows_k, columns_n, dtype;
+  if (!lookup_buffer(env, a.argv[0], &codes, &codes_bytes) || !lookup_buffer(env, a.argv[1], &scales, &scales_bytes) ||
+      !get_int64(env, a.argv[2], &block) || !get_int64(env, a.argv[3], &start) || !get_int64(env, a.argv[4], &rows_k) ||
+      !get_int64(env, a.argv[5], &columns_n) || !lookup_buffer(env, a.argv[6], &dst, &dst_bytes) ||
+      !get_int64(env, a.argv[7], &dtype))
+    return nullptr;
+  if (block <= 0 || start < 0 || rows_k <= 0 || columns_n <= 0 || rows_k > INT32_MAX || columns_n > INT32_MAX ||
+      (dtype != AFHIP_F32 && dtype != AFHIP_F16)) {
+    throw_js(env, {true, "packWeightQ8Block: invalid block, range, shape or dtype"});
+    return nullptr;
+  }
+  const int64_t count = rows_k * columns_n;
+  if (start + count > (int64_t)codes_bytes) {
+    throw_js(env, {true, "packWeightQ8Block: tensor range is out of bounds"});
+    return nullptr;
+  }
+  if ((start + count - 1) / block >= (int64_t)(scales_bytes / 2)) {
+    throw_js(env, {true, "packWeightQ8Block: int8 tensor has too few scales"});
+    return nullptr;
+  }
+  if (count * (dtype == AFHIP_F16 ? 2 : 4) > (int64_t)dst_bytes) {
+    throw_js(env, {true, "packWeightQ8Block: destination buffer is too small"});
+    return nullptr;
+  }
+  if (!check(env,
+             afhip_pack_weight_q8_block((const int8_t*)codes, (const uint16_t*)scales, (int32_t)block, start,
+                                        (int32_t)rows_k, (int32_t)columns_n, dst, (int32_t)dtype, nullptr),
+             "packWeightQ8Block"))
+    return nullptr;
+  return nullptr;
+}
+
 // ---------------------------------------------------------------------------
 // Operators with host arrays (upload, prepare, run, read back)
 // ---------------------------------------------------------------------------
@@ -740,7 +782,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"bufferRead", BufferRead}, {"synchronize", Synchronize}, {"gemmGrid", GemmGrid}, {"gemmSelect", GemmSelect},
       {"gemmCalibrate", GemmCalibrate}, {"gemmForceVariant", GemmForceVariant}, {"calibrationLoad", CalibrationLoad},
       {"calibrationSave", CalibrationSave}, {"gemmPlanCreate", GemmPlanCreate}, {"gemmPlanDestroy", GemmPlanDestroy},
-      {"gemmWorkspaceSize", GemmWorkspaceSize}, {"gemmRun", GemmRun}, {"triangleRun", TriangleRun},
+      {"gemmWorkspaceSize", GemmWorkspaceSize}, {"gemmRun", GemmRun}, {"packWeightQ8Block", PackWeightQ8Block}, {"triangleRun", TriangleRun},
       {"opmRun", OpmRun}, {"transitionRun", TransitionRun}, {"timingEnable", TimingEnable},
       {"timingReset", TimingReset}, {"timingReport", TimingReport},
   };

@@ -139,6 +139,12 @@ export declare function calibrateGemmVariant(desc: GemmDesc): GemmVariant;
 export declare function forceGemmVariant(variant?: Partial<GemmVariant> | null): void;
 export declare function calibrationLoad(file: string): void;
 export declare function calibrationSave(file: string): void;
+/** Decodes the bundle's mixed-q8 weight [rowsK][columnsN] (int8 codes and f16
+ * scale bits in device buffers, flat blocks of `block`, from element `start`)
+ * into the packed GEMM operand W[n][k] of `dtype` in buffer `dst`
+ * (readTensorRange's int8 branch, src/reference/dtype.ts:66-99, on the device). */
+export declare function packWeightQ8Block(codes: number, scales: number, block: number, start: number, rowsK: number,
+                                          columnsN: number, dst: number, dtype: 0 | 1): void;
 export declare function validateTriangleInput(input: TriangleMultiplicationInput): void;
 export declare function packTriangleWeights(weights: TriangleMultiplicationWeights): Float32Array;
 export declare function errorMetrics(

@@ -220,6 +220,11 @@ module.exports = {
   forceGemmVariant: function (variant) { addon().gemmForceVariant(variant === undefined ? null : variant); },
   calibrationLoad: function (file) { addon().calibrationLoad(file); },
   calibrationSave: function (file) { addon().calibrationSave(file); },
+  // The bundle's mixed-q8 weight (int8 codes and f16 scale bits, in device
+  // buffers) decoded straight into a packed GEMM operand buffer.
+  packWeightQ8Block: function (codes, scales, block, start, rowsK, columnsN, dst, dtype) {
+    addon().packWeightQ8Block(codes, scales, block, start, rowsK, columnsN, dst, dtype);
+  },
   TRIANGLE_ORDER: TRIANGLE_ORDER,
   DTYPE: { f32: F32, f16: F16, i8: I8 },
   PRECISION: PRECISION,

@@ -224,6 +224,19 @@ AFHIP_API int afhip_dequant_q8_channel(const int8_t* q, const float* scale, int3
  * branch of readTensorRange (src/reference/dtype.ts:66-99). */
 AFHIP_API int afhip_dequant_q8_block(const int8_t* codes, const uint16_t* scales_f16, int32_t block, int64_t start,
                            int64_t count, float* out, void* stream);
+/* The same bundle format straight into a GEMM operand, with no f32 copy of
+ * the weight: the tensor [rows_k][columns_n] ([in][out], as the bundle stores
+ * it) starting at element `start` is decoded as above (bit-exact) and
+ * written packed k-contiguous, W[n][k], in F32 or F16 (round to nearest
+ * even), ready for a plan with w_layout AFHIP_WEIGHT_K_CONTIGUOUS and w_dtype
+ * dst_dtype.
+ * Block scales vary with k as well as n (scale index (start + k N + n) /
+ * block), so they are applied here, not in the GEMM epilogue. Replaces
+ * readTensorRange's int8 branch (src/reference/dtype.ts:66-99) followed by
+ * the host upload and packing of the decoded f32 weight. */
+AFHIP_API int afhip_pack_weight_q8_block(const int8_t* codes, const uint16_t* scales_f16, int32_t block,
+                                         int64_t start, int32_t rows_k, int32_t columns_n, void* dst,
+                                         int32_t dst_dtype, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Triangle multiplication                                                 */

@@ -8,7 +8,7 @@ var native = afhip.addon();
 var expected = ["open", "close", "abiVersion", "deviceReport", "bufferCreate", "bufferDestroy", "bufferWrite",
   "bufferRead", "synchronize", "gemmGrid", "gemmSelect", "gemmCalibrate", "gemmForceVariant", "calibrationLoad",
   "calibrationSave", "gemmPlanCreate", "gemmPlanDestroy", "gemmWorkspaceSize", "gemmRun", "triangleRun", "opmRun",
-  "transitionRun", "timingEnable", "timingReset", "timingReport"];
+  "transitionRun", "timingEnable", "timingReset", "timingReport", "packWeightQ8Block"];
 expected.forEach(function (n) { assert.strictEqual(typeof native[n], "function", n); });
 assert.strictEqual(native.abiVersion(), 1);
 
@@ -28,6 +28,10 @@ assert.strictEqual(v.tileRows, 192);
 var bad = { shape: [2, 3, 4], z: new Float32Array(5), mask: new Float32Array(4), weights: {} };
 assert.throws(function () { new afhip.TriangleMultiplicationOutgoingGpu().run(bad); }, /z has 5 values/);
 assert.throws(function () { afhip.validateTriangleInput({ shape: [0, 3, 4] }); }, RangeError);
+
+// packWeightQ8Block checks its handles before any device work.
+assert.throws(function () { afhip.packWeightQ8Block(999999, 999998, 64, 0, 4, 4, 999997, afhip.DTYPE.f16); },
+  /unknown buffer handle/);
 
 // errorMetrics (test/cpu-reference.test.ts:36-42).
 var m = afhip.errorMetrics(new Float32Array([1, 3]), new Float32Array([2, 1]));

@@ -67,4 +67,57 @@ function transposePairs(data, L, C) {
   report.cases.push({ opmClosedFormMaxRelative: worst });
 })();
 
+// The bundle's mixed-q8 weight through device buffers, as a TypeScript host
+// holding the bundle would run it: packWeightQ8Block decodes it straight into
+// the packed operand W[n][k] (bit-exact against the decode of
+// src/reference/dtype.ts:66-99, value = code * f32(scale)), and an f32 plan
+// on that operand matches a double-precision product.
+(function () {
+  var native = afhip.addon();
+  var K = 96, N = 80, M = 40, block = 64, start = 37;
+  var total = start + K * N + 11;
+  var codes = new Int8Array(total), scales = new Uint16Array(Math.ceil(total / block));
+  for (var i = 0; i < total; i++) codes[i] = ((i * 37) % 255) - 127;
+  for (var j = 0; j < scales.length; j++) scales[j] = 0x2000 + (j * 97) % 0x1000;
+  function halfToNumber(bits) {
+    var e = (bits >> 10) & 31, m = bits & 1023, s = bits & 0x8000 ? -1 : 1;
+    if (e === 0) return s * m * Math.pow(2, -24);
+    if (e === 31) return m ? NaN : s * Infinity;
+    return s * (1 + m / 1024) * Math.pow(2, e - 15);
+  }
+  var x = new Float32Array(M * K);
+  for (var t = 0; t < x.length; t++) x[t] = Math.sin(t * 0.37);
+  var bc = native.bufferCreate(total), bs = native.bufferCreate(scales.length * 2);
+  var bw = native.bufferCreate(K * N * 4), ba = native.bufferCreate(M * K * 4), bo = native.bufferCreate(M * N * 4);
+  native.bufferWrite(bc, 0, codes);
+  native.bufferWrite(bs, 0, scales);
+  native.bufferWrite(ba, 0, x);
+  afhip.packWeightQ8Block(bc, bs, block, start, K, N, bw, afhip.DTYPE.f32);
+  var packed = new Float32Array(K * N);
+  native.bufferRead(bw, 0, packed);
+  var differing = 0;
+  for (var k = 0; k < K; k++) for (var n = 0; n < N; n++) {
+    var e = start + k * N + n;
+    if (packed[n * K + k] !== Math.fround(codes[e] * halfToNumber(scales[Math.floor(e / block)]))) differing++;
+  }
+  assert.strictEqual(differing, 0, "packed q8 weight differs from the decode");
+  var plan = native.gemmPlanCreate({ rows: M, inner: K, columns: N, precision: afhip.PRECISION.f32,
+    aDtype: afhip.DTYPE.f32, wDtype: afhip.DTYPE.f32, wLayout: 1, outDtype: afhip.DTYPE.f32 });
+  native.gemmRun(plan, { a: ba, w: bw, c: bo });
+  native.synchronize();
+  var out = new Float32Array(M * N);
+  native.bufferRead(bo, 0, out);
+  var worst = 0, largest = 0;
+  for (var r = 0; r < M; r++) for (var c = 0; c < N; c++) {
+    var acc = 0;
+    for (var kk = 0; kk < K; kk++) acc += x[r * K + kk] * packed[c * K + kk];
+    worst = Math.max(worst, Math.abs(out[r * N + c] - acc));
+    largest = Math.max(largest, Math.abs(acc));
+  }
+  native.gemmPlanDestroy(plan);
+  [bc, bs, bw, ba, bo].forEach(function (b) { native.bufferDestroy(b); });
+  assert.ok(worst <= 1e-5 * largest, "q8 gemm " + worst / largest);
+  report.cases.push({ q8PackedGemmMaxRelative: worst / largest });
+})();
+
 console.log(JSON.stringify(report));

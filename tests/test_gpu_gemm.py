@@ -281,6 +281,45 @@ def test_q8_block_dequant_known_answer_and_bit_exact(dev):
     assert np.array_equal(got.view(np.uint32), ref.q8_block_decode(c, s, 64, 100, 3000).view(np.uint32))
 
 
+@pytest.mark.parametrize("K,N,start,dtype", [(256, 1024, 0, "f16"), (130, 96, 100, "f32"), (37, 200, 64, "f16")])
+def test_q8_bundle_packs_straight_into_gemm_operand(dev, K, N, start, dtype):
+    # A mixed-q8 bundle tensor [in][out] inside a longer int8 stream, with
+    # block-64 f16 scales that vary with k as well as n (quantize-web-model.ts:
+    # 98-119): the device decode into the packed operand W[n][k] equals the
+    # host decode (dtype.ts:66-99) bit for bit (then rounded to nearest even
+    # for f16), and a plan on that operand matches the f64 product over the
+    # host-decoded weight.
+    from afhip import gemm
+
+    total = start + K * N + 50
+    codes, scales = ref.q8_block_encode(ref.normal(0xAF2011 + K, (total,), 0.02), 64)
+    decoded = ref.q8_block_decode(codes, scales, 64, start, K * N).reshape(K, N)
+    expect_w = np.ascontiguousarray(decoded.T)
+    if dtype == "f16":
+        expect_w = ref.round_f16(expect_w)
+    packed = gemm.pack_weight_q8_block(to_dev(codes, dev), to_dev(scales.view(np.int16), dev), K, N, start=start,
+                                       dtype=dtype)
+    got = packed.float().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), expect_w.astype(np.float32).view(np.uint32))
+    x = ref.normal(0xAF2012 + N, (300, K))
+    x = x if dtype == "f32" else ref.round_f16(x)
+    plan = gemm.TiledGemm(300, K, N, precision=dtype, a_dtype=dtype, w_dtype=dtype, w_layout="k", out_dtype="f32")
+    xd = to_dev(x, dev) if dtype == "f32" else to_dev(x, dev).half()
+    out = plan.run(xd, packed).cpu().numpy()
+    assert rel_max(out, ref.gemm_f64(x, decoded)) <= (1e-5 if dtype == "f32" else 1e-2)
+
+
+def test_q8_bundle_pack_rejects_bad_ranges(dev):
+    from afhip import _lib, gemm
+
+    codes, scales = ref.q8_block_encode(ref.normal(7, (1000,), 0.02), 64)
+    c, s = to_dev(codes, dev), to_dev(scales.view(np.int16), dev)
+    with pytest.raises(_lib.RangeError, match="out of bounds"):
+        gemm.pack_weight_q8_block(c, s, 40, 30, start=1)
+    with pytest.raises(_lib.RangeError, match="invalid block size"):
+        gemm.pack_weight_q8_block(c, s, 10, 10, block=0)
+
+
 def _config2_inputs(rows):
     seed = 0xAF2001
     x = ref.round_f16(ref.normal(seed, (rows, 256)))
