@@ -98,6 +98,16 @@ class TransitionDesc(ctypes.Structure):
     ]
 
 
+class PairStackDesc(ctypes.Structure):
+    _fields_ = [("opm", OpmDesc), ("outgoing", TriangleDesc), ("incoming", TriangleDesc),
+                ("transition", TransitionDesc)]
+
+
+class PairStackWeights(ctypes.Structure):
+    _fields_ = [("opm", ctypes.c_void_p), ("outgoing", ctypes.c_void_p), ("incoming", ctypes.c_void_p),
+                ("transition", ctypes.c_void_p)]
+
+
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
 _i32 = ctypes.c_int32
@@ -142,6 +152,20 @@ SIGNATURES = {
     "afhip_transition_workspace_size": [ctypes.POINTER(TransitionDesc), _szp],
     "afhip_transition_prepare_weights": [ctypes.POINTER(TransitionDesc), _vp, _vp, _vp],
     "afhip_transition_run": [ctypes.POINTER(TransitionDesc), _vp, _vp, _vp, _vp, _sz, _vp],
+    "afhip_set_memory_budget": [ctypes.c_uint64],
+    "afhip_memory_resident": [ctypes.POINTER(ctypes.c_uint64)],
+    "afhip_execution_create": [ctypes.c_uint64, _vp, ctypes.POINTER(_vp)],
+    "afhip_execution_destroy": [_vp],
+    "afhip_execution_allocate": [_vp, ctypes.c_char_p, ctypes.c_uint64, ctypes.POINTER(_vp)],
+    "afhip_execution_upload": [_vp, ctypes.c_char_p, _vp, ctypes.c_uint64, ctypes.POINTER(_vp)],
+    "afhip_execution_release": [_vp, _vp],
+    "afhip_execution_checkpoint": [_vp, ctypes.POINTER(ctypes.c_uint64)],
+    "afhip_execution_release_since": [_vp, ctypes.c_uint64],
+    "afhip_execution_note_submitted": [_vp],
+    "afhip_execution_snapshot": [_vp, ctypes.c_char_p, _sz],
+    "afhip_execution_add_in_place": [_vp, _vp, _i32, _vp, _i32, _i64],
+    "afhip_execution_pair_stack": [_vp, ctypes.POINTER(PairStackDesc), ctypes.POINTER(PairStackWeights), _vp, _vp,
+                                   _vp, _vp],
     "afhip_timing_enable": [ctypes.c_int],
     "afhip_timing_reset": [],
     "afhip_timing_report": [ctypes.c_char_p, _sz],

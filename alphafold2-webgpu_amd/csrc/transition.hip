@@ -235,7 +235,8 @@ int afhip_transition_weights_size(const afhip_transition_desc* desc, size_t* byt
 int afhip_transition_workspace_size(const afhip_transition_desc* desc, size_t* bytes) {
   if (int s = validate(desc)) return s;
   AFHIP_REQUIRE(bytes != nullptr, "output is NULL");
-  *bytes = workspace(*desc).total;
+  // The fused kernel keeps the normalised rows and the hidden activation on chip.
+  *bytes = transition_fused_shape(*desc) ? 0 : workspace(*desc).total;
   return AFHIP_OK;
 }
 
@@ -265,14 +266,10 @@ int afhip_transition_run(const afhip_transition_desc* desc, const void* activati
   const auto& d = *desc;
   const TransitionWeights w = layout(d);
   const TransitionWorkspace ws = workspace(d);
-  AFHIP_REQUIRE(workspace_ptr != nullptr && workspace_bytes >= ws.total, "workspace of %zu bytes is smaller than %zu",
-                workspace_bytes, ws.total);
   hipStream_t st = (hipStream_t)stream;
   const bool f16 = d.precision == AFHIP_PRECISION_F16;
   const int ct = f16 ? AFHIP_F16 : AFHIP_F32;
   const char* wb = (const char*)prepared;
-  char* normalized = (char*)workspace_ptr + ws.normalized;
-  char* hidden = (char*)workspace_ptr + ws.hidden;
   if (transition_fused_eligible(d, activations, out)) {
     FusedTransitionArgs f{};
     f.x = activations;
@@ -288,6 +285,12 @@ int afhip_transition_run(const afhip_transition_desc* desc, const void* activati
     f.b2 = (const float*)(wb + w.b2);
     return launch_transition_fused(f, d.in_dtype, d.out_dtype, st);
   }
+  AFHIP_REQUIRE(!transition_fused_shape(d) || workspace_bytes >= ws.total,
+                "this transition shape runs fused and needs activations and output 16-byte aligned");
+  AFHIP_REQUIRE(workspace_ptr != nullptr && workspace_bytes >= ws.total, "workspace of %zu bytes is smaller than %zu",
+                workspace_bytes, ws.total);
+  char* normalized = (char*)workspace_ptr + ws.normalized;
+  char* hidden = (char*)workspace_ptr + ws.hidden;
   const size_t ie = dtype_size(d.in_dtype), oe = dtype_size(d.out_dtype);
   for (int64_t r0 = 0; r0 < d.rows; r0 += ws.chunk) {
     const int64_t rows = std::min<int64_t>(ws.chunk, d.rows - r0);

@@ -20,6 +20,9 @@ struct FusedTransitionArgs {
   const float* b2;     // [128]
 };
 
+// The shape the fused kernel covers (it needs no workspace), and whether a
+// call of that shape can take it (x and out 16-byte aligned).
+bool transition_fused_shape(const afhip_transition_desc& d);
 bool transition_fused_eligible(const afhip_transition_desc& d, const void* x, const void* out);
 int launch_transition_fused(const FusedTransitionArgs& a, int in_dtype, int out_dtype, hipStream_t s);
 

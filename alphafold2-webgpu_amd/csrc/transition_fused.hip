@@ -306,10 +306,14 @@ template <typename IT, typename OT> int launch_fused(const FusedTransitionArgs& 
 
 }  // namespace
 
-bool transition_fused_eligible(const afhip_transition_desc& d, const void* x, const void* out) {
+bool transition_fused_shape(const afhip_transition_desc& d) {
   return d.precision == AFHIP_PRECISION_F16 && d.channels == kC && d.hidden == kH &&
-         (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
          d.rows * (int64_t)kC * 4 < (int64_t)kOutOfRange;
+}
+
+bool transition_fused_eligible(const afhip_transition_desc& d, const void* x, const void* out) {
+  return transition_fused_shape(d) && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(out) & 15) == 0;
 }
 
 int launch_transition_fused(const FusedTransitionArgs& a, int in_dtype, int out_dtype, hipStream_t s) {

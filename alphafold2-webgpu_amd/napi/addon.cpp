@@ -190,10 +190,19 @@ napi_value make_number(napi_env env, double d) {
 // (native/wgpu-backend/src/device.rs:60-95) for HIP buffers and plans.
 // ---------------------------------------------------------------------------
 
+struct ExecutionEntry {
+  afhip_execution* ex = nullptr;
+  // (allocation index in the execution, buffer handle) of each tensor this
+  // addon handed out, so release_since can retire the handles it frees.
+  std::vector<std::pair<uint64_t, uint32_t>> handles;
+};
+
 struct Registry {
   uint32_t next = 1;
   std::map<uint32_t, std::pair<void*, size_t>> buffers;
   std::map<uint32_t, afhip_gemm_plan*> plans;
+  std::map<uint32_t, ExecutionEntry> executions;
+  std::map<uint32_t, uint32_t> owner;  // buffer handle -> execution handle, for pooled tensors
 };
 Registry g_reg;
 
@@ -225,10 +234,14 @@ napi_value Open(napi_env env, napi_callback_info info) {
 }
 
 napi_value Close(napi_env env, napi_callback_info) {
-  for (auto& kv : g_reg.buffers) afhip_buffer_destroy(kv.second.first);
+  for (auto& kv : g_reg.buffers)
+    if (!g_reg.owner.count(kv.first)) afhip_buffer_destroy(kv.second.first);
+  for (auto& kv : g_reg.executions) afhip_execution_destroy(kv.second.ex);
   for (auto& kv : g_reg.plans) afhip_gemm_plan_destroy(kv.second);
   g_reg.buffers.clear();
   g_reg.plans.clear();
+  g_reg.executions.clear();
+  g_reg.owner.clear();
   if (!check(env, afhip_close(), "close")) return nullptr;
   return nullptr;
 }
@@ -283,6 +296,10 @@ napi_value BufferDestroy(napi_env env, napi_callback_info info) {
   if (!get_int64(env, a.argv[0], &h)) return nullptr;
   auto it = g_reg.buffers.find((uint32_t)h);
   if (it == g_reg.buffers.end()) return nullptr;
+  if (g_reg.owner.count((uint32_t)h)) {
+    throw_js(env, {true, "the buffer belongs to an execution; release it there"});
+    return nullptr;
+  }
   afhip_buffer_destroy(it->second.first);
   g_reg.buffers.erase(it);
   return nullptr;
@@ -565,6 +582,362 @@ napi_value PackWeightQ8Block(napi_env env, napi_callback_info info) {
 }
 
 // ---------------------------------------------------------------------------
+// Execution layer (afhip_execution_*): pooled device tensors as buffer
+// handles, usable wherever a buffer handle is (gemmRun, packWeightQ8Block),
+// and the pair stack chained on the device.
+// ---------------------------------------------------------------------------
+
+bool lookup_execution(napi_env env, napi_value v, uint32_t* handle, ExecutionEntry** out) {
+  int64_t h;
+  if (!get_int64(env, v, &h)) return false;
+  auto it = g_reg.executions.find((uint32_t)h);
+  if (it == g_reg.executions.end()) {
+    throw_js(env, {true, "unknown execution handle " + std::to_string(h)});
+    return false;
+  }
+  *handle = (uint32_t)h;
+  *out = &it->second;
+  return true;
+}
+
+void forget_buffer(uint32_t h) {
+  g_reg.buffers.erase(h);
+  g_reg.owner.erase(h);
+}
+
+// Registers the execution's newest allocation (pointer p) as a buffer handle.
+napi_value register_pooled(napi_env env, uint32_t exh, ExecutionEntry& e, void* p, size_t bytes) {
+  uint64_t count = 0;
+  afhip_execution_checkpoint(e.ex, &count);
+  const uint32_t h = g_reg.next++;
+  g_reg.buffers[h] = {p, bytes};
+  g_reg.owner[h] = exh;
+  e.handles.push_back({count - 1, h});
+  return make_number(env, h);
+}
+
+// executionCreate(maxPooledBytes = 0) -> handle
+napi_value ExecutionCreate(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 0)) return nullptr;
+  int64_t cap = 0;
+  if (a.argc > 0 && !get_int64(env, a.argv[0], &cap)) return nullptr;
+  if (cap < 0) {
+    throw_js(env, {true, "maxPooledBytes must not be negative"});
+    return nullptr;
+  }
+  afhip_execution* ex = nullptr;
+  if (!check(env, afhip_execution_create((uint64_t)cap, nullptr, &ex), "executionCreate")) return nullptr;
+  const uint32_t h = g_reg.next++;
+  g_reg.executions[h].ex = ex;
+  return make_number(env, h);
+}
+
+napi_value ExecutionDestroy(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  if (!lookup_execution(env, a.argv[0], &exh, &e)) return nullptr;
+  for (auto& ih : e->handles) forget_buffer(ih.second);
+  afhip_execution_destroy(e->ex);
+  g_reg.executions.erase(exh);
+  return nullptr;
+}
+
+// executionAllocate(ex, label, bytes) -> buffer handle
+napi_value ExecutionAllocate(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  std::string label;
+  int64_t bytes;
+  if (!lookup_execution(env, a.argv[0], &exh, &e) || !get_string(env, a.argv[1], &label) ||
+      !get_int64(env, a.argv[2], &bytes))
+    return nullptr;
+  if (bytes <= 0) {
+    throw_js(env, {true, "invalid allocation size " + std::to_string(bytes) + " for " + label});
+    return nullptr;
+  }
+  void* p = nullptr;
+  if (!check(env, afhip_execution_allocate(e->ex, label.c_str(), (uint64_t)bytes, &p), "executionAllocate"))
+    return nullptr;
+  return register_pooled(env, exh, *e, p, (size_t)bytes);
+}
+
+// executionUpload(ex, label, typedArray) -> buffer handle
+napi_value ExecutionUpload(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 3)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  std::string label;
+  HostView src;
+  if (!lookup_execution(env, a.argv[0], &exh, &e) || !get_string(env, a.argv[1], &label) ||
+      !get_view(env, a.argv[2], &src))
+    return nullptr;
+  void* p = nullptr;
+  if (!check(env, afhip_execution_upload(e->ex, label.c_str(), src.data, src.bytes, &p), "executionUpload"))
+    return nullptr;
+  return register_pooled(env, exh, *e, p, src.bytes);
+}
+
+// executionRelease(ex, buffer)
+napi_value ExecutionRelease(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  int64_t h;
+  if (!lookup_execution(env, a.argv[0], &exh, &e) || !get_int64(env, a.argv[1], &h)) return nullptr;
+  auto o = g_reg.owner.find((uint32_t)h);
+  if (o == g_reg.owner.end() || o->second != exh) {
+    throw_js(env, {true, "the buffer is not a tensor of this execution"});
+    return nullptr;
+  }
+  if (!check(env, afhip_execution_release(e->ex, g_reg.buffers[(uint32_t)h].first), "executionRelease"))
+    return nullptr;
+  forget_buffer((uint32_t)h);
+  for (auto it = e->handles.begin(); it != e->handles.end(); ++it)
+    if (it->second == (uint32_t)h) {
+      e->handles.erase(it);
+      break;
+    }
+  return nullptr;
+}
+
+napi_value ExecutionCheckpoint(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  if (!lookup_execution(env, a.argv[0], &exh, &e)) return nullptr;
+  uint64_t n = 0;
+  if (!check(env, afhip_execution_checkpoint(e->ex, &n), "executionCheckpoint")) return nullptr;
+  return make_number(env, (double)n);
+}
+
+napi_value ExecutionReleaseSince(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 2)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  int64_t mark;
+  if (!lookup_execution(env, a.argv[0], &exh, &e) || !get_int64(env, a.argv[1], &mark)) return nullptr;
+  if (mark < 0) {
+    throw_js(env, {true, "invalid GPU allocation checkpoint " + std::to_string(mark)});
+    return nullptr;
+  }
+  if (!check(env, afhip_execution_release_since(e->ex, (uint64_t)mark), "executionReleaseSince")) return nullptr;
+  std::vector<std::pair<uint64_t, uint32_t>> kept;
+  for (auto& ih : e->handles) {
+    if (ih.first >= (uint64_t)mark) forget_buffer(ih.second);
+    else kept.push_back(ih);
+  }
+  e->handles.swap(kept);
+  return nullptr;
+}
+
+napi_value ExecutionNoteSubmitted(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  if (!lookup_execution(env, a.argv[0], &exh, &e)) return nullptr;
+  check(env, afhip_execution_note_submitted(e->ex), "executionNoteSubmitted");
+  return nullptr;
+}
+
+// executionSnapshot(ex) -> JSON text of the AllocationSnapshot
+napi_value ExecutionSnapshot(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  if (!lookup_execution(env, a.argv[0], &exh, &e)) return nullptr;
+  std::vector<char> buf(1 << 16);
+  if (!check(env, afhip_execution_snapshot(e->ex, buf.data(), buf.size()), "executionSnapshot")) return nullptr;
+  napi_value s;
+  NAPI_OK(napi_create_string_utf8(env, buf.data(), NAPI_AUTO_LENGTH, &s));
+  return s;
+}
+
+size_t dtype_bytes(int64_t d) { return d == AFHIP_F16 ? 2 : 4; }
+
+// executionAddInPlace(ex, base, baseDtype, update, updateDtype, elements)
+napi_value ExecutionAddInPlace(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 6)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  void *base, *update;
+  size_t nb, nu;
+  int64_t bd, ud, n;
+  if (!lookup_execution(env, a.argv[0], &exh, &e) || !lookup_buffer(env, a.argv[1], &base, &nb) ||
+      !get_int64(env, a.argv[2], &bd) || !lookup_buffer(env, a.argv[3], &update, &nu) ||
+      !get_int64(env, a.argv[4], &ud) || !get_int64(env, a.argv[5], &n))
+    return nullptr;
+  if (n <= 0 || (size_t)n * dtype_bytes(bd) > nb || (size_t)n * dtype_bytes(ud) > nu) {
+    throw_js(env, {true, "residual tensors must hold the element count"});
+    return nullptr;
+  }
+  check(env, afhip_execution_add_in_place(e->ex, base, (int32_t)bd, update, (int32_t)ud, n), "executionAddInPlace");
+  return nullptr;
+}
+
+// The pair stack's shape from {length, sequences, cM, cZ = 128, cOuter = 32,
+// cHidden = 128, transitionFactor = 4, precision = PRECISION.f16,
+// pairDtype = DTYPE.f16, msaDtype = DTYPE.f16, opmRowBlock = 0,
+// triangleBlockRows = 0}.
+bool read_stack_desc(napi_env env, napi_value o, afhip_pair_stack_desc* d) {
+  int64_t L, S, cm, cz, co, ch, tf, prec, pdt, mdt, rb, br;
+  if (!prop_int(env, o, "length", 0, &L) || !prop_int(env, o, "sequences", 0, &S) ||
+      !prop_int(env, o, "cM", 0, &cm) || !prop_int(env, o, "cZ", 128, &cz) || !prop_int(env, o, "cOuter", 32, &co) ||
+      !prop_int(env, o, "cHidden", 128, &ch) || !prop_int(env, o, "transitionFactor", 4, &tf) ||
+      !prop_int(env, o, "precision", AFHIP_PRECISION_F16, &prec) || !prop_int(env, o, "pairDtype", AFHIP_F16, &pdt) ||
+      !prop_int(env, o, "msaDtype", AFHIP_F16, &mdt) || !prop_int(env, o, "opmRowBlock", 0, &rb) ||
+      !prop_int(env, o, "triangleBlockRows", 0, &br))
+    return false;
+  if (L <= 0 || L > 65535 || cz <= 0 || ch <= 0 || tf <= 0 || S < 0 || cm < 0 || co <= 0) {
+    throw_js(env, {true, "pair stack dimensions must be positive"});
+    return false;
+  }
+  std::memset(d, 0, sizeof(*d));
+  d->opm = {(int32_t)S, (int32_t)L, (int32_t)cm, (int32_t)co, (int32_t)cz, (int32_t)prec, (int32_t)mdt, (int32_t)pdt,
+            (int32_t)rb, 1, 1e-5f, 1e-3f};
+  d->outgoing = {(int32_t)L, (int32_t)cz, (int32_t)ch, AFHIP_TRIANGLE_OUTGOING, (int32_t)prec, (int32_t)pdt,
+                 (int32_t)pdt, (int32_t)br, 1, 1e-5f};
+  d->incoming = d->outgoing;
+  d->incoming.direction = AFHIP_TRIANGLE_INCOMING;
+  d->transition = {(int64_t)L * L, (int32_t)cz, (int32_t)(tf * cz), (int32_t)prec, (int32_t)pdt, (int32_t)pdt, 1,
+                   1e-5f};
+  return true;
+}
+
+// executionPrepareWeights(ex, kind, stackDesc, Float32Array packed) -> buffer
+// handle of the prepared weights in the execution's pool; kind is
+// "outerProductMean", "triangleOutgoing", "triangleIncoming" or
+// "pairTransition", packed in that operator's reference order.
+napi_value ExecutionPrepareWeights(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 4)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  std::string kind;
+  afhip_pair_stack_desc d;
+  HostView packed;
+  if (!lookup_execution(env, a.argv[0], &exh, &e) || !get_string(env, a.argv[1], &kind) ||
+      !read_stack_desc(env, a.argv[2], &d) || !get_view(env, a.argv[3], &packed))
+    return nullptr;
+  size_t bytes = 0;
+  int st;
+  if (kind == "outerProductMean") st = afhip_opm_weights_size(&d.opm, &bytes);
+  else if (kind == "triangleOutgoing") st = afhip_triangle_weights_size(&d.outgoing, &bytes);
+  else if (kind == "triangleIncoming") st = afhip_triangle_weights_size(&d.incoming, &bytes);
+  else if (kind == "pairTransition") st = afhip_transition_weights_size(&d.transition, &bytes);
+  else {
+    throw_js(env, {true, "unknown weight kind " + kind});
+    return nullptr;
+  }
+  if (!check(env, st, "executionPrepareWeights")) return nullptr;
+  void *src = nullptr, *dst = nullptr;
+  const std::string label = "pair-stack." + kind;
+  if (!check(env, afhip_execution_upload(e->ex, (label + ".weights-f32").c_str(), packed.data, packed.bytes, &src),
+             "executionPrepareWeights"))
+    return nullptr;
+  if (!check(env, afhip_execution_allocate(e->ex, (label + ".weights").c_str(), bytes, &dst),
+             "executionPrepareWeights")) {
+    afhip_execution_release(e->ex, src);
+    return nullptr;
+  }
+  napi_value handle = register_pooled(env, exh, *e, dst, bytes);
+  const float* f = (const float*)src;
+  if (kind == "outerProductMean") st = afhip_opm_prepare_weights(&d.opm, f, dst, nullptr);
+  else if (kind == "triangleOutgoing") st = afhip_triangle_prepare_weights(&d.outgoing, f, dst, nullptr);
+  else if (kind == "triangleIncoming") st = afhip_triangle_prepare_weights(&d.incoming, f, dst, nullptr);
+  else st = afhip_transition_prepare_weights(&d.transition, f, dst, nullptr);
+  if (st == AFHIP_OK) st = afhip_synchronize(nullptr);
+  afhip_execution_release(e->ex, src);
+  if (!check(env, st, "executionPrepareWeights")) return nullptr;
+  return handle;
+}
+
+// executionPairStack(ex, stackDesc, {outerProductMean?, triangleOutgoing?,
+// triangleIncoming?, pairTransition?}, pair, pairMask, msa?, msaMask?)
+napi_value ExecutionPairStack(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 5)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  afhip_pair_stack_desc d;
+  if (!lookup_execution(env, a.argv[0], &exh, &e) || !read_stack_desc(env, a.argv[1], &d)) return nullptr;
+  const char* names[4] = {"outerProductMean", "triangleOutgoing", "triangleIncoming", "pairTransition"};
+  void* w[4] = {};
+  for (int i = 0; i < 4; i++) {
+    bool has = false;
+    napi_has_named_property(env, a.argv[2], names[i], &has);
+    if (!has) continue;
+    napi_value v;
+    napi_get_named_property(env, a.argv[2], names[i], &v);
+    napi_valuetype t;
+    napi_typeof(env, v, &t);
+    if (t == napi_undefined || t == napi_null) continue;
+    if (!lookup_buffer(env, v, &w[i], nullptr)) return nullptr;
+  }
+  void *pair, *pmask, *msa = nullptr, *mmask = nullptr;
+  size_t np, npm, nm = 0, nmm = 0;
+  if (!lookup_buffer(env, a.argv[3], &pair, &np) || !lookup_buffer(env, a.argv[4], &pmask, &npm)) return nullptr;
+  if (a.argc > 6) {
+    napi_valuetype t;
+    napi_typeof(env, a.argv[5], &t);
+    if (t != napi_undefined && t != napi_null) {
+      if (!lookup_buffer(env, a.argv[5], &msa, &nm) || !lookup_buffer(env, a.argv[6], &mmask, &nmm)) return nullptr;
+    }
+  }
+  const size_t pairs = (size_t)d.outgoing.length * d.outgoing.length;
+  if (np < pairs * d.outgoing.c_z * dtype_bytes(d.outgoing.pair_dtype) || npm < pairs * 4) {
+    throw_js(env, {true, "the pair or its mask buffer is too small"});
+    return nullptr;
+  }
+  if (w[0]) {
+    const size_t rows = (size_t)d.opm.sequences * d.opm.length;
+    if (!msa || nm < rows * d.opm.c_m * dtype_bytes(d.opm.msa_dtype) || nmm < rows * 4) {
+      throw_js(env, {true, "the outer-product mean needs the MSA and its mask buffers"});
+      return nullptr;
+    }
+  }
+  afhip_pair_stack_weights pw{w[0], w[1], w[2], w[3]};
+  check(env, afhip_execution_pair_stack(e->ex, &d, &pw, msa, (const float*)mmask, pair, (const float*)pmask),
+        "executionPairStack");
+  return nullptr;
+}
+
+// setMemoryBudget(bytes | null), memoryResident() -> bytes
+napi_value SetMemoryBudget(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 1)) return nullptr;
+  napi_valuetype t;
+  napi_typeof(env, a.argv[0], &t);
+  int64_t bytes = 0;
+  if (t != napi_undefined && t != napi_null) {
+    if (!get_int64(env, a.argv[0], &bytes)) return nullptr;
+    if (bytes <= 0) {
+      throw_js(env, {true, "GPU memory budget must be a positive safe integer"});
+      return nullptr;
+    }
+  }
+  check(env, afhip_set_memory_budget((uint64_t)bytes), "setMemoryBudget");
+  return nullptr;
+}
+
+napi_value MemoryResident(napi_env env, napi_callback_info) {
+  uint64_t bytes = 0;
+  if (!check(env, afhip_memory_resident(&bytes), "memoryResident")) return nullptr;
+  return make_number(env, (double)bytes);
+}
+
+// ---------------------------------------------------------------------------
 // Operators with host arrays (upload, prepare, run, read back)
 // ---------------------------------------------------------------------------
 
@@ -782,7 +1155,14 @@ napi_value Init(napi_env env, napi_value exports) {
       {"bufferRead", BufferRead}, {"synchronize", Synchronize}, {"gemmGrid", GemmGrid}, {"gemmSelect", GemmSelect},
       {"gemmCalibrate", GemmCalibrate}, {"gemmForceVariant", GemmForceVariant}, {"calibrationLoad", CalibrationLoad},
       {"calibrationSave", CalibrationSave}, {"gemmPlanCreate", GemmPlanCreate}, {"gemmPlanDestroy", GemmPlanDestroy},
-      {"gemmWorkspaceSize", GemmWorkspaceSize}, {"gemmRun", GemmRun}, {"packWeightQ8Block", PackWeightQ8Block}, {"triangleRun", TriangleRun},
+      {"gemmWorkspaceSize", GemmWorkspaceSize}, {"gemmRun", GemmRun}, {"packWeightQ8Block", PackWeightQ8Block},
+      {"executionCreate", ExecutionCreate}, {"executionDestroy", ExecutionDestroy},
+      {"executionAllocate", ExecutionAllocate}, {"executionUpload", ExecutionUpload},
+      {"executionRelease", ExecutionRelease}, {"executionCheckpoint", ExecutionCheckpoint},
+      {"executionReleaseSince", ExecutionReleaseSince}, {"executionNoteSubmitted", ExecutionNoteSubmitted},
+      {"executionSnapshot", ExecutionSnapshot}, {"executionAddInPlace", ExecutionAddInPlace},
+      {"executionPrepareWeights", ExecutionPrepareWeights}, {"executionPairStack", ExecutionPairStack},
+      {"setMemoryBudget", SetMemoryBudget}, {"memoryResident", MemoryResident}, {"triangleRun", TriangleRun},
       {"opmRun", OpmRun}, {"transitionRun", TransitionRun}, {"timingEnable", TimingEnable},
       {"timingReset", TimingReset}, {"timingReport", TimingReport},
   };

@@ -100,6 +100,71 @@ export declare class TransitionGpu {
   run(input: TransitionInput, options?: { precision?: Precision }): OperatorResult;
 }
 
+/** Shape of the chained pair steps (include/afhip.h afhip_pair_stack_desc). */
+export interface PairStackShape {
+  length: number;
+  sequences?: number;
+  cM?: number;
+  cZ?: number;
+  cOuter?: number;
+  cHidden?: number;
+  transitionFactor?: number;
+  precision?: 0 | 1;
+  pairDtype?: 0 | 1;
+  msaDtype?: 0 | 1;
+  opmRowBlock?: number;
+  triangleBlockRows?: number;
+}
+
+export interface PairStackWeights {
+  outerProductMean?: OuterProductMeanWeights;
+  triangleMultiplicationOutgoing?: TriangleMultiplicationWeights;
+  triangleMultiplicationIncoming?: TriangleMultiplicationWeights;
+  pairTransition?: TransitionWeights;
+}
+
+/** Prepared weight buffers, as preparePairStack returns them. */
+export interface PreparedPairStack {
+  outerProductMean?: number;
+  triangleOutgoing?: number;
+  triangleIncoming?: number;
+  pairTransition?: number;
+}
+
+/** AllocationSnapshot (src/runtime/allocator.ts:8-25). */
+export interface AllocationSnapshot {
+  currentBytes: number;
+  peakBytes: number;
+  peakComposition: { label: string; bytes: number; count: number }[];
+  residentBytes: number;
+  peakResidentBytes: number;
+  pooledBytes: number;
+  allocationCount: number;
+  bufferCount: number;
+}
+
+/** WebGpuExecution's counterpart (src/runtime/execution.ts:153-555): device
+ * tensors as buffer handles from a pool, and the pair steps of an Evoformer
+ * block chained on the device (src/evoformer/block.ts:1683-1750). */
+export declare class HipExecution {
+  constructor(options?: { maxPooledBytes?: number });
+  upload(label: string, data: ArrayBufferView): number;
+  allocate(label: string, bytes: number): number;
+  read<T extends ArrayBufferView>(buffer: number, target: T): T;
+  releaseTensor(buffer: number): void;
+  checkpoint(): number;
+  releaseSince(checkpoint: number): void;
+  noteSubmitted(): void;
+  snapshot(): AllocationSnapshot;
+  addInPlace(base: number, update: number, elements: number, baseDtype?: 0 | 1, updateDtype?: 0 | 1): void;
+  preparePairStack(shape: PairStackShape, weights: PairStackWeights): PreparedPairStack;
+  pairStack(shape: PairStackShape, prepared: PreparedPairStack, pair: number, pairMask: number, msa?: number,
+            msaMask?: number): void;
+  release(): void;
+}
+export declare function setGpuMemoryBudget(bytes?: number | null): void;
+export declare function gpuMemoryResident(): number;
+
 /** The GEMM plan description (include/afhip.h afhip_gemm_desc). */
 export interface GemmDesc {
   rows: number;

@@ -183,6 +183,62 @@ TransitionGpu.prototype.run = function (input, options) {
 };
 
 // gemmGrid (src/runtime/gemm.ts:368-379).
+// The execution layer (src/runtime/execution.ts:153-555, allocator.ts:168-388):
+// device tensors as buffer handles drawn from a pool that outlives each
+// call, and the pair steps of an Evoformer block chained on the device
+// (src/evoformer/block.ts:1683-1750). Buffer handles work with gemmRun and
+// packWeightQ8Block as well.
+function HipExecution(options) {
+  requestHipDevice();
+  this.handle = addon().executionCreate((options && options.maxPooledBytes) || 0);
+}
+HipExecution.prototype.upload = function (label, data) { return addon().executionUpload(this.handle, label, data); };
+HipExecution.prototype.allocate = function (label, bytes) {
+  return addon().executionAllocate(this.handle, label, bytes);
+};
+HipExecution.prototype.read = function (buffer, target) { addon().synchronize(); addon().bufferRead(buffer, 0, target); return target; };
+HipExecution.prototype.releaseTensor = function (buffer) { addon().executionRelease(this.handle, buffer); };
+HipExecution.prototype.checkpoint = function () { return addon().executionCheckpoint(this.handle); };
+HipExecution.prototype.releaseSince = function (mark) { addon().executionReleaseSince(this.handle, mark); };
+HipExecution.prototype.noteSubmitted = function () { addon().executionNoteSubmitted(this.handle); };
+HipExecution.prototype.snapshot = function () { return JSON.parse(addon().executionSnapshot(this.handle)); };
+HipExecution.prototype.addInPlace = function (base, update, elements, baseDtype, updateDtype) {
+  addon().executionAddInPlace(this.handle, base, baseDtype === undefined ? F32 : baseDtype, update,
+    updateDtype === undefined ? F32 : updateDtype, elements);
+};
+// shape: {length, sequences, cM, cZ, cOuter, cHidden, transitionFactor,
+// precision, pairDtype, msaDtype}; weights: {outerProductMean,
+// triangleMultiplicationOutgoing, triangleMultiplicationIncoming,
+// pairTransition}, each the operator's weight object (a missing one skips
+// that step). Returns the prepared weight buffers.
+HipExecution.prototype.preparePairStack = function (shape, weights) {
+  var native = addon(), h = this.handle, out = {};
+  if (weights.outerProductMean) {
+    out.outerProductMean = native.executionPrepareWeights(h, "outerProductMean", shape,
+      packOrdered(weights.outerProductMean, OPM_ORDER));
+  }
+  if (weights.triangleMultiplicationOutgoing) {
+    out.triangleOutgoing = native.executionPrepareWeights(h, "triangleOutgoing", shape,
+      packTriangleWeights(weights.triangleMultiplicationOutgoing));
+  }
+  if (weights.triangleMultiplicationIncoming) {
+    out.triangleIncoming = native.executionPrepareWeights(h, "triangleIncoming", shape,
+      packTriangleWeights(weights.triangleMultiplicationIncoming));
+  }
+  if (weights.pairTransition) {
+    out.pairTransition = native.executionPrepareWeights(h, "pairTransition", shape,
+      packOrdered(weights.pairTransition, TRANSITION_ORDER));
+  }
+  return out;
+};
+HipExecution.prototype.pairStack = function (shape, prepared, pair, pairMask, msa, msaMask) {
+  addon().executionPairStack(this.handle, shape, prepared, pair, pairMask, msa === undefined ? null : msa,
+    msaMask === undefined ? null : msaMask);
+};
+HipExecution.prototype.release = function () {
+  if (this.handle !== undefined) { addon().executionDestroy(this.handle); this.handle = undefined; }
+};
+
 function gemmGrid(rows, columns, tileColumns, tileRows) {
   return addon().gemmGrid(rows, columns, tileColumns === undefined ? 128 : tileColumns,
     tileRows === undefined ? 64 : tileRows);
@@ -210,6 +266,9 @@ module.exports = {
   TriangleMultiplicationOutgoingGpu: TriangleMultiplicationOutgoingGpu,
   TriangleMultiplicationIncomingGpu: TriangleMultiplicationIncomingGpu,
   OuterProductMeanGpu: OuterProductMeanGpu,
+  HipExecution: HipExecution,
+  setGpuMemoryBudget: function (bytes) { requestHipDevice(); addon().setMemoryBudget(bytes === undefined ? null : bytes); },
+  gpuMemoryResident: function () { return addon().memoryResident(); },
   TransitionGpu: TransitionGpu,
   validateTriangleInput: validateTriangleInput,
   packTriangleWeights: packTriangleWeights,

@@ -333,6 +333,84 @@ AFHIP_API int afhip_transition_run(const afhip_transition_desc* desc, const void
                          void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Execution layer                                                         */
+/* ---------------------------------------------------------------------- */
+
+/* Device-resident tensors across operator calls, so a block's steps chain on
+ * the device without host round trips. Replaces WebGpuExecution
+ * (src/runtime/execution.ts:153-555) and its GpuBufferAllocator
+ * (src/runtime/allocator.ts:168-388): requests of 1 MiB or more take whole
+ * mebibytes; a released tensor's buffer goes to an idle pool, and a request
+ * takes the smallest idle buffer that covers it and is at most twice its
+ * size; idle buffers untouched for four submitted boundaries are freed and
+ * the pool is trimmed to its cap. One execution is used from one thread. */
+typedef struct afhip_execution afhip_execution;
+
+/* Caps the resident bytes of every execution on the open device together;
+ * 0 removes the cap. Replaces setGpuMemoryBudget (allocator.ts:66-71). */
+AFHIP_API int afhip_set_memory_budget(uint64_t bytes);
+/* Replaces gpuMemoryResident (allocator.ts:74). */
+AFHIP_API int afhip_memory_resident(uint64_t* bytes);
+/* max_pooled_bytes: the idle pool's cap, 0 for 864 MiB (COMPACT_GPU_POOL_BYTES,
+ * allocator.ts:30); stream: where uploads and chained steps run. Replaces
+ * the WebGpuExecution constructor (execution.ts:183-199). */
+AFHIP_API int afhip_execution_create(uint64_t max_pooled_bytes, void* stream, afhip_execution** out);
+/* Releases every tensor and frees the pool (WebGpuExecution.release,
+ * execution.ts:549-554). */
+AFHIP_API int afhip_execution_destroy(afhip_execution* ex);
+/* allocate and upload (execution.ts:201-221; allocator.ts:197-285). Past the
+ * budget: AFHIP_ERR_OUT_OF_MEMORY with a message naming the label
+ * (GpuMemoryBudgetError, allocator.ts:76-90). Labels differing only in a
+ * trailing index share a group in the snapshot (allocator.ts:110). */
+AFHIP_API int afhip_execution_allocate(afhip_execution* ex, const char* label, uint64_t bytes, void** out);
+AFHIP_API int afhip_execution_upload(afhip_execution* ex, const char* label, const void* host, uint64_t bytes,
+                                     void** out);
+/* One tensor back to the idle pool (AllocatedGpuBuffer.release,
+ * allocator.ts:159-165). */
+AFHIP_API int afhip_execution_release(afhip_execution* ex, void* tensor);
+/* checkpoint and releaseSince (execution.ts:531-547): every tensor allocated
+ * after the checkpoint goes back to the pool. */
+AFHIP_API int afhip_execution_checkpoint(const afhip_execution* ex, uint64_t* out);
+AFHIP_API int afhip_execution_release_since(afhip_execution* ex, uint64_t checkpoint);
+/* A submitted boundary (noteSubmitted, execution.ts:533; allocator.ts:332-341). */
+AFHIP_API int afhip_execution_note_submitted(afhip_execution* ex);
+/* JSON AllocationSnapshot (allocator.ts:8-25, :376-387): currentBytes,
+ * peakBytes, peakComposition, residentBytes, peakResidentBytes, pooledBytes,
+ * allocationCount, bufferCount. */
+AFHIP_API int afhip_execution_snapshot(const afhip_execution* ex, char* json, size_t capacity);
+/* base += update over `elements` values, each f32 or f16 (addInPlace,
+ * execution.ts:415-450). */
+AFHIP_API int afhip_execution_add_in_place(afhip_execution* ex, void* base, int32_t base_dtype, const void* update,
+                                           int32_t update_dtype, int64_t elements);
+
+typedef struct afhip_pair_stack_desc {
+  afhip_opm_desc opm;               /* out_dtype = the pair's dtype */
+  afhip_triangle_desc outgoing;     /* pair_dtype = out_dtype = the pair's dtype */
+  afhip_triangle_desc incoming;
+  afhip_transition_desc transition; /* rows = L * L, channels = c_z, in/out dtype = the pair's */
+} afhip_pair_stack_desc;
+
+/* Prepared weight buffers (afhip_*_prepare_weights); NULL skips a step. */
+typedef struct afhip_pair_stack_weights {
+  const void* opm;
+  const void* outgoing;
+  const void* incoming;
+  const void* transition;
+} afhip_pair_stack_weights;
+
+/* The pair-representation steps of encodeEvoformerBlock
+ * (src/evoformer/block.ts:1673-1759) that this library builds, in the
+ * block's order, each adding into `pair` in place: outer-product mean
+ * (:1683-1689, :1718), triangle multiplication outgoing then incoming
+ * (:1720-1725), pair transition (:1747-1750). The triangle attentions between
+ * them (:1727-1745) are outside this library and are not run. Each step's
+ * workspace comes from the execution's pool and returns to it once the step
+ * is queued; the descriptors' residual flags and directions are set here. */
+AFHIP_API int afhip_execution_pair_stack(afhip_execution* ex, const afhip_pair_stack_desc* desc,
+                                         const afhip_pair_stack_weights* weights, const void* msa,
+                                         const float* msa_mask, void* pair, const float* pair_mask);
+
+/* ---------------------------------------------------------------------- */
 /* Kernel timing                                                           */
 /* ---------------------------------------------------------------------- */
 

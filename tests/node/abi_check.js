@@ -8,7 +8,10 @@ var native = afhip.addon();
 var expected = ["open", "close", "abiVersion", "deviceReport", "bufferCreate", "bufferDestroy", "bufferWrite",
   "bufferRead", "synchronize", "gemmGrid", "gemmSelect", "gemmCalibrate", "gemmForceVariant", "calibrationLoad",
   "calibrationSave", "gemmPlanCreate", "gemmPlanDestroy", "gemmWorkspaceSize", "gemmRun", "triangleRun", "opmRun",
-  "transitionRun", "timingEnable", "timingReset", "timingReport", "packWeightQ8Block"];
+  "transitionRun", "timingEnable", "timingReset", "timingReport", "packWeightQ8Block", "executionCreate",
+  "executionDestroy", "executionAllocate", "executionUpload", "executionRelease", "executionCheckpoint",
+  "executionReleaseSince", "executionNoteSubmitted", "executionSnapshot", "executionAddInPlace",
+  "executionPrepareWeights", "executionPairStack", "setMemoryBudget", "memoryResident"];
 expected.forEach(function (n) { assert.strictEqual(typeof native[n], "function", n); });
 assert.strictEqual(native.abiVersion(), 1);
 
@@ -32,6 +35,9 @@ assert.throws(function () { afhip.validateTriangleInput({ shape: [0, 3, 4] }); }
 // packWeightQ8Block checks its handles before any device work.
 assert.throws(function () { afhip.packWeightQ8Block(999999, 999998, 64, 0, 4, 4, 999997, afhip.DTYPE.f16); },
   /unknown buffer handle/);
+
+// Execution handles are checked before any device work.
+assert.throws(function () { native.executionSnapshot(424242); }, /unknown execution handle/);
 
 // errorMetrics (test/cpu-reference.test.ts:36-42).
 var m = afhip.errorMetrics(new Float32Array([1, 3]), new Float32Array([2, 1]));

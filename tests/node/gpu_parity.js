@@ -120,4 +120,66 @@ function transposePairs(data, L, C) {
   report.cases.push({ q8PackedGemmMaxRelative: worst / largest });
 })();
 
+// The execution layer from Node: the pair steps chained on the device
+// (HipExecution.pairStack) against the four operators run one by one through
+// their host-array entry points, the updates added on the host in the
+// block's order (src/evoformer/block.ts:1683-1750).
+(function () {
+  var L = 12, S = 5, cM = 8, cO = 4, cZ = 16, cH = 16, hidden = 4 * cZ;
+  function fill(n, f) { var a = new Float32Array(n); for (var i = 0; i < n; i++) a[i] = f(i); return a; }
+  function wave(n, scale, phase, center) { return fill(n, function (i) { return (center || 0) + scale * Math.sin(0.7 * i + phase); }); }
+  function triangleWeights(phase) {
+    var sizes = { layerNormInWeight: cZ, layerNormInBias: cZ, linearAPWeight: cH * cZ, linearAPBias: cH,
+      linearAGWeight: cH * cZ, linearAGBias: cH, linearBPWeight: cH * cZ, linearBPBias: cH, linearBGWeight: cH * cZ,
+      linearBGBias: cH, layerNormOutWeight: cH, layerNormOutBias: cH, linearZWeight: cZ * cH, linearZBias: cZ,
+      linearGWeight: cZ * cZ, linearGBias: cZ };
+    var w = {};
+    afhip.TRIANGLE_ORDER.forEach(function (n, k) {
+      w[n] = n.indexOf("layerNorm") === 0 && n.indexOf("Weight") > 0 ? wave(sizes[n], 0.1, phase + k, 1)
+        : wave(sizes[n], n.indexOf("Bias") > 0 ? 0.05 : 0.25, phase + k);
+    });
+    return w;
+  }
+  var weights = {
+    outerProductMean: { layerNormScale: wave(cM, 0.1, 1, 1), layerNormOffset: wave(cM, 0.05, 2),
+      leftWeight: wave(cM * cO, 0.3, 3), leftBias: wave(cO, 0.05, 4), rightWeight: wave(cM * cO, 0.3, 5),
+      rightBias: wave(cO, 0.05, 6), outputWeight: wave(cO * cO * cZ, 0.2, 7), outputBias: wave(cZ, 0.05, 8) },
+    triangleMultiplicationOutgoing: triangleWeights(10),
+    triangleMultiplicationIncoming: triangleWeights(40),
+    pairTransition: { layerNormScale: wave(cZ, 0.1, 70, 1), layerNormOffset: wave(cZ, 0.05, 71),
+      firstWeight: wave(cZ * hidden, 0.2, 72), firstBias: wave(hidden, 0.05, 73),
+      secondWeight: wave(hidden * cZ, 0.1, 74), secondBias: wave(cZ, 0.05, 75) },
+  };
+  var msa = wave(S * L * cM, 1, 0.3), msaMask = fill(S * L, function (i) { return i % 7 === 3 ? 0 : 1; });
+  var pair = wave(L * L * cZ, 1, 0.9), pairMask = fill(L * L, function (i) { return i % 11 === 5 ? 0 : 1; });
+
+  var z = Float32Array.from(pair);
+  function addInto(base, update) { for (var i = 0; i < base.length; i++) base[i] = Math.fround(base[i] + update[i]); }
+  addInto(z, new afhip.OuterProductMeanGpu().run({ shape: [S, L, cM, cO, cZ], activations: msa, mask: msaMask,
+    weights: weights.outerProductMean }).output);
+  addInto(z, new afhip.TriangleMultiplicationOutgoingGpu().run({ shape: [L, cZ, cH], z: z, mask: pairMask,
+    weights: weights.triangleMultiplicationOutgoing }).output);
+  addInto(z, new afhip.TriangleMultiplicationIncomingGpu().run({ shape: [L, cZ, cH], z: z, mask: pairMask,
+    weights: weights.triangleMultiplicationIncoming }).output);
+  addInto(z, new afhip.TransitionGpu().run({ shape: [L * L, cZ, hidden], activations: z,
+    weights: weights.pairTransition }).output);
+
+  var ex = new afhip.HipExecution();
+  var shape = { length: L, sequences: S, cM: cM, cZ: cZ, cOuter: cO, cHidden: cH, transitionFactor: 4,
+    precision: afhip.PRECISION.f32, pairDtype: afhip.DTYPE.f32, msaDtype: afhip.DTYPE.f32 };
+  var prepared = ex.preparePairStack(shape, weights);
+  var bPair = ex.upload("pair", pair), bMask = ex.upload("pair-mask", pairMask);
+  var bMsa = ex.upload("msa", msa), bMsaMask = ex.upload("msa-mask", msaMask);
+  ex.pairStack(shape, prepared, bPair, bMask, bMsa, bMsaMask);
+  var got = ex.read(bPair, new Float32Array(L * L * cZ));
+  var m = afhip.errorMetrics(got, z);
+  var largest = 0;
+  for (var i = 0; i < z.length; i++) largest = Math.max(largest, Math.abs(z[i]));
+  assert.ok(m.maxAbsoluteError <= 1e-5 * largest, "pair stack " + JSON.stringify(m));
+  var snap = ex.snapshot();
+  assert.ok(snap.peakComposition.length > 0 && snap.residentBytes >= snap.currentBytes);
+  ex.release();
+  report.cases.push({ pairStackVsOperators: m });
+})();
+
 console.log(JSON.stringify(report));

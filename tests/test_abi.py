@@ -46,6 +46,17 @@ def test_abi_version_and_not_open_errors():
     assert lib.afhip_triangle_workspace_size(ctypes.byref(desc), ctypes.byref(size)) == _lib.OK
     # a, b (f16, channel-major) and the contracted block: 3 x 128 x 147456 x 2 bytes
     assert size.value >= 3 * 128 * 147456 * 2
+    # The pair transition at f16 precision runs fused: no workspace. At f32 it
+    # needs the normalised rows and the hidden activation.
+    tdesc = _lib.TransitionDesc(1 << 20, 128, 512, 1, 1, 1, 1, 1e-5)
+    assert lib.afhip_transition_workspace_size(ctypes.byref(tdesc), ctypes.byref(size)) == _lib.OK
+    assert size.value == 0
+    tdesc.precision = 0
+    assert lib.afhip_transition_workspace_size(ctypes.byref(tdesc), ctypes.byref(size)) == _lib.OK
+    assert size.value >= (1 << 20) * (128 + 512) * 4
+    # The execution layer needs the device as well.
+    handle = ctypes.c_void_p()
+    assert lib.afhip_execution_create(0, None, ctypes.byref(handle)) == _lib.ERR_NOT_OPEN
 
 
 def test_gemm_grid_matches_reference():
