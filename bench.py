@@ -15,7 +15,7 @@ the stream it is launched on (afhip_timing_*) during the same run;
 `roofline` is the dominant one (largest average duration). `traffic` is the
 HBM bytes per launch from rocprofv3's FETCH_SIZE and WRITE_SIZE counters,
 scaled against a plain copy, as recorded in
-profiles/triangle_l384_hbm_traffic.md. `configs` measures BASELINE's other
+profiles/hbm_traffic_by_kernel.md. `configs` measures BASELINE's other
 configurations the same way. `cpu_baseline` is the CPU oracle
 (oracle/afref.c, one thread) on a bounded sample.
 """
@@ -38,7 +38,7 @@ PEAK_F32_TFLOPS = 157.3    # MI355X fp32, published
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, published
 L, CZ, CH = 384, 128, 128
 SEED = 0xAF2000
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_triangle_l384_and_q8_projection.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_by_kernel.md")
 
 
 def triangle_flops(length: int, cz: int, ch: int) -> dict:
@@ -246,7 +246,8 @@ def measure_configs(steps: int, warmup: int, which=(1, 2, 4, 5)) -> dict:
                  "triangle_tflops": round((f5["project"] + f5["contract"] + f5["output"] + f5["gate"]) / (ms * 1e-3) / 1e12, 2),
                  "triangle_kernel_ms": {kk: round(v, 5) for kk, v in k.items()}}
         if "triangle.contract" in k:
-            entry["contract"] = rate("triangle.contract", k["triangle.contract"], flops=f5["contract"])
+            entry["contract"] = rate("triangle.contract", k["triangle.contract"], flops=f5["contract"],
+                                     traffic=recorded_traffic().get("config5.contract"))
         rows5 = L5 * L5
         tw = {"layerNormScale": ref.normal(s + 20, (CZ,), 0.01, 1.0), "layerNormOffset": ref.normal(s + 21, (CZ,), 0.01),
               "firstWeight": ref.normal(s + 22, (CZ, 4 * CZ), 1 / CZ), "firstBias": ref.normal(s + 23, (4 * CZ,), 0.02),
@@ -259,6 +260,11 @@ def measure_configs(steps: int, warmup: int, which=(1, 2, 4, 5)) -> dict:
         ft = 2 * 2 * rows5 * CZ * 4 * CZ
         entry.update({"transition_ms": round(ms_t, 4), "transition_tflops": round(ft / (ms_t * 1e-3) / 1e12, 2),
                       "transition_kernel_ms": {kk: round(v, 5) for kk, v in k_t.items()}})
+        # The fused transition keeps the hidden activation on chip: MFMA-bound
+        # (274.9 GFLOP against 537 MB of f16 rows in and out).
+        if "transition.fused" in k_t:
+            entry["transition"] = rate("transition.fused", k_t["transition.fused"], flops=ft,
+                                       traffic=recorded_traffic().get("config5.transition"))
         out["5_long_complex_pair_stack_l1024"] = entry
     return out
 
