@@ -340,7 +340,7 @@ template <typename ZT, typename OT> struct OutputLayout {
   static constexpr int ZROW = kC * (int)sizeof(ZT);
   static constexpr int XBYTES = kC * kTile * 2;      // contraction tile, [128 channels][64 pairs] f16
   static constexpr int ZBYTES = kTile * ZROW;
-  static constexpr int RAW_STAGE = XBYTES + ZBYTES;
+  static constexpr int STAGE = XBYTES + ZBYTES;
   static constexpr int STAGES = sizeof(ZT) == 2 ? 3 : 2;
   static constexpr int XLOADS = XBYTES / 1024;       // 8 channel rows per load
   static constexpr int ZLOADS = ZBYTES / 1024;
@@ -348,24 +348,28 @@ template <typename ZT, typename OT> struct OutputLayout {
   static constexpr int ZROWS_PER_LOAD = 1024 / ZROW;
   static constexpr int ZLANES_PER_ROW = 64 / ZROWS_PER_LOAD;
   static constexpr int OROW = kC * (int)sizeof(OT);  // bytes of one output row
-  // The output tile is staged in the stage it came from (dead by then), rows
-  // padded by 16 bytes so the 32 pair rows one store instruction covers
-  // fall in different bank groups.
+  // The output tile is staged in a buffer of its own and written out while
+  // the next tile is normalised; rows padded by 16 bytes so the 32 pair rows
+  // one store instruction covers fall in different bank groups.
   static constexpr int OPITCH = OROW + 16;
-  static constexpr int STAGE = RAW_STAGE > kTile * OPITCH ? RAW_STAGE : kTile * OPITCH;
-  static constexpr int HN = STAGES * STAGE;
-  static constexpr int GN = HN + kTile * kPitch * 2;
+  // The normalised hidden tile (hn) lives in the tile's own stage, dead once
+  // its statistics and z's x_hat are taken.
+  static_assert(kTile * kPitch * 2 <= STAGE, "hn fits its stage");
+  static constexpr int GN = STAGES * STAGE;
   static constexpr int PART = GN + kTile * kPitch * 2;   // [8 waves][64 pairs] x (mean, m2)
-  static constexpr int BYTES = PART + 8 * kTile * 2 * 4;
+  static constexpr int OUT = PART + 8 * kTile * 2 * 4;
+  static constexpr int BYTES = OUT + kTile * OPITCH;
 };
+static_assert(OutputLayout<half_t, float>::BYTES <= 160 * 1024 && OutputLayout<float, float>::BYTES <= 160 * 1024,
+              "LDS budget");
 
 template <typename ZT, typename OT>
 __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputArgs a, int ntiles) {
   using Lay = OutputLayout<ZT, OT>;
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
-  half_t* hn = reinterpret_cast<half_t*>(smem + Lay::HN);
   half_t* gn = reinterpret_cast<half_t*>(smem + Lay::GN);
   float2* part = reinterpret_cast<float2*>(smem + Lay::PART);
+  unsigned char* const ob = smem + Lay::OUT;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -418,6 +422,39 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
     }
   };
 
+  // Waves 4-7 write a staged output tile: 64 pair rows of OROW bytes in
+  // 16-byte chunks, straight to [pair][128], the residual added when asked.
+  auto store_tile = [&](int t) {
+    constexpr int CHUNKS = Lay::OROW / 16;
+    constexpr int PER_LANE = kTile * CHUNKS / 256;
+    const int t4 = tid - kLoaderWaves * 64;
+    const int q0 = t * kTile;
+    static_assert(PER_LANE % 4 == 0, "stores go in groups of four");
+#pragma unroll
+    for (int k0 = 0; k0 < PER_LANE; k0 += 4) {
+      u32x4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int idx = t4 + 256 * (k0 + k);
+        const int q = idx / CHUNKS, chunk = idx % CHUNKS;
+        v[k] = *reinterpret_cast<const u32x4*>(ob + q * Lay::OPITCH + chunk * 16);
+        unsigned char* dst =
+            reinterpret_cast<unsigned char*>(a.out) + ((size_t)a.pair0 + q0 + q) * Lay::OROW + chunk * 16;
+        if (q0 + q >= a.pairs) continue;
+        if (a.residual) {
+          const u32x4 r = *reinterpret_cast<const u32x4*>(dst);
+          constexpr int E = 16 / (int)sizeof(OT);
+          OT* vv = reinterpret_cast<OT*>(&v[k]);
+          const OT* rr = reinterpret_cast<const OT*>(&r);
+#pragma unroll
+          for (int e = 0; e < E; e++) vv[e] = (OT)((float)vv[e] + (float)rr[e]);
+        }
+        *reinterpret_cast<u32x4*>(dst) = v[k];
+      }
+      stores_read(v[0], v[1], v[2], v[3]);
+    }
+  };
+
   int tile = blockIdx.x;
   if (wave < kLoaderWaves) {
 #pragma unroll
@@ -428,9 +465,13 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
   for (int it = 0; tile < ntiles; it++, tile += G) {
     const int stage = it % Lay::STAGES;
     if (wave < kLoaderWaves) wait_stage<(Lay::STAGES - 2) * Lay::LPW>(tile + (Lay::STAGES - 2) * G < ntiles);
-    block_barrier();  // B1: stage `it` complete; the previous tile's staging is written out
-    if (wave < kLoaderWaves && tile + (Lay::STAGES - 1) * G < ntiles)
-      issue(tile + (Lay::STAGES - 1) * G, (it + Lay::STAGES - 1) % Lay::STAGES);
+    block_barrier();  // B1: stage `it` complete; the previous tile is staged
+    if (wave < kLoaderWaves) {
+      if (tile + (Lay::STAGES - 1) * G < ntiles)
+        issue(tile + (Lay::STAGES - 1) * G, (it + Lay::STAGES - 1) % Lay::STAGES);
+    } else if (it > 0) {
+      store_tile(tile - G);  // the staging is read out before B3 and rewritten after it
+    }
 
     unsigned char* st = smem + stage * Lay::STAGE;
     // Hidden statistics, partial: wave w holds channels [16 w, 16 w + 16) of pair `lane`.
@@ -461,7 +502,8 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
       read8<ZT>(st + Lay::XBYTES + row * Lay::ZROW + c0 * (int)sizeof(ZT), x);
       normalize16(x, a.eps, gn + row * kPitch + c0);
     }
-    block_barrier();  // B2: partial statistics and gn complete
+    block_barrier();  // B2: partial statistics and gn complete; the stage is dead
+    half_t* const hn = reinterpret_cast<half_t*>(st);
     {
       // Chan et al.: merge eight (mean, M2) over 16 channels each.
       float mean = 0.0f;
@@ -487,7 +529,7 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
       reinterpret_cast<half8*>(dst)[0] = h0;
       reinterpret_cast<half8*>(dst)[1] = h1;
     }
-    block_barrier();  // B3: hn complete; the stage is dead and becomes the output staging
+    block_barrier();  // B3: hn complete; the staging has been read out
 
     // W (A operand) x x_hat^T (B operand): the accumulator's column is the
     // pair rh + lane % 32 and its rows come in runs of four consecutive
@@ -506,7 +548,7 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
       accg = mfma_f16(fg[s], *reinterpret_cast<const half8*>(grow + 16 * s), accg);
     }
     {
-      unsigned char* orow = st + (rh + (lane & 31)) * Lay::OPITCH;
+      unsigned char* orow = ob + (rh + (lane & 31)) * Lay::OPITCH;
 #pragma unroll
       for (int g4 = 0; g4 < 4; g4++) {
         const int n0 = nt + 8 * g4 + 4 * (lane >> 5);
@@ -523,40 +565,9 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
         }
       }
     }
-    block_barrier();  // B4: the output tile is staged
-
-    if (wave >= kLoaderWaves) {
-      // 64 pair rows of OROW bytes in 16-byte chunks, straight to [pair][128].
-      constexpr int CHUNKS = Lay::OROW / 16;
-      constexpr int PER_LANE = kTile * CHUNKS / 256;
-      const int t4 = tid - kLoaderWaves * 64;
-      const int q0 = tile * kTile;
-      static_assert(PER_LANE % 4 == 0, "stores go in groups of four");
-#pragma unroll
-      for (int k0 = 0; k0 < PER_LANE; k0 += 4) {
-        u32x4 v[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const int idx = t4 + 256 * (k0 + k);
-          const int q = idx / CHUNKS, chunk = idx % CHUNKS;
-          v[k] = *reinterpret_cast<const u32x4*>(st + q * Lay::OPITCH + chunk * 16);
-          unsigned char* dst =
-              reinterpret_cast<unsigned char*>(a.out) + ((size_t)a.pair0 + q0 + q) * Lay::OROW + chunk * 16;
-          if (q0 + q >= a.pairs) continue;
-          if (a.residual) {
-            const u32x4 r = *reinterpret_cast<const u32x4*>(dst);
-            constexpr int E = 16 / (int)sizeof(OT);
-            OT* vv = reinterpret_cast<OT*>(&v[k]);
-            const OT* rr = reinterpret_cast<const OT*>(&r);
-#pragma unroll
-            for (int e = 0; e < E; e++) vv[e] = (OT)((float)vv[e] + (float)rr[e]);
-          }
-          *reinterpret_cast<u32x4*>(dst) = v[k];
-        }
-        stores_read(v[0], v[1], v[2], v[3]);
-      }
-    }
   }
+  block_barrier();  // the last tile is staged
+  if (wave >= kLoaderWaves) store_tile(tile - G);
 }
 
 int grid_for(int tiles) {
