@@ -317,37 +317,26 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
       return;
     }
   }
-  if (g.flags == 0) {
-    // Plain store straight from the accumulators: lane holds row
-    // m0 + wm + 32 i + lane % 32 and, per group g4, columns
-    // n0 + wn + 32 j + 8 g4 + 4 (lane / 32) + [0, 4).
-    TC* C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
-    const bool vec4 = (g.ldc & 3) == 0 && ((reinterpret_cast<uintptr_t>(C) & (4 * sizeof(TC) - 1)) == 0);
+  if ((g.flags & ~gemm_detail::kRowwiseEpilogue) == 0) {
+    // Row-wise epilogues (plain, scale, bias, ReLU, residual, the
+    // outer-product-mean output's bias / (eps + count)) straight from the
+    // accumulators: lane holds row m0 + wm + 32 i + lane % 32 and, per group
+    // g4, columns n0 + wn + 32 j + 8 g4 + 4 (lane / 32) + [0, 4).
+    auto aligned4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & (4 * sizeof(TC) - 1)) == 0; };
+    const bool vec4 = (g.ldc & 3) == 0 && (g.sc & 3) == 0 && aligned4(g.c) &&
+                      (!(g.flags & AFHIP_EPILOGUE_RESIDUAL) || aligned4(g.residual));
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int row = m0 + wm + 32 * i + (lane & 31);
       if (row >= g.M) continue;
-      TC* crow = C + (int64_t)row * g.ldc;
 #pragma unroll
       for (int j = 0; j < TN; j++)
 #pragma unroll
         for (int g4 = 0; g4 < 4; g4++) {
           const int col = n0 + wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
-          if (vec4 && col + 3 < g.N) {
-            if constexpr (sizeof(TC) == 2) {
-              half4 h;
-#pragma unroll
-              for (int e = 0; e < 4; e++) h[e] = (half_t)acc[i][j][4 * g4 + e];
-              *reinterpret_cast<half4*>(crow + col) = h;
-            } else {
-              *reinterpret_cast<floatx4*>(crow + col) =
-                  floatx4{acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3]};
-            }
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-              if (col + e < g.N) crow[col + e] = (TC)acc[i][j][4 * g4 + e];
-          }
+          if (col >= g.N) continue;
+          float y[4] = {acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3]};
+          gemm_detail::epilogue_row4<TC>(g, bt, row, col, y, min(4, g.N - col), vec4);
         }
     }
     return;

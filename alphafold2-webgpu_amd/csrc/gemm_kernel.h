@@ -141,6 +141,50 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int b, int row
   reinterpret_cast<TC*>(g.c)[at] = (TC)y;
 }
 
+// Epilogue flags that act on one output row elementwise (everything but
+// ATTENTION, whose column blocks differ, and OPM_CONTRACT, which scatters).
+constexpr uint32_t kRowwiseEpilogue = AFHIP_EPILOGUE_SCALE | AFHIP_EPILOGUE_BIAS | AFHIP_EPILOGUE_RELU |
+                                      AFHIP_EPILOGUE_RESIDUAL | EPILOGUE_OPM_OUTPUT;
+
+// epilogue_store for `n` (<= 4) consecutive columns of one row, the same
+// steps in the same order with the same roundings, written with one vector
+// access when `vec` (all four columns present, row start and ldc aligned to
+// four elements).
+template <typename TC>
+__device__ __forceinline__ void epilogue_row4(const GemmArgs& g, int b, int row, int col, float* y, int n, bool vec) {
+#pragma clang fp contract(off)
+  const uint32_t flags = g.flags;
+  float denom = 0.0f;
+  if (flags & EPILOGUE_OPM_OUTPUT) denom = g.opm_eps + g.opm_count[(int64_t)g.opm_row0 + row];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    if (e >= n) break;
+    if (flags & AFHIP_EPILOGUE_SCALE) y[e] *= g.scale[col + e];
+    if (flags & AFHIP_EPILOGUE_BIAS) y[e] += g.bias[col + e];
+    if (flags & EPILOGUE_OPM_OUTPUT) y[e] += g.bias[col + e] / denom;
+    if (flags & AFHIP_EPILOGUE_RELU) y[e] = fmaxf(y[e], 0.0f);
+  }
+  const int64_t at = (int64_t)b * g.sc + (int64_t)row * g.ldc + col;
+  TC* c = reinterpret_cast<TC*>(g.c) + at;
+  if (vec && n == 4) {
+    typedef TC tc4 __attribute__((ext_vector_type(4)));
+    tc4 v;
+    if (flags & AFHIP_EPILOGUE_RESIDUAL) {
+      const tc4 r = *reinterpret_cast<const tc4*>(reinterpret_cast<const TC*>(g.residual) + at);
+#pragma unroll
+      for (int e = 0; e < 4; e++) y[e] += (float)r[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = (TC)y[e];
+    *reinterpret_cast<tc4*>(c) = v;
+    return;
+  }
+  for (int e = 0; e < n; e++) {
+    if (flags & AFHIP_EPILOGUE_RESIDUAL) y[e] += (float)reinterpret_cast<const TC*>(g.residual)[at + e];
+    c[e] = (TC)y[e];
+  }
+}
+
 template <int BM, int BN, bool F16MATH, typename TA, typename TB, typename TC, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(KernelArgs ka) {
   using CT = typename std::conditional<F16MATH, half_t, float>::type;

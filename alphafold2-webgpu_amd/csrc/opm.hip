@@ -64,7 +64,7 @@ OpmWeights opm_layout(const afhip_opm_desc& d) {
 }
 
 struct OpmWorkspace {
-  size_t left, right, outer, count, mask_t, total;
+  size_t left, right, outer, count, total;
   int64_t sp;  // sequence stride of left/right rows
   int row_block;
 };
@@ -85,7 +85,6 @@ OpmWorkspace opm_workspace(const afhip_opm_desc& d) {
   w.right = take(es * rows * w.sp);
   w.outer = take(es * (size_t)w.row_block * d.length * d.c_outer * d.c_outer);
   w.count = take(4 * (size_t)d.length * d.length);
-  w.mask_t = take(4 * (size_t)d.length * w.sp);
   w.total = at;
   return w;
 }
@@ -205,22 +204,45 @@ __global__ __launch_bounds__(256) void opm_project_kernel(ProjectArgs a) {
   }
 }
 
-// mask [S][L] -> mask_t [L][sp] (sequence axis contiguous, zero padded), the
-// k-contiguous operand layout of the pair-count GEMM. 32 x 32 tiles through LDS.
-__global__ __launch_bounds__(256) void opm_mask_transpose_kernel(const float* __restrict__ mask, int S, int L, int sp,
-                                                                 float* __restrict__ mask_t) {
-  __shared__ float tile[32][33];
-  const int s0 = blockIdx.x * 32, i0 = blockIdx.y * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-  for (int r = ty; r < 32; r += 8) {
-    const int s = s0 + r, i = i0 + tx;
-    tile[r][tx] = s < S && i < L ? mask[(int64_t)s * L + i] : 0.0f;
+// Pair counts count[i][j] = sum_s mask[s][i] mask[s][j] (the masked
+// sequence count per pair, outer-product-mean.ts:317-332): one 32 x 32 tile
+// of counts per workgroup. Its sixteen waves take interleaved two-sequence
+// steps of the f32 MFMA, both operands read straight from the [S][L] mask
+// (A = mask[s][i0 + m], B = mask[s][j0 + n]), then sum their partial tiles in
+// LDS in wave order, so the result does not depend on timing.
+constexpr int kCountWaves = 16;
+__global__ __launch_bounds__(64 * kCountWaves) void opm_pair_count_kernel(const float* __restrict__ mask, int S, int L,
+                                                                          float* __restrict__ count) {
+  __shared__ float part[kCountWaves][16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tiles = (L + 31) / 32;
+  const int i0 = (blockIdx.x / tiles) * 32, j0 = (blockIdx.x % tiles) * 32;
+  const int col = lane & 31, hi = lane >> 5;
+  const bool in_i = i0 + col < L, in_j = j0 + col < L;
+  floatx16 acc = {};
+  // Four steps' loads go out together before their MFMAs.
+  for (int s0 = 2 * wave; s0 < S; s0 += 8 * kCountWaves) {
+    float a[4], b[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int s = s0 + 2 * kCountWaves * u + hi;
+      a[u] = s < S && in_i ? mask[(int64_t)s * L + i0 + col] : 0.0f;
+      b[u] = s < S && in_j ? mask[(int64_t)s * L + j0 + col] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) acc = mfma_f32(a[u], b[u], acc);
   }
+#pragma unroll
+  for (int v = 0; v < 16; v++) part[wave][v][lane] = acc[v];
   __syncthreads();
-  for (int r = ty; r < 32; r += 8) {
-    const int i = i0 + r, s = s0 + tx;
-    if (i < L && s < sp) mask_t[(int64_t)i * sp + s] = tile[tx][r];
-  }
+  // Element (m, n) of the tile sits at row v = 4 (m / 8) + m % 4 of lane
+  // n + 32 ((m / 4) % 2).
+  const int m = threadIdx.x >> 5, n = threadIdx.x & 31;
+  const int v = 4 * (m >> 3) + (m & 3), l = n + 32 * ((m >> 2) & 1);
+  float sum = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kCountWaves; w++) sum += part[w][v][l];
+  if (i0 + m < L && j0 + n < L) count[(int64_t)(i0 + m) * L + j0 + n] = sum;
 }
 
 // ---------------------------------------------------------------------------
@@ -552,23 +574,11 @@ int afhip_opm_run(const afhip_opm_desc* desc, const void* activations, const flo
   if (s) return s;
 
   float* count = (float*)(wsb + ws.count);
-  float* mask_t = (float*)(wsb + ws.mask_t);
-  if ((s = launch("opm.mask_transpose", opm_mask_transpose_kernel,
-                  dim3((unsigned)ceil_div(ws.sp, 32), (unsigned)ceil_div(L, 32)), dim3(256), 0, st, mask, S, L,
-                  (int)ws.sp, mask_t)))
-    return s;
   {
-    GemmArgs g;
-    g.a = mask_t;
-    g.b = mask_t;
-    g.c = count;
-    g.M = L;
-    g.N = L;
-    g.K = (int)ws.sp;  // the zero padding adds nothing
-    g.lda = g.ldb = ws.sp;
-    g.ldc = L;
-    GemmTypes tc{AFHIP_PRECISION_F32, AFHIP_F32, AFHIP_F32, AFHIP_F32};
-    if ((s = run_gemm(g, tc, select_variant(tc, g.M, g.N, g.K, 1), "opm.pair_count", st))) return s;
+    const int64_t tiles = ceil_div(L, 32);
+    if ((s = launch("opm.pair_count", opm_pair_count_kernel, dim3((unsigned)(tiles * tiles)), dim3(64 * kCountWaves),
+                    0, st, mask, S, L, count)))
+      return s;
   }
 
   const int ct = f16 ? AFHIP_F16 : AFHIP_F32;

@@ -130,6 +130,47 @@ def test_lds_dma_tiles_match_register_kernel_bitwise(dev, out_dtype, shape):
         assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), key
 
 
+@pytest.mark.parametrize("out_dtype", ["f16", "f32"])
+@pytest.mark.parametrize("epilogue", [("bias", "relu"), ("scale", "bias", "residual"), ("bias", "relu", "residual")])
+def test_lds_dma_epilogues_match_register_kernel_bitwise(dev, out_dtype, epilogue):
+    # The row-wise epilogues the LDS_DMA family applies straight from its
+    # accumulators (four columns a lane, vector residual reads and stores)
+    # round every step as the register-staged kernel does: the same bits, a
+    # ragged last row and column tile included.
+    import torch
+
+    from afhip import gemm
+
+    M, K, N = 333, 192, 200
+    a = ref.round_f16(ref.normal(41, (M, K)))
+    w = ref.round_f16(ref.normal(42, (N, K), 1 / K))
+    scale = to_dev(ref.uniform(43, (N,), 0.5, 2.0), dev)
+    bias = to_dev(ref.normal(44, (N,), 0.1), dev)
+    tdt = torch.float16 if out_dtype == "f16" else torch.float32
+    base = to_dev(ref.round_f16(ref.normal(45, (M, N))), dev).to(tdt)
+    ad, wd = to_dev(a, dev).half(), to_dev(w, dev).half()
+    results = {}
+    for kernel, tiles in (("register", [(128, 128)]), ("lds_dma", LDS_DMA_TILES)):
+        for tr, tc in tiles:
+            gemm.force_variant(gemm.GemmVariant("f16", tr, tc, source="pinned", kernel=kernel))
+            try:
+                plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
+                                      out_dtype=out_dtype, epilogue=epilogue)
+                assert plan.variant().kernel == kernel
+                out = base.clone()
+                kw = {"bias": bias}
+                if "scale" in epilogue:
+                    kw["scale"] = scale
+                if "residual" in epilogue:
+                    kw["residual"] = out
+                results[(kernel, tr, tc)] = plan.run(ad, wd, out=out, **kw).float().cpu().numpy()
+            finally:
+                gemm.force_variant(None)
+    base_r = results[("register", 128, 128)]
+    for key, got in results.items():
+        assert np.array_equal(got.view(np.uint32), base_r.view(np.uint32)), key
+
+
 @pytest.mark.parametrize("shape", [
     # rows, K, N, weight dtype, epilogue, lda
     (5000, 256, 1024, "i8", ("scale", "attention"), 0),  # config 2's shape, ragged last tile

@@ -70,6 +70,25 @@ def test_opm_synthetic(dev, S, L, cm, co, cz):
     assert np.abs(out16.reshape(expect.shape) - expect).max() <= 1e-2 * scale
 
 
+@pytest.mark.parametrize("S,L", [(37, 45), (512, 33), (3, 70)])
+def test_opm_fractional_mask_counts(dev, S, L):
+    # Fractional mask values (the count is a sum of products, not of ones)
+    # with S and L off the 32-wide count tiles, against the oracle.
+    from afhip import opm
+
+    cm, co, cz = 16, 8, 12
+    act = ref.normal(S * 7 + L, (S, L, cm))
+    mask = ref.uniform(S + 3 * L, (S, L), 0, 1)
+    mask[mask < 0.2] = 0.0
+    w = {"layerNormScale": ref.normal(1, (cm,), 0.01, 1.0), "layerNormOffset": ref.normal(2, (cm,), 0.01),
+         "leftWeight": ref.normal(3, (cm, co), 1 / cm), "leftBias": ref.normal(4, (co,), 0.02),
+         "rightWeight": ref.normal(5, (cm, co), 1 / cm), "rightBias": ref.normal(6, (co,), 0.02),
+         "outputWeight": ref.normal(7, (co * co, cz), 1 / (co * co)), "outputBias": ref.normal(8, (cz,), 0.02)}
+    expect = ref.opm(act, mask, w)
+    out = opm.OuterProductMeanGpu().run(opm_input(act, mask, w))["output"].reshape(expect.shape)
+    assert np.abs(out - expect).max() <= 1e-5 * max(1.0, float(np.abs(expect).max()))
+
+
 @pytest.mark.parametrize("S,L,cm,msa_dtype", [(100, 9, 256, "f16"), (130, 5, 64, "f32"), (64, 7, 128, "f16")])
 def test_opm_f16_fast_projection(dev, S, L, cm, msa_dtype):
     # The persistent f16 projection (c_outer 32, c_m 64/128/256): ragged
