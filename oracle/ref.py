@@ -35,6 +35,9 @@ PINS = {
     "opm": "numpy float64 restatement of AlphaFold's OuterProductMean; closed forms (rank one, all-ones "
            "mask count = S)",
     "transition": "numpy float64 restatement; closed form with ReLU inactive",
+    "attention": "closed forms: a fully masked row averages v (the logit clamp), a one-hot pair bias "
+                 "selects one key, zero query weights give uniform weights; transpose equivalence; a "
+                 "loop-over-keys restatement with an explicit running softmax at small sizes",
 }
 
 
@@ -329,3 +332,87 @@ def error_metrics(actual, expected) -> dict:
     d = np.abs(a - e)
     return {"meanAbsoluteError": float(d.mean()), "maxAbsoluteError": float(d.max()),
             "rootMeanSquareError": float(np.sqrt((d * d).mean()))}
+
+
+# --- attention ----------------------------------------------------------------
+
+ATTENTION_ORDER = ("queryNormScale", "queryNormOffset", "queryWeight", "keyWeight", "valueWeight",
+                   "gatingWeight", "gatingBias", "outputWeight", "outputBias")
+
+
+def pack_attention_weights(weights: dict, pair_bias: dict | None = None) -> np.ndarray:
+    """src/evoformer/attention.ts:179-201 (packAttentionWeights): the nine
+    tensors, then for a separate pair bias its LayerNorm scale and offset and
+    projection, or for a normalized-input bias its projection."""
+    tensors = [_c32(weights[n]).reshape(-1) for n in ATTENTION_ORDER]
+    if pair_bias is not None:
+        if pair_bias["source"] == "separate":
+            tensors += [_c32(pair_bias[n]).reshape(-1) for n in ("layerNormScale", "layerNormOffset",
+                                                                  "projectionWeight")]
+        else:
+            tensors.append(_c32(pair_bias["projectionWeight"]).reshape(-1))
+    return np.concatenate(tensors)
+
+
+def _layer_norm64(x, scale, offset, eps):
+    """Row LayerNorm, two-pass mean and biased variance, eps inside the root
+    (attention.ts:312-324)."""
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    return (x - mean) / np.sqrt(var + eps) * scale + offset
+
+
+def attention(activations, mask, weights: dict, batch: int, queries: int, channels: int, heads: int,
+              transpose: bool = False, pair_bias: dict | None = None, epsilon: float = 1e-5) -> np.ndarray:
+    """src/evoformer/attention.ts:1334-1452 (AttentionGpu.run), in float64.
+
+    Rows are taken in attention order: entry (b, q) of the batch is source row
+    b * queries + q, or q * batch + b when transposed (:312-317), as is the
+    mask (:428-433). LayerNorm with the query norm; q = x_hat Wq / sqrt(d),
+    k, v = x_hat Wk, x_hat Wv, g = sigmoid(x_hat Wg + bg) (:497-560, weights
+    [in][out]); a pair bias bias[h][q][k] = y[q][k] . Wb[:, h] with y the
+    normalised input in attention order (normalized-input, which needs
+    batch == queries) or the LayerNormed separate pair activations
+    (:631-661, :1378-1420); logits q.k + 1e9 (mask[b][k] - 1) + bias, clamped
+    to [-1e8, 1e8], softmax over keys, times the gate (:688-723); then
+    y Wo + bo written back in source order (:1261-1316)."""
+    B, Q, C, H = batch, queries, channels, heads
+    d = C // H
+    x = np.asarray(activations, np.float64).reshape(-1)
+    m = np.asarray(mask, np.float64).reshape(-1)
+    if transpose:
+        X = x.reshape(Q, B, C).transpose(1, 0, 2)
+        M = m.reshape(Q, B).T
+    else:
+        X = x.reshape(B, Q, C)
+        M = m.reshape(B, Q)
+    w = {k: np.asarray(v, np.float64) for k, v in weights.items()}
+    Xn = _layer_norm64(X, w["queryNormScale"], w["queryNormOffset"], epsilon)
+    q = (Xn @ w["queryWeight"].reshape(C, C)).reshape(B, Q, H, d) / np.sqrt(d)
+    k = (Xn @ w["keyWeight"].reshape(C, C)).reshape(B, Q, H, d)
+    v = (Xn @ w["valueWeight"].reshape(C, C)).reshape(B, Q, H, d)
+    g = 1.0 / (1.0 + np.exp(-(Xn @ w["gatingWeight"].reshape(C, C) + w["gatingBias"]))).reshape(B, Q, H, d)
+    logits = np.einsum("bqhd,bkhd->bhqk", q, k) + 1e9 * (M[:, None, None, :] - 1.0)
+    if pair_bias is not None:
+        if pair_bias["source"] == "separate":
+            P = np.asarray(pair_bias["activations"], np.float64)
+            Cp = int(pair_bias["channels"])
+            P = _layer_norm64(P.reshape(Q, Q, Cp), np.asarray(pair_bias["layerNormScale"], np.float64),
+                              np.asarray(pair_bias["layerNormOffset"], np.float64), epsilon)
+            Wb = np.asarray(pair_bias["projectionWeight"], np.float64).reshape(Cp, H)
+        else:
+            if B != Q:
+                raise ValueError("a normalized-input pair bias needs batch == queries")
+            P = Xn
+            Wb = np.asarray(pair_bias["projectionWeight"], np.float64).reshape(C, H)
+        bias = np.einsum("qkc,ch->hqk", P, Wb)
+        logits = logits + bias[None]
+    logits = np.clip(logits, -1e8, 1e8)
+    logits = logits - logits.max(axis=-1, keepdims=True)
+    a = np.exp(logits)
+    a /= a.sum(axis=-1, keepdims=True)
+    o = np.einsum("bhqk,bkhd->bqhd", a, v) * g
+    y = o.reshape(B, Q, C) @ w["outputWeight"].reshape(C, C) + w["outputBias"]
+    if transpose:
+        y = y.transpose(1, 0, 2)
+    return y.reshape(-1).astype(np.float32)

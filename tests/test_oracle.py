@@ -294,3 +294,187 @@ def test_error_metrics_exact():
     # test/cpu-reference.test.ts:36-42
     m = ref.error_metrics(np.array([1, 3], np.float32), np.array([2, 1], np.float32))
     assert m == {"meanAbsoluteError": 1.5, "maxAbsoluteError": 2.0, "rootMeanSquareError": np.sqrt(2.5)}
+
+
+# --- attention (src/evoformer/attention.ts:1334-1452) ------------------------
+# The reference's attention goldens (test/evoformer-attention.gpu.test.ts
+# against test/fixtures/evoformer/model1-query-59-block0) are not in the
+# reference tree, so the oracle is pinned by closed forms and by a second,
+# loop-over-keys restatement with a running softmax.
+
+def _pattern_rows(n_rows, C, seed):
+    """Rows a_r * u_r with u_r a +-1 pattern of zero mean and unit variance:
+    their LayerNorm is u_r * a_r / sqrt(a_r^2 + eps) exactly (scale 1,
+    offset 0)."""
+    rng = np.random.default_rng(seed)
+    u = np.empty((n_rows, C))
+    for r in range(n_rows):
+        signs = np.array([1.0] * (C // 2) + [-1.0] * (C // 2))
+        u[r] = rng.permutation(signs)
+    a = rng.uniform(0.5, 2.0, (n_rows, 1))
+    return (u * a).astype(np.float32), u * a / np.sqrt(a * a + 1e-5)
+
+
+def _attention_weights(C, seed, zero_qk=False):
+    rng = np.random.default_rng(seed)
+    w = {"queryNormScale": np.ones(C, np.float32), "queryNormOffset": np.zeros(C, np.float32),
+         "queryWeight": rng.normal(0, C ** -0.5, (C, C)).astype(np.float32),
+         "keyWeight": rng.normal(0, C ** -0.5, (C, C)).astype(np.float32),
+         "valueWeight": rng.normal(0, C ** -0.5, (C, C)).astype(np.float32),
+         "gatingWeight": rng.normal(0, C ** -0.5, (C, C)).astype(np.float32),
+         "gatingBias": rng.normal(0, 0.3, C).astype(np.float32),
+         "outputWeight": rng.normal(0, C ** -0.5, (C, C)).astype(np.float32),
+         "outputBias": rng.normal(0, 0.1, C).astype(np.float32)}
+    if zero_qk:
+        w["queryWeight"][:] = 0
+        w["keyWeight"][:] = 0
+    return w
+
+
+def _sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_attention_uniform_weights_closed_form(transpose):
+    # Zero query and key weights and no bias: every key weighs 1/Q, so the
+    # output is mean_k(v) * g projected, with v and g from closed-form x_hat.
+    B, Q, C, H = 3, 5, 8, 2
+    x, xhat = _pattern_rows(B * Q, C, 1)
+    w = _attention_weights(C, 2, zero_qk=True)
+    got = ref.attention(x, np.ones(B * Q), w, B, Q, C, H, transpose=transpose).reshape(-1, C)
+    # attention order: entry (b, q) is source row b Q + q, or q B + b transposed
+    rows = lambda b, q: q * B + b if transpose else b * Q + q
+    for b in range(B):
+        v = np.stack([xhat[rows(b, k)] @ w["valueWeight"] for k in range(Q)])
+        for q in range(Q):
+            g = _sigmoid(xhat[rows(b, q)] @ w["gatingWeight"] + w["gatingBias"])
+            y = (v.mean(axis=0) * g) @ w["outputWeight"] + w["outputBias"]
+            assert np.allclose(got[rows(b, q)], y, rtol=1e-5, atol=1e-6)
+
+
+def test_attention_fully_masked_row_averages_values():
+    # Every key of batch row 1 masked: each logit is q.k - 1e9, clamped to
+    # -1e8, so the weights are uniform whatever q and k are.
+    B, Q, C, H = 3, 6, 8, 4
+    x, xhat = _pattern_rows(B * Q, C, 3)
+    w = _attention_weights(C, 4)
+    mask = np.ones(B * Q)
+    mask[Q:2 * Q] = 0
+    got = ref.attention(x, mask, w, B, Q, C, H).reshape(B, Q, C)
+    v = xhat[Q:2 * Q] @ w["valueWeight"]
+    for q in range(Q):
+        g = _sigmoid(xhat[Q + q] @ w["gatingWeight"] + w["gatingBias"])
+        y = (v.mean(axis=0) * g) @ w["outputWeight"] + w["outputBias"]
+        assert np.allclose(got[1, q], y, rtol=1e-5, atol=1e-6)
+
+
+def test_attention_one_hot_pair_bias_selects_a_key():
+    # Normalized-input bias through channel 0 only, +-1 there by construction,
+    # times 40 per head: the chosen key outweighs every other by e^80, so the
+    # output is that key's value times the query's gate.
+    Q, C, H = 6, 8, 2
+    B = Q
+    rng = np.random.default_rng(5)
+    pick = rng.integers(0, Q, Q)  # the key each query attends to (the same in every batch row)
+    u = np.empty((B * Q, C))
+    for b in range(B):
+        for k in range(Q):
+            first = 1.0 if k == pick[b] else -1.0
+            # the other seven channels bring the row to four +1 and four -1
+            rest = rng.permutation([1.0] * (3 if first > 0 else 4) + [-1.0] * (4 if first > 0 else 3))
+            u[b * Q + k] = np.concatenate([[first], rest])
+    # each row has four +1 and four -1 entries: zero mean, unit variance
+    assert np.allclose(u.mean(axis=1), 0) and np.allclose((u * u).mean(axis=1), 1)
+    x = u.astype(np.float32)
+    xhat = u / np.sqrt(1 + 1e-5)
+    w = _attention_weights(C, 6, zero_qk=True)
+    wb = np.zeros((C, H), np.float32)
+    wb[0, :] = 40.0
+    got = ref.attention(x, np.ones(B * Q), w, B, Q, C, H,
+                        pair_bias={"source": "normalized-input", "projectionWeight": wb}).reshape(B, Q, C)
+    for b in range(B):
+        for q in range(Q):
+            # bias[h][q][k] = xhat[q][k] . wb: query q of every batch row favours key pick[q]
+            v = xhat[b * Q + pick[q]] @ w["valueWeight"]
+            g = _sigmoid(xhat[b * Q + q] @ w["gatingWeight"] + w["gatingBias"])
+            assert np.allclose(got[b, q], (v * g) @ w["outputWeight"] + w["outputBias"], rtol=1e-6, atol=1e-6)
+
+
+def _attention_by_loops(x, mask, w, B, Q, C, H, transpose, pair_bias, eps=1e-5):
+    """A second restatement: per (b, h, q) a loop over keys with a running
+    maximum and sum (the reference's flash recurrence, attention.ts:688-723)."""
+    d = C // H
+    x = np.asarray(x, np.float64).reshape(-1, C)
+    src = lambda b, q: q * B + b if transpose else b * Q + q
+    xn = np.zeros((B, Q, C))
+    for b in range(B):
+        for q in range(Q):
+            r = x[src(b, q)]
+            mu = sum(r) / C
+            var = sum((r - mu) ** 2) / C
+            xn[b, q] = (r - mu) / np.sqrt(var + eps) * w["queryNormScale"] + w["queryNormOffset"]
+    bias = None
+    if pair_bias is not None:
+        if pair_bias["source"] == "separate":
+            Cp = pair_bias["channels"]
+            P = np.asarray(pair_bias["activations"], np.float64).reshape(Q, Q, Cp)
+            mu = P.mean(axis=-1, keepdims=True)
+            var = ((P - mu) ** 2).mean(axis=-1, keepdims=True)
+            Pn = (P - mu) / np.sqrt(var + eps) * pair_bias["layerNormScale"] + pair_bias["layerNormOffset"]
+            Wb = np.asarray(pair_bias["projectionWeight"], np.float64).reshape(Cp, H)
+        else:
+            Pn, Wb = xn, np.asarray(pair_bias["projectionWeight"], np.float64).reshape(C, H)
+        bias = lambda h, q, k: float(Pn[q, k] @ Wb[:, h])
+    out = np.zeros((B * Q, C))
+    for b in range(B):
+        qs = xn[b] @ w["queryWeight"] / np.sqrt(d)
+        ks = xn[b] @ w["keyWeight"]
+        vs = xn[b] @ w["valueWeight"]
+        gs = _sigmoid(xn[b] @ w["gatingWeight"] + w["gatingBias"])
+        o = np.zeros((Q, C))
+        for h in range(H):
+            cols = slice(h * d, (h + 1) * d)
+            for q in range(Q):
+                run_max, run_sum, acc = -1e30, 0.0, np.zeros(d)
+                for k in range(Q):
+                    mk = mask[k * B + b] if transpose else mask[b * Q + k]
+                    logit = float(qs[q, cols] @ ks[k, cols]) + 1e9 * (mk - 1.0)
+                    if bias is not None:
+                        logit += bias(h, q, k)
+                    logit = min(max(logit, -1e8), 1e8)
+                    new_max = max(run_max, logit)
+                    scale, weight = np.exp(run_max - new_max), np.exp(logit - new_max)
+                    run_sum = run_sum * scale + weight
+                    acc = acc * scale + weight * vs[k, cols]
+                    run_max = new_max
+                o[q, cols] = acc / run_sum * gs[q, cols]
+        y = o @ w["outputWeight"] + w["outputBias"]
+        for q in range(Q):
+            out[src(b, q)] = y[q]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("transpose,source", [(False, "separate"), (True, None), (False, "normalized-input"),
+                                              (True, "normalized-input")])
+def test_attention_matches_loop_restatement(transpose, source):
+    rng = np.random.default_rng(7)
+    Q, C, H, Cp = 5, 8, 2, 6
+    B = Q if source == "normalized-input" else 3
+    x = rng.normal(0, 1, B * Q * C).astype(np.float32)
+    mask = (rng.uniform(0, 1, B * Q) > 0.3).astype(np.float32)
+    mask[:Q] = 0.0  # one fully masked stretch of the mask as well
+    w = _attention_weights(C, 8)
+    w["queryNormScale"] = rng.normal(1, 0.1, C).astype(np.float32)
+    w["queryNormOffset"] = rng.normal(0, 0.1, C).astype(np.float32)
+    pb = None
+    if source == "separate":
+        pb = {"source": "separate", "activations": rng.normal(0, 1, Q * Q * Cp).astype(np.float32), "channels": Cp,
+              "layerNormScale": rng.normal(1, 0.1, Cp).astype(np.float32),
+              "layerNormOffset": rng.normal(0, 0.1, Cp).astype(np.float32),
+              "projectionWeight": rng.normal(0, 1, Cp * H).astype(np.float32)}
+    elif source is not None:
+        pb = {"source": source, "projectionWeight": rng.normal(0, 1, C * H).astype(np.float32)}
+    got = ref.attention(x, mask, w, B, Q, C, H, transpose=transpose, pair_bias=pb)
+    expect = _attention_by_loops(x, mask, w, B, Q, C, H, transpose, pb)
+    assert np.allclose(got, expect, rtol=1e-5, atol=1e-6)
