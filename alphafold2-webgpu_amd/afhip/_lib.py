@@ -38,6 +38,10 @@ KERNEL_STREAM = 2
 TRIANGLE_OUTGOING = 0
 TRIANGLE_INCOMING = 1
 
+PAIR_BIAS_NONE = 0
+PAIR_BIAS_NORMALIZED_INPUT = 1
+PAIR_BIAS_SEPARATE = 2
+
 
 class AfhipUnavailable(RuntimeError):
     """libafhip.so is not built or cannot be loaded; nothing falls back."""
@@ -98,6 +102,15 @@ class TransitionDesc(ctypes.Structure):
     ]
 
 
+class AttentionDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32), ("queries", ctypes.c_int32), ("channels", ctypes.c_int32),
+        ("heads", ctypes.c_int32), ("transpose", ctypes.c_int32), ("pair_bias", ctypes.c_int32),
+        ("pair_channels", ctypes.c_int32), ("precision", ctypes.c_int32), ("in_dtype", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32), ("residual", ctypes.c_int32), ("epsilon", ctypes.c_float),
+    ]
+
+
 class PairStackDesc(ctypes.Structure):
     _fields_ = [("opm", OpmDesc), ("outgoing", TriangleDesc), ("incoming", TriangleDesc),
                 ("transition", TransitionDesc)]
@@ -152,6 +165,10 @@ SIGNATURES = {
     "afhip_transition_workspace_size": [ctypes.POINTER(TransitionDesc), _szp],
     "afhip_transition_prepare_weights": [ctypes.POINTER(TransitionDesc), _vp, _vp, _vp],
     "afhip_transition_run": [ctypes.POINTER(TransitionDesc), _vp, _vp, _vp, _vp, _sz, _vp],
+    "afhip_attention_weights_size": [ctypes.POINTER(AttentionDesc), _szp],
+    "afhip_attention_workspace_size": [ctypes.POINTER(AttentionDesc), _szp],
+    "afhip_attention_prepare_weights": [ctypes.POINTER(AttentionDesc), _vp, _vp, _vp],
+    "afhip_attention_run": [ctypes.POINTER(AttentionDesc), _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "afhip_set_memory_budget": [ctypes.c_uint64],
     "afhip_memory_resident": [ctypes.POINTER(ctypes.c_uint64)],
     "afhip_execution_create": [ctypes.c_uint64, _vp, ctypes.POINTER(_vp)],

@@ -333,6 +333,53 @@ AFHIP_API int afhip_transition_run(const afhip_transition_desc* desc, const void
                          void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Gated attention with pair bias                                          */
+/* ---------------------------------------------------------------------- */
+
+/* Pair bias sources (AttentionPairBias, src/evoformer/attention.ts:31-45). */
+#define AFHIP_PAIR_BIAS_NONE 0
+#define AFHIP_PAIR_BIAS_NORMALIZED_INPUT 1 /* the normalised input itself; batch == queries */
+#define AFHIP_PAIR_BIAS_SEPARATE 2         /* pair activations [queries][queries][pair_channels] */
+
+/* Replaces AttentionGpu.run (src/evoformer/attention.ts:1321-1452) and the
+ * block encoder's encodeAttention (src/evoformer/block.ts): MSA row attention
+ * with pair bias (separate), MSA column attention (transposed, no bias),
+ * triangle attention starting and ending node (normalized-input, the ending
+ * node transposed). Limits as validate (attention.ts:102-141): head
+ * dimension channels / heads integral and at most 32. */
+typedef struct afhip_attention_desc {
+  int32_t batch;         /* B */
+  int32_t queries;       /* Q (AttentionInput.queryLength) */
+  int32_t channels;      /* C */
+  int32_t heads;         /* H, at most 8 */
+  int32_t transpose;     /* entry (b, q) is source row q*B + b instead of b*Q + q */
+  int32_t pair_bias;     /* AFHIP_PAIR_BIAS_* */
+  int32_t pair_channels; /* SEPARATE only */
+  int32_t precision;     /* AFHIP_PRECISION_* */
+  int32_t in_dtype;      /* activations and pair activations: AFHIP_F32 | AFHIP_F16 */
+  int32_t out_dtype;     /* AFHIP_F32 | AFHIP_F16 */
+  int32_t residual;      /* out += result */
+  float epsilon;         /* LayerNorm epsilon, 1e-5 by default */
+} afhip_attention_desc;
+
+AFHIP_API int afhip_attention_weights_size(const afhip_attention_desc* desc, size_t* bytes);
+AFHIP_API int afhip_attention_workspace_size(const afhip_attention_desc* desc, size_t* bytes);
+/* packed: f32 in the order of packAttentionWeights (attention.ts:179-201):
+ * queryNormScale [C], queryNormOffset [C], query/key/value/gatingWeight
+ * [C][C] each ([in][out]), gatingBias [C], outputWeight [C][C], outputBias
+ * [C]; then for SEPARATE the pair layerNormScale and layerNormOffset
+ * [pair_channels] and projectionWeight [pair_channels][H], for
+ * NORMALIZED_INPUT projectionWeight [C][H]. */
+AFHIP_API int afhip_attention_prepare_weights(const afhip_attention_desc* desc, const float* packed, void* prepared,
+                                    void* stream);
+/* activations [B*Q][C] in source order; mask [B*Q] f32 in source order;
+ * pair_activations [Q][Q][pair_channels] (SEPARATE, else NULL); out [B*Q][C]
+ * in source order. */
+AFHIP_API int afhip_attention_run(const afhip_attention_desc* desc, const void* activations, const float* mask,
+                        const void* pair_activations, const void* prepared, void* out, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* Execution layer                                                         */
 /* ---------------------------------------------------------------------- */
 

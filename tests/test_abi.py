@@ -94,6 +94,25 @@ def test_descriptor_validation_is_host_side():
     assert lib.afhip_opm_workspace_size(ctypes.byref(opm), ctypes.byref(size)) == _lib.OK
     tr = _lib.TransitionDesc(0, 128, 512, 1, 1, 0, 0, 1e-5)
     assert lib.afhip_transition_workspace_size(ctypes.byref(tr), ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+    # attention: validate (src/evoformer/attention.ts:102-141) and the pair bias sources
+    att = _lib.AttentionDesc(64, 64, 128, 4, 0, _lib.PAIR_BIAS_NORMALIZED_INPUT, 0, 1, 1, 1, 1, 1e-5)
+    assert lib.afhip_attention_workspace_size(ctypes.byref(att), ctypes.byref(size)) == _lib.OK
+    assert lib.afhip_attention_weights_size(ctypes.byref(att), ctypes.byref(size)) == _lib.OK
+    att.heads = 3
+    assert lib.afhip_attention_workspace_size(ctypes.byref(att), ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+    assert "head dimension no larger than 32" in _lib.last_error()
+    att.heads, att.channels = 2, 128  # head dimension 64
+    assert lib.afhip_attention_workspace_size(ctypes.byref(att), ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+    att.heads, att.batch = 4, 63
+    assert lib.afhip_attention_workspace_size(ctypes.byref(att), ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+    assert "batch == queries" in _lib.last_error()
+    att.pair_bias = _lib.PAIR_BIAS_SEPARATE
+    assert lib.afhip_attention_workspace_size(ctypes.byref(att), ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+    assert "pair channels" in _lib.last_error()
+    att.pair_channels = 128
+    assert lib.afhip_attention_workspace_size(ctypes.byref(att), ctypes.byref(size)) == _lib.OK
+    assert lib.afhip_attention_run(ctypes.byref(att), None, None, None, None, None, None, 0,
+                                   None) == _lib.ERR_NOT_OPEN
 
 
 def test_variant_selection_without_device():
