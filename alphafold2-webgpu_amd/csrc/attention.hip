@@ -12,13 +12,21 @@
 //   o = softmax_k(clamp(q.k + 1e9 (mask[b][k] - 1) + bias, -1e8, 1e8)) v * g;
 //   out = o Wo + bo (+ out), back in source order.
 //
-// The attention step itself is a flash kernel. At f16 precision with
-// head_dim 32 it runs on the MFMA as S^T = K Q^T and O^T = V^T P^T: a lane
-// then holds one query's scores for 16 keys and the same query's output for
-// 16 channels, so the running maximum, sum and rescale stay inside the lane
-// (one exchange with the lane 32 away), and the probabilities feed the second
-// MFMA from the registers they were computed in. Any other head dimension or
-// f32 precision runs a one-thread-per-query kernel in f32.
+// Kernels: a row kernel (LayerNorm in attention order, the key bias, and the
+// normalized-input pair bias from the same registers), the projection GEMM,
+// a row kernel for a separate pair source, the flash kernel, the output GEMM.
+//
+// At f16 precision with head dimension 32 the flash kernel runs on the MFMA
+// as S^T = K Q^T and O^T = V^T P^T: a lane then holds one query's scores for
+// 16 keys and the same query's output for 16 channels, so the running maximum,
+// sum and rescale stay inside the lane (one exchange with the lane 32 away),
+// and the probabilities feed the second MFMA from the registers they were
+// computed in. V^T comes from a pre-pass that lays each 32-key block out in
+// the key order of those registers, so every fragment is one 16-byte load.
+// Its logits are kept in base-2 units (q, the key bias and the pair bias
+// carry a factor log2(e)), which changes nothing but the rounding:
+// exp2(log2(e) x) = exp(x). Any other head dimension, or f32 precision, runs
+// a one-thread-per-query kernel in f32 on the natural units.
 #include <algorithm>
 #include <cmath>
 #include <utility>
@@ -28,6 +36,12 @@
 namespace afhip {
 
 namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+bool fast_path(const afhip_attention_desc& d) {
+  return d.precision == AFHIP_PRECISION_F16 && d.channels == 32 * d.heads;
+}
 
 // Prepared weights: everything the kernels read, in their dtypes.
 struct AttentionWeights {
@@ -58,26 +72,39 @@ AttentionWeights weights_layout(const afhip_attention_desc& d) {
   return w;
 }
 
+// Workspace. The key bias [B][stride] and the pair bias [H][Q][stride] rows
+// are padded to a multiple of four keys, so the flash kernels read them as
+// float4; the padding is never used as a live key. On the fast path the
+// flash kernel reads one key block ahead of the one it computes, up to 63
+// keys past the last, so the tensors it reads end in that much padding.
 struct AttentionWorkspace {
-  size_t normalized, key_bias, qkvg, bias, weighted, total;
-  int bias_stride;
+  size_t normalized, key_bias, key_mask, qkvg, bias, vt, weighted, total;
+  int stride, key_blocks;
 };
+
+constexpr int kReadAhead = 64;  // keys
 
 AttentionWorkspace workspace_layout(const afhip_attention_desc& d) {
   AttentionWorkspace w{};
   const size_t es = d.precision == AFHIP_PRECISION_F16 ? 2 : 4;
   const size_t rows = (size_t)d.batch * d.queries, C = d.channels;
+  const bool fast = fast_path(d);
   size_t at = 0;
   auto take = [&](size_t bytes) {
     size_t here = at;
     at = round_up((int64_t)(at + bytes), 256);
     return here;
   };
-  w.bias_stride = (int)round_up(d.queries, 4);
+  w.stride = (int)round_up(d.queries, 4);
+  w.key_blocks = (int)ceil_div(d.queries, 32);
   w.normalized = take(es * rows * C);
-  w.key_bias = take(4 * rows);
-  w.qkvg = take(es * rows * 4 * C);
-  w.bias = take(d.pair_bias ? 4 * (size_t)d.heads * d.queries * w.bias_stride : 0);
+  w.key_bias = take(fast ? 0 : 4 * (size_t)d.batch * w.stride);
+  // f16 key mask codes [B][stride] (fast path)
+  w.key_mask = take(fast ? 2 * ((size_t)d.batch * w.stride + kReadAhead) : 0);
+  w.qkvg = take(es * (rows + (fast ? kReadAhead : 0)) * 4 * C);
+  w.bias = take(d.pair_bias ? 4 * ((size_t)d.heads * d.queries * w.stride + (fast ? kReadAhead : 0)) : 0);
+  // V^T blocks [B][H][key block][32 channels][32 keys] (fast path), and two spare blocks
+  w.vt = take(fast ? 2 * ((size_t)d.batch * d.heads * w.key_blocks + 2) * 1024 : 0);
   w.weighted = take(es * rows * C);
   w.total = at;
   return w;
@@ -101,6 +128,8 @@ int validate(const afhip_attention_desc* dp) {
   AFHIP_REQUIRE(valid_precision(d.precision), "unknown precision %d", d.precision);
   AFHIP_REQUIRE(valid_float_dtype(d.in_dtype) && valid_float_dtype(d.out_dtype), "attention dtypes are f32 or f16");
   AFHIP_REQUIRE((int64_t)d.batch * d.queries < ((int64_t)1 << 31), "attention has too many rows");
+  AFHIP_REQUIRE((int64_t)d.heads * d.queries * round_up(d.queries, 4) < ((int64_t)1 << 31),
+                "attention has too many queries");
   return AFHIP_OK;
 }
 
@@ -170,90 +199,169 @@ __global__ void attention_prepare_kernel(const float* __restrict__ packed, int C
   }
 }
 
-// LayerNorm of the rows in attention order, one wave a row: x_hat in the
-// compute dtype, and the row's key bias 1e9 (mask - 1) (attention.ts:688-690).
-template <typename IT, typename CT>
-__global__ __launch_bounds__(256) void attention_norm_kernel(const IT* __restrict__ x, const float* __restrict__ mask,
-                                                             int B, int Q, int C, int transpose,
-                                                             const float* __restrict__ scale,
-                                                             const float* __restrict__ offset, float eps,
-                                                             CT* __restrict__ out, float* __restrict__ key_bias) {
+// One row pass over [rows][C]: LayerNorm (two-pass mean and biased variance,
+// eps inside the root, attention.ts:312-324) and, as asked, the normalised
+// row, the row's key bias key_scale (mask - 1) (:688-690), and the pair bias
+// bias[h][r / Q][r % Q] = bias_scale (y . w[:, h]) (:631-661).
+struct RowsArgs {
+  const void* x;
+  int64_t rows;
+  int C, B, Q, transpose;  // row r = (b, q) = (r / Q, r % Q) reads source row q B + b when transposed
+  const float* scale;
+  const float* offset;
+  float eps;
+  void* out;                // [rows][C] in attention order, or null
+  const float* mask;        // source order, or null (no key bias)
+  float* key_bias;          // [B][stride] f32, or null
+  float key_scale;
+  half_t* key_mask;         // [B][stride] f16 codes (mask - 1) kMaskCode, or null
+  const float* w;           // [C][H], or null (no pair bias)
+  int H;
+  float bias_scale;
+  float* bias;              // [H][Q][stride]
+  int stride;
+};
+
+// The key mask code of the fast path: (mask - 1) 32768 in f16 (exact for a
+// 0/1 mask). Times kMaskScale, the f16 nearest 1e9 log2(e) / 32768, it is the
+// key bias 1e9 (mask - 1) in base-2 units to within 1.1e-4 relative.
+constexpr float kMaskCode = 32768.0f;
+constexpr float kMaskScale = 44032.0f;
+
+__device__ __forceinline__ void key_bias_store(const RowsArgs& a, int64_t at, float mask) {
+  if (a.key_bias) a.key_bias[at] = a.key_scale * (mask - 1.0f);
+  if (a.key_mask) a.key_mask[at] = (half_t)((mask - 1.0f) * kMaskCode);
+}
+
+template <typename T> __device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    const half8 h = *reinterpret_cast<const half8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = (float)h[e];
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  }
+}
+
+template <typename T> __device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    half8 h;
+#pragma unroll
+    for (int e = 0; e < 8; e++) h[e] = (half_t)v[e];
+    *reinterpret_cast<half8*>(p) = h;
+  } else {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// Vectorised rows: LANES lanes a row, eight channels a lane (C = 8 LANES);
+// a workgroup walks 256 / LANES rows at a time through the tensor, the head
+// weights (zero past H, H <= 8) staged once in LDS.
+template <typename IT, typename OT, int LANES>
+__global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
+  constexpr int C = 8 * LANES;
+  constexpr int kRows = 256 / LANES;
+  __shared__ __attribute__((aligned(16))) float wl[C * 8];
+  if (a.w) {
+    // channel c = 8 j + e at [e][j][8]: the lanes of a row read adjacent
+    // 32-byte pieces for each e
+    for (int i = threadIdx.x; i < C * 8; i += 256) {
+      const int c = i >> 3, h = i & 7;
+      wl[((c & 7) * LANES + (c >> 3)) * 8 + h] = h < a.H ? a.w[c * a.H + h] : 0.0f;
+    }
+    __syncthreads();
+  }
+  const int j = threadIdx.x % LANES;
+  for (int64_t r0 = (int64_t)blockIdx.x * kRows; r0 < a.rows; r0 += (int64_t)gridDim.x * kRows) {
+    const int64_t r = r0 + threadIdx.x / LANES;
+    const bool live = r < a.rows;
+    const int64_t rr = live ? r : a.rows - 1;  // past the end: recompute the last row, store nothing
+    const int64_t b = rr / a.Q, q = rr % a.Q;
+    const int64_t src = a.transpose ? q * a.B + b : rr;
+    float v[8];
+    load8(reinterpret_cast<const IT*>(a.x) + src * C + 8 * j, v);
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) s += v[e];
+    const float mean = lane_sum<LANES>(s) / (float)C;
+    float var = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float dlt = v[e] - mean;
+      var += dlt * dlt;
+    }
+    const float rstd = 1.0f / sqrtf(lane_sum<LANES>(var) / (float)C + a.eps);
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = (v[e] - mean) * rstd * a.scale[8 * j + e] + a.offset[8 * j + e];
+    if (a.out && live) store8(reinterpret_cast<OT*>(a.out) + rr * C + 8 * j, v);
+    if (a.mask && live && j == 0) key_bias_store(a, b * a.stride + q, a.mask[src]);
+    if (a.w) {
+      float acc[8] = {};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float4 w0 = *reinterpret_cast<const float4*>(&wl[(e * LANES + j) * 8]);
+        const float4 w1 = *reinterpret_cast<const float4*>(&wl[(e * LANES + j) * 8 + 4]);
+        acc[0] += v[e] * w0.x, acc[1] += v[e] * w0.y, acc[2] += v[e] * w0.z, acc[3] += v[e] * w0.w;
+        acc[4] += v[e] * w1.x, acc[5] += v[e] * w1.y, acc[6] += v[e] * w1.z, acc[7] += v[e] * w1.w;
+      }
+      float mine = 0.0f;
+#pragma unroll
+      for (int h = 0; h < 8; h++) {
+        const float t = lane_sum<LANES>(acc[h]);
+        if (h == j) mine = t;
+      }
+      if (live && j < a.H) a.bias[((int64_t)j * a.Q + b) * a.stride + q] = a.bias_scale * mine;
+    }
+  }
+}
+
+// The same pass for any width: one wave a row.
+template <typename IT, typename OT>
+__global__ __launch_bounds__(256) void attention_rows_any_kernel(RowsArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t rows = (int64_t)B * Q;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int64_t b = row / Q, q = row % Q;
-  const int64_t src = transpose ? q * B + b : row;
-  const IT* xr = x + src * C;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.rows) return;  // the whole wave
+  const int64_t b = r / a.Q, q = r % a.Q;
+  const int64_t src = a.transpose ? q * a.B + b : r;
+  const int C = a.C;
+  const IT* xr = reinterpret_cast<const IT*>(a.x) + src * C;
   float s = 0.0f;
   for (int c = lane; c < C; c += 64) s += ld(xr, c);
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
   const float mean = s / (float)C;
-  float v = 0.0f;
+  float var = 0.0f;
   for (int c = lane; c < C; c += 64) {
     const float dlt = ld(xr, c) - mean;
-    v += dlt * dlt;
+    var += dlt * dlt;
   }
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  const float rstd = 1.0f / sqrtf(v / (float)C + eps);
-  for (int c = lane; c < C; c += 64) out[row * C + c] = (CT)((ld(xr, c) - mean) * rstd * scale[c] + offset[c]);
-  if (lane == 0) key_bias[row] = 1e9f * (mask[src] - 1.0f);
-}
-
-// The pair bias bias[h][q][k] (attention.ts:631-661) for q, k < Q: sixteen
-// lanes a row (q, k), each taking every sixteenth channel, eight heads a pass.
-// Normalized-input: the row is x_hat[q Q + k] as is. Separate: the row is the
-// pair activation [q][k], LayerNormed with its own affine first.
-template <typename PT>
-__global__ __launch_bounds__(256) void attention_bias_kernel(const PT* __restrict__ src, int Q, int Cp, int H,
-                                                             int normalize, const float* __restrict__ scale,
-                                                             const float* __restrict__ offset, float eps,
-                                                             const float* __restrict__ w, int stride,
-                                                             float* __restrict__ bias) {
-  const int lane16 = threadIdx.x & 15;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const bool live = row < (int64_t)Q * Q;
-  const int64_t r = live ? row : 0;  // a row past the end still reduces (over row 0), storing nothing
-  const PT* pr = src + r * Cp;
-  float mean = 0.0f, rstd = 1.0f;
-  if (normalize) {
-    float s = 0.0f;
-    for (int c = lane16; c < Cp; c += 16) s += ld(pr, c);
-    s = row_sum16(s);
-    mean = s / (float)Cp;
-    float v = 0.0f;
-    for (int c = lane16; c < Cp; c += 16) {
-      const float dlt = ld(pr, c) - mean;
-      v += dlt * dlt;
+  for (int o = 32; o > 0; o >>= 1) var += __shfl_xor(var, o);
+  const float rstd = 1.0f / sqrtf(var / (float)C + a.eps);
+  if (a.out)
+    for (int c = lane; c < C; c += 64)
+      reinterpret_cast<OT*>(a.out)[r * C + c] = (OT)((ld(xr, c) - mean) * rstd * a.scale[c] + a.offset[c]);
+  if (a.mask && lane == 0) key_bias_store(a, b * a.stride + q, a.mask[src]);
+  if (a.w) {
+    for (int h = 0; h < a.H; h++) {
+      float acc = 0.0f;
+      for (int c = lane; c < C; c += 64)
+        acc += ((ld(xr, c) - mean) * rstd * a.scale[c] + a.offset[c]) * a.w[(int64_t)c * a.H + h];
+      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+      if (lane == 0) a.bias[((int64_t)h * a.Q + b) * a.stride + q] = a.bias_scale * acc;
     }
-    rstd = 1.0f / sqrtf(row_sum16(v) / (float)Cp + eps);
-  }
-  const int64_t q = row / Q, k = row % Q;
-  for (int h0 = 0; h0 < H; h0 += 8) {  // eight heads a pass
-    float acc[8] = {};
-    for (int c = lane16; c < Cp; c += 16) {
-      float y = ld(pr, c);
-      if (normalize) y = (y - mean) * rstd * scale[c] + offset[c];
-#pragma unroll
-      for (int h = 0; h < 8; h++)
-        if (h0 + h < H) acc[h] += y * w[(int64_t)c * H + h0 + h];
-    }
-    float mine = 0.0f;
-#pragma unroll
-    for (int h = 0; h < 8; h++) {
-      const float t = row_sum16(acc[h]);
-      if (h == lane16) mine = t;
-    }
-    if (live && lane16 < 8 && h0 + lane16 < H) bias[((int64_t)(h0 + lane16) * Q + q) * stride + k] = mine;
   }
 }
 
 struct FlashArgs {
-  const void* qkvg;         // [B Q][4C]: q (scaled), k, v, g (sigmoid)
-  const float* key_bias;    // [B][Q] in attention order
-  const float* bias;        // [H][Q][stride] or null
-  void* weighted;           // [B Q][C] in source order
-  int B, Q, C, H, d, transpose, stride;
+  const void* qkvg;       // [B Q][4C]: q (scaled), k, v, g (sigmoid)
+  const float* key_bias;  // [B][stride] (general kernel)
+  const half_t* key_mask; // [B][stride] codes (f16 kernel)
+  const float* bias;      // [H][Q][stride] or null
+  const half_t* vt;       // V^T blocks (f16 path)
+  void* weighted;         // [B Q][C] in source order
+  int B, Q, C, H, d, transpose, stride, key_blocks;
+  float clamp;
 };
 
 // One thread per (b, h, q), f32 arithmetic: the reference's recurrence
@@ -282,9 +390,9 @@ __global__ __launch_bounds__(256) void attention_flash_generic_kernel(FlashArgs 
     float dot = 0.0f;
 #pragma unroll
     for (int e = 0; e < D; e++) dot += qv[e] * (float)kr[e];
-    float logit = dot + a.key_bias[b * a.Q + k];
+    float logit = dot + a.key_bias[b * a.stride + k];
     if (a.bias) logit += a.bias[((int64_t)h * a.Q + q) * a.stride + k];
-    logit = fminf(fmaxf(logit, -1e8f), 1e8f);
+    logit = fminf(fmaxf(logit, -a.clamp), a.clamp);
     const float new_max = fmaxf(run_max, logit);
     const float scale = expf(run_max - new_max), weight = expf(logit - new_max);
     run_sum = run_sum * scale + weight;
@@ -308,117 +416,239 @@ int launch_flash_generic(const FlashArgs& fa, hipStream_t st, std::integer_seque
   return launch("attention.flash", table[fa.d - 1], dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, st, fa);
 }
 
+// V^T blocks for the f16 flash kernel: block (b, h, kb) is [32 channels][32
+// positions], position 16 s + 8 hi + e holding key 32 kb + 16 s + 8 (e / 4) +
+// 4 hi + e % 4 (zero past the last key): the keys a lane's probabilities
+// cover, in the order they fill the second MFMA's B operand.
+__global__ __launch_bounds__(256) void attention_vt_kernel(const half_t* __restrict__ qkvg, int B, int Q, int C,
+                                                           int H, int key_blocks, half_t* __restrict__ vt) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)B * H * key_blocks * 128) return;
+  const int d = (int)(i & 31);
+  const int part = (int)((i >> 5) & 3);  // 2 s + hi
+  const int64_t t = i >> 7;
+  const int kb = (int)(t % key_blocks);
+  const int64_t bh = t / key_blocks;
+  const int h = (int)(bh % H);
+  const int64_t b = bh / H;
+  const int s = part >> 1, hi = part & 1;
+  const half_t* src = qkvg + b * Q * 4 * (int64_t)C + 2 * C + h * 32 + d;
+  half8 val;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const int key = 32 * kb + 16 * s + 8 * (e >> 2) + 4 * hi + (e & 3);
+    val[e] = key < Q ? src[(int64_t)key * 4 * C] : (half_t)0.0f;
+  }
+  *reinterpret_cast<half8*>(vt + t * 1024 + d * 32 + 16 * s + 8 * hi) = val;
+}
+
 // f16 operands, head_dim 32: one wave per 32 queries of one (b, h), keys in
 // blocks of 32. S^T = K Q^T: A = K [key][d] straight from the projection
 // output, B = Q^T (the wave's queries, held for the whole loop); the result
 // gives lane l query l % 32 and keys 8 (v / 4) + 4 (l / 32) + v % 4. The
 // probabilities, packed to f16 in that key order, are the B operand of
-// O^T = V^T P^T; V^T's A fragment takes the same key order from an LDS copy
-// of the block transposed to [d][key]. Both k-steps of the second MFMA sum
-// over the block's 32 keys in a permuted order, the same on both operands.
-constexpr int kFlashWaves = 4;
+// O^T = V^T P^T, whose A operand is the V^T block in the same order.
+//
+// The MFMA does the per-logit additions: the accumulator starts from the pair
+// bias (loaded in the accumulator's own layout), and a 32x32x8 step adds
+// code[key] kMaskScale - m, with A = (code, 1) per key and B = (kMaskScale,
+// -m) per query, m an f16 offset that stands in for the running maximum. m
+// moves only when a block's logits exceed it by more than kSlack (and once,
+// to the first block's maximum), so probabilities stay below 2^kSlack and
+// the rescale of the accumulator is rare. The clamp is kept relative to m.
+// On this path the clamp is +-kLogitBound (base 2; 20794 in natural units)
+// rather than +-1e8: the same softmax wherever a row's largest logit lies
+// within those bounds, and a row whose every key is masked still averages
+// its values.
+//
+// A workgroup is two batch entries by 128 queries of one head: eight waves,
+// wave (bi, qi) taking queries 32 qi.. of batch entry bi. Each key block's
+// K and V^T tiles (shared by a batch entry's four query waves) and pair-bias
+// tile (shared by both batch entries) pass through LDS, double-buffered:
+// every lane holds its share of block j + 1 in registers while block j is
+// computed, stores it to LDS after, and after the block's one barrier loads
+// its share of block j + 2. Loads past the last key land in the workspace's
+// padding, and those keys are masked.
+constexpr int kFlashBatch = 2;
+constexpr int kFlashQueryWaves = 4;
+constexpr int kFlashThreads = 64 * kFlashBatch * kFlashQueryWaves;
+constexpr float kLogitBound = 30000.0f;
+constexpr float kSlack = 8.0f;
 
-__global__ __launch_bounds__(64 * kFlashWaves) void attention_flash_f16_kernel(FlashArgs a) {
-  __shared__ __attribute__((aligned(16))) half_t vt_all[kFlashWaves][32][32 + 8];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+struct FlashTile {
+  half_t k[kFlashBatch][32][40];   // [bi][key][channel], rows padded to 80 bytes
+  half_t vt[kFlashBatch][32][40];  // [bi][channel][position]
+  float bias[32 * kFlashQueryWaves][36];  // [query][key], rows padded to 144 bytes
+};
+
+template <bool BIAS>
+__global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(FlashArgs a) {
+  __shared__ FlashTile tiles[2];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, hi = lane >> 5;
-  const int qblocks = (a.Q + 32 * kFlashWaves - 1) / (32 * kFlashWaves);
-  const int64_t bh = blockIdx.x / qblocks;
-  const int h = (int)(bh % a.H);
-  const int64_t b = bh / a.H;
-  const int q0 = (int)(blockIdx.x % qblocks) * 32 * kFlashWaves + 32 * wave;
-  if (q0 >= a.Q) return;  // the whole wave: no barrier below spans waves
-  half_t(*vt)[32 + 8] = vt_all[wave];
-
+  const int bi = wave / kFlashQueryWaves, qi = wave % kFlashQueryWaves;
+  const int Q = a.Q;
+  const int qblocks = (Q + 32 * kFlashQueryWaves - 1) / (32 * kFlashQueryWaves);
+  const int qb = (int)(blockIdx.x % qblocks);
+  const int h = (int)((blockIdx.x / qblocks) % a.H);
+  const int64_t b0 = (int64_t)(blockIdx.x / qblocks / a.H) * kFlashBatch;
   const half_t* base = reinterpret_cast<const half_t*>(a.qkvg);
   const int64_t ld4 = 4 * (int64_t)a.C;
-  const int64_t row0 = b * a.Q;
-  const int myq = q0 + col;
-  const bool qlive = myq < a.Q;
-  // Q^T fragments: Q[myq][16 s + 8 hi .. + 8].
-  half8 qf[2];
+  const int qbase = qb * 32 * kFlashQueryWaves;
+
+  // This lane's share of a block's loads, at key block 0; block k0 adds
+  // uniform offsets: one 16-byte piece of a tile (lanes 0-127 and 128-255 the
+  // K tiles of batch entries 0 and 1, lanes 256-383 and 384-511 their V^T
+  // tiles) and two of the bias tile (lane t: pieces t and t + 512, piece c
+  // holding row c / 8, keys 4 (c % 8)..).
+  const half_t* tile_src;
+  int64_t tile_step;  // elements per key block
+  half_t* tile_dst[2];
   {
-    const half_t* qr = base + (row0 + (qlive ? myq : 0)) * ld4 + h * 32;
-#pragma unroll
-    for (int s = 0; s < 2; s++) qf[s] = qlive ? *reinterpret_cast<const half8*>(qr + 16 * s + 8 * hi) : half8{};
-  }
-  const float* brow = a.bias ? a.bias + ((int64_t)h * a.Q + (qlive ? myq : 0)) * a.stride : nullptr;
-  const float* kb = a.key_bias + row0;
-
-  floatx16 o = {};  // O^T: lane holds query myq, channels 8 (v / 4) + 4 hi + v % 4
-  float run_max = -1e30f, run_sum = 0.0f;
-  constexpr float kLog2e = 1.4426950408889634f;
-  for (int k0 = 0; k0 < a.Q; k0 += 32) {
-    const int mykey = k0 + col;
-    const bool klive = mykey < a.Q;
-    const half_t* kr = base + (row0 + (klive ? mykey : 0)) * ld4 + a.C + h * 32;
-    half8 kf[2], vraw[2];
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-      kf[s] = klive ? *reinterpret_cast<const half8*>(kr + 16 * s + 8 * hi) : half8{};
-      vraw[s] = klive ? *reinterpret_cast<const half8*>(kr + a.C + 16 * s + 8 * hi) : half8{};
+    const int part = tid >> 7;
+    const int u = tid & 127;
+    const int e = part & 1;
+    const int64_t be = min(b0 + e, (int64_t)a.B - 1);
+    if (part < 2) {
+      tile_src = base + (be * Q + (u >> 2)) * ld4 + a.C + h * 32 + 8 * (u & 3);
+      tile_step = 32 * ld4;
+    } else {
+      tile_src = a.vt + (be * a.H + h) * a.key_blocks * 1024 + u * 8;
+      tile_step = 1024;
     }
-    // V^T for this block: vt[d][key], d = 16 s + 8 hi + e, key = col.
-#pragma unroll
-    for (int s = 0; s < 2; s++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) vt[16 * s + 8 * hi + e][col] = vraw[s][e];
+    for (int t = 0; t < 2; t++)
+      tile_dst[t] = part < 2 ? &tiles[t].k[e][u >> 2][8 * (u & 3)] : &tiles[t].vt[e][u >> 2][8 * (u & 3)];
+  }
+  const float* bias_src[2] = {nullptr, nullptr};
+  float* bias_dst[2][2] = {};
+  if (BIAS) {
+    for (int i = 0; i < 2; i++) {
+      const int c = tid + kFlashThreads * i;
+      const int r = c >> 3;
+      const int q = min(qbase + r, Q - 1);
+      bias_src[i] = a.bias + ((int64_t)h * Q + q) * a.stride + 4 * (c & 7);
+      for (int t = 0; t < 2; t++) bias_dst[t][i] = &tiles[t].bias[r][4 * (c & 7)];
+    }
+  }
+  static_assert(2 * kFlashThreads * 4 == 32 * kFlashQueryWaves * 32, "two bias pieces a lane cover the tile");
+  uint4 staged[3];
+  auto fetch = [&](int k0) {
+    staged[0] = *reinterpret_cast<const uint4*>(tile_src + (k0 >> 5) * tile_step);
+    if (BIAS) {
+      staged[1] = *reinterpret_cast<const uint4*>(bias_src[0] + k0);
+      staged[2] = *reinterpret_cast<const uint4*>(bias_src[1] + k0);
+    }
+  };
+  auto stash = [&](int t) {
+    *reinterpret_cast<uint4*>(tile_dst[t]) = staged[0];
+    if (BIAS) {
+      *reinterpret_cast<uint4*>(bias_dst[t][0]) = staged[1];
+      *reinterpret_cast<uint4*>(bias_dst[t][1]) = staged[2];
+    }
+  };
 
-    floatx16 st = {};
-#pragma unroll
-    for (int s = 0; s < 2; s++) st = mfma_f16(kf[s], qf[s], st);
+  // This wave's batch entry and queries.
+  const int64_t b = b0 + bi;
+  const int q0 = qbase + 32 * qi;
+  const bool active = b < a.B && q0 < Q;  // idle waves still load and meet every barrier
+  const int64_t bc = active ? b : 0;
+  const int64_t row0 = bc * Q;
+  const int myq = q0 + col;
+  const int qrow = myq < Q ? myq : Q - 1;
+  half8 qf[2] = {};
+  if (active) {
+    const half_t* qr = base + (row0 + qrow) * ld4 + h * 32 + 8 * hi;
+    qf[0] = *reinterpret_cast<const half8*>(qr);
+    qf[1] = *reinterpret_cast<const half8*>(qr + 16);
+  }
+  const half_t* cp = a.key_mask + bc * a.stride + col;
 
-    // Logits of this lane's query for keys k0 + 8 g + 4 hi + i (g, i < 4).
-    float lg[16];
-    float bm = -1e30f;
+  floatx16 o = {};       // O^T: lane holds query myq, channels 8 (v / 4) + 4 hi + v % 4
+  float run_sum = 0.0f;  // over this lane's keys; the lane 32 away holds the rest
+  float m = 0.0f;        // f16-representable, subtracted by the MFMA
+  float lo = -kLogitBound, up = kLogitBound;  // clamp bounds relative to m
+  half4 bm_frag = hi ? half4{} : half4{(half_t)kMaskScale, (half_t)0.0f, (half_t)0.0f, (half_t)0.0f};
+  const half_t one = (half_t)1.0f;
+
+  auto step = [&](const FlashTile& tl, half_t code, int k0, bool first) {
+    floatx16 sc = {};
+    if constexpr (BIAS) {
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const int key = k0 + 8 * g + 4 * hi;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int kk = key + i;
-        float x = -1e30f;  // keys past the end take no weight
-        if (kk < a.Q) {
-          x = st[4 * g + i] + kb[kk];
-          if (brow) x += brow[kk];
-          x = fminf(fmaxf(x, -1e8f), 1e8f);
-        }
-        lg[4 * g + i] = x;
-        bm = fmaxf(bm, x);
+      for (int g = 0; g < 4; g++) {
+        const float4 t = *reinterpret_cast<const float4*>(&tl.bias[32 * qi + col][8 * g + 4 * hi]);
+        sc[4 * g] = t.x, sc[4 * g + 1] = t.y, sc[4 * g + 2] = t.z, sc[4 * g + 3] = t.w;
       }
     }
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
-    const float new_max = fmaxf(run_max, bm);
-    const float scale = __builtin_amdgcn_exp2f((run_max - new_max) * kLog2e);
-    float ps = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+      sc = mfma_f16(*reinterpret_cast<const half8*>(&tl.k[bi][col][16 * s + 8 * hi]), qf[s], sc);
+    const half4 am = hi ? half4{} : half4{code, one, (half_t)0.0f, (half_t)0.0f};
+    sc = __builtin_amdgcn_mfma_f32_32x32x8f16(am, bm_frag, sc, 0, 0, 0);
+    float x[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) x[v] = __builtin_amdgcn_fmed3f(sc[v], lo, up);
+    if (k0 + 32 > Q) {  // the last block: keys past the end take no weight
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (k0 + 8 * g + 4 * hi + i >= Q) x[4 * g + i] = -INFINITY;
+    }
+    float bm = x[0];
+#pragma unroll
+    for (int v = 1; v < 16; v++) bm = fmaxf(bm, x[v]);
+    if (first || __builtin_amdgcn_ballot_w64(bm > kSlack)) {
+      // Move m to the pair's maximum, rounded to the nearest f16: the first
+      // block sets it, a later one only raises it. Within [-kLogitBound,
+      // kLogitBound] the rounding is at most 8, so every probability stays
+      // within [2^-8, 2^8] of the largest one's 1.
+      const float pm = fmaxf(bm, __shfl_xor(bm, 32));
+      const float want = first ? pm : m + fmaxf(pm, 0.0f);
+      const float mn = (float)(half_t)want;
+      const float delta = mn - m;
+#pragma unroll
+      for (int v = 0; v < 16; v++) x[v] -= delta;
+      lo -= delta;
+      up -= delta;
+      if (!first) {
+        const float f = __builtin_amdgcn_exp2f(-delta);
+        run_sum *= f;
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[v] *= f;
+      }
+      m = mn;
+      if (!hi) bm_frag[1] = (half_t)(-mn);
+    }
     half8 pf[2];
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const float p = __builtin_amdgcn_exp2f((lg[v] - new_max) * kLog2e);
-      ps += p;
-      pf[v >> 3][v & 7] = (half_t)p;
+    for (int v = 0; v < 16; v += 2) {
+      const half2v pp = half2v{(half_t)__builtin_amdgcn_exp2f(x[v]), (half_t)__builtin_amdgcn_exp2f(x[v + 1])};
+      run_sum = __builtin_amdgcn_fdot2(pp, half2v{one, one}, run_sum, false);
+      pf[v >> 3][v & 7] = pp[0];
+      pf[v >> 3][(v & 7) + 1] = pp[1];
     }
-    ps += __shfl_xor(ps, 32);
-    run_sum = run_sum * scale + ps;
-    run_max = new_max;
 #pragma unroll
-    for (int v = 0; v < 16; v++) o[v] *= scale;
+    for (int s = 0; s < 2; s++)
+      o = mfma_f16(*reinterpret_cast<const half8*>(&tl.vt[bi][col][16 * s + 8 * hi]), pf[s], o);
+  };
 
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's V^T writes are done
-    __builtin_amdgcn_wave_barrier();
-    // V^T A fragments in the key order of P: keys 16 s + 4 hi + [0, 4) and
-    // 16 s + 8 + 4 hi + [0, 4) for channel col.
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-      const half4 lo = *reinterpret_cast<const half4*>(&vt[col][16 * s + 4 * hi]);
-      const half4 up = *reinterpret_cast<const half4*>(&vt[col][16 * s + 8 + 4 * hi]);
-      const half8 vf = half8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-      o = mfma_f16(vf, pf[s], o);
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // the reads are done before the next block overwrites vt
-    __builtin_amdgcn_wave_barrier();
+  fetch(0);
+  half_t code = cp[0];
+  stash(0);
+  __syncthreads();
+  fetch(32);  // in the padding when there is one block
+  for (int k0 = 0, t = 0; k0 < Q; k0 += 32, t ^= 1) {
+    const half_t next_code = cp[k0 + 32];
+    if (active) step(tiles[t], code, k0, k0 == 0);
+    code = next_code;
+    if (k0 + 32 >= Q) break;
+    stash(t ^ 1);
+    __syncthreads();
+    fetch(k0 + 64);
   }
-  if (!qlive) return;
+  run_sum += __shfl_xor(run_sum, 32);
+  if (!active || myq >= Q) return;
   const float inv = 1.0f / run_sum;
   const half_t* gr = base + (row0 + myq) * ld4 + 3 * a.C + h * 32;
   const int64_t src = a.transpose ? (int64_t)myq * a.B + b : row0 + myq;
@@ -432,6 +662,29 @@ __global__ __launch_bounds__(64 * kFlashWaves) void attention_flash_f16_kernel(F
     for (int i = 0; i < 4; i++) r[i] = (half_t)(o[4 * g + i] * inv * (float)gv[i]);
     *reinterpret_cast<half4*>(out + c0) = r;
   }
+}
+
+template <typename IT, typename OT>
+int launch_rows_typed(const RowsArgs& r, const char* label, hipStream_t st) {
+  const bool vec = (reinterpret_cast<uintptr_t>(r.x) & 15) == 0 &&
+                   (!r.out || (reinterpret_cast<uintptr_t>(r.out) & 15) == 0);
+  const dim3 block(256);
+  const bool heads_ok = !r.w || r.H <= 8;
+  if (vec && heads_ok && r.C == 64)
+    return launch(label, attention_rows_kernel<IT, OT, 8>, dim3((unsigned)std::min<int64_t>(ceil_div(r.rows, 32), 4096)), block, 0, st, r);
+  if (vec && heads_ok && r.C == 128)
+    return launch(label, attention_rows_kernel<IT, OT, 16>, dim3((unsigned)std::min<int64_t>(ceil_div(r.rows, 16), 4096)), block, 0, st, r);
+  if (vec && heads_ok && r.C == 256)
+    return launch(label, attention_rows_kernel<IT, OT, 32>, dim3((unsigned)std::min<int64_t>(ceil_div(r.rows, 8), 4096)), block, 0, st, r);
+  return launch(label, attention_rows_any_kernel<IT, OT>, dim3((unsigned)ceil_div(r.rows, 4)), block, 0, st, r);
+}
+
+int launch_rows(const RowsArgs& r, int in_dtype, int out_dtype, const char* label, hipStream_t st) {
+  if (in_dtype == AFHIP_F16)
+    return out_dtype == AFHIP_F16 ? launch_rows_typed<half_t, half_t>(r, label, st)
+                                  : launch_rows_typed<half_t, float>(r, label, st);
+  return out_dtype == AFHIP_F16 ? launch_rows_typed<float, half_t>(r, label, st)
+                                : launch_rows_typed<float, float>(r, label, st);
 }
 
 }  // namespace
@@ -489,33 +742,64 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
                 workspace_bytes, ws.total);
   hipStream_t st = (hipStream_t)stream;
   const bool f16 = d.precision == AFHIP_PRECISION_F16;
+  const bool fast = fast_path(d);
+  const float unit = fast ? kLog2e : 1.0f;  // logits in base-2 units on the fast path
   const int ct = f16 ? AFHIP_F16 : AFHIP_F32;
   const char* wp = (const char*)prepared;
   char* wsb = (char*)workspace;
   const int B = d.batch, Q = d.queries, C = d.channels, H = d.heads;
   const int64_t rows = (int64_t)B * Q;
+  float* bias = d.pair_bias ? (float*)(wsb + ws.bias) : nullptr;
   int s;
 
-  // 1. LayerNorm in attention order, and the key bias.
+  // 1. LayerNorm in attention order, the key bias, and a normalized-input pair bias.
   {
-    const dim3 grid((unsigned)ceil_div(rows, 4));
-    const float* sc = (const float*)(wp + w.ln_scale);
-    const float* of = (const float*)(wp + w.ln_offset);
-    float* kb = (float*)(wsb + ws.key_bias);
-    void* xn = wsb + ws.normalized;
-    if (d.in_dtype == AFHIP_F32)
-      s = f16 ? launch("attention.norm", attention_norm_kernel<float, half_t>, grid, dim3(256), 0, st,
-                       (const float*)activations, mask, B, Q, C, d.transpose, sc, of, d.epsilon, (half_t*)xn, kb)
-              : launch("attention.norm", attention_norm_kernel<float, float>, grid, dim3(256), 0, st,
-                       (const float*)activations, mask, B, Q, C, d.transpose, sc, of, d.epsilon, (float*)xn, kb);
-    else
-      s = f16 ? launch("attention.norm", attention_norm_kernel<half_t, half_t>, grid, dim3(256), 0, st,
-                       (const half_t*)activations, mask, B, Q, C, d.transpose, sc, of, d.epsilon, (half_t*)xn, kb)
-              : launch("attention.norm", attention_norm_kernel<half_t, float>, grid, dim3(256), 0, st,
-                       (const half_t*)activations, mask, B, Q, C, d.transpose, sc, of, d.epsilon, (float*)xn, kb);
-    if (s) return s;
+    RowsArgs r{};
+    r.x = activations;
+    r.rows = rows;
+    r.C = C;
+    r.B = B;
+    r.Q = Q;
+    r.transpose = d.transpose;
+    r.scale = (const float*)(wp + w.ln_scale);
+    r.offset = (const float*)(wp + w.ln_offset);
+    r.eps = d.epsilon;
+    r.out = wsb + ws.normalized;
+    r.mask = mask;
+    if (fast) {
+      r.key_mask = (half_t*)(wsb + ws.key_mask);
+    } else {
+      r.key_bias = (float*)(wsb + ws.key_bias);
+      r.key_scale = 1e9f;
+    }
+    if (d.pair_bias == AFHIP_PAIR_BIAS_NORMALIZED_INPUT) {
+      r.w = (const float*)(wp + w.w_bias);
+      r.H = H;
+      r.bias_scale = unit;
+      r.bias = bias;
+    }
+    r.stride = ws.stride;
+    if ((s = launch_rows(r, d.in_dtype, ct, "attention.norm", st))) return s;
   }
-  // 2. q, k, v, g in one GEMM with the ATTENTION epilogue.
+  // 2. A separate pair source: its own LayerNorm, projected to the heads.
+  if (d.pair_bias == AFHIP_PAIR_BIAS_SEPARATE) {
+    RowsArgs r{};
+    r.x = pair_activations;
+    r.rows = (int64_t)Q * Q;
+    r.C = d.pair_channels;
+    r.B = Q;
+    r.Q = Q;
+    r.scale = (const float*)(wp + w.pair_scale);
+    r.offset = (const float*)(wp + w.pair_offset);
+    r.eps = d.epsilon;
+    r.w = (const float*)(wp + w.w_bias);
+    r.H = H;
+    r.bias_scale = unit;
+    r.bias = bias;
+    r.stride = ws.stride;
+    if ((s = launch_rows(r, d.in_dtype, AFHIP_F32, "attention.pair_bias", st))) return s;
+  }
+  // 3. q, k, v, g in one GEMM with the ATTENTION epilogue.
   {
     GemmArgs g;
     g.a = wsb + ws.normalized;
@@ -530,34 +814,18 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
     g.ldc = 4 * C;
     g.flags = AFHIP_EPILOGUE_BIAS | AFHIP_EPILOGUE_ATTENTION;
     g.head_cols = C;
-    g.q_scale = 1.0f / sqrtf((float)(C / H));
+    g.q_scale = unit / sqrtf((float)(C / H));
     GemmTypes t{d.precision, ct, ct, ct};
     if ((s = run_gemm(g, t, select_variant(t, g.M, g.N, g.K, 1), "attention.project", st))) return s;
-  }
-  // 3. The pair bias.
-  float* bias = nullptr;
-  if (d.pair_bias) {
-    bias = (float*)(wsb + ws.bias);
-    const bool sep = d.pair_bias == AFHIP_PAIR_BIAS_SEPARATE;
-    const int Cp = sep ? d.pair_channels : C;
-    const dim3 grid((unsigned)ceil_div((int64_t)Q * Q, 16));
-    const float* ps = (const float*)(wp + w.pair_scale);
-    const float* po = (const float*)(wp + w.pair_offset);
-    const float* wb = (const float*)(wp + w.w_bias);
-    const bool src16 = sep ? d.in_dtype == AFHIP_F16 : f16;
-    const void* src = sep ? pair_activations : (const void*)(wsb + ws.normalized);
-    s = src16 ? launch("attention.pair_bias", attention_bias_kernel<half_t>, grid, dim3(256), 0, st,
-                       (const half_t*)src, Q, Cp, H, (int)sep, ps, po, d.epsilon, wb, ws.bias_stride, bias)
-              : launch("attention.pair_bias", attention_bias_kernel<float>, grid, dim3(256), 0, st,
-                       (const float*)src, Q, Cp, H, (int)sep, ps, po, d.epsilon, wb, ws.bias_stride, bias);
-    if (s) return s;
   }
   // 4. Attention.
   {
     FlashArgs fa{};
     fa.qkvg = wsb + ws.qkvg;
     fa.key_bias = (const float*)(wsb + ws.key_bias);
+    fa.key_mask = (const half_t*)(wsb + ws.key_mask);
     fa.bias = bias;
+    fa.vt = (const half_t*)(wsb + ws.vt);
     fa.weighted = wsb + ws.weighted;
     fa.B = B;
     fa.Q = Q;
@@ -565,12 +833,21 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
     fa.H = H;
     fa.d = C / H;
     fa.transpose = d.transpose;
-    fa.stride = ws.bias_stride;
-    if (f16 && fa.d == 32) {
-      const int64_t qblocks = ceil_div(Q, 32 * kFlashWaves);
-      AFHIP_REQUIRE((int64_t)B * H * qblocks < ((int64_t)1 << 31), "attention grid too large");
-      s = launch("attention.flash", attention_flash_f16_kernel, dim3((unsigned)(B * H * qblocks)),
-                 dim3(64 * kFlashWaves), 0, st, fa);
+    fa.stride = ws.stride;
+    fa.key_blocks = ws.key_blocks;
+    fa.clamp = 1e8f;
+    if (fast) {
+      const int64_t vt_threads = (int64_t)B * H * ws.key_blocks * 128;
+      AFHIP_REQUIRE(ceil_div(vt_threads, 256) < ((int64_t)1 << 31), "attention grid too large");
+      if ((s = launch("attention.vt", attention_vt_kernel, dim3((unsigned)ceil_div(vt_threads, 256)), dim3(256), 0,
+                      st, (const half_t*)(wsb + ws.qkvg), B, Q, C, H, ws.key_blocks, (half_t*)(wsb + ws.vt))))
+        return s;
+      const int64_t groups = ceil_div(B, kFlashBatch) * H * ceil_div(Q, 32 * kFlashQueryWaves);
+      AFHIP_REQUIRE(groups < ((int64_t)1 << 31), "attention grid too large");
+      s = bias ? launch("attention.flash", attention_flash_f16_kernel<true>, dim3((unsigned)groups),
+                        dim3(kFlashThreads), 0, st, fa)
+               : launch("attention.flash", attention_flash_f16_kernel<false>, dim3((unsigned)groups),
+                        dim3(kFlashThreads), 0, st, fa);
     } else {
       s = f16 ? launch_flash_generic<half_t>(fa, st, std::make_integer_sequence<int, 32>{})
               : launch_flash_generic<float>(fa, st, std::make_integer_sequence<int, 32>{});
@@ -593,7 +870,11 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
     g.ldc = C;
     g.flags = AFHIP_EPILOGUE_BIAS | (d.residual ? AFHIP_EPILOGUE_RESIDUAL : 0u);
     GemmTypes t{d.precision, ct, ct, d.out_dtype};
-    if ((s = run_gemm(g, t, select_variant(t, g.M, g.N, g.K, 1), "attention.output", st))) return s;
+    if (stream_eligible(g, t)) {
+      if ((s = run_gemm_stream(g, t, "attention.output", st))) return s;
+    } else if ((s = run_gemm(g, t, select_variant(t, g.M, g.N, g.K, 1), "attention.output", st))) {
+      return s;
+    }
   }
   return AFHIP_OK;
 }
