@@ -113,11 +113,12 @@ class AttentionDesc(ctypes.Structure):
 
 class PairStackDesc(ctypes.Structure):
     _fields_ = [("opm", OpmDesc), ("outgoing", TriangleDesc), ("incoming", TriangleDesc),
-                ("transition", TransitionDesc)]
+                ("attention_start", AttentionDesc), ("attention_end", AttentionDesc), ("transition", TransitionDesc)]
 
 
 class PairStackWeights(ctypes.Structure):
     _fields_ = [("opm", ctypes.c_void_p), ("outgoing", ctypes.c_void_p), ("incoming", ctypes.c_void_p),
+                ("attention_start", ctypes.c_void_p), ("attention_end", ctypes.c_void_p),
                 ("transition", ctypes.c_void_p)]
 
 

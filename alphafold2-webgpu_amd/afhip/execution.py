@@ -17,6 +17,7 @@ import json
 import numpy as np
 
 from . import _lib
+from . import attention as _attention
 from . import opm as _opm
 from . import transition as _transition
 from . import triangle as _triangle
@@ -121,14 +122,14 @@ class Execution:
 class PairStack:
     """The pair steps of an Evoformer block, in the block's order, each adding
     into the pair in place: outer-product mean, triangle multiplication
-    outgoing and incoming, pair transition (block.ts:1683-1750; the triangle
-    attentions between them are not part of this library). Weights are
-    prepared once into the execution's pool."""
+    outgoing and incoming, triangle attention around the starting and the
+    ending node, pair transition (block.ts:1683-1750). Weights are prepared
+    once into the execution's pool."""
 
     def __init__(self, execution: Execution, length: int, *, sequences: int, c_m: int, c_z: int = 128,
                  c_outer: int = 32, c_hidden: int = 128, transition_factor: int = 4, precision: str = "f16",
                  pair_dtype: str = "f16", msa_dtype: str = "f16", opm_row_block: int = 0,
-                 triangle_block_rows: int = 0):
+                 triangle_block_rows: int = 0, attention_heads: int = 4):
         self.execution = execution
         prec = _lib.PRECISION_F16 if precision == "f16" else _lib.PRECISION_F32
         pdt = _DT[pair_dtype]
@@ -139,6 +140,9 @@ class PairStack:
                                                triangle_block_rows, 1, 1e-5)
         self.desc.incoming = _lib.TriangleDesc(length, c_z, c_hidden, _lib.TRIANGLE_INCOMING, prec, pdt, pdt,
                                                triangle_block_rows, 1, 1e-5)
+        for attr, transpose in (("attention_start", 0), ("attention_end", 1)):
+            setattr(self.desc, attr, _lib.AttentionDesc(length, length, c_z, attention_heads, transpose,
+                                                        _lib.PAIR_BIAS_NORMALIZED_INPUT, 0, prec, pdt, pdt, 1, 1e-5))
         self.desc.transition = _lib.TransitionDesc(length * length, c_z, transition_factor * c_z, prec, pdt, pdt, 1,
                                                    1e-5)
         self.weights = _lib.PairStackWeights()
@@ -157,9 +161,11 @@ class PairStack:
 
     def prepare(self, weights: dict) -> None:
         """weights: {"outerProductMean", "triangleMultiplicationOutgoing",
-        "triangleMultiplicationIncoming", "pairTransition"}, each the
-        operator's weight dict (or its packed f32 array); a missing one skips
-        that step."""
+        "triangleMultiplicationIncoming", "triangleAttentionStarting",
+        "triangleAttentionEnding", "pairTransition"}, each the operator's
+        weight dict (or its packed f32 array) — the attentions as the block's
+        {"attention": AttentionWeights, "pairProjectionWeight": [c_z][heads]}
+        (block.ts:1727-1745); a missing one skips that step."""
         d = self.desc
         if weights.get("outerProductMean") is not None:
             w = weights["outerProductMean"]
@@ -172,6 +178,15 @@ class PairStack:
                 setattr(self.weights, attr, self._prepare(
                     f"triangle-{attr}", desc, _triangle.pack_weights(w) if isinstance(w, dict) else w,
                     "afhip_triangle_weights_size", "afhip_triangle_prepare_weights"))
+        for key, attr in (("triangleAttentionStarting", "attention_start"),
+                          ("triangleAttentionEnding", "attention_end")):
+            if weights.get(key) is not None:
+                w = weights[key]
+                packed = w if not isinstance(w, dict) else _attention.pack_weights(
+                    w["attention"], {"source": "normalized-input", "projectionWeight": w["pairProjectionWeight"]})
+                setattr(self.weights, attr, self._prepare(
+                    attr.replace("_", "-"), getattr(d, attr), packed, "afhip_attention_weights_size",
+                    "afhip_attention_prepare_weights"))
         if weights.get("pairTransition") is not None:
             w = weights["pairTransition"]
             self.weights.transition = self._prepare(

@@ -310,6 +310,25 @@ int afhip_execution_pair_stack(afhip_execution* ex, const afhip_pair_stack_desc*
             }))
       return s;
   }
+  afhip_attention_desc att[2] = {d.attention_start, d.attention_end};
+  const void* att_w[2] = {weights->attention_start, weights->attention_end};
+  const char* att_label[2] = {"pair-stack.triangle-attention-starting", "pair-stack.triangle-attention-ending"};
+  for (int i = 0; i < 2; i++) {
+    if (!att_w[i]) continue;
+    afhip_attention_desc& ad = att[i];
+    ad.transpose = i;
+    ad.pair_bias = AFHIP_PAIR_BIAS_NORMALIZED_INPUT;
+    ad.residual = 1;
+    AFHIP_REQUIRE(ad.batch == L && ad.queries == L && ad.channels == out.c_z && ad.in_dtype == pdt &&
+                      ad.out_dtype == pdt,
+                  "the triangle attention does not match the pair");
+    if (int s = pooled_step(
+            ex, att_label[i], [&](size_t* b) { return afhip_attention_workspace_size(&ad, b); },
+            [&](void* ws, size_t b) {
+              return afhip_attention_run(&ad, pair, pair_mask, nullptr, att_w[i], pair, ws, b, ex->stream);
+            }))
+      return s;
+  }
   if (weights->transition) {
     AFHIP_REQUIRE(tr.rows == (int64_t)L * L && tr.channels == out.c_z && tr.in_dtype == pdt && tr.out_dtype == pdt,
                   "the pair transition does not match the pair");

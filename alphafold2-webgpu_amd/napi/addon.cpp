@@ -789,17 +789,17 @@ napi_value ExecutionAddInPlace(napi_env env, napi_callback_info info) {
 // The pair stack's shape from {length, sequences, cM, cZ = 128, cOuter = 32,
 // cHidden = 128, transitionFactor = 4, precision = PRECISION.f16,
 // pairDtype = DTYPE.f16, msaDtype = DTYPE.f16, opmRowBlock = 0,
-// triangleBlockRows = 0}.
+// triangleBlockRows = 0, attentionHeads = 4}.
 bool read_stack_desc(napi_env env, napi_value o, afhip_pair_stack_desc* d) {
-  int64_t L, S, cm, cz, co, ch, tf, prec, pdt, mdt, rb, br;
+  int64_t L, S, cm, cz, co, ch, tf, prec, pdt, mdt, rb, br, heads;
   if (!prop_int(env, o, "length", 0, &L) || !prop_int(env, o, "sequences", 0, &S) ||
       !prop_int(env, o, "cM", 0, &cm) || !prop_int(env, o, "cZ", 128, &cz) || !prop_int(env, o, "cOuter", 32, &co) ||
       !prop_int(env, o, "cHidden", 128, &ch) || !prop_int(env, o, "transitionFactor", 4, &tf) ||
       !prop_int(env, o, "precision", AFHIP_PRECISION_F16, &prec) || !prop_int(env, o, "pairDtype", AFHIP_F16, &pdt) ||
       !prop_int(env, o, "msaDtype", AFHIP_F16, &mdt) || !prop_int(env, o, "opmRowBlock", 0, &rb) ||
-      !prop_int(env, o, "triangleBlockRows", 0, &br))
+      !prop_int(env, o, "triangleBlockRows", 0, &br) || !prop_int(env, o, "attentionHeads", 4, &heads))
     return false;
-  if (L <= 0 || L > 65535 || cz <= 0 || ch <= 0 || tf <= 0 || S < 0 || cm < 0 || co <= 0) {
+  if (L <= 0 || L > 65535 || cz <= 0 || ch <= 0 || tf <= 0 || S < 0 || cm < 0 || co <= 0 || heads <= 0) {
     throw_js(env, {true, "pair stack dimensions must be positive"});
     return false;
   }
@@ -810,6 +810,10 @@ bool read_stack_desc(napi_env env, napi_value o, afhip_pair_stack_desc* d) {
                  (int32_t)pdt, (int32_t)br, 1, 1e-5f};
   d->incoming = d->outgoing;
   d->incoming.direction = AFHIP_TRIANGLE_INCOMING;
+  d->attention_start = {(int32_t)L, (int32_t)L, (int32_t)cz, (int32_t)heads, 0, AFHIP_PAIR_BIAS_NORMALIZED_INPUT, 0,
+                        (int32_t)prec, (int32_t)pdt, (int32_t)pdt, 1, 1e-5f};
+  d->attention_end = d->attention_start;
+  d->attention_end.transpose = 1;
   d->transition = {(int64_t)L * L, (int32_t)cz, (int32_t)(tf * cz), (int32_t)prec, (int32_t)pdt, (int32_t)pdt, 1,
                    1e-5f};
   return true;
@@ -817,8 +821,9 @@ bool read_stack_desc(napi_env env, napi_value o, afhip_pair_stack_desc* d) {
 
 // executionPrepareWeights(ex, kind, stackDesc, Float32Array packed) -> buffer
 // handle of the prepared weights in the execution's pool; kind is
-// "outerProductMean", "triangleOutgoing", "triangleIncoming" or
-// "pairTransition", packed in that operator's reference order.
+// "outerProductMean", "triangleOutgoing", "triangleIncoming",
+// "triangleAttentionStarting", "triangleAttentionEnding" or "pairTransition",
+// packed in that operator's reference order.
 napi_value ExecutionPrepareWeights(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a, 4)) return nullptr;
@@ -835,6 +840,8 @@ napi_value ExecutionPrepareWeights(napi_env env, napi_callback_info info) {
   if (kind == "outerProductMean") st = afhip_opm_weights_size(&d.opm, &bytes);
   else if (kind == "triangleOutgoing") st = afhip_triangle_weights_size(&d.outgoing, &bytes);
   else if (kind == "triangleIncoming") st = afhip_triangle_weights_size(&d.incoming, &bytes);
+  else if (kind == "triangleAttentionStarting") st = afhip_attention_weights_size(&d.attention_start, &bytes);
+  else if (kind == "triangleAttentionEnding") st = afhip_attention_weights_size(&d.attention_end, &bytes);
   else if (kind == "pairTransition") st = afhip_transition_weights_size(&d.transition, &bytes);
   else {
     throw_js(env, {true, "unknown weight kind " + kind});
@@ -856,6 +863,8 @@ napi_value ExecutionPrepareWeights(napi_env env, napi_callback_info info) {
   if (kind == "outerProductMean") st = afhip_opm_prepare_weights(&d.opm, f, dst, nullptr);
   else if (kind == "triangleOutgoing") st = afhip_triangle_prepare_weights(&d.outgoing, f, dst, nullptr);
   else if (kind == "triangleIncoming") st = afhip_triangle_prepare_weights(&d.incoming, f, dst, nullptr);
+  else if (kind == "triangleAttentionStarting") st = afhip_attention_prepare_weights(&d.attention_start, f, dst, nullptr);
+  else if (kind == "triangleAttentionEnding") st = afhip_attention_prepare_weights(&d.attention_end, f, dst, nullptr);
   else st = afhip_transition_prepare_weights(&d.transition, f, dst, nullptr);
   if (st == AFHIP_OK) st = afhip_synchronize(nullptr);
   afhip_execution_release(e->ex, src);
@@ -864,7 +873,8 @@ napi_value ExecutionPrepareWeights(napi_env env, napi_callback_info info) {
 }
 
 // executionPairStack(ex, stackDesc, {outerProductMean?, triangleOutgoing?,
-// triangleIncoming?, pairTransition?}, pair, pairMask, msa?, msaMask?)
+// triangleIncoming?, triangleAttentionStarting?, triangleAttentionEnding?,
+// pairTransition?}, pair, pairMask, msa?, msaMask?)
 napi_value ExecutionPairStack(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a, 5)) return nullptr;
@@ -872,9 +882,10 @@ napi_value ExecutionPairStack(napi_env env, napi_callback_info info) {
   ExecutionEntry* e;
   afhip_pair_stack_desc d;
   if (!lookup_execution(env, a.argv[0], &exh, &e) || !read_stack_desc(env, a.argv[1], &d)) return nullptr;
-  const char* names[4] = {"outerProductMean", "triangleOutgoing", "triangleIncoming", "pairTransition"};
-  void* w[4] = {};
-  for (int i = 0; i < 4; i++) {
+  const char* names[6] = {"outerProductMean", "triangleOutgoing", "triangleIncoming", "triangleAttentionStarting",
+                          "triangleAttentionEnding", "pairTransition"};
+  void* w[6] = {};
+  for (int i = 0; i < 6; i++) {
     bool has = false;
     napi_has_named_property(env, a.argv[2], names[i], &has);
     if (!has) continue;
@@ -907,7 +918,7 @@ napi_value ExecutionPairStack(napi_env env, napi_callback_info info) {
       return nullptr;
     }
   }
-  afhip_pair_stack_weights pw{w[0], w[1], w[2], w[3]};
+  afhip_pair_stack_weights pw{w[0], w[1], w[2], w[3], w[4], w[5]};
   check(env, afhip_execution_pair_stack(e->ex, &d, &pw, msa, (const float*)mmask, pair, (const float*)pmask),
         "executionPairStack");
   return nullptr;
@@ -1119,6 +1130,69 @@ napi_value TransitionRun(napi_env env, napi_callback_info info) {
   return result_object(env, out, ms, act.bytes * 2 + packed.bytes + wbytes + wsbytes);
 }
 
+// attentionRun(desc {batch, queries, channels, heads, transpose, pairBias
+// (0 none, 1 normalized-input, 2 separate), pairChannels, precision,
+// epsilon}, activations: Float32Array, mask: Float32Array, pairActivations:
+// Float32Array | null, packed: Float32Array) -- AttentionGpu.run
+// (src/evoformer/attention.ts:1334-1452) over host arrays.
+napi_value AttentionRun(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 5)) return nullptr;
+  afhip_attention_desc d{};
+  int64_t v[8];
+  double eps;
+  napi_value o = a.argv[0];
+  const char* keys[8] = {"batch", "queries", "channels", "heads", "transpose", "pairBias", "pairChannels",
+                         "precision"};
+  const int64_t defaults[8] = {0, 0, 0, 0, 0, AFHIP_PAIR_BIAS_NONE, 0, AFHIP_PRECISION_F32};
+  for (int i = 0; i < 8; i++)
+    if (!prop_int(env, o, keys[i], defaults[i], &v[i])) return nullptr;
+  if (!prop_double(env, o, "epsilon", 1e-5, &eps)) return nullptr;
+  d = {(int32_t)v[0], (int32_t)v[1], (int32_t)v[2], (int32_t)v[3], (int32_t)v[4], (int32_t)v[5], (int32_t)v[6],
+       (int32_t)v[7], AFHIP_F32, AFHIP_F32, 0, (float)eps};
+  HostView act, mask, pair, packed;
+  napi_valuetype pt;
+  napi_typeof(env, a.argv[3], &pt);
+  const bool has_pair = pt != napi_undefined && pt != napi_null;
+  if (!get_view(env, a.argv[1], &act) || !get_view(env, a.argv[2], &mask) ||
+      (has_pair && !get_view(env, a.argv[3], &pair)) || !get_view(env, a.argv[4], &packed))
+    return nullptr;
+  size_t wbytes = 0, wsbytes = 0;
+  if (!check(env, afhip_attention_weights_size(&d, &wbytes), "attention") ||
+      !check(env, afhip_attention_workspace_size(&d, &wsbytes), "attention"))
+    return nullptr;
+  const size_t rows = (size_t)d.batch * d.queries;
+  if (act.bytes != rows * d.channels * 4 || mask.bytes != rows * 4) {
+    throw_js(env, {true, "activations or mask do not match the descriptor's shape"});
+    return nullptr;
+  }
+  if (d.pair_bias == AFHIP_PAIR_BIAS_SEPARATE &&
+      (!has_pair || pair.bytes != (size_t)d.queries * d.queries * d.pair_channels * 4)) {
+    throw_js(env, {true, "a separate pair bias needs pair activations [queries][queries][pairChannels]"});
+    return nullptr;
+  }
+  const double t0 = now_ms();
+  DeviceBuf da, dm, dpair, dp, dw, dws, dout;
+  if (!check(env, da.alloc(act.bytes), "attention") || !check(env, dm.alloc(mask.bytes), "attention") ||
+      !check(env, dp.alloc(packed.bytes), "attention") || !check(env, dw.alloc(wbytes), "attention") ||
+      !check(env, dws.alloc(wsbytes), "attention") || !check(env, dout.alloc(act.bytes), "attention") ||
+      (has_pair && !check(env, dpair.alloc(pair.bytes), "attention")))
+    return nullptr;
+  if (!check(env, afhip_buffer_write(da.p, 0, act.data, act.bytes), "attention") ||
+      !check(env, afhip_buffer_write(dm.p, 0, mask.data, mask.bytes), "attention") ||
+      (has_pair && !check(env, afhip_buffer_write(dpair.p, 0, pair.data, pair.bytes), "attention")) ||
+      !check(env, afhip_buffer_write(dp.p, 0, packed.data, packed.bytes), "attention") ||
+      !check(env, afhip_attention_prepare_weights(&d, (const float*)dp.p, dw.p, nullptr), "attention") ||
+      !check(env, afhip_attention_run(&d, da.p, (const float*)dm.p, has_pair ? dpair.p : nullptr, dw.p, dout.p,
+                                      dws.p, wsbytes, nullptr),
+             "attention"))
+    return nullptr;
+  std::vector<float> out(act.bytes / 4);
+  if (!check(env, afhip_buffer_read(dout.p, 0, out.data(), act.bytes), "attention")) return nullptr;
+  const double ms = now_ms() - t0;
+  return result_object(env, out, ms, act.bytes * 2 + mask.bytes + pair.bytes + packed.bytes + wbytes + wsbytes);
+}
+
 // ---------------------------------------------------------------------------
 // Kernel timing (WebGpuExecution's timestamp profile, execution.ts:329-345)
 // ---------------------------------------------------------------------------
@@ -1163,7 +1237,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"executionSnapshot", ExecutionSnapshot}, {"executionAddInPlace", ExecutionAddInPlace},
       {"executionPrepareWeights", ExecutionPrepareWeights}, {"executionPairStack", ExecutionPairStack},
       {"setMemoryBudget", SetMemoryBudget}, {"memoryResident", MemoryResident}, {"triangleRun", TriangleRun},
-      {"opmRun", OpmRun}, {"transitionRun", TransitionRun}, {"timingEnable", TimingEnable},
+      {"opmRun", OpmRun}, {"transitionRun", TransitionRun}, {"attentionRun", AttentionRun}, {"timingEnable", TimingEnable},
       {"timingReset", TimingReset}, {"timingReport", TimingReport},
   };
   for (const auto& f : fns) {

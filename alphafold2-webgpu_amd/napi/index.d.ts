@@ -114,12 +114,62 @@ export interface PairStackShape {
   msaDtype?: 0 | 1;
   opmRowBlock?: number;
   triangleBlockRows?: number;
+  attentionHeads?: number;
+}
+
+/** AttentionWeights (src/evoformer/attention.ts:19-29). */
+export interface AttentionWeights {
+  queryNormScale: Float32Array;
+  queryNormOffset: Float32Array;
+  queryWeight: Float32Array;
+  keyWeight: Float32Array;
+  valueWeight: Float32Array;
+  gatingWeight: Float32Array;
+  gatingBias: Float32Array;
+  outputWeight: Float32Array;
+  outputBias: Float32Array;
+}
+
+/** AttentionPairBias (src/evoformer/attention.ts:31-45). */
+export type AttentionPairBias =
+  | { source: "separate"; activations: Float32Array; channels: number; layerNormScale: Float32Array;
+      layerNormOffset: Float32Array; projectionWeight: Float32Array }
+  | { source: "normalized-input"; projectionWeight: Float32Array };
+
+/** AttentionInput (src/evoformer/attention.ts:47-58). */
+export interface AttentionInput {
+  activations: Float32Array;
+  mask: Float32Array;
+  batch: number;
+  queryLength: number;
+  channels: number;
+  heads: number;
+  transpose?: boolean;
+  weights: AttentionWeights;
+  pairBias?: AttentionPairBias;
+  epsilon?: number;
+}
+
+/** AttentionGpu (src/evoformer/attention.ts:1321-1452). */
+export declare class AttentionGpu {
+  run(input: AttentionInput, options?: { precision?: Precision }): OperatorResult;
+}
+
+export declare function packAttentionWeights(weights: AttentionWeights, pairBias?: AttentionPairBias): Float32Array;
+
+/** The block's triangle attention weights (src/evoformer/block.ts:1727-1745). */
+export interface TriangleAttentionWeights {
+  heads?: number;
+  attention: AttentionWeights;
+  pairProjectionWeight: Float32Array;
 }
 
 export interface PairStackWeights {
   outerProductMean?: OuterProductMeanWeights;
   triangleMultiplicationOutgoing?: TriangleMultiplicationWeights;
   triangleMultiplicationIncoming?: TriangleMultiplicationWeights;
+  triangleAttentionStarting?: TriangleAttentionWeights;
+  triangleAttentionEnding?: TriangleAttentionWeights;
   pairTransition?: TransitionWeights;
 }
 
@@ -128,6 +178,8 @@ export interface PreparedPairStack {
   outerProductMean?: number;
   triangleOutgoing?: number;
   triangleIncoming?: number;
+  triangleAttentionStarting?: number;
+  triangleAttentionEnding?: number;
   pairTransition?: number;
 }
 

@@ -8,6 +8,8 @@
 //     src/evoformer/outer-product-mean.ts:21-40, :549-646
 //   TransitionGpu(device).run(input, options)
 //     src/evoformer/transition.ts:18-31, :264-361
+//   AttentionGpu(device).run(input, options)
+//     src/evoformer/attention.ts:19-58, :102-201, :1321-1452
 //   gemmGrid, the GEMM variant selection and its persisted calibration
 //     src/runtime/gemm.ts:213-228, :368-379; src/runtime/gemm-selection.ts:122-125, :560-660
 //
@@ -182,6 +184,75 @@ TransitionGpu.prototype.run = function (input, options) {
   }, input.activations, packOrdered(input.weights, TRANSITION_ORDER));
 };
 
+var ATTENTION_ORDER = ["queryNormScale", "queryNormOffset", "queryWeight", "keyWeight", "valueWeight",
+  "gatingWeight", "gatingBias", "outputWeight", "outputBias"];
+var PAIR_BIAS = { "normalized-input": 1, separate: 2 };
+
+// packAttentionWeights (src/evoformer/attention.ts:179-201): the nine
+// tensors, then a separate bias's LayerNorm scale, offset and projection, or
+// a normalized-input bias's projection.
+function packAttentionWeights(weights, pairBias) {
+  var parts = ATTENTION_ORDER.map(function (n) { return weights[n]; });
+  if (pairBias !== undefined && pairBias !== null) {
+    if (pairBias.source === "separate") {
+      parts.push(pairBias.layerNormScale, pairBias.layerNormOffset, pairBias.projectionWeight);
+    } else {
+      parts.push(pairBias.projectionWeight);
+    }
+  }
+  var total = 0;
+  parts.forEach(function (t) { total += t.length; });
+  var out = new Float32Array(total);
+  var at = 0;
+  parts.forEach(function (t) { out.set(t, at); at += t.length; });
+  return out;
+}
+
+function expectCount(name, value, size) {
+  if (value.length !== size) throw new RangeError(name + " has " + value.length + " values; expected " + size);
+}
+
+// AttentionGpu.run (src/evoformer/attention.ts:1334-1452), with validate's
+// checks and messages (:102-141). input: the reference's AttentionInput.
+function AttentionGpu() {}
+AttentionGpu.prototype.run = function (input, options) {
+  options = options || {};
+  var b = input.batch, q = input.queryLength, c = input.channels, h = input.heads;
+  [b, q, c, h].forEach(function (v) {
+    if (!Number.isSafeInteger(v) || v <= 0) throw new RangeError("attention dimensions must be positive safe integers");
+  });
+  if (c % h !== 0 || c / h > 32) {
+    throw new RangeError("the fused WebGPU attention path requires an integral head dimension no larger than 32");
+  }
+  var w = input.weights;
+  expectCount("activations", input.activations, b * q * c);
+  expectCount("mask", input.mask, b * q);
+  expectCount("queryNormScale", w.queryNormScale, c);
+  expectCount("queryNormOffset", w.queryNormOffset, c);
+  ["queryWeight", "keyWeight", "valueWeight", "gatingWeight"].forEach(function (n) { expectCount(n, w[n], c * c); });
+  expectCount("gatingBias", w.gatingBias, c);
+  expectCount("outputWeight", w.outputWeight, c * c);
+  expectCount("outputBias", w.outputBias, c);
+  var pair = input.pairBias;
+  var pairChannels = 0;
+  if (pair !== undefined && pair !== null && pair.source === "separate") {
+    pairChannels = pair.channels;
+    expectCount("pair activations", pair.activations, q * q * pairChannels);
+    expectCount("pair norm scale", pair.layerNormScale, pairChannels);
+    expectCount("pair norm offset", pair.layerNormOffset, pairChannels);
+    expectCount("pair projection", pair.projectionWeight, pairChannels * h);
+  } else if (pair !== undefined && pair !== null && pair.projectionWeight.length !== c * h) {
+    throw new RangeError("normalized-input pair projection has an invalid size");
+  }
+  var precision = options.precision === undefined ? "f32" : options.precision;
+  requestHipDevice();
+  return addon().attentionRun({
+    batch: b, queries: q, channels: c, heads: h, transpose: input.transpose === true ? 1 : 0,
+    pairBias: pair === undefined || pair === null ? 0 : PAIR_BIAS[pair.source], pairChannels: pairChannels,
+    precision: PRECISION[precision], epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
+  }, input.activations, input.mask, pairChannels > 0 ? pair.activations : null, packAttentionWeights(w, pair));
+};
+
 // gemmGrid (src/runtime/gemm.ts:368-379).
 // The execution layer (src/runtime/execution.ts:153-555, allocator.ts:168-388):
 // device tensors as buffer handles drawn from a pool that outlives each
@@ -207,10 +278,13 @@ HipExecution.prototype.addInPlace = function (base, update, elements, baseDtype,
     updateDtype === undefined ? F32 : updateDtype, elements);
 };
 // shape: {length, sequences, cM, cZ, cOuter, cHidden, transitionFactor,
-// precision, pairDtype, msaDtype}; weights: {outerProductMean,
-// triangleMultiplicationOutgoing, triangleMultiplicationIncoming,
-// pairTransition}, each the operator's weight object (a missing one skips
-// that step). Returns the prepared weight buffers.
+// precision, pairDtype, msaDtype, attentionHeads}; weights:
+// {outerProductMean, triangleMultiplicationOutgoing,
+// triangleMultiplicationIncoming, triangleAttentionStarting,
+// triangleAttentionEnding, pairTransition}, each the operator's weight
+// object, the attentions as the block's {attention, pairProjectionWeight}
+// (src/evoformer/block.ts:1727-1745); a missing one skips that step.
+// Returns the prepared weight buffers.
 HipExecution.prototype.preparePairStack = function (shape, weights) {
   var native = addon(), h = this.handle, out = {};
   if (weights.outerProductMean) {
@@ -225,6 +299,13 @@ HipExecution.prototype.preparePairStack = function (shape, weights) {
     out.triangleIncoming = native.executionPrepareWeights(h, "triangleIncoming", shape,
       packTriangleWeights(weights.triangleMultiplicationIncoming));
   }
+  ["triangleAttentionStarting", "triangleAttentionEnding"].forEach(function (kind) {
+    var a = weights[kind];
+    if (a) {
+      out[kind] = native.executionPrepareWeights(h, kind, shape, packAttentionWeights(a.attention,
+        { source: "normalized-input", projectionWeight: a.pairProjectionWeight }));
+    }
+  });
   if (weights.pairTransition) {
     out.pairTransition = native.executionPrepareWeights(h, "pairTransition", shape,
       packOrdered(weights.pairTransition, TRANSITION_ORDER));
@@ -270,6 +351,8 @@ module.exports = {
   setGpuMemoryBudget: function (bytes) { requestHipDevice(); addon().setMemoryBudget(bytes === undefined ? null : bytes); },
   gpuMemoryResident: function () { return addon().memoryResident(); },
   TransitionGpu: TransitionGpu,
+  AttentionGpu: AttentionGpu,
+  packAttentionWeights: packAttentionWeights,
   validateTriangleInput: validateTriangleInput,
   packTriangleWeights: packTriangleWeights,
   errorMetrics: errorMetrics,

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define AFHIP_ABI_VERSION 1
+#define AFHIP_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define AFHIP_API __attribute__((visibility("default")))
@@ -434,6 +434,8 @@ typedef struct afhip_pair_stack_desc {
   afhip_opm_desc opm;               /* out_dtype = the pair's dtype */
   afhip_triangle_desc outgoing;     /* pair_dtype = out_dtype = the pair's dtype */
   afhip_triangle_desc incoming;
+  afhip_attention_desc attention_start; /* batch = queries = L, channels = c_z, dtypes the pair's */
+  afhip_attention_desc attention_end;
   afhip_transition_desc transition; /* rows = L * L, channels = c_z, in/out dtype = the pair's */
 } afhip_pair_stack_desc;
 
@@ -442,17 +444,20 @@ typedef struct afhip_pair_stack_weights {
   const void* opm;
   const void* outgoing;
   const void* incoming;
+  const void* attention_start;
+  const void* attention_end;
   const void* transition;
 } afhip_pair_stack_weights;
 
 /* The pair-representation steps of encodeEvoformerBlock
- * (src/evoformer/block.ts:1673-1759) that this library builds, in the
- * block's order, each adding into `pair` in place: outer-product mean
- * (:1683-1689, :1718), triangle multiplication outgoing then incoming
- * (:1720-1725), pair transition (:1747-1750). The triangle attentions between
- * them (:1727-1745) are outside this library and are not run. Each step's
- * workspace comes from the execution's pool and returns to it once the step
- * is queued; the descriptors' residual flags and directions are set here. */
+ * (src/evoformer/block.ts:1673-1759), in the block's order, each adding into
+ * `pair` in place: outer-product mean (:1683-1689, :1718), triangle
+ * multiplication outgoing then incoming (:1720-1725), triangle attention
+ * around the starting node then the ending node (:1727-1745, normalized-input
+ * pair bias, the ending node transposed), pair transition (:1747-1750). Each
+ * step's workspace comes from the execution's pool and returns to it once the
+ * step is queued; the descriptors' residual flags, directions, transposes and
+ * pair bias sources are set here. */
 AFHIP_API int afhip_execution_pair_stack(afhip_execution* ex, const afhip_pair_stack_desc* desc,
                                          const afhip_pair_stack_weights* weights, const void* msa,
                                          const float* msa_mask, void* pair, const float* pair_mask);

@@ -8,12 +8,12 @@ var native = afhip.addon();
 var expected = ["open", "close", "abiVersion", "deviceReport", "bufferCreate", "bufferDestroy", "bufferWrite",
   "bufferRead", "synchronize", "gemmGrid", "gemmSelect", "gemmCalibrate", "gemmForceVariant", "calibrationLoad",
   "calibrationSave", "gemmPlanCreate", "gemmPlanDestroy", "gemmWorkspaceSize", "gemmRun", "triangleRun", "opmRun",
-  "transitionRun", "timingEnable", "timingReset", "timingReport", "packWeightQ8Block", "executionCreate",
+  "transitionRun", "attentionRun", "timingEnable", "timingReset", "timingReport", "packWeightQ8Block", "executionCreate",
   "executionDestroy", "executionAllocate", "executionUpload", "executionRelease", "executionCheckpoint",
   "executionReleaseSince", "executionNoteSubmitted", "executionSnapshot", "executionAddInPlace",
   "executionPrepareWeights", "executionPairStack", "setMemoryBudget", "memoryResident"];
 expected.forEach(function (n) { assert.strictEqual(typeof native[n], "function", n); });
-assert.strictEqual(native.abiVersion(), 1);
+assert.strictEqual(native.abiVersion(), 2);
 
 // gemmGrid known answers (test/gemm-selection.test.ts:239-262, test/gemm.test.ts:37-61).
 assert.deepStrictEqual(afhip.gemmGrid(65536 * 64, 128), [2, 65535]);
@@ -28,6 +28,12 @@ assert.strictEqual(v.kernel, afhip.KERNEL.lds_dma);
 assert.strictEqual(v.tileRows, 192);
 
 // Input validation happens before any device work (RangeError, types.ts:42-52).
+var attInput = { activations: new Float32Array(3 * 4 * 8), mask: new Float32Array(12), batch: 3, queryLength: 4,
+  channels: 8, heads: 3, weights: {} };
+assert.throws(function () { new afhip.AttentionGpu().run(attInput); }, /integral head dimension no larger than 32/);
+attInput.heads = 2;
+attInput.mask = new Float32Array(11);
+assert.throws(function () { new afhip.AttentionGpu().run(attInput); }, /mask has 11 values; expected 12/);
 var bad = { shape: [2, 3, 4], z: new Float32Array(5), mask: new Float32Array(4), weights: {} };
 assert.throws(function () { new afhip.TriangleMultiplicationOutgoingGpu().run(bad); }, /z has 5 values/);
 assert.throws(function () { afhip.validateTriangleInput({ shape: [0, 3, 4] }); }, RangeError);

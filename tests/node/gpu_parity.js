@@ -120,8 +120,54 @@ function transposePairs(data, L, C) {
   report.cases.push({ q8PackedGemmMaxRelative: worst / largest });
 })();
 
+// AttentionGpu with zero query and key weights and no bias: every key
+// weighs 1/Q, so row (b, q) is mean_k(v[b][k]) * g[b][q], then the output
+// projection -- computed here in float64 from the LayerNormed rows.
+(function () {
+  var B = 3, Q = 5, C = 8, H = 2;
+  function fill(n, f) { var a = new Float32Array(n); for (var i = 0; i < n; i++) a[i] = f(i); return a; }
+  var x = fill(B * Q * C, function (i) { return Math.sin(1.3 * i) + 0.1 * (i % 5); });
+  var w = { queryNormScale: fill(C, function () { return 1; }), queryNormOffset: fill(C, function () { return 0; }),
+    queryWeight: new Float32Array(C * C), keyWeight: new Float32Array(C * C),
+    valueWeight: fill(C * C, function (i) { return 0.3 * Math.cos(0.7 * i); }),
+    gatingWeight: fill(C * C, function (i) { return 0.2 * Math.sin(0.4 * i); }),
+    gatingBias: fill(C, function (i) { return 0.1 * i; }),
+    outputWeight: fill(C * C, function (i) { return 0.25 * Math.sin(0.9 * i + 1); }),
+    outputBias: fill(C, function (i) { return 0.01 * i; }) };
+  var out = new afhip.AttentionGpu().run({ activations: x, mask: fill(B * Q, function () { return 1; }), batch: B,
+    queryLength: Q, channels: C, heads: H, weights: w }, { precision: "f32" }).output;
+  var worst = 0, largest = 0;
+  for (var b = 0; b < B; b++) {
+    var xn = [], vmean = new Array(C).fill(0);
+    for (var q = 0; q < Q; q++) {
+      var row = Array.from(x.subarray((b * Q + q) * C, (b * Q + q + 1) * C));
+      var mean = row.reduce(function (s, v) { return s + v; }, 0) / C;
+      var vr = row.reduce(function (s, v) { return s + (v - mean) * (v - mean); }, 0) / C;
+      xn.push(row.map(function (v) { return (v - mean) / Math.sqrt(vr + 1e-5); }));
+    }
+    for (q = 0; q < Q; q++)
+      for (var c = 0; c < C; c++) for (var k = 0; k < C; k++) vmean[c] += xn[q][k] * w.valueWeight[k * C + c] / Q;
+    for (q = 0; q < Q; q++) {
+      var o = [];
+      for (c = 0; c < C; c++) {
+        var g = w.gatingBias[c];
+        for (k = 0; k < C; k++) g += xn[q][k] * w.gatingWeight[k * C + c];
+        o.push(vmean[c] / (1 + Math.exp(-g)));
+      }
+      for (c = 0; c < C; c++) {
+        var y = w.outputBias[c];
+        for (k = 0; k < C; k++) y += o[k] * w.outputWeight[k * C + c];
+        worst = Math.max(worst, Math.abs(out[(b * Q + q) * C + c] - y));
+        largest = Math.max(largest, Math.abs(y));
+      }
+    }
+  }
+  assert.ok(worst <= 1e-5 * largest, "attention closed form " + worst / largest);
+  report.cases.push({ attentionClosedFormMaxRelative: worst / largest });
+})();
+
 // The execution layer from Node: the pair steps chained on the device
-// (HipExecution.pairStack) against the four operators run one by one through
+// (HipExecution.pairStack) against the six operators run one by one through
 // their host-array entry points, the updates added on the host in the
 // block's order (src/evoformer/block.ts:1683-1750).
 (function () {
@@ -140,12 +186,22 @@ function transposePairs(data, L, C) {
     });
     return w;
   }
+  function attentionWeights(phase) {
+    return { heads: 2, pairProjectionWeight: wave(cZ * 2, 0.3, phase + 9), attention: {
+      queryNormScale: wave(cZ, 0.1, phase, 1), queryNormOffset: wave(cZ, 0.05, phase + 1),
+      queryWeight: wave(cZ * cZ, 0.25, phase + 2), keyWeight: wave(cZ * cZ, 0.25, phase + 3),
+      valueWeight: wave(cZ * cZ, 0.25, phase + 4), gatingWeight: wave(cZ * cZ, 0.25, phase + 5),
+      gatingBias: wave(cZ, 0.1, phase + 6, 1), outputWeight: wave(cZ * cZ, 0.25, phase + 7),
+      outputBias: wave(cZ, 0.05, phase + 8) } };
+  }
   var weights = {
     outerProductMean: { layerNormScale: wave(cM, 0.1, 1, 1), layerNormOffset: wave(cM, 0.05, 2),
       leftWeight: wave(cM * cO, 0.3, 3), leftBias: wave(cO, 0.05, 4), rightWeight: wave(cM * cO, 0.3, 5),
       rightBias: wave(cO, 0.05, 6), outputWeight: wave(cO * cO * cZ, 0.2, 7), outputBias: wave(cZ, 0.05, 8) },
     triangleMultiplicationOutgoing: triangleWeights(10),
     triangleMultiplicationIncoming: triangleWeights(40),
+    triangleAttentionStarting: attentionWeights(50),
+    triangleAttentionEnding: attentionWeights(60),
     pairTransition: { layerNormScale: wave(cZ, 0.1, 70, 1), layerNormOffset: wave(cZ, 0.05, 71),
       firstWeight: wave(cZ * hidden, 0.2, 72), firstBias: wave(hidden, 0.05, 73),
       secondWeight: wave(hidden * cZ, 0.1, 74), secondBias: wave(cZ, 0.05, 75) },
@@ -161,12 +217,18 @@ function transposePairs(data, L, C) {
     weights: weights.triangleMultiplicationOutgoing }).output);
   addInto(z, new afhip.TriangleMultiplicationIncomingGpu().run({ shape: [L, cZ, cH], z: z, mask: pairMask,
     weights: weights.triangleMultiplicationIncoming }).output);
+  [["triangleAttentionStarting", false], ["triangleAttentionEnding", true]].forEach(function (step) {
+    var a = weights[step[0]];
+    addInto(z, new afhip.AttentionGpu().run({ activations: z, mask: pairMask, batch: L, queryLength: L, channels: cZ,
+      heads: 2, transpose: step[1], weights: a.attention,
+      pairBias: { source: "normalized-input", projectionWeight: a.pairProjectionWeight } }).output);
+  });
   addInto(z, new afhip.TransitionGpu().run({ shape: [L * L, cZ, hidden], activations: z,
     weights: weights.pairTransition }).output);
 
   var ex = new afhip.HipExecution();
   var shape = { length: L, sequences: S, cM: cM, cZ: cZ, cOuter: cO, cHidden: cH, transitionFactor: 4,
-    precision: afhip.PRECISION.f32, pairDtype: afhip.DTYPE.f32, msaDtype: afhip.DTYPE.f32 };
+    precision: afhip.PRECISION.f32, pairDtype: afhip.DTYPE.f32, msaDtype: afhip.DTYPE.f32, attentionHeads: 2 };
   var prepared = ex.preparePairStack(shape, weights);
   var bPair = ex.upload("pair", pair), bMask = ex.upload("pair-mask", pairMask);
   var bMsa = ex.upload("msa", msa), bMsaMask = ex.upload("msa-mask", msaMask);

@@ -92,17 +92,27 @@ def _block_weights(seed, cz, ch, cm, co, h):
     tr_w = {"layerNormScale": ref.normal(seed + 8, (cz,), 0.01, 1.0), "layerNormOffset": ref.normal(seed + 9, (cz,), 0.01),
             "firstWeight": ref.normal(seed + 10, (cz, h), 1 / cz), "firstBias": ref.normal(seed + 11, (h,), 0.02),
             "secondWeight": ref.normal(seed + 12, (h, cz), 1 / h), "secondBias": ref.normal(seed + 13, (cz,), 0.02)}
+    def att(s0):
+        a = {"queryNormScale": ref.normal(s0, (cz,), 0.01, 1.0), "queryNormOffset": ref.normal(s0 + 1, (cz,), 0.01),
+             "queryWeight": ref.normal(s0 + 2, (cz, cz), 1 / cz), "keyWeight": ref.normal(s0 + 3, (cz, cz), 1 / cz),
+             "valueWeight": ref.normal(s0 + 4, (cz, cz), 1 / cz), "gatingWeight": ref.normal(s0 + 5, (cz, cz), 1 / cz),
+             "gatingBias": ref.normal(s0 + 6, (cz,), 0.1, 1.0), "outputWeight": ref.normal(s0 + 7, (cz, cz), 1 / cz),
+             "outputBias": ref.normal(s0 + 8, (cz,), 0.01)}
+        return {"heads": 4, "attention": a, "pairProjectionWeight": ref.normal(s0 + 9, (cz, 4), 1 / cz)}
+
     return {"outerProductMean": opm_w, "triangleMultiplicationOutgoing": triangle_weights(seed + 20, cz, ch),
-            "triangleMultiplicationIncoming": triangle_weights(seed + 40, cz, ch), "pairTransition": tr_w}
+            "triangleMultiplicationIncoming": triangle_weights(seed + 40, cz, ch),
+            "triangleAttentionStarting": att(seed + 60), "triangleAttentionEnding": att(seed + 80),
+            "pairTransition": tr_w}
 
 
 def test_pair_stack_is_the_operators_in_sequence(dev):
     # f16 at AlphaFold's widths (the fused kernels): the chained stack gives
-    # the result of the four operators called one after another on the same
+    # the result of the six operators called one after another on the same
     # pair, bit for bit, with its workspaces drawn from the pool.
     import torch
 
-    from afhip import opm, transition, triangle
+    from afhip import attention, opm, transition, triangle
     from afhip.execution import Execution, PairStack
 
     L, S, cm, co, cz, ch = 64, 16, 64, 32, 128, 128
@@ -121,6 +131,13 @@ def test_pair_stack_is_the_operators_in_sequence(dev):
                                             out_dtype="f16", residual=True)
         t.prepare(w[key])
         t(expect, pair_mask, out=expect)
+    for tp, key in ((False, "triangleAttentionStarting"), (True, "triangleAttentionEnding")):
+        a = attention.Attention(L, L, cz, 4, transpose=tp, pair_bias="normalized-input", precision="f16",
+                                in_dtype="f16", out_dtype="f16", residual=True)
+        a.prepare(attention.pack_weights(w[key]["attention"], {"source": "normalized-input",
+                                                              "projectionWeight": w[key]["pairProjectionWeight"]}))
+        flat = expect.reshape(L * L, cz)
+        a(flat, pair_mask.reshape(-1), out=flat)
     tr = transition.Transition(L * L, cz, 4 * cz, precision="f16", in_dtype="f16", out_dtype="f16", residual=True)
     tr.prepare(w["pairTransition"])
     tr(expect, out=expect)
@@ -144,7 +161,7 @@ def test_pair_stack_is_the_operators_in_sequence(dev):
 def test_pair_stack_against_the_oracle(dev):
     # f32 at small widths (the general kernels) against the oracle composed in
     # the block's order: z += OPM(m); z += outgoing(z); z += incoming(z);
-    # z += transition(z).
+    # z += attention_start(z); z += attention_end(z); z += transition(z).
     from afhip.execution import Execution, PairStack
 
     L, S, cm, co, cz, ch = 24, 8, 16, 8, 32, 32
@@ -156,6 +173,10 @@ def test_pair_stack_against_the_oracle(dev):
     expect = z + ref.opm(msa, msa_mask, w["outerProductMean"])
     expect = expect + ref.triangle("outgoing", expect, pair_mask, w["triangleMultiplicationOutgoing"])
     expect = expect + ref.triangle("incoming", expect, pair_mask, w["triangleMultiplicationIncoming"])
+    for tp, key in ((False, "triangleAttentionStarting"), (True, "triangleAttentionEnding")):
+        pb = {"source": "normalized-input", "projectionWeight": w[key]["pairProjectionWeight"]}
+        expect = expect + ref.attention(expect, pair_mask, w[key]["attention"], L, L, cz, 4, transpose=tp,
+                                        pair_bias=pb).reshape(L, L, cz)
     expect = expect + ref.transition(expect.reshape(L * L, cz), w["pairTransition"]).reshape(L, L, cz)
 
     ex = Execution()
@@ -167,6 +188,22 @@ def test_pair_stack_against_the_oracle(dev):
     stack(pz, pzm, pm, pmm)
     got = ex.download(pz, (L, L, cz))
     assert np.abs(got - expect).max() <= 1e-4 * np.abs(expect).max()
+    ex.release()
+
+
+def test_pair_stack_rejects_mismatched_attention(dev):
+    from afhip import _lib
+    from afhip.execution import Execution, PairStack
+
+    ex = Execution()
+    stack = PairStack(ex, 16, sequences=4, c_m=16, c_z=32, c_outer=8, c_hidden=32, precision="f32",
+                      pair_dtype="f32", msa_dtype="f32")
+    stack.desc.attention_end.channels = 64
+    stack.weights.attention_end = 1  # never read: the shapes are checked first
+    pz = ex.allocate("pair", 16 * 16 * 32 * 4)
+    pm = ex.allocate("pair-mask", 16 * 16 * 4)
+    with pytest.raises(_lib.RangeError, match="triangle attention does not match"):
+        stack(pz, pm)
     ex.release()
 
 
