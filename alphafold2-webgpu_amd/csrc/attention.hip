@@ -664,6 +664,22 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   }
 }
 
+// out += y over f16 tensors (f32 sum, one rounding): the residual step of
+// an output projection the streaming kernel computed without it.
+__global__ __launch_bounds__(256) void attention_residual_kernel(half_t* __restrict__ out,
+                                                                 const half_t* __restrict__ y, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i + 8 <= n) {
+    half8 a = *reinterpret_cast<const half8*>(out + i);
+    const half8 b = *reinterpret_cast<const half8*>(y + i);
+#pragma unroll
+    for (int e = 0; e < 8; e++) a[e] = (half_t)((float)a[e] + (float)b[e]);
+    *reinterpret_cast<half8*>(out + i) = a;
+  } else {
+    for (int64_t j = i; j < n; j++) out[j] = (half_t)((float)out[j] + (float)y[j]);
+  }
+}
+
 template <typename IT, typename OT>
 int launch_rows_typed(const RowsArgs& r, const char* label, hipStream_t st) {
   const bool vec = (reinterpret_cast<uintptr_t>(r.x) & 15) == 0 &&
@@ -870,8 +886,22 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
     g.ldc = C;
     g.flags = AFHIP_EPILOGUE_BIAS | (d.residual ? AFHIP_EPILOGUE_RESIDUAL : 0u);
     GemmTypes t{d.precision, ct, ct, d.out_dtype};
-    if (stream_eligible(g, t)) {
-      if ((s = run_gemm_stream(g, t, "attention.output", st))) return s;
+    // The streaming kernel has no residual epilogue: with a residual it
+    // writes the projection to the (by now unused) normalised rows, and a
+    // vectorised pass adds them in.
+    GemmArgs gs = g;
+    gs.flags &= ~AFHIP_EPILOGUE_RESIDUAL;
+    gs.residual = nullptr;
+    if (d.residual) gs.c = wsb + ws.normalized;
+    const bool aligned = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    if (stream_eligible(gs, t) && (!d.residual || aligned)) {
+      if ((s = run_gemm_stream(gs, t, "attention.output", st))) return s;
+      if (d.residual) {
+        const int64_t n = rows * C;
+        if ((s = launch("attention.residual", attention_residual_kernel, dim3((unsigned)ceil_div(n, 2048)),
+                        dim3(256), 0, st, (half_t*)out, (const half_t*)(wsb + ws.normalized), n)))
+          return s;
+      }
     } else if ((s = run_gemm(g, t, select_variant(t, g.M, g.N, g.K, 1), "attention.output", st))) {
       return s;
     }

@@ -266,6 +266,59 @@ def measure_configs(steps: int, warmup: int, which=(1, 2, 4, 5)) -> dict:
             entry["transition"] = rate("transition.fused", k_t["transition.fused"], flops=ft,
                                        traffic=recorded_traffic().get("config5.transition"))
         out["5_long_complex_pair_stack_l1024"] = entry
+        del z, mask, tri, zo, trans, zf, to
+        torch.cuda.empty_cache()
+    if "attention" in which:
+        out["attention"] = measure_attention(steps, warmup)
+    return out
+
+
+def measure_attention(steps: int, warmup: int) -> dict:
+    """The Evoformer's attentions at f16 (head dimension 32, the MFMA flash
+    kernel), synthetic inputs: triangle attention around the starting node at
+    N_res=384 (c_z 128, 4 heads, normalized-input pair bias) and MSA row
+    attention at N_seq=512, N_res=256 (c_m 256, 8 heads, pair bias from a
+    [256, 256, 128] pair). Flash FLOPs: 4 d per (batch, head, query, key)."""
+    import numpy as np
+    import torch
+
+    from afhip import attention, device
+    from oracle import ref
+
+    dev = device.device()
+    out = {}
+    for name, B, Q, C, H, pair, Cp, s in (("triangle_start_l384", 384, 384, 128, 4, "normalized-input", 0, SEED + 5),
+                                          ("msa_row_s512_l256", 512, 256, 256, 8, "separate", 128, SEED + 6)):
+        w = {"queryNormScale": ref.normal(s, (C,), 0.01, 1.0), "queryNormOffset": ref.normal(s + 1, (C,), 0.01),
+             "queryWeight": ref.normal(s + 2, (C, C), 1 / C), "keyWeight": ref.normal(s + 3, (C, C), 1 / C),
+             "valueWeight": ref.normal(s + 4, (C, C), 1 / C), "gatingWeight": ref.normal(s + 5, (C, C), 1 / C),
+             "gatingBias": ref.normal(s + 6, (C,), 0.1, 1.0), "outputWeight": ref.normal(s + 7, (C, C), 1 / C),
+             "outputBias": ref.normal(s + 8, (C,), 0.01)}
+        pc = Cp or C
+        pb = {"source": pair, "projectionWeight": ref.normal(s + 9, (pc, H), 1 / pc)}
+        if pair == "separate":
+            pb.update(channels=Cp, layerNormScale=ref.normal(s + 10, (Cp,), 0.01, 1.0),
+                      layerNormOffset=ref.normal(s + 11, (Cp,), 0.01))
+        op = attention.Attention(B, Q, C, H, pair_bias=pair, pair_channels=Cp, precision="f16", in_dtype="f16",
+                                 out_dtype="f16", residual=True)
+        op.prepare(attention.pack_weights(w, pb))
+        x = torch.from_numpy(ref.round_f16(ref.normal(s + 12, (B * Q, C)))).half().to(dev)
+        mask = torch.ones(B * Q, dtype=torch.float32, device=dev)
+        p = None
+        if pair == "separate":
+            p = torch.from_numpy(ref.round_f16(ref.normal(s + 13, (Q * Q * Cp,)))).half().to(dev)
+        y = x.clone()
+        ms, k = timed(lambda: op(x, mask, p, out=y), max(5, steps // 5), warmup)
+        d = C // H
+        flash = 4 * B * H * Q * Q * d
+        total = flash + 2 * B * Q * C * 4 * C + 2 * B * Q * C * C + 2 * Q * Q * pc * H
+        entry = {"ms": round(ms, 4), "tflops": round(total / (ms * 1e-3) / 1e12, 2),
+                 "kernel_ms": {kk: round(v, 5) for kk, v in k.items()}}
+        if "attention.flash" in k:
+            entry["flash"] = rate("attention.flash", k["attention.flash"], flops=flash)
+        out[name] = entry
+        del op, x, mask, p, y
+        torch.cuda.empty_cache()
     return out
 
 
@@ -278,8 +331,9 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--headline-only", action="store_true", help="skip BASELINE configs 1, 2, 4 and 5")
-    parser.add_argument("--configs", default="1,2,4,5",
-                        help="comma-separated BASELINE configs to measure besides the headline (config 3)")
+    parser.add_argument("--configs", default="1,2,4,5,attention",
+                        help="comma-separated BASELINE configs to measure besides the headline (config 3), and "
+                             "'attention' for the Evoformer attentions")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                         help="only run a plain device-to-device copy of MIB MiB 10 times (the known-size kernel "
                              "rocprof's FETCH_SIZE / WRITE_SIZE readings are scaled by) and exit")
@@ -355,7 +409,8 @@ def main() -> None:
         "kernels": kernels,
         "kernel_ms": {k: round(v, 5) for k, v in per_kernel.items()},
     }
-    which = tuple(int(c) for c in args.configs.split(",") if c.strip()) if not args.headline_only else ()
+    which = tuple(c.strip() if c.strip() == "attention" else int(c) for c in args.configs.split(",")
+                  if c.strip()) if not args.headline_only else ()
     if which:
         del ops, zd, md
         torch.cuda.empty_cache()
