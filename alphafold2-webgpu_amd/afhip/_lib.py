@@ -122,6 +122,16 @@ class PairStackWeights(ctypes.Structure):
                 ("transition", ctypes.c_void_p)]
 
 
+class EvoformerBlockDesc(ctypes.Structure):
+    _fields_ = [("msa_row", AttentionDesc), ("msa_column", AttentionDesc), ("msa_transition", TransitionDesc),
+                ("pair", PairStackDesc), ("opm_first", ctypes.c_int32)]
+
+
+class EvoformerBlockWeights(ctypes.Structure):
+    _fields_ = [("msa_row", ctypes.c_void_p), ("msa_column", ctypes.c_void_p), ("msa_transition", ctypes.c_void_p),
+                ("pair", PairStackWeights)]
+
+
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
 _i32 = ctypes.c_int32
@@ -184,6 +194,8 @@ SIGNATURES = {
     "afhip_execution_add_in_place": [_vp, _vp, _i32, _vp, _i32, _i64],
     "afhip_execution_pair_stack": [_vp, ctypes.POINTER(PairStackDesc), ctypes.POINTER(PairStackWeights), _vp, _vp,
                                    _vp, _vp],
+    "afhip_execution_evoformer_block": [_vp, ctypes.POINTER(EvoformerBlockDesc), ctypes.POINTER(EvoformerBlockWeights),
+                                        _vp, _vp, _vp, _vp],
     "afhip_timing_enable": [ctypes.c_int],
     "afhip_timing_reset": [],
     "afhip_timing_report": [ctypes.c_char_p, _sz],

@@ -4,9 +4,10 @@ pair-representation steps of an Evoformer block chained on the device.
 `Execution` mirrors WebGpuExecution (src/runtime/execution.ts:153-555) with
 its pooled allocator (src/runtime/allocator.ts:168-388): allocate, upload,
 release, checkpoint / release_since, note_submitted, snapshot, add_in_place.
-`PairStack` runs the steps of encodeEvoformerBlock (src/evoformer/block.ts:
-1673-1759) that this library builds, in place on one pair tensor, with every
-workspace taken from the execution's pool. Tensors are plain device pointers
+`PairStack` runs the pair steps of encodeEvoformerBlock (src/evoformer/block.ts:
+1673-1759) in place on one pair tensor, and `EvoformerBlock` the whole block
+(the MSA steps, then the pair steps), with every workspace taken from the
+execution's pool. Tensors are plain device pointers
 (ints); torch tensors are accepted wherever a pointer is.
 """
 from __future__ import annotations
@@ -195,4 +196,61 @@ class PairStack:
 
     def __call__(self, pair, pair_mask, msa=None, msa_mask=None) -> None:
         _lib.call("afhip_execution_pair_stack", self.execution.handle, ctypes.byref(self.desc),
+                  ctypes.byref(self.weights), _address(msa), _address(msa_mask), _address(pair), _address(pair_mask))
+
+
+class EvoformerBlock:
+    """encodeEvoformerBlock (block.ts:1673-1759): MSA row attention with the
+    pair bias, MSA column attention, MSA transition, then the pair steps
+    (outer-product mean first instead when opm_first). The MSA and the pair
+    are updated in place and share one dtype."""
+
+    def __init__(self, execution: Execution, length: int, *, sequences: int, c_m: int = 256, c_z: int = 128,
+                 msa_heads: int = 8, pair_heads: int = 4, msa_transition_factor: int = 4, opm_first: bool = False,
+                 precision: str = "f16", dtype: str = "f16", **pair_options):
+        self.execution = execution
+        self.stack = PairStack(execution, length, sequences=sequences, c_m=c_m, c_z=c_z, precision=precision,
+                               pair_dtype=dtype, msa_dtype=dtype, attention_heads=pair_heads, **pair_options)
+        prec = _lib.PRECISION_F16 if precision == "f16" else _lib.PRECISION_F32
+        dt = _DT[dtype]
+        self.desc = _lib.EvoformerBlockDesc()
+        self.desc.msa_row = _lib.AttentionDesc(sequences, length, c_m, msa_heads, 0, _lib.PAIR_BIAS_SEPARATE, c_z, prec,
+                                               dt, dt, 1, 1e-5)
+        self.desc.msa_column = _lib.AttentionDesc(length, sequences, c_m, msa_heads, 1, _lib.PAIR_BIAS_NONE, 0, prec,
+                                                  dt, dt, 1, 1e-5)
+        self.desc.msa_transition = _lib.TransitionDesc(sequences * length, c_m, msa_transition_factor * c_m, prec, dt,
+                                                       dt, 1, 1e-5)
+        self.desc.opm_first = int(opm_first)
+        self.weights = _lib.EvoformerBlockWeights()
+
+    def prepare(self, weights: dict) -> None:
+        """weights: the pair stack's keys, plus "msaRowAttention" ({"attention",
+        "pairLayerNormScale", "pairLayerNormOffset", "pairProjectionWeight"},
+        block.ts:1690-1702), "msaColumnAttention" ({"attention"}) and
+        "msaTransition" (a transition weight dict); a missing one skips that
+        step."""
+        st, d = self.stack, self.desc
+        st.prepare(weights)
+        row = weights.get("msaRowAttention")
+        if row is not None:
+            pb = {"source": "separate", "layerNormScale": row["pairLayerNormScale"],
+                  "layerNormOffset": row["pairLayerNormOffset"], "projectionWeight": row["pairProjectionWeight"]}
+            self.weights.msa_row = st._prepare("msa-row-attention", d.msa_row,
+                                               _attention.pack_weights(row["attention"], pb),
+                                               "afhip_attention_weights_size", "afhip_attention_prepare_weights")
+        col = weights.get("msaColumnAttention")
+        if col is not None:
+            self.weights.msa_column = st._prepare("msa-column-attention", d.msa_column,
+                                                  _attention.pack_weights(col["attention"]),
+                                                  "afhip_attention_weights_size", "afhip_attention_prepare_weights")
+        tr = weights.get("msaTransition")
+        if tr is not None:
+            self.weights.msa_transition = st._prepare(
+                "msa-transition", d.msa_transition, _transition.pack_weights(tr) if isinstance(tr, dict) else tr,
+                "afhip_transition_weights_size", "afhip_transition_prepare_weights")
+        self.desc.pair = st.desc
+        self.weights.pair = st.weights
+
+    def __call__(self, msa, msa_mask, pair, pair_mask) -> None:
+        _lib.call("afhip_execution_evoformer_block", self.execution.handle, ctypes.byref(self.desc),
                   ctypes.byref(self.weights), _address(msa), _address(msa_mask), _address(pair), _address(pair_mask))

@@ -342,4 +342,63 @@ int afhip_execution_pair_stack(afhip_execution* ex, const afhip_pair_stack_desc*
   return AFHIP_OK;
 }
 
+int afhip_execution_evoformer_block(afhip_execution* ex, const afhip_evoformer_block_desc* desc,
+                                    const afhip_evoformer_block_weights* weights, void* msa, const float* msa_mask,
+                                    void* pair, const float* pair_mask) {
+  if (int s = require_execution(ex)) return s;
+  AFHIP_REQUIRE(desc && weights && msa && msa_mask && pair && pair_mask, "NULL argument");
+  const afhip_evoformer_block_desc& d = *desc;
+  const afhip_pair_stack_desc& ps = d.pair;
+  const int L = ps.outgoing.length, S = ps.opm.sequences, cm = ps.opm.c_m, cz = ps.outgoing.c_z;
+  const int dt = ps.outgoing.pair_dtype;
+  AFHIP_REQUIRE(L > 0 && S > 0 && cm > 0, "the block needs positive sequences, length and MSA channels");
+  afhip_attention_desc row = d.msa_row, col = d.msa_column;
+  afhip_transition_desc mt = d.msa_transition;
+  row.transpose = 0;
+  row.pair_bias = AFHIP_PAIR_BIAS_SEPARATE;
+  col.transpose = 1;
+  col.pair_bias = AFHIP_PAIR_BIAS_NONE;
+  row.residual = col.residual = mt.residual = 1;
+  AFHIP_REQUIRE(row.batch == S && row.queries == L && row.channels == cm && row.pair_channels == cz &&
+                    row.in_dtype == dt && row.out_dtype == dt,
+                "the MSA row attention does not match the block");
+  AFHIP_REQUIRE(col.batch == L && col.queries == S && col.channels == cm && col.in_dtype == dt && col.out_dtype == dt,
+                "the MSA column attention does not match the block");
+  AFHIP_REQUIRE(mt.rows == (int64_t)S * L && mt.channels == cm && mt.in_dtype == dt && mt.out_dtype == dt,
+                "the MSA transition does not match the block");
+  AFHIP_REQUIRE(ps.opm.msa_dtype == dt, "the MSA and the pair share one dtype");
+  const afhip_pair_stack_weights& pw = weights->pair;
+  const afhip_pair_stack_weights opm_only{pw.opm, nullptr, nullptr, nullptr, nullptr, nullptr};
+  afhip_pair_stack_weights rest = pw;
+  if (d.opm_first) {
+    if (int s = afhip_execution_pair_stack(ex, &ps, &opm_only, msa, msa_mask, pair, pair_mask)) return s;
+    rest.opm = nullptr;
+  }
+  if (weights->msa_row) {
+    if (int s = pooled_step(
+            ex, "evoformer.msa-row-attention", [&](size_t* b) { return afhip_attention_workspace_size(&row, b); },
+            [&](void* ws, size_t b) {
+              return afhip_attention_run(&row, msa, msa_mask, pair, weights->msa_row, msa, ws, b, ex->stream);
+            }))
+      return s;
+  }
+  if (weights->msa_column) {
+    if (int s = pooled_step(
+            ex, "evoformer.msa-column-attention", [&](size_t* b) { return afhip_attention_workspace_size(&col, b); },
+            [&](void* ws, size_t b) {
+              return afhip_attention_run(&col, msa, msa_mask, nullptr, weights->msa_column, msa, ws, b, ex->stream);
+            }))
+      return s;
+  }
+  if (weights->msa_transition) {
+    if (int s = pooled_step(
+            ex, "evoformer.msa-transition", [&](size_t* b) { return afhip_transition_workspace_size(&mt, b); },
+            [&](void* ws, size_t b) {
+              return afhip_transition_run(&mt, msa, weights->msa_transition, msa, ws, b, ex->stream);
+            }))
+      return s;
+  }
+  return afhip_execution_pair_stack(ex, &ps, &rest, msa, msa_mask, pair, pair_mask);
+}
+
 }  // extern "C"

@@ -462,6 +462,32 @@ AFHIP_API int afhip_execution_pair_stack(afhip_execution* ex, const afhip_pair_s
                                          const afhip_pair_stack_weights* weights, const void* msa,
                                          const float* msa_mask, void* pair, const float* pair_mask);
 
+/* A whole Evoformer block: encodeEvoformerBlock (src/evoformer/block.ts:
+ * 1673-1759). MSA row attention with the pair bias (separate source: the
+ * pair, :1690-1702), MSA column attention (transposed, :1704-1711), MSA
+ * transition (:1713-1716), then the pair stack above; the outer-product mean
+ * runs first instead when opm_first is set (outerProductMeanFirst,
+ * :1689). Everything updates `msa` and `pair` in place. The MSA and the pair
+ * share one dtype. */
+typedef struct afhip_evoformer_block_desc {
+  afhip_attention_desc msa_row;        /* batch = S, queries = L, channels = c_m, pair_channels = c_z */
+  afhip_attention_desc msa_column;     /* batch = L, queries = S, channels = c_m */
+  afhip_transition_desc msa_transition; /* rows = S * L, channels = c_m */
+  afhip_pair_stack_desc pair;
+  int32_t opm_first;
+} afhip_evoformer_block_desc;
+
+typedef struct afhip_evoformer_block_weights {
+  const void* msa_row;        /* afhip_attention_prepare_weights, SEPARATE pair bias */
+  const void* msa_column;     /* afhip_attention_prepare_weights, no pair bias */
+  const void* msa_transition; /* afhip_transition_prepare_weights */
+  afhip_pair_stack_weights pair;
+} afhip_evoformer_block_weights;
+
+AFHIP_API int afhip_execution_evoformer_block(afhip_execution* ex, const afhip_evoformer_block_desc* desc,
+                                              const afhip_evoformer_block_weights* weights, void* msa,
+                                              const float* msa_mask, void* pair, const float* pair_mask);
+
 /* ---------------------------------------------------------------------- */
 /* Kernel timing                                                           */
 /* ---------------------------------------------------------------------- */

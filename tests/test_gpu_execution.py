@@ -221,3 +221,100 @@ def test_pair_stack_rejects_mismatched_steps(dev):
     with pytest.raises(_lib.RangeError, match="transition does not match"):
         stack(pz, pm)
     ex.release()
+
+
+def _msa_weights(seed, cm, cz, heads=8):
+    def att(s0):
+        return {"queryNormScale": ref.normal(s0, (cm,), 0.01, 1.0), "queryNormOffset": ref.normal(s0 + 1, (cm,), 0.01),
+                "queryWeight": ref.normal(s0 + 2, (cm, cm), 1 / cm), "keyWeight": ref.normal(s0 + 3, (cm, cm), 1 / cm),
+                "valueWeight": ref.normal(s0 + 4, (cm, cm), 1 / cm),
+                "gatingWeight": ref.normal(s0 + 5, (cm, cm), 1 / cm), "gatingBias": ref.normal(s0 + 6, (cm,), 0.1, 1.0),
+                "outputWeight": ref.normal(s0 + 7, (cm, cm), 1 / cm), "outputBias": ref.normal(s0 + 8, (cm,), 0.01)}
+    return {"msaRowAttention": {"attention": att(seed), "pairLayerNormScale": ref.normal(seed + 20, (cz,), 0.01, 1.0),
+                                "pairLayerNormOffset": ref.normal(seed + 21, (cz,), 0.01),
+                                "pairProjectionWeight": ref.normal(seed + 22, (cz, heads), 1 / cz)},
+            "msaColumnAttention": {"attention": att(seed + 40)},
+            "msaTransition": {"layerNormScale": ref.normal(seed + 60, (cm,), 0.01, 1.0),
+                              "layerNormOffset": ref.normal(seed + 61, (cm,), 0.01),
+                              "firstWeight": ref.normal(seed + 62, (cm, 4 * cm), 1 / cm),
+                              "firstBias": ref.normal(seed + 63, (4 * cm,), 0.02),
+                              "secondWeight": ref.normal(seed + 64, (4 * cm, cm), 1 / (4 * cm)),
+                              "secondBias": ref.normal(seed + 65, (cm,), 0.02)}}
+
+
+def _oracle_block(msa, msa_mask, z, pair_mask, w, S, L, cm, cz, opm_first, heads=8):
+    m, z = msa.astype(np.float64), z.astype(np.float64)
+    if opm_first:
+        z = z + ref.opm(m, msa_mask, w["outerProductMean"])
+    row = w["msaRowAttention"]
+    pb = {"source": "separate", "activations": z, "channels": cz, "layerNormScale": row["pairLayerNormScale"],
+          "layerNormOffset": row["pairLayerNormOffset"], "projectionWeight": row["pairProjectionWeight"]}
+    m = m + ref.attention(m, msa_mask, row["attention"], S, L, cm, heads, pair_bias=pb).reshape(S, L, cm)
+    m = m + ref.attention(m, msa_mask, w["msaColumnAttention"]["attention"], L, S, cm, heads,
+                          transpose=True).reshape(S, L, cm)
+    m = m + ref.transition(m.reshape(S * L, cm), w["msaTransition"]).reshape(S, L, cm)
+    if not opm_first:
+        z = z + ref.opm(m, msa_mask, w["outerProductMean"])
+    z = z + ref.triangle("outgoing", z, pair_mask, w["triangleMultiplicationOutgoing"])
+    z = z + ref.triangle("incoming", z, pair_mask, w["triangleMultiplicationIncoming"])
+    for tp, key in ((False, "triangleAttentionStarting"), (True, "triangleAttentionEnding")):
+        pbz = {"source": "normalized-input", "projectionWeight": w[key]["pairProjectionWeight"]}
+        z = z + ref.attention(z, pair_mask, w[key]["attention"], L, L, cz, 4, transpose=tp,
+                              pair_bias=pbz).reshape(L, L, cz)
+    z = z + ref.transition(z.reshape(L * L, cz), w["pairTransition"]).reshape(L, L, cz)
+    return m, z
+
+
+@pytest.mark.parametrize("opm_first", [False, True])
+def test_evoformer_block_against_the_oracle(dev, opm_first):
+    # f32 at small widths: the whole block against the oracle composed in the
+    # block's order (block.ts:1673-1759).
+    from afhip.execution import EvoformerBlock, Execution
+
+    L, S, cm, co, cz, ch = 20, 6, 32, 8, 32, 32
+    w = _block_weights(0xAF2300, cz, ch, cm, co, 4 * cz)
+    w.update(_msa_weights(0xAF2400, cm, cz))
+    msa = ref.normal(9, (S, L, cm))
+    msa_mask = (ref.uniform(10, (S, L), 0, 1) > 0.1).astype(np.float32)
+    pair_mask = (ref.uniform(11, (L, L), 0, 1) > 0.15).astype(np.float32)
+    z = ref.normal(12, (L, L, cz))
+    em, ez = _oracle_block(msa, msa_mask, z, pair_mask, w, S, L, cm, cz, opm_first)
+    ex = Execution()
+    blk = EvoformerBlock(ex, L, sequences=S, c_m=cm, c_z=cz, c_outer=co, c_hidden=ch, opm_first=opm_first,
+                         precision="f32", dtype="f32")
+    blk.prepare(w)
+    pm, pmm = ex.upload("msa", msa), ex.upload("msa-mask", msa_mask)
+    pz, pzm = ex.upload("pair", z), ex.upload("pair-mask", pair_mask)
+    blk(pm, pmm, pz, pzm)
+    gm, gz = ex.download(pm, (S, L, cm)), ex.download(pz, (L, L, cz))
+    assert np.abs(gm - em).max() <= 1e-4 * np.abs(em).max()
+    assert np.abs(gz - ez).max() <= 1e-4 * np.abs(ez).max()
+    ex.release()
+
+
+def test_evoformer_block_f16_at_alphafold_widths(dev):
+    # f16 at AlphaFold's widths (c_m 256 over 8 heads, c_z 128 over 4; the MFMA
+    # flash kernel and the fused kernels), 50 residues and 9 sequences, within
+    # 1e-2 of the oracle's largest value.
+    import torch
+
+    from afhip.execution import EvoformerBlock, Execution
+
+    L, S, cm, co, cz, ch = 50, 9, 256, 32, 128, 128
+    w = _block_weights(0xAF2500, cz, ch, cm, co, 4 * cz)
+    w.update(_msa_weights(0xAF2600, cm, cz))
+    msa = ref.round_f16(ref.normal(13, (S, L, cm)))
+    msa_mask = (ref.uniform(14, (S, L), 0, 1) > 0.1).astype(np.float32)
+    pair_mask = (ref.uniform(15, (L, L), 0, 1) > 0.15).astype(np.float32)
+    z = ref.round_f16(ref.normal(16, (L, L, cz)))
+    em, ez = _oracle_block(msa, msa_mask, z, pair_mask, w, S, L, cm, cz, False)
+    ex = Execution()
+    blk = EvoformerBlock(ex, L, sequences=S, c_m=cm, c_z=cz, c_outer=co, c_hidden=ch)
+    blk.prepare(w)
+    tm = torch.from_numpy(msa).half().to(dev)
+    tz = torch.from_numpy(z).half().to(dev)
+    blk(tm, torch.from_numpy(msa_mask).to(dev), tz, torch.from_numpy(pair_mask).to(dev))
+    torch.cuda.synchronize()
+    assert np.abs(tm.float().cpu().numpy() - em).max() <= 1e-2 * np.abs(em).max()
+    assert np.abs(tz.float().cpu().numpy() - ez).max() <= 1e-2 * np.abs(ez).max()
+    ex.release()
