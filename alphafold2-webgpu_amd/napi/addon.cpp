@@ -819,6 +819,35 @@ bool read_stack_desc(napi_env env, napi_value o, afhip_pair_stack_desc* d) {
   return true;
 }
 
+// The block's shape: the pair stack's, plus msaHeads = 8,
+// msaTransitionFactor = 4, opmFirst = false.
+bool read_block_desc(napi_env env, napi_value o, afhip_evoformer_block_desc* d) {
+  std::memset(d, 0, sizeof(*d));
+  if (!read_stack_desc(env, o, &d->pair)) return false;
+  int64_t mh, mf;
+  bool opm_first = false;
+  if (!prop_int(env, o, "msaHeads", 8, &mh) || !prop_int(env, o, "msaTransitionFactor", 4, &mf)) return false;
+  bool has = false;
+  napi_has_named_property(env, o, "opmFirst", &has);
+  if (has) {
+    napi_value v;
+    napi_get_named_property(env, o, "opmFirst", &v);
+    napi_get_value_bool(env, v, &opm_first);
+  }
+  if (mh <= 0 || mf <= 0) {
+    throw_js(env, {true, "block dimensions must be positive"});
+    return false;
+  }
+  const afhip_opm_desc& o_ = d->pair.opm;
+  const int32_t S = o_.sequences, L = o_.length, cm = o_.c_m, cz = o_.c_z, prec = o_.precision,
+                dt = d->pair.outgoing.pair_dtype;
+  d->msa_row = {S, L, cm, (int32_t)mh, 0, AFHIP_PAIR_BIAS_SEPARATE, cz, prec, dt, dt, 1, 1e-5f};
+  d->msa_column = {L, S, cm, (int32_t)mh, 1, AFHIP_PAIR_BIAS_NONE, 0, prec, dt, dt, 1, 1e-5f};
+  d->msa_transition = {(int64_t)S * L, cm, (int32_t)(mf * cm), prec, dt, dt, 1, 1e-5f};
+  d->opm_first = opm_first ? 1 : 0;
+  return true;
+}
+
 // executionPrepareWeights(ex, kind, stackDesc, Float32Array packed) -> buffer
 // handle of the prepared weights in the execution's pool; kind is
 // "outerProductMean", "triangleOutgoing", "triangleIncoming",
@@ -830,11 +859,12 @@ napi_value ExecutionPrepareWeights(napi_env env, napi_callback_info info) {
   uint32_t exh;
   ExecutionEntry* e;
   std::string kind;
-  afhip_pair_stack_desc d;
+  afhip_evoformer_block_desc bd;
   HostView packed;
   if (!lookup_execution(env, a.argv[0], &exh, &e) || !get_string(env, a.argv[1], &kind) ||
-      !read_stack_desc(env, a.argv[2], &d) || !get_view(env, a.argv[3], &packed))
+      !read_block_desc(env, a.argv[2], &bd) || !get_view(env, a.argv[3], &packed))
     return nullptr;
+  const afhip_pair_stack_desc& d = bd.pair;
   size_t bytes = 0;
   int st;
   if (kind == "outerProductMean") st = afhip_opm_weights_size(&d.opm, &bytes);
@@ -843,6 +873,9 @@ napi_value ExecutionPrepareWeights(napi_env env, napi_callback_info info) {
   else if (kind == "triangleAttentionStarting") st = afhip_attention_weights_size(&d.attention_start, &bytes);
   else if (kind == "triangleAttentionEnding") st = afhip_attention_weights_size(&d.attention_end, &bytes);
   else if (kind == "pairTransition") st = afhip_transition_weights_size(&d.transition, &bytes);
+  else if (kind == "msaRowAttention") st = afhip_attention_weights_size(&bd.msa_row, &bytes);
+  else if (kind == "msaColumnAttention") st = afhip_attention_weights_size(&bd.msa_column, &bytes);
+  else if (kind == "msaTransition") st = afhip_transition_weights_size(&bd.msa_transition, &bytes);
   else {
     throw_js(env, {true, "unknown weight kind " + kind});
     return nullptr;
@@ -865,6 +898,9 @@ napi_value ExecutionPrepareWeights(napi_env env, napi_callback_info info) {
   else if (kind == "triangleIncoming") st = afhip_triangle_prepare_weights(&d.incoming, f, dst, nullptr);
   else if (kind == "triangleAttentionStarting") st = afhip_attention_prepare_weights(&d.attention_start, f, dst, nullptr);
   else if (kind == "triangleAttentionEnding") st = afhip_attention_prepare_weights(&d.attention_end, f, dst, nullptr);
+  else if (kind == "msaRowAttention") st = afhip_attention_prepare_weights(&bd.msa_row, f, dst, nullptr);
+  else if (kind == "msaColumnAttention") st = afhip_attention_prepare_weights(&bd.msa_column, f, dst, nullptr);
+  else if (kind == "msaTransition") st = afhip_transition_prepare_weights(&bd.msa_transition, f, dst, nullptr);
   else st = afhip_transition_prepare_weights(&d.transition, f, dst, nullptr);
   if (st == AFHIP_OK) st = afhip_synchronize(nullptr);
   afhip_execution_release(e->ex, src);
@@ -921,6 +957,48 @@ napi_value ExecutionPairStack(napi_env env, napi_callback_info info) {
   afhip_pair_stack_weights pw{w[0], w[1], w[2], w[3], w[4], w[5]};
   check(env, afhip_execution_pair_stack(e->ex, &d, &pw, msa, (const float*)mmask, pair, (const float*)pmask),
         "executionPairStack");
+  return nullptr;
+}
+
+// executionEvoformerBlock(ex, blockDesc, {msaRowAttention?, msaColumnAttention?,
+// msaTransition?, and the pair stack's}, msa, msaMask, pair, pairMask)
+napi_value ExecutionEvoformerBlock(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 7)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  afhip_evoformer_block_desc d;
+  if (!lookup_execution(env, a.argv[0], &exh, &e) || !read_block_desc(env, a.argv[1], &d)) return nullptr;
+  const char* names[9] = {"msaRowAttention", "msaColumnAttention", "msaTransition", "outerProductMean",
+                          "triangleOutgoing", "triangleIncoming", "triangleAttentionStarting",
+                          "triangleAttentionEnding", "pairTransition"};
+  void* w[9] = {};
+  for (int i = 0; i < 9; i++) {
+    bool has = false;
+    napi_has_named_property(env, a.argv[2], names[i], &has);
+    if (!has) continue;
+    napi_value v;
+    napi_get_named_property(env, a.argv[2], names[i], &v);
+    napi_valuetype t;
+    napi_typeof(env, v, &t);
+    if (t == napi_undefined || t == napi_null) continue;
+    if (!lookup_buffer(env, v, &w[i], nullptr)) return nullptr;
+  }
+  void *msa, *mmask, *pair, *pmask;
+  size_t nm, nmm, np, npm;
+  if (!lookup_buffer(env, a.argv[3], &msa, &nm) || !lookup_buffer(env, a.argv[4], &mmask, &nmm) ||
+      !lookup_buffer(env, a.argv[5], &pair, &np) || !lookup_buffer(env, a.argv[6], &pmask, &npm))
+    return nullptr;
+  const size_t rows = (size_t)d.pair.opm.sequences * d.pair.opm.length;
+  const size_t pairs = (size_t)d.pair.outgoing.length * d.pair.outgoing.length;
+  const size_t es = dtype_bytes(d.pair.outgoing.pair_dtype);
+  if (nm < rows * d.pair.opm.c_m * es || nmm < rows * 4 || np < pairs * d.pair.outgoing.c_z * es || npm < pairs * 4) {
+    throw_js(env, {true, "the MSA, the pair or a mask buffer is too small"});
+    return nullptr;
+  }
+  afhip_evoformer_block_weights bw{w[0], w[1], w[2], {w[3], w[4], w[5], w[6], w[7], w[8]}};
+  check(env, afhip_execution_evoformer_block(e->ex, &d, &bw, msa, (const float*)mmask, pair, (const float*)pmask),
+        "executionEvoformerBlock");
   return nullptr;
 }
 
@@ -1236,6 +1314,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"executionReleaseSince", ExecutionReleaseSince}, {"executionNoteSubmitted", ExecutionNoteSubmitted},
       {"executionSnapshot", ExecutionSnapshot}, {"executionAddInPlace", ExecutionAddInPlace},
       {"executionPrepareWeights", ExecutionPrepareWeights}, {"executionPairStack", ExecutionPairStack},
+      {"executionEvoformerBlock", ExecutionEvoformerBlock},
       {"setMemoryBudget", SetMemoryBudget}, {"memoryResident", MemoryResident}, {"triangleRun", TriangleRun},
       {"opmRun", OpmRun}, {"transitionRun", TransitionRun}, {"attentionRun", AttentionRun}, {"timingEnable", TimingEnable},
       {"timingReset", TimingReset}, {"timingReport", TimingReport},

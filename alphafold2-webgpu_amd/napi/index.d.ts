@@ -117,6 +117,26 @@ export interface PairStackShape {
   attentionHeads?: number;
 }
 
+export interface EvoformerBlockShape extends PairStackShape {
+  msaHeads?: number;
+  msaTransitionFactor?: number;
+  opmFirst?: boolean;
+}
+
+/** The block's MSA weights (src/evoformer/block.ts:86-88) with the pair stack's. */
+export interface EvoformerBlockWeights extends PairStackWeights {
+  msaRowAttention?: { attention: AttentionWeights; pairLayerNormScale: Float32Array;
+    pairLayerNormOffset: Float32Array; pairProjectionWeight: Float32Array };
+  msaColumnAttention?: { attention: AttentionWeights };
+  msaTransition?: TransitionWeights;
+}
+
+export interface PreparedEvoformerBlock extends PreparedPairStack {
+  msaRowAttention?: number;
+  msaColumnAttention?: number;
+  msaTransition?: number;
+}
+
 /** AttentionWeights (src/evoformer/attention.ts:19-29). */
 export interface AttentionWeights {
   queryNormScale: Float32Array;
@@ -210,6 +230,10 @@ export declare class HipExecution {
   snapshot(): AllocationSnapshot;
   addInPlace(base: number, update: number, elements: number, baseDtype?: 0 | 1, updateDtype?: 0 | 1): void;
   preparePairStack(shape: PairStackShape, weights: PairStackWeights): PreparedPairStack;
+  /** encodeEvoformerBlock (src/evoformer/block.ts:1673-1759): MSA steps, then the pair steps. */
+  prepareEvoformerBlock(shape: EvoformerBlockShape, weights: EvoformerBlockWeights): PreparedEvoformerBlock;
+  evoformerBlock(shape: EvoformerBlockShape, prepared: PreparedEvoformerBlock, msa: number, msaMask: number,
+    pair: number, pairMask: number): void;
   pairStack(shape: PairStackShape, prepared: PreparedPairStack, pair: number, pairMask: number, msa?: number,
             msaMask?: number): void;
   release(): void;

@@ -312,6 +312,32 @@ HipExecution.prototype.preparePairStack = function (shape, weights) {
   }
   return out;
 };
+// The whole block (src/evoformer/block.ts:1673-1759). shape: the pair
+// stack's plus {msaHeads, msaTransitionFactor, opmFirst}; weights: the pair
+// stack's plus {msaRowAttention: {attention, pairLayerNormScale,
+// pairLayerNormOffset, pairProjectionWeight}, msaColumnAttention:
+// {attention}, msaTransition} (block.ts:86-88).
+HipExecution.prototype.prepareEvoformerBlock = function (shape, weights) {
+  var native = addon(), h = this.handle, out = this.preparePairStack(shape, weights);
+  var row = weights.msaRowAttention;
+  if (row) {
+    out.msaRowAttention = native.executionPrepareWeights(h, "msaRowAttention", shape, packAttentionWeights(
+      row.attention, { source: "separate", layerNormScale: row.pairLayerNormScale,
+        layerNormOffset: row.pairLayerNormOffset, projectionWeight: row.pairProjectionWeight }));
+  }
+  if (weights.msaColumnAttention) {
+    out.msaColumnAttention = native.executionPrepareWeights(h, "msaColumnAttention", shape,
+      packAttentionWeights(weights.msaColumnAttention.attention));
+  }
+  if (weights.msaTransition) {
+    out.msaTransition = native.executionPrepareWeights(h, "msaTransition", shape,
+      packOrdered(weights.msaTransition, TRANSITION_ORDER));
+  }
+  return out;
+};
+HipExecution.prototype.evoformerBlock = function (shape, prepared, msa, msaMask, pair, pairMask) {
+  addon().executionEvoformerBlock(this.handle, shape, prepared, msa, msaMask, pair, pairMask);
+};
 HipExecution.prototype.pairStack = function (shape, prepared, pair, pairMask, msa, msaMask) {
   addon().executionPairStack(this.handle, shape, prepared, pair, pairMask, msa === undefined ? null : msa,
     msaMask === undefined ? null : msaMask);

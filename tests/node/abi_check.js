@@ -11,7 +11,7 @@ var expected = ["open", "close", "abiVersion", "deviceReport", "bufferCreate", "
   "transitionRun", "attentionRun", "timingEnable", "timingReset", "timingReport", "packWeightQ8Block", "executionCreate",
   "executionDestroy", "executionAllocate", "executionUpload", "executionRelease", "executionCheckpoint",
   "executionReleaseSince", "executionNoteSubmitted", "executionSnapshot", "executionAddInPlace",
-  "executionPrepareWeights", "executionPairStack", "setMemoryBudget", "memoryResident"];
+  "executionPrepareWeights", "executionPairStack", "executionEvoformerBlock", "setMemoryBudget", "memoryResident"];
 expected.forEach(function (n) { assert.strictEqual(typeof native[n], "function", n); });
 assert.strictEqual(native.abiVersion(), 2);
 

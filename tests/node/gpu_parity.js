@@ -242,6 +242,57 @@ function transposePairs(data, L, C) {
   assert.ok(snap.peakComposition.length > 0 && snap.residentBytes >= snap.currentBytes);
   ex.release();
   report.cases.push({ pairStackVsOperators: m });
+
+  // The whole block (HipExecution.evoformerBlock) against its MSA steps run
+  // through the host-array operators, followed by the device pair stack
+  // checked above (src/evoformer/block.ts:1690-1716).
+  var msaW = {
+    msaRowAttention: { attention: attentionWeights(80).attention, pairLayerNormScale: wave(cZ, 0.1, 90, 1),
+      pairLayerNormOffset: wave(cZ, 0.05, 91), pairProjectionWeight: wave(cZ * 2, 0.3, 92) },
+    msaColumnAttention: { attention: attentionWeights(100).attention },
+    msaTransition: { layerNormScale: wave(cM, 0.1, 110, 1), layerNormOffset: wave(cM, 0.05, 111),
+      firstWeight: wave(cM * 4 * cM, 0.2, 112), firstBias: wave(4 * cM, 0.05, 113),
+      secondWeight: wave(4 * cM * cM, 0.1, 114), secondBias: wave(cM, 0.05, 115) },
+  };
+  // Attention over the MSA needs c_m heads of at most 32 channels: cM = 8 over 2 heads.
+  msaW.msaRowAttention.attention = Object.assign({}, msaW.msaRowAttention.attention);
+  ["queryNormScale", "queryNormOffset", "gatingBias", "outputBias"].forEach(function (n, k) {
+    msaW.msaRowAttention.attention[n] = wave(cM, 0.1, 120 + k, n === "queryNormScale" ? 1 : 0);
+    msaW.msaColumnAttention.attention[n] = wave(cM, 0.1, 130 + k, n === "queryNormScale" ? 1 : 0);
+  });
+  ["queryWeight", "keyWeight", "valueWeight", "gatingWeight", "outputWeight"].forEach(function (n, k) {
+    msaW.msaRowAttention.attention[n] = wave(cM * cM, 0.25, 140 + k);
+    msaW.msaColumnAttention.attention[n] = wave(cM * cM, 0.25, 150 + k);
+  });
+  var m2 = Float32Array.from(msa);
+  var rw = msaW.msaRowAttention;
+  addInto(m2, new afhip.AttentionGpu().run({ activations: m2, mask: msaMask, batch: S, queryLength: L, channels: cM,
+    heads: 2, weights: rw.attention, pairBias: { source: "separate", activations: pair, channels: cZ,
+      layerNormScale: rw.pairLayerNormScale, layerNormOffset: rw.pairLayerNormOffset,
+      projectionWeight: rw.pairProjectionWeight } }).output);
+  addInto(m2, new afhip.AttentionGpu().run({ activations: m2, mask: msaMask, batch: L, queryLength: S, channels: cM,
+    heads: 2, transpose: true, weights: msaW.msaColumnAttention.attention }).output);
+  addInto(m2, new afhip.TransitionGpu().run({ shape: [S * L, cM, 4 * cM], activations: m2,
+    weights: msaW.msaTransition }).output);
+  var ex2 = new afhip.HipExecution();
+  var ePair = ex2.upload("pair", pair), eMask = ex2.upload("pair-mask", pairMask);
+  var eMsa = ex2.upload("msa", m2), eMsaMask = ex2.upload("msa-mask", msaMask);
+  ex2.pairStack(shape, ex2.preparePairStack(shape, weights), ePair, eMask, eMsa, eMsaMask);
+  var zExpect = ex2.read(ePair, new Float32Array(L * L * cZ));
+  var blockShape = Object.assign({ msaHeads: 2 }, shape);
+  var preparedBlock = ex2.prepareEvoformerBlock(blockShape, Object.assign({}, weights, msaW));
+  var gPair = ex2.upload("pair", pair), gMsa = ex2.upload("msa", msa);
+  ex2.evoformerBlock(blockShape, preparedBlock, gMsa, eMsaMask, gPair, eMask);
+  var mGot = ex2.read(gMsa, new Float32Array(S * L * cM)), zGot = ex2.read(gPair, new Float32Array(L * L * cZ));
+  function rel(a, b) {
+    var worst = 0, big = 0;
+    for (var i = 0; i < a.length; i++) { worst = Math.max(worst, Math.abs(a[i] - b[i])); big = Math.max(big, Math.abs(b[i])); }
+    return worst / big;
+  }
+  var rm = rel(mGot, m2), rz = rel(zGot, zExpect);
+  assert.ok(rm <= 1e-5 && rz <= 1e-5, "evoformer block msa " + rm + " pair " + rz);
+  ex2.release();
+  report.cases.push({ evoformerBlockVsOperators: { msa: rm, pair: rz } });
 })();
 
 console.log(JSON.stringify(report));

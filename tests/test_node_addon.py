@@ -27,7 +27,7 @@ def run_node(script, timeout=120):
 @needs_addon
 def test_addon_loads_and_validates_without_gpu():
     out = run_node("abi_check.js")
-    assert out["ok"] and out["exports"] == 41
+    assert out["ok"] and out["exports"] == 42
 
 
 @pytest.mark.gpu
@@ -35,4 +35,4 @@ def test_addon_loads_and_validates_without_gpu():
 @needs_addon
 def test_addon_parity_on_gpu():
     out = run_node("gpu_parity.js")
-    assert len(out["cases"]) == 6
+    assert len(out["cases"]) == 7
