@@ -417,13 +417,15 @@ void dma_heuristic_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int* tm,
   //  L = 512     52       55       48       49
   //  L = 384     28       25       30       36
   //  OPM 8192x8192x512       123 / 96 / 104 / 95;  OPM 65536x128x1024   28 / 37 / 36 / 34
-  // so: 256 x 256 for long K on large outputs; else 192 x 192 when its
+  //  131072x256x1024 (MSA transition, second linear, + residual)  188 / 225 / 162 / 159
+  //  131072x128x1024                                                98 / 127 / 128 / 128
+  // so: 256 x 256 for long K on large outputs with 256-aligned columns; else 192 x 192 when its
   // ragged edges waste at most 1/20 of the work and there are at least two
   // tiles a CU; else 128 x 256 when K and the output are wide enough; else
   // 128 x 128, which keeps ragged-edge waste low and the tile count high.
   const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
   auto waste = [](int64_t x, int64_t t) { return (double)(ceil_div(x, t) * t - x) / (double)x; };
-  if (K >= 1024 && M >= 1024 && N >= 1024 && waste(M, 256) <= 0.05 && waste(N, 256) <= 0.05 &&
+  if (K >= 1024 && M >= 1024 && N >= 256 && waste(M, 256) <= 0.05 && waste(N, 256) <= 0.05 &&
       ceil_div(M, 256) * ceil_div(N, 256) * batch >= cus) {
     *tm = *tn = 256;
     return;

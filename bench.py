@@ -270,7 +270,72 @@ def measure_configs(steps: int, warmup: int, which=(1, 2, 4, 5)) -> dict:
         torch.cuda.empty_cache()
     if "attention" in which:
         out["attention"] = measure_attention(steps, warmup)
+    if "block" in which:
+        out["evoformer_block"] = measure_block(steps, warmup)
     return out
+
+
+def measure_block(steps: int, warmup: int) -> dict:
+    """One whole Evoformer block on the device (afhip_execution_evoformer_block:
+    MSA row and column attention, MSA transition, outer-product mean, the two
+    triangle multiplications and attentions, pair transition) at config 4's
+    shape: N_seq = 512, N_res = 256, c_m = 256, c_z = 128, f16, synthetic
+    weights ~N(0, 1/fan_in) and activations ~N(0, 1), all-ones masks."""
+    import torch
+
+    from afhip import device
+    from afhip.execution import EvoformerBlock, Execution
+    from oracle import ref
+
+    dev = device.device()
+    S, L, cm, cz, co, ch = 512, 256, 256, 128, 32, 128
+    s = SEED + 7
+    counter = iter(range(1000))
+
+    def n(shape, fan_in=None, mean=0.0):
+        return ref.normal(s + next(counter), shape, 1.0 / fan_in if fan_in else 0.01, mean)
+
+    def att(c):
+        return {"queryNormScale": n((c,), mean=1.0), "queryNormOffset": n((c,)), "queryWeight": n((c, c), c),
+                "keyWeight": n((c, c), c), "valueWeight": n((c, c), c), "gatingWeight": n((c, c), c),
+                "gatingBias": n((c,), mean=1.0), "outputWeight": n((c, c), c), "outputBias": n((c,))}
+
+    def trans(c):
+        return {"layerNormScale": n((c,), mean=1.0), "layerNormOffset": n((c,)), "firstWeight": n((c, 4 * c), c),
+                "firstBias": n((4 * c,)), "secondWeight": n((4 * c, c), 4 * c), "secondBias": n((c,))}
+
+    w = {"msaRowAttention": {"attention": att(cm), "pairLayerNormScale": n((cz,), mean=1.0),
+                             "pairLayerNormOffset": n((cz,)), "pairProjectionWeight": n((cz, 8), cz)},
+         "msaColumnAttention": {"attention": att(cm)}, "msaTransition": trans(cm),
+         "outerProductMean": {"layerNormScale": n((cm,), mean=1.0), "layerNormOffset": n((cm,)),
+                              "leftWeight": n((cm, co), cm), "leftBias": n((co,)), "rightWeight": n((cm, co), cm),
+                              "rightBias": n((co,)), "outputWeight": n((co * co, cz), co * co), "outputBias": n((cz,))},
+         "triangleMultiplicationOutgoing": triangle_weights(s + 500, cz, ch),
+         "triangleMultiplicationIncoming": triangle_weights(s + 600, cz, ch),
+         "triangleAttentionStarting": {"attention": att(cz), "pairProjectionWeight": n((cz, 4), cz)},
+         "triangleAttentionEnding": {"attention": att(cz), "pairProjectionWeight": n((cz, 4), cz)},
+         "pairTransition": trans(cz)}
+    ex = Execution()
+    blk = EvoformerBlock(ex, L, sequences=S, c_m=cm, c_z=cz, c_outer=co, c_hidden=ch)
+    blk.prepare(w)
+    msa = torch.from_numpy(ref.round_f16(ref.normal(s + 900, (S, L, cm)))).half().to(dev)
+    pair = torch.from_numpy(ref.round_f16(ref.normal(s + 901, (L, L, cz)))).half().to(dev)
+    msa_mask = torch.ones((S, L), dtype=torch.float32, device=dev)
+    pair_mask = torch.ones((L, L), dtype=torch.float32, device=dev)
+    m0, z0 = msa.clone(), pair.clone()
+
+    def step():
+        msa.copy_(m0)
+        pair.copy_(z0)
+        blk(msa, msa_mask, pair, pair_mask)
+
+    ms, k = timed(step, max(5, steps // 10), warmup)
+    entry = {"ms": round(ms, 4), "workload": f"Evoformer block, N_seq={S}, N_res={L}, c_m={cm}, c_z={cz}, f16",
+             "kernel_avg_ms": {kk: round(v, 5) for kk, v in sorted(k.items(), key=lambda kv: -kv[1])}}
+    entry["note"] = ("ms includes two device copies that reset the MSA and the pair before each block; "
+                     "kernel_avg_ms averages every launch under a label, whichever step made it")
+    ex.release()
+    return entry
 
 
 def measure_attention(steps: int, warmup: int) -> dict:
@@ -331,9 +396,9 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--headline-only", action="store_true", help="skip BASELINE configs 1, 2, 4 and 5")
-    parser.add_argument("--configs", default="1,2,4,5,attention",
-                        help="comma-separated BASELINE configs to measure besides the headline (config 3), and "
-                             "'attention' for the Evoformer attentions")
+    parser.add_argument("--configs", default="1,2,4,5,attention,block",
+                        help="comma-separated BASELINE configs to measure besides the headline (config 3), "
+                             "'attention' for the Evoformer attentions and 'block' for a whole Evoformer block")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                         help="only run a plain device-to-device copy of MIB MiB 10 times (the known-size kernel "
                              "rocprof's FETCH_SIZE / WRITE_SIZE readings are scaled by) and exit")
@@ -409,7 +474,7 @@ def main() -> None:
         "kernels": kernels,
         "kernel_ms": {k: round(v, 5) for k, v in per_kernel.items()},
     }
-    which = tuple(c.strip() if c.strip() == "attention" else int(c) for c in args.configs.split(",")
+    which = tuple(c.strip() if c.strip() in ("attention", "block") else int(c) for c in args.configs.split(",")
                   if c.strip()) if not args.headline_only else ()
     if which:
         del ops, zd, md
