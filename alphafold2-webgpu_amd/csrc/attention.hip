@@ -422,24 +422,32 @@ int launch_flash_generic(const FlashArgs& fa, hipStream_t st, std::integer_seque
 // cover, in the order they fill the second MFMA's B operand.
 __global__ __launch_bounds__(256) void attention_vt_kernel(const half_t* __restrict__ qkvg, int B, int Q, int C,
                                                            int H, int key_blocks, half_t* __restrict__ vt) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)B * H * key_blocks * 128) return;
-  const int d = (int)(i & 31);
-  const int part = (int)((i >> 5) & 3);  // 2 s + hi
-  const int64_t t = i >> 7;
-  const int kb = (int)(t % key_blocks);
-  const int64_t bh = t / key_blocks;
-  const int h = (int)(bh % H);
-  const int64_t b = bh / H;
-  const int s = part >> 1, hi = part & 1;
-  const half_t* src = qkvg + b * Q * 4 * (int64_t)C + 2 * C + h * 32 + d;
-  half8 val;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const int key = 32 * kb + 16 * s + 8 * (e >> 2) + 4 * hi + (e & 3);
-    val[e] = key < Q ? src[(int64_t)key * 4 * C] : (half_t)0.0f;
+  // Two blocks a workgroup: 128 lanes load one block's 32 keys x 32
+  // channels as 16-byte row pieces into LDS, then write its [channel][position]
+  // rows as 16-byte pieces.
+  __shared__ __attribute__((aligned(16))) half_t tile[2][32][40];
+  const int sub = threadIdx.x >> 7, u = threadIdx.x & 127;
+  const int64_t t = (int64_t)blockIdx.x * 2 + sub;
+  const bool live = t < (int64_t)B * H * key_blocks;
+  int64_t b = 0;
+  int h = 0, kb = 0;
+  if (live) {
+    kb = (int)(t % key_blocks);
+    const int64_t bh = t / key_blocks;
+    h = (int)(bh % H);
+    b = bh / H;
+    const int key = 32 * kb + (u >> 2);
+    half8 v = {};
+    if (key < Q) v = *reinterpret_cast<const half8*>(qkvg + (b * Q + key) * 4 * (int64_t)C + 2 * C + h * 32 + 8 * (u & 3));
+    *reinterpret_cast<half8*>(&tile[sub][u >> 2][8 * (u & 3)]) = v;
   }
-  *reinterpret_cast<half8*>(vt + t * 1024 + d * 32 + 16 * s + 8 * hi) = val;
+  __syncthreads();
+  if (!live) return;
+  const int d = u >> 2, s = (u >> 1) & 1, hi = u & 1;
+  half8 o;
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = tile[sub][16 * s + 8 * (e >> 2) + 4 * hi + (e & 3)][d];
+  *reinterpret_cast<half8*>(vt + t * 1024 + d * 32 + 16 * s + 8 * hi) = o;
 }
 
 // f16 operands, head_dim 32: one wave per 32 queries of one (b, h), keys in
@@ -853,9 +861,9 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
     fa.key_blocks = ws.key_blocks;
     fa.clamp = 1e8f;
     if (fast) {
-      const int64_t vt_threads = (int64_t)B * H * ws.key_blocks * 128;
-      AFHIP_REQUIRE(ceil_div(vt_threads, 256) < ((int64_t)1 << 31), "attention grid too large");
-      if ((s = launch("attention.vt", attention_vt_kernel, dim3((unsigned)ceil_div(vt_threads, 256)), dim3(256), 0,
+      const int64_t vt_blocks = (int64_t)B * H * ws.key_blocks;
+      AFHIP_REQUIRE(ceil_div(vt_blocks, 2) < ((int64_t)1 << 31), "attention grid too large");
+      if ((s = launch("attention.vt", attention_vt_kernel, dim3((unsigned)ceil_div(vt_blocks, 2)), dim3(256), 0,
                       st, (const half_t*)(wsb + ws.qkvg), B, Q, C, H, ws.key_blocks, (half_t*)(wsb + ws.vt))))
         return s;
       const int64_t groups = ceil_div(B, kFlashBatch) * H * ceil_div(Q, 32 * kFlashQueryWaves);
