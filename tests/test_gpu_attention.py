@@ -200,3 +200,52 @@ def test_workspace_and_operands_are_checked(dev):
     with pytest.raises(_lib.RangeError, match="workspace of 16 bytes"):
         _lib.call("afhip_attention_run", ctypes.byref(op.desc), ptr(x), ptr(m), ptr(x), ptr(op.prepared), ptr(out),
                   ptr(op.workspace), 16, stream_handle())
+
+
+def test_full_size_ending_node_is_transposed_starting_node(dev):
+    # At the headline's size (L = 384, c_z 128, 4 heads, f16): triangle
+    # attention around the ending node of z equals the starting node applied
+    # to z transposed, transposed back, bit for bit -- the same rows reach the
+    # same kernels in the same attention order.
+    import torch
+
+    from afhip import attention
+
+    L, C, H = 384, 128, 4
+    w, pb = weights(0xA7B00, C, H, "normalized-input")
+    z = torch.from_numpy(ref.round_f16(ref.normal(0xA7B10, (L, L, C)))).half().to(dev)
+    mask = torch.from_numpy((ref.uniform(0xA7B11, (L, L), 0, 1) > 0.1).astype(np.float32)).to(dev)
+    packed = attention.pack_weights(w, pb)
+    outs = []
+    for tp, zz, mm in ((True, z, mask), (False, z.transpose(0, 1).contiguous(), mask.t().contiguous())):
+        op = attention.Attention(L, L, C, H, transpose=tp, pair_bias="normalized-input", precision="f16",
+                                 in_dtype="f16", out_dtype="f16")
+        op.prepare(packed)
+        outs.append(op(zz.reshape(L * L, C), mm.reshape(-1)).reshape(L, L, C))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1].transpose(0, 1))
+    assert torch.isfinite(outs[0].float()).all()
+
+
+def test_full_size_msa_row_attention_commutes_with_sequence_order(dev):
+    # MSA row attention at N_seq 512 x N_res 256 (c_m 256, 8 heads, pair bias
+    # from a [256, 256, 128] pair): permuting the sequences permutes the
+    # output, bit for bit, although a workgroup pairs two sequences.
+    import torch
+
+    from afhip import attention
+
+    S, L, C, H, Cp = 512, 256, 256, 8, 128
+    w, pb = weights(0xA7C00, C, H, "separate", Cp)
+    x = torch.from_numpy(ref.round_f16(ref.normal(0xA7C10, (S, L, C)))).half().to(dev)
+    mask = torch.from_numpy((ref.uniform(0xA7C11, (S, L), 0, 1) > 0.1).astype(np.float32)).to(dev)
+    pair = torch.from_numpy(ref.round_f16(ref.normal(0xA7C12, (L * L * Cp,)))).half().to(dev)
+    perm = torch.from_numpy(np.random.default_rng(5).permutation(S)).to(dev)
+    op = attention.Attention(S, L, C, H, pair_bias="separate", pair_channels=Cp, precision="f16", in_dtype="f16",
+                             out_dtype="f16")
+    op.prepare(attention.pack_weights(w, pb))
+    a = op(x.reshape(S * L, C), mask.reshape(-1), pair).reshape(S, L, C).clone()
+    b = op(x[perm].contiguous().reshape(S * L, C), mask[perm].contiguous().reshape(-1), pair).reshape(S, L, C)
+    torch.cuda.synchronize()
+    assert torch.equal(a[perm], b)
+    assert torch.isfinite(a.float()).all()
