@@ -16,7 +16,8 @@
 // normalized-input pair bias from the same registers), the projection GEMM,
 // a row kernel for a separate pair source, the flash kernel, the output GEMM.
 //
-// At f16 precision with head dimension 32 the flash kernel runs on the MFMA
+// At f16 precision with a head dimension of 8, 16, 24 or 32 (heads padded to
+// 32 channels with zeros) the flash kernel runs on the MFMA
 // as S^T = K Q^T and O^T = V^T P^T: a lane then holds one query's scores for
 // 16 keys and the same query's output for 16 channels, so the running maximum,
 // sum and rescale stay inside the lane (one exchange with the lane 32 away),
@@ -39,8 +40,10 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// The f16 MFMA flash kernel takes head dimensions 8, 16, 24 and 32 (heads
+// padded to 32 channels with zeros).
 bool fast_path(const afhip_attention_desc& d) {
-  return d.precision == AFHIP_PRECISION_F16 && d.channels == 32 * d.heads;
+  return d.precision == AFHIP_PRECISION_F16 && (d.channels / d.heads) % 8 == 0;
 }
 
 // Prepared weights: everything the kernels read, in their dtypes.
@@ -421,7 +424,7 @@ int launch_flash_generic(const FlashArgs& fa, hipStream_t st, std::integer_seque
 // 4 hi + e % 4 (zero past the last key): the keys a lane's probabilities
 // cover, in the order they fill the second MFMA's B operand.
 __global__ __launch_bounds__(256) void attention_vt_kernel(const half_t* __restrict__ qkvg, int B, int Q, int C,
-                                                           int H, int key_blocks, half_t* __restrict__ vt) {
+                                                           int H, int D, int key_blocks, half_t* __restrict__ vt) {
   // Two blocks a workgroup: 128 lanes load one block's 32 keys x 32
   // channels as 16-byte row pieces into LDS, then write its [channel][position]
   // rows as 16-byte pieces.
@@ -438,7 +441,8 @@ __global__ __launch_bounds__(256) void attention_vt_kernel(const half_t* __restr
     b = bh / H;
     const int key = 32 * kb + (u >> 2);
     half8 v = {};
-    if (key < Q) v = *reinterpret_cast<const half8*>(qkvg + (b * Q + key) * 4 * (int64_t)C + 2 * C + h * 32 + 8 * (u & 3));
+    if (key < Q && 8 * (u & 3) < D)  // channels past the head dimension are zero
+      v = *reinterpret_cast<const half8*>(qkvg + (b * Q + key) * 4 * (int64_t)C + 2 * C + h * D + 8 * (u & 3));
     *reinterpret_cast<half8*>(&tile[sub][u >> 2][8 * (u & 3)]) = v;
   }
   __syncthreads();
@@ -519,7 +523,7 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
     const int e = part & 1;
     const int64_t be = min(b0 + e, (int64_t)a.B - 1);
     if (part < 2) {
-      tile_src = base + (be * Q + (u >> 2)) * ld4 + a.C + h * 32 + 8 * (u & 3);
+      tile_src = base + (be * Q + (u >> 2)) * ld4 + a.C + h * a.d + 8 * (u & 3);
       tile_step = 32 * ld4;
     } else {
       tile_src = a.vt + (be * a.H + h) * a.key_blocks * 1024 + u * 8;
@@ -540,9 +544,13 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
     }
   }
   static_assert(2 * kFlashThreads * 4 == 32 * kFlashQueryWaves * 32, "two bias pieces a lane cover the tile");
+  // K channels past the head dimension are zero (their loads, kept for a
+  // uniform count, read the row's next columns).
+  const bool tile_zero = (tid >> 7) < 2 && 8 * (tid & 3) >= a.d;
   uint4 staged[3];
   auto fetch = [&](int k0) {
     staged[0] = *reinterpret_cast<const uint4*>(tile_src + (k0 >> 5) * tile_step);
+    if (tile_zero) staged[0] = uint4{0u, 0u, 0u, 0u};
     if (BIAS) {
       staged[1] = *reinterpret_cast<const uint4*>(bias_src[0] + k0);
       staged[2] = *reinterpret_cast<const uint4*>(bias_src[1] + k0);
@@ -566,9 +574,9 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   const int qrow = myq < Q ? myq : Q - 1;
   half8 qf[2] = {};
   if (active) {
-    const half_t* qr = base + (row0 + qrow) * ld4 + h * 32 + 8 * hi;
-    qf[0] = *reinterpret_cast<const half8*>(qr);
-    qf[1] = *reinterpret_cast<const half8*>(qr + 16);
+    const half_t* qr = base + (row0 + qrow) * ld4 + h * a.d + 8 * hi;
+    if (8 * hi < a.d) qf[0] = *reinterpret_cast<const half8*>(qr);
+    if (16 + 8 * hi < a.d) qf[1] = *reinterpret_cast<const half8*>(qr + 16);
   }
   const half_t* cp = a.key_mask + bc * a.stride + col;
 
@@ -658,12 +666,13 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   run_sum += __shfl_xor(run_sum, 32);
   if (!active || myq >= Q) return;
   const float inv = 1.0f / run_sum;
-  const half_t* gr = base + (row0 + myq) * ld4 + 3 * a.C + h * 32;
+  const half_t* gr = base + (row0 + myq) * ld4 + 3 * a.C + h * a.d;
   const int64_t src = a.transpose ? (int64_t)myq * a.B + b : row0 + myq;
-  half_t* out = reinterpret_cast<half_t*>(a.weighted) + src * a.C + h * 32;
+  half_t* out = reinterpret_cast<half_t*>(a.weighted) + src * a.C + h * a.d;
 #pragma unroll
   for (int g = 0; g < 4; g++) {
     const int c0 = 8 * g + 4 * hi;
+    if (c0 >= a.d) break;
     const half4 gv = *reinterpret_cast<const half4*>(gr + c0);
     half4 r;
 #pragma unroll
@@ -864,7 +873,8 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
       const int64_t vt_blocks = (int64_t)B * H * ws.key_blocks;
       AFHIP_REQUIRE(ceil_div(vt_blocks, 2) < ((int64_t)1 << 31), "attention grid too large");
       if ((s = launch("attention.vt", attention_vt_kernel, dim3((unsigned)ceil_div(vt_blocks, 2)), dim3(256), 0,
-                      st, (const half_t*)(wsb + ws.qkvg), B, Q, C, H, ws.key_blocks, (half_t*)(wsb + ws.vt))))
+                      st, (const half_t*)(wsb + ws.qkvg), B, Q, C, H, C / H, ws.key_blocks,
+                      (half_t*)(wsb + ws.vt))))
         return s;
       const int64_t groups = ceil_div(B, kFlashBatch) * H * ceil_div(Q, 32 * kFlashQueryWaves);
       AFHIP_REQUIRE(groups < ((int64_t)1 << 31), "attention grid too large");

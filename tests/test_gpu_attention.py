@@ -249,3 +249,14 @@ def test_full_size_msa_row_attention_commutes_with_sequence_order(dev):
     torch.cuda.synchronize()
     assert torch.equal(a[perm], b)
     assert torch.isfinite(a.float()).all()
+
+
+@pytest.mark.parametrize("name", ["msa_row", "msa_column", "triangle_start", "triangle_end"])
+@pytest.mark.parametrize("C,H", [(64, 8), (64, 4), (96, 4)])
+def test_f16_mfma_narrow_heads(dev, name, C, H):
+    # Head dimensions 8, 16 and 24 on the f16 MFMA kernel (each head padded to
+    # 32 channels with zeros): extra-MSA row attention is c_e 64 over 8 heads.
+    x, mask, B, Q, tr, w, pb = case(name, S=7, L=45, C=C, H=H, Cp=64, seed=0xA7D00)
+    expect = ref.attention(x, mask, w, B, Q, C, H, transpose=tr, pair_bias=pb)
+    got = run_case(dev, x, mask, B, Q, C, H, tr, w, pb, precision="f16", out_dtype="f16")
+    assert np.abs(got - expect).max() <= 1e-2 * np.abs(expect).max()
