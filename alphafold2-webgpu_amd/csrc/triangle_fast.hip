@@ -308,7 +308,7 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
 #pragma unroll
     for (int i = 0; i < 32; i++) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // then five VALU
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then four VALU (five measured 3% slower)
     }
     block_barrier();  // B2: the staged tile and zn[(it + 1) % 2] are complete
 
