@@ -16,9 +16,9 @@
 // make the compiler's own vmcnt waits stricter, never looser, since every
 // vector-memory instruction completes in order.
 //
-// M0 is written inside the statement and not listed as clobbered: the
-// compiler treats M0 as reserved and sets it right before each of its own
-// uses, and nothing here relies on it across the statement.
+// M0 is an input operand of each statement ("{m0}"): the compiler writes it
+// itself right before the statement and knows what M0 holds afterwards, so
+// it never assumes a value of its own survived there.
 #pragma once
 
 #include "internal.h"
@@ -35,8 +35,7 @@ constexpr uint32_t kOutOfRange = 0x80000000u;
 // its use.
 __device__ __forceinline__ void dma16(int32x4_t rsrc, uint32_t lds, uint32_t voffset) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset),
-               "s"(rsrc)
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(m0)
                : "memory");
 }
 
@@ -44,8 +43,8 @@ __device__ __forceinline__ void dma16(int32x4_t rsrc, uint32_t lds, uint32_t vof
 __device__ __forceinline__ void dma16_so(int32x4_t rsrc, uint32_t lds, uint32_t voffset, uint32_t soffset) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   const uint32_t so = __builtin_amdgcn_readfirstlane(soffset);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0), "v"(voffset),
-               "s"(rsrc), "s"(so)
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voffset), "s"(rsrc), "s"(so),
+               "{m0}"(m0)
                : "memory");
 }
 
@@ -53,8 +52,8 @@ __device__ __forceinline__ void dma16_so(int32x4_t rsrc, uint32_t lds, uint32_t 
 __device__ __forceinline__ void dma4_so(int32x4_t rsrc, uint32_t lds, uint32_t voffset, uint32_t soffset) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   const uint32_t so = __builtin_amdgcn_readfirstlane(soffset);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(m0), "v"(voffset),
-               "s"(rsrc), "s"(so)
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voffset), "s"(rsrc), "s"(so),
+               "{m0}"(m0)
                : "memory");
 }
 
@@ -65,17 +64,15 @@ __device__ __forceinline__ void dma16_if(int32x4_t rsrc, uint32_t lds, uint32_t 
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   const int on = __builtin_amdgcn_readfirstlane(enable);
   asm volatile(
-      "s_cmp_eq_u32 %3, 0\n\ts_cbranch_scc1 1f\n\ts_mov_b32 m0, %0\n\ts_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds\n1:" ::"s"(m0),
-      "v"(voffset), "s"(rsrc), "s"(on)
+      "s_cmp_eq_u32 %2, 0\n\ts_cbranch_scc1 1f\n\ts_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds\n1:" ::"v"(voffset), "s"(rsrc), "s"(on), "{m0}"(m0)
       : "memory", "scc");
 }
 
 // 4 bytes per lane into LDS [lds, lds + 256).
 __device__ __forceinline__ void dma4(int32x4_t rsrc, uint32_t lds, uint32_t voffset) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset),
-               "s"(rsrc)
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voffset), "s"(rsrc), "{m0}"(m0)
                : "memory");
 }
 
