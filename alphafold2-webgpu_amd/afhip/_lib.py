@@ -154,6 +154,8 @@ SIGNATURES = {
     "afhip_gemm_plan_destroy": [_vp],
     "afhip_gemm_workspace_size": [_vp, _szp],
     "afhip_gemm_run": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    "afhip_gemm_run_static": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "afhip_gemm_static_scratch_bytes": [_szp],
     "afhip_gemm_grid": [_i64, _i64, _i32, _i32, ctypes.POINTER(ctypes.c_uint32)],
     "afhip_gemm_select": [ctypes.POINTER(GemmDesc), ctypes.POINTER(Variant)],
     "afhip_gemm_calibrate": [ctypes.POINTER(GemmDesc), ctypes.POINTER(Variant)],

@@ -72,6 +72,11 @@ afhip_variant select_variant(const GemmTypes& types, int64_t M, int64_t N, int64
 int pack_transpose(const void* src, int src_dtype, int rows_k, int cols_n, int64_t ld_src, void* dst,
                    int dst_dtype, int64_t ld_dst, hipStream_t stream);
 
+// afhip_gemm_run after its open check: `workspace` holds the plan's
+// afhip_gemm_workspace_size bytes (or more) when the plan needs any.
+int run_gemm_plan(const afhip_gemm_plan* plan, const void* a, const void* w, const float* scale, const float* bias,
+                  const void* residual, void* c, void* workspace, size_t workspace_bytes, void* stream);
+
 // Elementwise f32 -> dst dtype conversion (dst may be F32: plain copy).
 int convert_f32(const float* src, int64_t count, void* dst, int dst_dtype, hipStream_t stream);
 

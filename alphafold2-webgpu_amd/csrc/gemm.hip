@@ -429,6 +429,16 @@ int afhip_gemm_workspace_size(const afhip_gemm_plan* plan, size_t* bytes) {
 int afhip_gemm_run(const afhip_gemm_plan* plan, const void* a, const void* w, const float* scale, const float* bias,
                    const void* residual, void* c, void* workspace, size_t workspace_bytes, void* stream) {
   if (int s = require_open()) return s;
+  return afhip::run_gemm_plan(plan, a, w, scale, bias, residual, c, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+// The body of afhip_gemm_run, shared with the entry point that brings its own
+// workspace (gemm_static.hip).
+int afhip::run_gemm_plan(const afhip_gemm_plan* plan, const void* a, const void* w, const float* scale,
+                         const float* bias, const void* residual, void* c, void* workspace, size_t workspace_bytes,
+                         void* stream) {
   AFHIP_REQUIRE(plan != nullptr, "plan is NULL");
   const auto& d = plan->desc;
   hipStream_t st = (hipStream_t)stream;
@@ -476,6 +486,8 @@ int afhip_gemm_run(const afhip_gemm_plan* plan, const void* a, const void* w, co
   }
   return run_gemm(g, types, plan->variant, "gemm", st);
 }
+
+extern "C" {
 
 int afhip_pack_weight(const void* src, int32_t src_dtype, int32_t rows_k, int32_t columns_n, void* dst,
                       int32_t dst_dtype, void* stream) {

@@ -34,6 +34,13 @@ int hip_status(hipError_t err, const char* what);
 bool is_open();
 int require_open();
 int device_cu_count();
+// The ordinal afhip_open selected (-1 when closed).
+int current_device();
+
+// The allocation-free GEMM entry point's device array (gemm_static.hip):
+// records its address on `device`, which must be current; afhip_open calls
+// it once per device.
+int static_scratch_init(int device);
 
 // ---------------------------------------------------------------------------
 // Kernel timing: when enabled, each launch carries a start and a stop event
@@ -42,6 +49,12 @@ int device_cu_count();
 // between launches.
 // ---------------------------------------------------------------------------
 bool timing_enabled();
+// While a TimingOff is alive on a thread, its launches create no events
+// (an entry point that must not allocate anything runs under one).
+struct TimingOff {
+  TimingOff();
+  ~TimingOff();
+};
 // Two fresh events for one launch labelled `label` (false: timing skipped).
 bool timing_events(hipEvent_t* start, hipEvent_t* stop);
 void timing_record(const char* label, hipEvent_t start, hipEvent_t stop);

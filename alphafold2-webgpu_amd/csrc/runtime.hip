@@ -20,6 +20,7 @@ struct TimingRecord {
   std::string label;
 };
 bool g_timing = false;
+thread_local int g_timing_off = 0;
 std::vector<TimingRecord> g_pending;
 std::map<std::string, std::pair<long, double>> g_totals;
 }  // namespace
@@ -48,7 +49,12 @@ int require_open() {
 
 int device_cu_count() { return g_cu_count; }
 
-bool timing_enabled() { return g_timing; }
+bool timing_enabled() { return g_timing && g_timing_off == 0; }
+
+TimingOff::TimingOff() { g_timing_off++; }
+TimingOff::~TimingOff() { g_timing_off--; }
+
+int current_device() { return g_device; }
 
 int allow_lds(const void* kernel, size_t bytes) {
   if (bytes <= 65536) return AFHIP_OK;
@@ -110,6 +116,7 @@ int afhip_open(int device_ordinal) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return set_error(AFHIP_ERR_UNSUPPORTED, "afhip is built for gfx950; device %d is %s", device_ordinal,
                      prop.gcnArchName);
+  if (int s = static_scratch_init(device_ordinal)) return s;
   g_device = device_ordinal;
   g_cu_count = prop.multiProcessorCount;
   return AFHIP_OK;

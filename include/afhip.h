@@ -151,6 +151,19 @@ AFHIP_API int afhip_gemm_run(const afhip_gemm_plan* plan, const void* a, const v
                    const float* bias, const void* residual, void* c, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* afhip_gemm_run without a workspace argument and without allocating: the
+ * workspace the plan needs (afhip_gemm_workspace_size) lives in a device
+ * array of afhip_gemm_static_scratch_bytes (8 MiB) that the library holds on
+ * each GPU it runs on until the process ends. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). A plan
+ * whose workspace exceeds the array is refused (AFHIP_ERR_INVALID_ARGUMENT).
+ * Calls that overlap on one GPU share the array and race; no timing events
+ * are recorded for its launches. Same results as afhip_gemm_run. */
+AFHIP_API int afhip_gemm_run_static(const afhip_gemm_plan* plan, const void* a, const void* w, const float* scale,
+                                    const float* bias, const void* residual, void* c, void* stream);
+AFHIP_API int afhip_gemm_static_scratch_bytes(size_t* bytes);
+
 /* gemmGrid (src/runtime/gemm.ts:368-379): the reference's workgroup grid
  * for an M x N output, row tiles past 65,535 folded into x. Host logic kept
  * for callers that still size WebGPU-style grids. */
