@@ -31,6 +31,12 @@ EPILOGUE_RESIDUAL = 16
 WEIGHT_COLUMN_CONTIGUOUS = 0
 WEIGHT_K_CONTIGUOUS = 1
 
+SOURCE_K_CONTIGUOUS = 0
+SOURCE_ROW_CONTIGUOUS = 1
+
+OUTPUT_ROW_MAJOR = 0
+OUTPUT_COLUMN_MAJOR = 1
+
 KERNEL_REGISTER_STAGED = 0
 KERNEL_LDS_DMA = 1
 KERNEL_STREAM = 2
@@ -63,7 +69,7 @@ class GemmDesc(ctypes.Structure):
         ("epilogue", ctypes.c_uint32), ("heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
         ("lda", ctypes.c_int64), ("ldw", ctypes.c_int64), ("ldc", ctypes.c_int64),
         ("batch_stride_a", ctypes.c_int64), ("batch_stride_w", ctypes.c_int64),
-        ("batch_stride_c", ctypes.c_int64),
+        ("batch_stride_c", ctypes.c_int64), ("a_layout", ctypes.c_int32), ("c_layout", ctypes.c_int32),
     ]
 
 

@@ -83,9 +83,12 @@ def _code_of(tensor) -> str:
 
 
 class TiledGemm:
-    """A GEMM plan: C = epilogue(A[M][K] . W) with W given [K][N]
-    ("column", the linear's layout) or [N][K] ("k", the triangle's [out][in]).
+    """A GEMM plan: C = epilogue(A . W) with W given [K][N] ("column", the
+    linear's layout) or [N][K] ("k", the triangle's [out][in]).
 
+    a_layout is the reference's sourceContiguous (gemm.ts:308-321): "k" for
+    A[M][K], "row" for A stored [K][M] (GemmOperandArray.columnMajor,
+    :341-360). c_layout "row" stores C[M][N], "column" stores it [N][M].
     epilogue: any of "scale", "bias", "attention", "relu", "residual", applied
     in that order to the f32 accumulator (see include/afhip.h).
     """
@@ -93,7 +96,12 @@ class TiledGemm:
     def __init__(self, rows: int, inner: int, columns: int, *, precision: str = "f32", a_dtype: str = "f32",
                  w_dtype: str = "f32", w_layout: str = "column", out_dtype: str = "f32", epilogue=(),
                  heads: int = 0, head_dim: int = 0, batch: int = 1, lda: int = 0, ldw: int = 0, ldc: int = 0,
-                 batch_stride_a: int = 0, batch_stride_w: int = 0, batch_stride_c: int = 0):
+                 batch_stride_a: int = 0, batch_stride_w: int = 0, batch_stride_c: int = 0, a_layout: str = "k",
+                 c_layout: str = "row"):
+        if a_layout not in ("k", "row"):
+            raise _lib.RangeError(f"unknown source layout {a_layout!r}")
+        if c_layout not in ("row", "column"):
+            raise _lib.RangeError(f"unknown output layout {c_layout!r}")
         open_device()
         flags = 0
         for e in epilogue:
@@ -104,7 +112,9 @@ class TiledGemm:
                                   _DTYPE_CODES[w_dtype],
                                   _lib.WEIGHT_COLUMN_CONTIGUOUS if w_layout == "column" else _lib.WEIGHT_K_CONTIGUOUS,
                                   _DTYPE_CODES[out_dtype], flags, heads, head_dim, lda, ldw, ldc, batch_stride_a,
-                                  batch_stride_w, batch_stride_c)
+                                  batch_stride_w, batch_stride_c,
+                                  _lib.SOURCE_ROW_CONTIGUOUS if a_layout == "row" else _lib.SOURCE_K_CONTIGUOUS,
+                                  _lib.OUTPUT_COLUMN_MAJOR if c_layout == "column" else _lib.OUTPUT_ROW_MAJOR)
         handle = ctypes.c_void_p()
         _lib.call("afhip_gemm_plan_create", ctypes.byref(self.desc), ctypes.byref(handle))
         self._plan = handle
@@ -115,6 +125,7 @@ class TiledGemm:
         self._workspace = empty_bytes(size.value) if size.value else None
         self.out_dtype = out_dtype
         self.shape = (batch, rows, columns)
+        self.c_layout = c_layout
 
     def __del__(self):
         # The destroy entry point is held by the object itself: at interpreter
@@ -135,8 +146,11 @@ class TiledGemm:
 
         batch, rows, columns = self.shape
         if out is None:
-            ldc = self.desc.ldc or columns
-            shape = (rows, ldc) if batch == 1 else (batch, rows, ldc)
+            if self.c_layout == "column":
+                shape = (columns, self.desc.ldc or rows)
+            else:
+                shape = (rows, self.desc.ldc or columns)
+            shape = shape if batch == 1 else (batch,) + shape
             out = torch.empty(shape, dtype=_torch_dtype(self.out_dtype), device=device())
         ws = self._workspace
         _lib.call("afhip_gemm_run", self._plan, ptr(a), ptr(w), ptr(scale), ptr(bias), ptr(residual), ptr(out),

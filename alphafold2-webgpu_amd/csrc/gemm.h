@@ -6,8 +6,10 @@
 namespace afhip {
 
 // One batched GEMM launch: C[b][m][n] = epilogue(sum_k A[b][m][k] * B[b][n][k]).
-// A is row-major [M][K] (row stride lda); B is [N][K] (row stride ldb), the
-// k-contiguous layout every kernel here consumes.
+// A is row-major [M][K] (row stride lda), or [K][M] when a_row_contiguous
+// (element (m, k) at k * lda + m); B is [N][K] (row stride ldb), the
+// k-contiguous layout every kernel here consumes. C is [M][N] (row stride
+// ldc), or [N][M] when c_column_major (element (m, n) at n * ldc + m).
 struct GemmArgs {
   const void* a = nullptr;
   const void* b = nullptr;
@@ -19,6 +21,8 @@ struct GemmArgs {
   int64_t lda = 0, ldb = 0, ldc = 0;
   int64_t sa = 0, sb = 0, sc = 0;
   int batch = 1;
+  bool a_row_contiguous = false;  // only the REGISTER_STAGED kernel takes it
+  bool c_column_major = false;    // only the REGISTER_STAGED kernel takes it
   uint32_t flags = 0;
   int head_cols = 0;  // heads * head_dim, ATTENTION only
   float q_scale = 1.0f;
@@ -67,6 +71,9 @@ int run_gemm_stream(const GemmArgs& args, const GemmTypes& types, const char* la
 
 // The variant plans of this shape should use (pinned, calibrated or heuristic).
 afhip_variant select_variant(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);
+// select_variant for a whole description (its layouts included), with the
+// weight dtype the kernels read.
+afhip_variant select_plan_variant(const afhip_gemm_desc& desc, const GemmTypes& kernel_types);
 
 // W[k][n] (src) -> W[n][k] (dst), with dtype conversion.
 int pack_transpose(const void* src, int src_dtype, int rows_k, int cols_n, int64_t ld_src, void* dst,

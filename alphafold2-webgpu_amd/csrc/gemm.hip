@@ -63,8 +63,10 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
   }
   AFHIP_REQUIRE(v.kernel == AFHIP_KERNEL_REGISTER_STAGED, "unknown kernel family %d", v.kernel);
   const int va = 16 / (int)dtype_size(t.a_dtype), vb = 16 / (int)dtype_size(t.b_dtype);
-  bool vec = g.K % va == 0 && g.K % vb == 0 && g.lda % va == 0 && g.ldb % vb == 0 && g.sa % va == 0 &&
-             g.sb % vb == 0 && aligned16(g.a) && aligned16(g.b);
+  // 16-byte operand loads run along k (or, for a row-contiguous A, along m,
+  // where the loader guards a ragged last chunk itself).
+  const bool vec_a = (g.a_row_contiguous || g.K % va == 0) && g.lda % va == 0 && g.sa % va == 0 && aligned16(g.a);
+  bool vec = vec_a && g.K % vb == 0 && g.ldb % vb == 0 && g.sb % vb == 0 && aligned16(g.b);
   if (t.precision == AFHIP_PRECISION_F16) {
     AFHIP_REQUIRE(t.b_dtype != AFHIP_F32, "f16 precision takes f16 or int8 weights (prepare them first)");
     if (t.a_dtype == AFHIP_F32) return gemm_dispatch_f16_a32(g, t, v, vec, label, stream);
@@ -308,6 +310,22 @@ void pin_variant(const afhip_variant* v) {
   if (v) g_pin = *v;
 }
 
+// The variant a description runs with. A row-contiguous source or a
+// column-major output is staged and stored by the REGISTER_STAGED family
+// only, so such a plan takes that family's variant whatever the selection
+// for its shape class says.
+afhip_variant select_plan_variant(const afhip_gemm_desc& d, const GemmTypes& kt) {
+  afhip_variant v = select_variant(kt, d.rows, d.columns, d.inner, d.batch);
+  if ((d.a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS || d.c_layout == AFHIP_OUTPUT_COLUMN_MAJOR) &&
+      v.kernel != AFHIP_KERNEL_REGISTER_STAGED) {
+    const int source = v.source;
+    v = heuristic_variant(GemmTypes{kt.precision, AFHIP_F32, AFHIP_F32, kt.c_dtype}, d.rows, d.columns, d.inner,
+                          d.batch);
+    v.source = source;
+  }
+  return v;
+}
+
 }  // namespace afhip
 
 // ---------------------------------------------------------------------------
@@ -363,12 +381,18 @@ static int validate_desc(const afhip_gemm_desc* d) {
   AFHIP_REQUIRE(!(d->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS && d->w_dtype != AFHIP_I8 &&
                   d->w_dtype != (d->precision == AFHIP_PRECISION_F16 ? AFHIP_F16 : AFHIP_F32)),
                 "k-contiguous weights must be given in the precision's dtype (f16 for f16, f32 for f32)");
-  int64_t lda = d->lda ? d->lda : d->inner;
+  AFHIP_REQUIRE(d->a_layout == AFHIP_SOURCE_K_CONTIGUOUS || d->a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS,
+                "unknown source layout %d", d->a_layout);
+  AFHIP_REQUIRE(d->c_layout == AFHIP_OUTPUT_ROW_MAJOR || d->c_layout == AFHIP_OUTPUT_COLUMN_MAJOR,
+                "unknown output layout %d", d->c_layout);
+  const int64_t a_run = d->a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS ? d->rows : d->inner;
+  const int64_t c_run = d->c_layout == AFHIP_OUTPUT_COLUMN_MAJOR ? d->rows : d->columns;
+  int64_t lda = d->lda ? d->lda : a_run;
   int64_t ldw = d->ldw ? d->ldw : (d->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS ? d->inner : d->columns);
-  int64_t ldc = d->ldc ? d->ldc : d->columns;
-  AFHIP_REQUIRE(lda >= d->inner, "lda %lld < inner %d", (long long)lda, d->inner);
+  int64_t ldc = d->ldc ? d->ldc : c_run;
+  AFHIP_REQUIRE(lda >= a_run, "lda %lld is shorter than a source run of %lld", (long long)lda, (long long)a_run);
   AFHIP_REQUIRE(ldw >= (d->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS ? d->inner : d->columns), "ldw too small");
-  AFHIP_REQUIRE(ldc >= d->columns, "ldc %lld < columns %d", (long long)ldc, d->columns);
+  AFHIP_REQUIRE(ldc >= c_run, "ldc %lld is shorter than an output run of %lld", (long long)ldc, (long long)c_run);
   if (d->batch > 1)
     AFHIP_REQUIRE(d->batch_stride_a >= 0 && d->batch_stride_w >= 0 && d->batch_stride_c > 0,
                   "batched GEMM needs batch strides");
@@ -382,14 +406,14 @@ int afhip_gemm_plan_create(const afhip_gemm_desc* desc, afhip_gemm_plan** out) {
   if (!p) return set_error(AFHIP_ERR_OUT_OF_MEMORY, "plan allocation failed");
   p->desc = *desc;
   p->types = {desc->precision, desc->a_dtype, desc->w_dtype, desc->out_dtype};
-  p->lda = desc->lda ? desc->lda : desc->inner;
+  p->lda = desc->lda ? desc->lda : (desc->a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS ? desc->rows : desc->inner);
   p->ldw = desc->ldw ? desc->ldw : (desc->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS ? desc->inner : desc->columns);
-  p->ldc = desc->ldc ? desc->ldc : desc->columns;
+  p->ldc = desc->ldc ? desc->ldc : (desc->c_layout == AFHIP_OUTPUT_COLUMN_MAJOR ? desc->rows : desc->columns);
   // Selected with the weight dtype the kernels will read (a column-contiguous
   // f32 weight is converted on its way into the workspace).
   GemmTypes kt = p->types;
   if (desc->precision == AFHIP_PRECISION_F16 && desc->w_dtype != AFHIP_I8) kt.b_dtype = AFHIP_F16;
-  p->variant = select_variant(kt, desc->rows, desc->columns, desc->inner, desc->batch);
+  p->variant = select_plan_variant(*desc, kt);
   *out = p;
   return AFHIP_OK;
 }
@@ -459,6 +483,8 @@ int afhip::run_gemm_plan(const afhip_gemm_plan* plan, const void* a, const void*
   g.sb = d.batch_stride_w;
   g.sc = d.batch_stride_c;
   g.batch = d.batch;
+  g.a_row_contiguous = d.a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS;
+  g.c_column_major = d.c_layout == AFHIP_OUTPUT_COLUMN_MAJOR;
   g.flags = d.epilogue;
   if (d.epilogue & AFHIP_EPILOGUE_ATTENTION) {
     g.head_cols = d.heads * d.head_dim;

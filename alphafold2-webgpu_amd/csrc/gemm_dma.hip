@@ -401,6 +401,7 @@ bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (t.precision != AFHIP_PRECISION_F16 || t.a_dtype != AFHIP_F16 || t.b_dtype != AFHIP_F16) return false;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return false;
+  if (g.a_row_contiguous || g.c_column_major) return false;
   if (!al16(g.a) || !al16(g.b)) return false;
   if (g.K % 8 || g.lda % 8 || g.ldb % 8 || g.sa % 8 || g.sb % 8) return false;
   if (g.lda < g.K || g.ldb < g.K) return false;

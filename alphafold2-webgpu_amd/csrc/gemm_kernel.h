@@ -110,6 +110,79 @@ template <typename T, typename CT, int ROWS, bool VEC> struct TileLoader {
   }
 };
 
+// The same LDS tile from an operand stored k-major, [k][row] at
+// base + k * ld + row (the reference's sourceContiguous "row",
+// GemmOperandArray.columnMajor, src/runtime/gemm.ts:321, :341-360). A lane
+// takes `n` consecutive rows at two consecutive k: two 16-byte loads along
+// the rows, then one LDS word (f16) or two (f32) per row holding the pair of
+// k values, so the tile lands k-contiguous as TileLoader leaves it and the
+// MFMA fragments read it the same way.
+template <typename T, typename CT, bool VEC>
+__device__ __forceinline__ void load_rows(const T* __restrict__ base, int64_t ld, int row, int k, int rows, int K,
+                                          CT* out) {
+  constexpr int n = Vec16<T>::n;
+  if (k >= K) {
+#pragma unroll
+    for (int e = 0; e < n; e++) out[e] = (CT)0.0f;
+    return;
+  }
+  const T* p = base + (int64_t)k * ld + row;
+  if (VEC && row + n <= rows) {
+    T tmp[n];
+    *reinterpret_cast<uint4*>(tmp) = *reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int e = 0; e < n; e++) out[e] = (CT)(float)tmp[e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < n; e++) out[e] = row + e < rows ? (CT)(float)p[e] : (CT)0.0f;
+  }
+}
+
+template <typename T, typename CT, int ROWS, bool VEC> struct TileLoaderKMajor {
+  static constexpr int n = Vec16<T>::n;
+  static constexpr int kpairs = kBK / 2;
+  static constexpr int chunks = (ROWS / n) * kpairs;
+  static constexpr int iters = (chunks + kThreads - 1) / kThreads;
+  CT regs[iters][2][n];
+
+  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t ld, int row0, int k0, int rows, int K,
+                                       int tid) {
+#pragma unroll
+    for (int it = 0; it < iters; it++) {
+      const int q = tid + it * kThreads;
+      if (chunks % kThreads == 0 || q < chunks) {
+        const int kp = q % kpairs, rc = q / kpairs;
+        load_rows<T, CT, VEC>(base, ld, row0 + rc * n, k0 + 2 * kp, rows, K, regs[it][0]);
+        load_rows<T, CT, VEC>(base, ld, row0 + rc * n, k0 + 2 * kp + 1, rows, K, regs[it][1]);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(CT* __restrict__ lds, int tid) {
+    constexpr int pitch = LdsPitch<CT>::value;
+#pragma unroll
+    for (int it = 0; it < iters; it++) {
+      const int q = tid + it * kThreads;
+      if (chunks % kThreads == 0 || q < chunks) {
+        const int kp = q % kpairs, rc = q / kpairs;
+#pragma unroll
+        for (int e = 0; e < n; e++) {
+          CT* dst = lds + (rc * n + e) * pitch + 2 * kp;
+          if constexpr (sizeof(CT) == 2) {
+            half2v v;
+            v[0] = regs[it][0][e];
+            v[1] = regs[it][1][e];
+            *reinterpret_cast<half2v*>(dst) = v;
+          } else {
+            dst[0] = regs[it][0][e];
+            dst[1] = regs[it][1][e];
+          }
+        }
+      }
+    }
+  }
+};
+
 template <typename TC>
 __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int b, int row, int col, float y) {
   // Every operation rounds on its own (no fused multiply-add), so each kernel
@@ -136,7 +209,7 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int b, int row
     reinterpret_cast<TC*>(g.c)[at] = (TC)y;
     return;
   }
-  int64_t at = (int64_t)b * g.sc + (int64_t)row * g.ldc + col;
+  const int64_t at = (int64_t)b * g.sc + (g.c_column_major ? (int64_t)col * g.ldc + row : (int64_t)row * g.ldc + col);
   if (flags & AFHIP_EPILOGUE_RESIDUAL) y += (float)reinterpret_cast<const TC*>(g.residual)[at];
   reinterpret_cast<TC*>(g.c)[at] = (TC)y;
 }
@@ -185,7 +258,7 @@ __device__ __forceinline__ void epilogue_row4(const GemmArgs& g, int b, int row,
   }
 }
 
-template <int BM, int BN, bool F16MATH, typename TA, typename TB, typename TC, bool VEC>
+template <int BM, int BN, bool F16MATH, typename TA, typename TB, typename TC, bool VEC, bool AKMAJOR>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(KernelArgs ka) {
   using CT = typename std::conditional<F16MATH, half_t, float>::type;
   constexpr int pitch = LdsPitch<CT>::value;
@@ -213,7 +286,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(KernelArgs ka) {
   const int wm = (wave >> 1) * WTM;
   const int wn = (wave & 1) * WTN;
 
-  TileLoader<TA, CT, BM, VEC> la;
+  typename std::conditional<AKMAJOR, TileLoaderKMajor<TA, CT, BM, VEC>, TileLoader<TA, CT, BM, VEC>>::type la;
   TileLoader<TB, CT, BN, VEC> lb;
 
   floatx16 acc[TM][TN];
@@ -303,8 +376,13 @@ int launch_tiles(const GemmArgs& g, bool vec, const char* label, hipStream_t str
   ka.total_tiles = (int)total;
   ka.per_xcd = (int)ceil_div(total, 8);
   dim3 grid((unsigned)(ka.per_xcd * 8));
-  if (vec) return launch(label, gemm_kernel<BM, BN, F16MATH, TA, TB, TC, true>, grid, dim3(kThreads), 0, stream, ka);
-  return launch(label, gemm_kernel<BM, BN, F16MATH, TA, TB, TC, false>, grid, dim3(kThreads), 0, stream, ka);
+  if (g.a_row_contiguous) {
+    if (vec)
+      return launch(label, gemm_kernel<BM, BN, F16MATH, TA, TB, TC, true, true>, grid, dim3(kThreads), 0, stream, ka);
+    return launch(label, gemm_kernel<BM, BN, F16MATH, TA, TB, TC, false, true>, grid, dim3(kThreads), 0, stream, ka);
+  }
+  if (vec) return launch(label, gemm_kernel<BM, BN, F16MATH, TA, TB, TC, true, false>, grid, dim3(kThreads), 0, stream, ka);
+  return launch(label, gemm_kernel<BM, BN, F16MATH, TA, TB, TC, false, false>, grid, dim3(kThreads), 0, stream, ka);
 }
 
 template <bool F16MATH, typename TA, typename TB, typename TC>

@@ -400,6 +400,7 @@ bool stream_shape_ok(const GemmTypes& t, int64_t M, int64_t N, int64_t K, int ba
 
 bool stream_eligible(const GemmArgs& g, const GemmTypes& t) {
   if (!stream_shape_ok(t, g.M, g.N, g.K, g.batch)) return false;
+  if (g.a_row_contiguous || g.c_column_major) return false;
   const uint32_t allowed = AFHIP_EPILOGUE_SCALE | AFHIP_EPILOGUE_BIAS | AFHIP_EPILOGUE_ATTENTION | AFHIP_EPILOGUE_RELU;
   if (g.flags & ~allowed) return false;
   // Each wave's 64 columns must lie in one attention block (q, k, v or gate).

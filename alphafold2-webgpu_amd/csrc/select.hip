@@ -184,7 +184,7 @@ int afhip_gemm_select(const afhip_gemm_desc* d, afhip_variant* out) {
   AFHIP_REQUIRE(d->rows > 0 && d->inner > 0 && d->columns > 0 && d->batch > 0, "GEMM dimensions must be positive");
   AFHIP_REQUIRE(valid_precision(d->precision), "unknown precision %d", d->precision);
   GemmTypes t{d->precision, d->a_dtype, d->w_dtype, d->out_dtype};
-  *out = select_variant(t, d->rows, d->columns, d->inner, d->batch);
+  *out = select_plan_variant(*d, t);
   return AFHIP_OK;
 }
 

@@ -372,6 +372,8 @@ bool read_gemm_desc(napi_env env, napi_value o, afhip_gemm_desc* d) {
   FIELD(batch_stride_a, "batchStrideA", 0)
   FIELD(batch_stride_w, "batchStrideW", 0)
   FIELD(batch_stride_c, "batchStrideC", 0)
+  FIELD(a_layout, "aLayout", AFHIP_SOURCE_K_CONTIGUOUS)
+  FIELD(c_layout, "cLayout", AFHIP_OUTPUT_ROW_MAJOR)
 #undef FIELD
   return true;
 }

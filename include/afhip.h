@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define AFHIP_ABI_VERSION 2
+#define AFHIP_ABI_VERSION 3
 
 #if defined(__GNUC__)
 #define AFHIP_API __attribute__((visibility("default")))
@@ -116,10 +116,28 @@ AFHIP_API int afhip_synchronize(void* stream);
 #define AFHIP_WEIGHT_COLUMN_CONTIGUOUS 0
 #define AFHIP_WEIGHT_K_CONTIGUOUS 1
 
+/* Source (A) layouts: the reference's sourceContiguous (gemm.ts:308-321)
+ * and GemmOperandArray.columnMajor (:341-360). K_CONTIGUOUS is A[m][k]
+ * (element at m*lda + k, the default); ROW_CONTIGUOUS is A stored [k][m]
+ * (element at k*lda + m), as the outer-product mean's sequence-accumulated
+ * operands (outer-product-mean.ts:376-389) and the incoming triangle
+ * contraction (src/triangle/shaders.ts:488) have it. */
+#define AFHIP_SOURCE_K_CONTIGUOUS 0
+#define AFHIP_SOURCE_ROW_CONTIGUOUS 1
+
+/* Output layouts. ROW_MAJOR is C[m][n] (element at m*ldc + n, the default);
+ * COLUMN_MAJOR is C stored [n][m] (element at n*ldc + m), the
+ * column-major result a matrixEpilogue writes (gemm.ts:268-285), as the
+ * triangle projections store their channel-major operands. */
+#define AFHIP_OUTPUT_ROW_MAJOR 0
+#define AFHIP_OUTPUT_COLUMN_MAJOR 1
+
 /* The plan a caller describes; the counterpart of TiledGemmShader
  * (src/runtime/gemm.ts:230-339) with its WGSL fragments replaced by an
  * enumerated description. C[b][m][n] = epilogue(sum_k A[b][m][k] W[b][k][n]).
- * A is row-major [m][k] with row stride lda. */
+ * lda, ldw and ldc are the strides between the operands' outer index
+ * (rows of A[m][k], or k of A[k][m]; and so on). A row-contiguous source or
+ * a column-major output runs on the REGISTER_STAGED family. */
 typedef struct afhip_gemm_desc {
   int32_t rows;          /* M */
   int32_t inner;         /* K */
@@ -135,6 +153,8 @@ typedef struct afhip_gemm_desc {
   int32_t head_dim;      /* ATTENTION only */
   int64_t lda, ldw, ldc; /* leading dimensions in elements; 0 = packed */
   int64_t batch_stride_a, batch_stride_w, batch_stride_c; /* elements */
+  int32_t a_layout;      /* AFHIP_SOURCE_* (0: A[m][k]) */
+  int32_t c_layout;      /* AFHIP_OUTPUT_* (0: C[m][n]) */
 } afhip_gemm_desc;
 
 typedef struct afhip_gemm_plan afhip_gemm_plan;
@@ -145,8 +165,8 @@ AFHIP_API int afhip_gemm_plan_destroy(afhip_gemm_plan* plan);
 /* Bytes of device workspace a run needs (a W transpose for the
  * column-contiguous layout; 0 otherwise). */
 AFHIP_API int afhip_gemm_workspace_size(const afhip_gemm_plan* plan, size_t* bytes);
-/* scale: f32 [N] (SCALE); bias: f32 [N] (BIAS); residual: [M][ldc] of the
- * output dtype (RESIDUAL). Unused pointers may be NULL. */
+/* scale: f32 [N] (SCALE); bias: f32 [N] (BIAS); residual: laid out as the
+ * output, of the output dtype (RESIDUAL). Unused pointers may be NULL. */
 AFHIP_API int afhip_gemm_run(const afhip_gemm_plan* plan, const void* a, const void* w, const float* scale,
                    const float* bias, const void* residual, void* c, void* workspace,
                    size_t workspace_bytes, void* stream);

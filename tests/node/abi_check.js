@@ -13,7 +13,7 @@ var expected = ["open", "close", "abiVersion", "deviceReport", "bufferCreate", "
   "executionReleaseSince", "executionNoteSubmitted", "executionSnapshot", "executionAddInPlace",
   "executionPrepareWeights", "executionPairStack", "executionEvoformerBlock", "setMemoryBudget", "memoryResident"];
 expected.forEach(function (n) { assert.strictEqual(typeof native[n], "function", n); });
-assert.strictEqual(native.abiVersion(), 2);
+assert.strictEqual(native.abiVersion(), 3);
 
 // gemmGrid known answers (test/gemm-selection.test.ts:239-262, test/gemm.test.ts:37-61).
 assert.deepStrictEqual(afhip.gemmGrid(65536 * 64, 128), [2, 65535]);

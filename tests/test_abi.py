@@ -37,7 +37,7 @@ def test_abi_version_and_not_open_errors():
     from afhip import _lib
 
     lib = _lib.library()
-    assert lib.afhip_abi_version() == 2
+    assert lib.afhip_abi_version() == 3
     size = ctypes.c_size_t()
     # A call that needs the device reports NOT_OPEN rather than touching HIP.
     assert lib.afhip_buffer_create(16, ctypes.byref(ctypes.c_void_p())) == _lib.ERR_NOT_OPEN

@@ -1,0 +1,138 @@
+"""Operand and output layouts of the GEMM plan against float64.
+
+The reference checks its staged kernel on every pairing of a row-contiguous
+source and a k-contiguous weight (test/gemm-matrix-units.gpu.test.ts:80-170:
+130 x 96 x 132, LCG operands, max|d|/max|ref| < 4e-3 for the f16 units).
+These are the same cases through afhip_gemm_desc's a_layout and w_layout,
+plus the column-major output (the reference's column-major matrixEpilogue,
+src/runtime/gemm.ts:268-285) and the outer-product mean's contraction
+written as a plan, both operands sequence-major as
+src/evoformer/outer-product-mean.ts:376-389 describes them.
+"""
+import numpy as np
+import pytest
+
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+TILES = [(64, 64), (64, 128), (128, 64), (128, 128)]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    from afhip import device
+
+    device.open_device(0)
+    return torch.device("cuda", 0)
+
+
+def rel_max(actual, expected):
+    a = np.asarray(actual, np.float64).reshape(-1)
+    e = np.asarray(expected, np.float64).reshape(-1)
+    return float(np.abs(a - e).max() / max(np.abs(e).max(), 1e-30))
+
+
+def to_dev(x, dev, half=False):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    return t.half() if half else t
+
+
+@pytest.mark.parametrize("precision,tol", [("f32", 1e-5), ("f16", 4e-3)])
+@pytest.mark.parametrize("source,weight", [("k", "column"), ("row", "column"), ("k", "k"), ("row", "k")])
+def test_reference_layout_cases(dev, precision, tol, source, weight):
+    # gemm-matrix-units.gpu.test.ts:84-89, :99-102, :155-168: the operands are
+    # written transposed when the layout says so, and every tile of the
+    # family that takes a row-contiguous source computes the same product.
+    from afhip import gemm
+
+    rows, inner, columns = 130, 96, 132
+    source_values = ref.lcg_values(0x2244668, rows * inner)
+    weight_values = ref.lcg_values(0x1133557, inner * columns)
+    a = source_values.reshape(inner, rows).T if source == "row" else source_values.reshape(rows, inner)
+    w = weight_values.reshape(columns, inner).T if weight == "k" else weight_values.reshape(inner, columns)
+    if precision == "f16":
+        a, w = ref.round_f16(a), ref.round_f16(w)
+    expect = a.astype(np.float64) @ w.astype(np.float64)
+    a_stored = source_values.reshape(inner, rows) if source == "row" else source_values.reshape(rows, inner)
+    w_stored = weight_values.reshape(columns, inner) if weight == "k" else weight_values.reshape(inner, columns)
+    dtype = precision
+    # a k-contiguous weight is given in the precision's dtype (the plan rule)
+    ad = to_dev(a_stored, dev, half=dtype == "f16")
+    wd = to_dev(w_stored, dev, half=dtype == "f16")
+    for tr, tc in TILES:
+        gemm.force_variant(gemm.GemmVariant(precision, tr, tc, source="pinned"))
+        try:
+            plan = gemm.TiledGemm(rows, inner, columns, precision=precision, a_dtype=dtype, w_dtype=dtype,
+                                  w_layout=weight, out_dtype="f32", a_layout=source)
+            assert plan.variant().kernel == "register"
+            out = plan.run(ad, wd).cpu().numpy()
+        finally:
+            gemm.force_variant(None)
+        assert rel_max(out, expect) <= tol, (tr, tc)
+
+
+@pytest.mark.parametrize("out_dtype", ["f32", "f16"])
+def test_row_contiguous_source_column_major_output_epilogue(dev, out_dtype):
+    # A batched plan with A stored [K][M] (ragged M whose rows are padded to
+    # 136, so the 16-byte loads run and the last chunk of each k-row is
+    # guarded) and C stored [N][M], through bias, ReLU and residual.
+    import torch
+
+    from afhip import gemm
+
+    B, M, K, N, lda = 3, 130, 72, 100, 136
+    a_stored = ref.round_f16(ref.normal(101, (B, K, lda)))
+    w = ref.round_f16(ref.normal(102, (B, N, K), 1 / K))
+    bias = ref.normal(103, (N,), 0.1)
+    residual = ref.round_f16(ref.normal(104, (B, N, M)))
+    a = np.transpose(a_stored[:, :, :M], (0, 2, 1))
+    expect = np.einsum("bmk,bnk->bmn", a.astype(np.float64), w.astype(np.float64)) + bias
+    expect = np.maximum(expect, 0) + np.transpose(residual, (0, 2, 1))
+    plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k", out_dtype=out_dtype,
+                          epilogue=("bias", "relu", "residual"), batch=B, lda=lda, batch_stride_a=K * lda,
+                          batch_stride_w=N * K, batch_stride_c=N * M, a_layout="row", c_layout="column")
+    assert plan.variant().kernel == "register"
+    res = to_dev(residual, dev).to(torch.float32 if out_dtype == "f32" else torch.float16)
+    out = plan.run(to_dev(a_stored, dev, half=True), to_dev(w, dev, half=True), bias=to_dev(bias, dev),
+                   residual=res, out=res.clone())
+    got = np.transpose(out.float().cpu().numpy(), (0, 2, 1))
+    assert rel_max(got, expect) <= (4e-3 if out_dtype == "f32" else 1e-2)
+
+
+def test_opm_contraction_as_a_plan(dev):
+    # outer[i a][j b] = sum_s left[s][i a] right[s][j b]: the outer-product
+    # mean's contraction with both operands accumulated over sequences, as
+    # the reference's plan describes it (sourceContiguous "row", the weight
+    # [k][column]); S and L * c_outer not multiples of a tile.
+    from afhip import gemm
+
+    S, L, co = 37, 5, 32
+    P = L * co
+    left = ref.round_f16(ref.normal(111, (S, P)))
+    right = ref.round_f16(ref.normal(112, (S, P)))
+    expect = left.T.astype(np.float64) @ right.astype(np.float64)
+    for precision in ("f16", "f32"):
+        dtype = "f16" if precision == "f16" else "f32"
+        plan = gemm.TiledGemm(P, S, P, precision=precision, a_dtype=dtype, w_dtype=dtype, w_layout="column",
+                              out_dtype="f32", a_layout="row")
+        out = plan.run(to_dev(left, dev, half=dtype == "f16"), to_dev(right, dev, half=dtype == "f16"))
+        assert rel_max(out.cpu().numpy(), expect) <= (4e-3 if precision == "f16" else 1e-5), precision
+
+
+def test_layouts_are_validated(dev):
+    from afhip import _lib, gemm
+
+    with pytest.raises(_lib.RangeError):
+        gemm.TiledGemm(64, 32, 64, a_layout="column")
+    with pytest.raises(_lib.RangeError):
+        gemm.TiledGemm(64, 32, 64, c_layout="k")
+    # a k-major source's stride runs over rows: shorter than M is refused
+    with pytest.raises(_lib.RangeError):
+        gemm.TiledGemm(64, 32, 64, a_layout="row", lda=63)
+    with pytest.raises(_lib.RangeError):
+        gemm.TiledGemm(64, 32, 48, c_layout="column", ldc=40)
