@@ -63,10 +63,19 @@ def synchronize() -> None:
 
 
 def memory_snapshot() -> dict:
-    """Counterpart of the allocator snapshot each reference run() returns (allocator.ts:8-29)."""
+    """The AllocationSnapshot fields each reference run() returns
+    (src/runtime/allocator.ts:8-29), read from the allocator that holds this
+    process's device tensors (PyTorch's caching allocator). Its pools are not
+    labelled, so peakComposition is empty."""
     torch = _torch()
-    return {"allocatedBytes": int(torch.cuda.memory_allocated()),
-            "peakBytes": int(torch.cuda.max_memory_allocated())}
+    stats = torch.cuda.memory_stats()
+    current = int(torch.cuda.memory_allocated())
+    resident = int(torch.cuda.memory_reserved())
+    return {"currentBytes": current, "peakBytes": int(torch.cuda.max_memory_allocated()), "peakComposition": [],
+            "residentBytes": resident, "peakResidentBytes": int(torch.cuda.max_memory_reserved()),
+            "pooledBytes": max(resident - current, 0),
+            "allocationCount": int(stats.get("allocation.all.allocated", 0)),
+            "bufferCount": int(stats.get("segment.all.current", 0))}
 
 
 def device_report() -> dict:

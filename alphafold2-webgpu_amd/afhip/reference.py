@@ -48,7 +48,7 @@ def load_triangle_reference_bundle(manifest_path: str) -> dict:
     return {
         "source": manifest.get("source", ""),
         "input": {
-            "shape": (int(shape["length"]), int(shape["cZ"]), int(shape["cHidden"])),
+            "shape": {"length": int(shape["length"]), "cZ": int(shape["cZ"]), "cHidden": int(shape["cHidden"])},
             "epsilon": float(manifest.get("epsilon", 1e-5)),
             "z": tensor("z"),
             "mask": tensor("mask"),

@@ -37,9 +37,19 @@ def _expect_length(name: str, value, length: int) -> None:
         raise _lib.RangeError(f"{name} has {n} values; expected {length}")
 
 
+def triangle_shape(inp: dict) -> tuple:
+    """(length, cZ, cHidden) of an input whose shape is the reference's
+    TriangleShape {length, cZ, cHidden} (src/triangle/types.ts:3-7) or a
+    (length, cZ, cHidden) tuple."""
+    shape = inp["shape"]
+    if isinstance(shape, dict):
+        return shape.get("length"), shape.get("cZ"), shape.get("cHidden")
+    return tuple(shape)
+
+
 def validate_triangle_input(inp: dict) -> None:
     """validateTriangleInput (src/triangle/types.ts:54-89)."""
-    length, cz, ch = inp["shape"]
+    length, cz, ch = triangle_shape(inp)
     _positive_integer("length", length)
     _positive_integer("cZ", cz)
     _positive_integer("cHidden", ch)
@@ -138,7 +148,7 @@ class _TriangleMultiplicationGpu:
 
         options = options or {}
         validate_triangle_input(inp)
-        length, cz, ch = inp["shape"]
+        length, cz, ch = triangle_shape(inp)
         precision = options.get("precision", "f32")
         if precision not in ("f32", "f16"):
             raise _lib.RangeError(f"unknown precision {precision}")

@@ -7,14 +7,17 @@
 //    addon (lib.rs:24-730 hands out u32 handles for every wgpu object);
 //    explicit destroy calls free them (lib.rs:706-730);
 //  - host data crosses as TypedArrays, copied in and out;
-//  - every call is synchronous on the JS thread;
+//  - every call is synchronous on the JS thread except the operator runs,
+//    which return Promises and do their device work on a libuv worker
+//    thread (the reference's run() is async, src/triangle/webgpu.ts:56);
 //  - failures become JS exceptions: RangeError for invalid arguments (the
 //    reference's RangeError, src/triangle/types.ts:42-52), Error otherwise,
 //    with libafhip's message.
-// The operator entry points (triangleRun, opmRun, transitionRun) upload,
-// run and read back in one call, as TriangleMultiplicationGpu.run does
-// (src/triangle/webgpu.ts:56-201), and report the elapsed wall time from
-// the first upload through the readback, as that method does (:189-196).
+// The operator entry points (triangleRun, opmRun, transitionRun,
+// attentionRun) upload, run and read back in one job, as
+// TriangleMultiplicationGpu.run does (src/triangle/webgpu.ts:56-201), and
+// report the elapsed wall time from the first upload through the readback,
+// as that method does (:189-196).
 #include <node_api.h>
 
 #include <chrono>
@@ -22,6 +25,8 @@
 #include <cstdint>
 #include <cstring>
 #include <map>
+#include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -179,6 +184,8 @@ napi_value make_float32(napi_env env, const std::vector<float>& v) {
   return arr;
 }
 
+size_t dtype_bytes(int64_t d) { return d == AFHIP_F16 ? 2 : d == AFHIP_I8 ? 1 : 4; }
+
 napi_value make_number(napi_env env, double d) {
   napi_value v;
   napi_create_double(env, d, &v);
@@ -201,6 +208,8 @@ struct Registry {
   uint32_t next = 1;
   std::map<uint32_t, std::pair<void*, size_t>> buffers;
   std::map<uint32_t, afhip_gemm_plan*> plans;
+  std::map<uint32_t, afhip_gemm_desc> plan_descs;  // what each plan's operands must hold
+  std::map<uint32_t, std::string> prepared;        // buffer handle -> weight kind it was prepared as
   std::map<uint32_t, ExecutionEntry> executions;
   std::map<uint32_t, uint32_t> owner;  // buffer handle -> execution handle, for pooled tensors
 };
@@ -224,12 +233,15 @@ double now_ms() {
 // Context
 // ---------------------------------------------------------------------------
 
+int g_ordinal = 0;  // the device Open selected; each worker thread selects it too
+
 napi_value Open(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a, 0)) return nullptr;
   int64_t ordinal = 0;
   if (a.argc > 0 && !get_int64(env, a.argv[0], &ordinal)) return nullptr;
   if (!check(env, afhip_open((int)ordinal), "open")) return nullptr;
+  g_ordinal = (int)ordinal;
   return nullptr;
 }
 
@@ -478,6 +490,7 @@ napi_value GemmPlanCreate(napi_env env, napi_callback_info info) {
   if (!check(env, afhip_gemm_plan_create(&d, &plan), "gemmPlanCreate")) return nullptr;
   const uint32_t h = g_reg.next++;
   g_reg.plans[h] = plan;
+  g_reg.plan_descs[h] = d;
   return make_number(env, h);
 }
 
@@ -490,6 +503,7 @@ napi_value GemmPlanDestroy(napi_env env, napi_callback_info info) {
   if (it != g_reg.plans.end()) {
     afhip_gemm_plan_destroy(it->second);
     g_reg.plans.erase(it);
+    g_reg.plan_descs.erase((uint32_t)h);
   }
   return nullptr;
 }
@@ -534,6 +548,38 @@ napi_value GemmRun(napi_env env, napi_callback_info info) {
     if (t == napi_undefined || t == napi_null) continue;
     if (!lookup_buffer(env, v, &ptrs[i], &sizes[i])) return nullptr;
   }
+  // Every operand the plan reads or writes must lie inside its buffer, as
+  // WebGPU validates a binding against its buffer's size.
+  const afhip_gemm_desc& d = g_reg.plan_descs[(uint32_t)h];
+  const int64_t M = d.rows, K = d.inner, N = d.columns, B = d.batch;
+  const bool a_rows = d.a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS, w_k = d.w_layout == AFHIP_WEIGHT_K_CONTIGUOUS,
+             c_cols = d.c_layout == AFHIP_OUTPUT_COLUMN_MAJOR;
+  const int64_t lda = d.lda ? d.lda : (a_rows ? M : K), ldw = d.ldw ? d.ldw : (w_k ? K : N),
+                ldc = d.ldc ? d.ldc : (c_cols ? M : N);
+  auto extent = [&](int64_t outer, int64_t ld, int64_t run, int64_t stride) {
+    return (B - 1) * stride + (outer - 1) * ld + run;  // elements
+  };
+  const size_t need[6] = {
+      (size_t)extent(a_rows ? K : M, lda, a_rows ? M : K, d.batch_stride_a) * dtype_bytes(d.a_dtype),
+      (size_t)extent(w_k ? N : K, ldw, w_k ? K : N, d.batch_stride_w) * dtype_bytes(d.w_dtype),
+      (d.epilogue & AFHIP_EPILOGUE_SCALE) ? (size_t)N * 4 : 0,
+      (d.epilogue & AFHIP_EPILOGUE_BIAS) ? (size_t)N * 4 : 0,
+      (d.epilogue & AFHIP_EPILOGUE_RESIDUAL)
+          ? (size_t)extent(c_cols ? N : M, ldc, c_cols ? M : N, d.batch_stride_c) * dtype_bytes(d.out_dtype)
+          : 0,
+      (size_t)extent(c_cols ? N : M, ldc, c_cols ? M : N, d.batch_stride_c) * dtype_bytes(d.out_dtype)};
+  for (int i = 0; i < 6; i++) {
+    if (need[i] == 0) continue;
+    if (ptrs[i] == nullptr) {
+      throw_js(env, {true, std::string("gemmRun: the plan needs operand ") + names[i]});
+      return nullptr;
+    }
+    if (sizes[i] < need[i]) {
+      throw_js(env, {true, std::string("gemmRun: buffer ") + names[i] + " holds " + std::to_string(sizes[i]) +
+                               " bytes; the plan reads or writes " + std::to_string(need[i])});
+      return nullptr;
+    }
+  }
   if (!check(env,
              afhip_gemm_run(it->second, ptrs[0], ptrs[1], (const float*)ptrs[2], (const float*)ptrs[3], ptrs[4],
                             ptrs[5], ptrs[6], sizes[6], nullptr),
@@ -552,16 +598,19 @@ napi_value PackWeightQ8Block(napi_env env, napi_callback_info info) {
   void *codes, *scales, *dst;
   size_t codes_bytes, scales_bytes, dst_bytes;
   int64_t block, start, rows_k, columns_n, dtype;
-  if (!lookup_buffer(env, a.argv[0], &codes, &codes_bytes) || !lookup_buffer(env, a.argv[1], &scales, &scales_bytes) ||
-      !get_int64(env, a.argv[2], &block) || !get_int64(env, a.argv[3], &start) || !get_int64(env, a.argv[4], &rows_k) ||
-      !get_int64(env, a.argv[5], &columns_n) || !lookup_buffer(env, a.argv[6], &dst, &dst_bytes) ||
-      !get_int64(env, a.argv[7], &dtype))
+  // The numbers first, so a block or shape that does not fit the C ABI's
+  // 32-bit arguments is refused before anything is looked up or cast.
+  if (!get_int64(env, a.argv[2], &block) || !get_int64(env, a.argv[3], &start) || !get_int64(env, a.argv[4], &rows_k) ||
+      !get_int64(env, a.argv[5], &columns_n) || !get_int64(env, a.argv[7], &dtype))
     return nullptr;
-  if (block <= 0 || start < 0 || rows_k <= 0 || columns_n <= 0 || rows_k > INT32_MAX || columns_n > INT32_MAX ||
-      (dtype != AFHIP_F32 && dtype != AFHIP_F16)) {
+  if (block <= 0 || block > INT32_MAX || start < 0 || rows_k <= 0 || columns_n <= 0 || rows_k > INT32_MAX ||
+      columns_n > INT32_MAX || (dtype != AFHIP_F32 && dtype != AFHIP_F16)) {
     throw_js(env, {true, "packWeightQ8Block: invalid block, range, shape or dtype"});
     return nullptr;
   }
+  if (!lookup_buffer(env, a.argv[0], &codes, &codes_bytes) || !lookup_buffer(env, a.argv[1], &scales, &scales_bytes) ||
+      !lookup_buffer(env, a.argv[6], &dst, &dst_bytes))
+    return nullptr;
   const int64_t count = rows_k * columns_n;
   if (start + count > (int64_t)codes_bytes) {
     throw_js(env, {true, "packWeightQ8Block: tensor range is out of bounds"});
@@ -605,6 +654,29 @@ bool lookup_execution(napi_env env, napi_value v, uint32_t* handle, ExecutionEnt
 void forget_buffer(uint32_t h) {
   g_reg.buffers.erase(h);
   g_reg.owner.erase(h);
+  g_reg.prepared.erase(h);
+}
+
+// A prepared-weight handle for a chained step: it must have been prepared as
+// `kind` and hold the bytes that step's prepared weights take.
+bool lookup_prepared(napi_env env, napi_value v, const char* kind, size_t need, void** p) {
+  size_t bytes = 0;
+  if (!lookup_buffer(env, v, p, &bytes)) return false;
+  int64_t h = 0;
+  get_int64(env, v, &h);
+  auto it = g_reg.prepared.find((uint32_t)h);
+  if (it == g_reg.prepared.end() || it->second != kind) {
+    throw_js(env, {true, std::string("weights for ") + kind + " must come from executionPrepareWeights(\"" + kind +
+                             "\"); handle " + std::to_string(h) + " was prepared as " +
+                             (it == g_reg.prepared.end() ? std::string("nothing") : "\"" + it->second + "\"")});
+    return false;
+  }
+  if (bytes < need) {
+    throw_js(env, {true, std::string("prepared weights for ") + kind + " hold " + std::to_string(bytes) +
+                             " bytes; this shape needs " + std::to_string(need)});
+    return false;
+  }
+  return true;
 }
 
 // Registers the execution's newest allocation (pointer p) as a buffer handle.
@@ -765,7 +837,6 @@ napi_value ExecutionSnapshot(napi_env env, napi_callback_info info) {
   return s;
 }
 
-size_t dtype_bytes(int64_t d) { return d == AFHIP_F16 ? 2 : 4; }
 
 // executionAddInPlace(ex, base, baseDtype, update, updateDtype, elements)
 napi_value ExecutionAddInPlace(napi_env env, napi_callback_info info) {
@@ -894,6 +965,11 @@ napi_value ExecutionPrepareWeights(napi_env env, napi_callback_info info) {
     return nullptr;
   }
   napi_value handle = register_pooled(env, exh, *e, dst, bytes);
+  {
+    int64_t h = 0;
+    get_int64(env, handle, &h);
+    g_reg.prepared[(uint32_t)h] = kind;
+  }
   const float* f = (const float*)src;
   if (kind == "outerProductMean") st = afhip_opm_prepare_weights(&d.opm, f, dst, nullptr);
   else if (kind == "triangleOutgoing") st = afhip_triangle_prepare_weights(&d.outgoing, f, dst, nullptr);
@@ -923,6 +999,13 @@ napi_value ExecutionPairStack(napi_env env, napi_callback_info info) {
   const char* names[6] = {"outerProductMean", "triangleOutgoing", "triangleIncoming", "triangleAttentionStarting",
                           "triangleAttentionEnding", "pairTransition"};
   void* w[6] = {};
+  size_t need[6] = {};
+  afhip_opm_weights_size(&d.opm, &need[0]);
+  afhip_triangle_weights_size(&d.outgoing, &need[1]);
+  afhip_triangle_weights_size(&d.incoming, &need[2]);
+  afhip_attention_weights_size(&d.attention_start, &need[3]);
+  afhip_attention_weights_size(&d.attention_end, &need[4]);
+  afhip_transition_weights_size(&d.transition, &need[5]);
   for (int i = 0; i < 6; i++) {
     bool has = false;
     napi_has_named_property(env, a.argv[2], names[i], &has);
@@ -932,7 +1015,7 @@ napi_value ExecutionPairStack(napi_env env, napi_callback_info info) {
     napi_valuetype t;
     napi_typeof(env, v, &t);
     if (t == napi_undefined || t == napi_null) continue;
-    if (!lookup_buffer(env, v, &w[i], nullptr)) return nullptr;
+    if (!lookup_prepared(env, v, names[i], need[i], &w[i])) return nullptr;
   }
   void *pair, *pmask, *msa = nullptr, *mmask = nullptr;
   size_t np, npm, nm = 0, nmm = 0;
@@ -975,6 +1058,16 @@ napi_value ExecutionEvoformerBlock(napi_env env, napi_callback_info info) {
                           "triangleOutgoing", "triangleIncoming", "triangleAttentionStarting",
                           "triangleAttentionEnding", "pairTransition"};
   void* w[9] = {};
+  size_t need[9] = {};
+  afhip_attention_weights_size(&d.msa_row, &need[0]);
+  afhip_attention_weights_size(&d.msa_column, &need[1]);
+  afhip_transition_weights_size(&d.msa_transition, &need[2]);
+  afhip_opm_weights_size(&d.pair.opm, &need[3]);
+  afhip_triangle_weights_size(&d.pair.outgoing, &need[4]);
+  afhip_triangle_weights_size(&d.pair.incoming, &need[5]);
+  afhip_attention_weights_size(&d.pair.attention_start, &need[6]);
+  afhip_attention_weights_size(&d.pair.attention_end, &need[7]);
+  afhip_transition_weights_size(&d.pair.transition, &need[8]);
   for (int i = 0; i < 9; i++) {
     bool has = false;
     napi_has_named_property(env, a.argv[2], names[i], &has);
@@ -984,7 +1077,7 @@ napi_value ExecutionEvoformerBlock(napi_env env, napi_callback_info info) {
     napi_valuetype t;
     napi_typeof(env, v, &t);
     if (t == napi_undefined || t == napi_null) continue;
-    if (!lookup_buffer(env, v, &w[i], nullptr)) return nullptr;
+    if (!lookup_prepared(env, v, names[i], need[i], &w[i])) return nullptr;
   }
   void *msa, *mmask, *pair, *pmask;
   size_t nm, nmm, np, npm;
@@ -1029,30 +1122,213 @@ napi_value MemoryResident(napi_env env, napi_callback_info) {
 }
 
 // ---------------------------------------------------------------------------
-// Operators with host arrays (upload, prepare, run, read back)
+// Operators with host arrays (upload, prepare, run, read back), as Promises
+//
+// The reference's run() is async (src/triangle/webgpu.ts:56,
+// outer-product-mean.ts:549, transition.ts:264): it validates and queues
+// synchronously, then awaits the GPU. Here the call copies its host arrays
+// on the JS thread and returns a Promise; a libuv worker thread uploads
+// through the operator's own execution (its allocator, allocator.ts:168-388,
+// so repeated runs reuse pooled buffers), prepares the weights, runs, reads
+// back and takes the execution's AllocationSnapshot while everything is
+// still live, as the reference does before releasing (webgpu.ts:197-201).
+// Runs on one execution take its lock in turn.
 // ---------------------------------------------------------------------------
 
-napi_value result_object(napi_env env, const std::vector<float>& out, double ms, size_t peak) {
-  napi_value o, mem;
-  napi_create_object(env, &o);
-  napi_value arr = make_float32(env, out);
-  if (!arr) return nullptr;
-  napi_set_named_property(env, o, "output", arr);
-  napi_set_named_property(env, o, "elapsedMilliseconds", make_number(env, ms));
-  napi_create_object(env, &mem);
-  napi_set_named_property(env, mem, "peakBytes", make_number(env, (double)peak));
-  napi_set_named_property(env, o, "memory", mem);
-  return o;
+struct OperatorJob {
+  napi_async_work work = nullptr;
+  napi_deferred deferred = nullptr;
+  afhip_execution* ex = nullptr;
+  std::mutex* lock = nullptr;
+  std::vector<std::vector<char>> inputs;  // host copies, in the order the body uploads them
+  int (*body)(OperatorJob&) = nullptr;
+  afhip_triangle_desc tri{};
+  afhip_opm_desc opm{};
+  afhip_transition_desc tra{};
+  afhip_attention_desc att{};
+  int status = AFHIP_OK;
+  std::string message;
+  std::vector<float> output;
+  double ms = 0.0;
+  std::string memory;
+};
+
+// Uploads input i under `label`.
+int job_upload(OperatorJob& j, size_t i, const char* label, void** out) {
+  return afhip_execution_upload(j.ex, label, j.inputs[i].data(), j.inputs[i].size(), out);
 }
 
-// triangleRun(desc, z: Float32Array | Uint16Array (f16 bits), mask: Float32Array, packed: Float32Array)
+// The common tail: wait, read the output back, snapshot the live allocation.
+int job_finish(OperatorJob& j, const void* out, size_t out_bytes, double t0) {
+  if (int s = afhip_synchronize(nullptr)) return s;
+  j.output.resize(out_bytes / 4);
+  if (int s = afhip_buffer_read(out, 0, j.output.data(), out_bytes)) return s;
+  j.ms = now_ms() - t0;
+  std::vector<char> json(1 << 16);
+  if (int s = afhip_execution_snapshot(j.ex, json.data(), json.size())) return s;
+  j.memory = json.data();
+  return AFHIP_OK;
+}
+
+int triangle_body(OperatorJob& j) {
+  const afhip_triangle_desc& d = j.tri;
+  size_t wbytes = 0, wsbytes = 0;
+  if (int s = afhip_triangle_weights_size(&d, &wbytes)) return s;
+  if (int s = afhip_triangle_workspace_size(&d, &wsbytes)) return s;
+  const size_t out_bytes = (size_t)d.length * d.length * d.c_z * 4;
+  const double t0 = now_ms();
+  void *z, *mask, *packed, *weights, *ws, *out;
+  if (int s = job_upload(j, 0, "triangle.z", &z)) return s;
+  if (int s = job_upload(j, 1, "triangle.mask", &mask)) return s;
+  if (int s = job_upload(j, 2, "triangle.weights-f32", &packed)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "triangle.weights", wbytes, &weights)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "triangle.workspace", wsbytes ? wsbytes : 1, &ws)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "triangle.output", out_bytes, &out)) return s;
+  if (int s = afhip_triangle_prepare_weights(&d, (const float*)packed, weights, nullptr)) return s;
+  if (int s = afhip_triangle_run(&d, z, (const float*)mask, weights, out, ws, wsbytes, nullptr)) return s;
+  return job_finish(j, out, out_bytes, t0);
+}
+
+int opm_body(OperatorJob& j) {
+  const afhip_opm_desc& d = j.opm;
+  size_t wbytes = 0, wsbytes = 0;
+  if (int s = afhip_opm_weights_size(&d, &wbytes)) return s;
+  if (int s = afhip_opm_workspace_size(&d, &wsbytes)) return s;
+  const size_t out_bytes = (size_t)d.length * d.length * d.c_z * 4;
+  const double t0 = now_ms();
+  void *act, *mask, *packed, *weights, *ws, *out;
+  if (int s = job_upload(j, 0, "outer-product-mean.activations", &act)) return s;
+  if (int s = job_upload(j, 1, "outer-product-mean.mask", &mask)) return s;
+  if (int s = job_upload(j, 2, "outer-product-mean.weights-f32", &packed)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "outer-product-mean.weights", wbytes, &weights)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "outer-product-mean.workspace", wsbytes ? wsbytes : 1, &ws)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "outer-product-mean.output", out_bytes, &out)) return s;
+  if (int s = afhip_opm_prepare_weights(&d, (const float*)packed, weights, nullptr)) return s;
+  if (int s = afhip_opm_run(&d, act, (const float*)mask, weights, out, ws, wsbytes, nullptr)) return s;
+  return job_finish(j, out, out_bytes, t0);
+}
+
+int transition_body(OperatorJob& j) {
+  const afhip_transition_desc& d = j.tra;
+  size_t wbytes = 0, wsbytes = 0;
+  if (int s = afhip_transition_weights_size(&d, &wbytes)) return s;
+  if (int s = afhip_transition_workspace_size(&d, &wsbytes)) return s;
+  const size_t out_bytes = (size_t)d.rows * d.channels * 4;
+  const double t0 = now_ms();
+  void *act, *packed, *weights, *ws, *out;
+  if (int s = job_upload(j, 0, "transition.activations", &act)) return s;
+  if (int s = job_upload(j, 1, "transition.weights-f32", &packed)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "transition.weights", wbytes, &weights)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "transition.workspace", wsbytes ? wsbytes : 1, &ws)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "transition.output", out_bytes, &out)) return s;
+  if (int s = afhip_transition_prepare_weights(&d, (const float*)packed, weights, nullptr)) return s;
+  if (int s = afhip_transition_run(&d, act, weights, out, ws, wsbytes, nullptr)) return s;
+  return job_finish(j, out, out_bytes, t0);
+}
+
+int attention_body(OperatorJob& j) {
+  const afhip_attention_desc& d = j.att;
+  size_t wbytes = 0, wsbytes = 0;
+  if (int s = afhip_attention_weights_size(&d, &wbytes)) return s;
+  if (int s = afhip_attention_workspace_size(&d, &wsbytes)) return s;
+  const size_t out_bytes = (size_t)d.batch * d.queries * d.channels * 4;
+  const double t0 = now_ms();
+  void *act, *mask, *pair = nullptr, *packed, *weights, *ws, *out;
+  if (int s = job_upload(j, 0, "attention.activations", &act)) return s;
+  if (int s = job_upload(j, 1, "attention.mask", &mask)) return s;
+  if (int s = job_upload(j, 2, "attention.weights-f32", &packed)) return s;
+  if (j.inputs.size() > 3)
+    if (int s = job_upload(j, 3, "attention.pair-activations", &pair)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "attention.weights", wbytes, &weights)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "attention.workspace", wsbytes ? wsbytes : 1, &ws)) return s;
+  if (int s = afhip_execution_allocate(j.ex, "attention.output", out_bytes, &out)) return s;
+  if (int s = afhip_attention_prepare_weights(&d, (const float*)packed, weights, nullptr)) return s;
+  if (int s = afhip_attention_run(&d, act, (const float*)mask, pair, weights, out, ws, wsbytes, nullptr)) return s;
+  return job_finish(j, out, out_bytes, t0);
+}
+
+void job_execute(napi_env, void* data) {
+  auto* j = static_cast<OperatorJob*>(data);
+  std::lock_guard<std::mutex> guard(*j->lock);
+  uint64_t mark = 0;
+  // HIP's current device is a per-thread setting: select the opened device
+  // on this worker before anything else.
+  int s = afhip_open(g_ordinal);
+  if (s == AFHIP_OK) s = afhip_execution_checkpoint(j->ex, &mark);
+  if (s == AFHIP_OK) s = j->body(*j);
+  if (s != AFHIP_OK) {
+    j->message = afhip_last_error();
+    (void)afhip_synchronize(nullptr);  // nothing queued may still use what is released below
+  }
+  (void)afhip_execution_release_since(j->ex, mark);
+  (void)afhip_execution_note_submitted(j->ex);
+  j->status = s;
+  j->inputs.clear();
+}
+
+void job_complete(napi_env env, napi_status, void* data) {
+  OperatorJob* j = static_cast<OperatorJob*>(data);
+  if (j->status == AFHIP_OK) {
+    napi_value o, mem;
+    napi_create_object(env, &o);
+    napi_value arr = make_float32(env, j->output);
+    napi_set_named_property(env, o, "output", arr);
+    napi_set_named_property(env, o, "elapsedMilliseconds", make_number(env, j->ms));
+    napi_create_string_utf8(env, j->memory.c_str(), NAPI_AUTO_LENGTH, &mem);
+    napi_set_named_property(env, o, "memoryJson", mem);
+    napi_resolve_deferred(env, j->deferred, o);
+  } else {
+    napi_value msg, err;
+    napi_create_string_utf8(env, j->message.c_str(), NAPI_AUTO_LENGTH, &msg);
+    if (j->status == AFHIP_ERR_INVALID_ARGUMENT) napi_create_range_error(env, nullptr, msg, &err);
+    else napi_create_error(env, nullptr, msg, &err);
+    napi_reject_deferred(env, j->deferred, err);
+  }
+  napi_delete_async_work(env, j->work);
+  delete j;
+}
+
+std::mutex& execution_lock(uint32_t handle) {
+  static std::map<uint32_t, std::unique_ptr<std::mutex>> locks;
+  auto& m = locks[handle];
+  if (!m) m.reset(new std::mutex);
+  return *m;
+}
+
+// Copies the TypedArray argument into the job's inputs.
+bool job_input(napi_env env, napi_value v, OperatorJob& j, HostView* view = nullptr) {
+  HostView h;
+  if (!get_view(env, v, &h)) return false;
+  const char* p = static_cast<const char*>(h.data);
+  j.inputs.emplace_back(p, p + h.bytes);
+  if (view) *view = h;
+  return true;
+}
+
+napi_value queue_job(napi_env env, OperatorJob* j, uint32_t exh, const char* name) {
+  j->lock = &execution_lock(exh);
+  napi_value promise, resource;
+  napi_create_promise(env, &j->deferred, &promise);
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &resource);
+  napi_create_async_work(env, nullptr, resource, job_execute, job_complete, j, &j->work);
+  napi_queue_async_work(env, j->work);
+  return promise;
+}
+
+// triangleRun(execution, desc, z: Float32Array | Uint16Array (f16 bits),
+// mask: Float32Array, packed: Float32Array) -> Promise<{output,
+// elapsedMilliseconds, memoryJson}>
 napi_value TriangleRun(napi_env env, napi_callback_info info) {
   Args a;
-  if (!get_args(env, info, a, 4)) return nullptr;
-  afhip_triangle_desc d{};
+  if (!get_args(env, info, a, 5)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  if (!lookup_execution(env, a.argv[0], &exh, &e)) return nullptr;
+  std::unique_ptr<OperatorJob> j(new OperatorJob);
+  afhip_triangle_desc& d = j->tri;
   int64_t v;
   double eps;
-  napi_value o = a.argv[0];
+  napi_value o = a.argv[1];
   if (!prop_int(env, o, "length", 0, &v)) return nullptr;
   d.length = (int32_t)v;
   if (!prop_int(env, o, "cZ", 0, &v)) return nullptr;
@@ -1069,48 +1345,35 @@ napi_value TriangleRun(napi_env env, napi_callback_info info) {
   d.epsilon = (float)eps;
   d.out_dtype = AFHIP_F32;
   d.residual = 0;
-  HostView z, mask, packed;
-  if (!get_view(env, a.argv[1], &z) || !get_view(env, a.argv[2], &mask) || !get_view(env, a.argv[3], &packed))
+  HostView z, mask;
+  if (!job_input(env, a.argv[2], *j, &z) || !job_input(env, a.argv[3], *j, &mask) || !job_input(env, a.argv[4], *j))
     return nullptr;
   d.pair_dtype = z.type == napi_uint16_array ? AFHIP_F16 : AFHIP_F32;
-  size_t wbytes = 0, wsbytes = 0;
-  if (!check(env, afhip_triangle_weights_size(&d, &wbytes), "triangle") ||
-      !check(env, afhip_triangle_workspace_size(&d, &wsbytes), "triangle"))
-    return nullptr;
+  size_t bytes = 0;
+  if (!check(env, afhip_triangle_weights_size(&d, &bytes), "triangle")) return nullptr;
   const size_t pairs = (size_t)d.length * d.length;
-  const size_t zbytes = pairs * d.c_z * (d.pair_dtype == AFHIP_F16 ? 2 : 4);
-  if (z.bytes != zbytes || mask.bytes != pairs * 4) {
+  if (z.bytes != pairs * d.c_z * (d.pair_dtype == AFHIP_F16 ? 2 : 4) || mask.bytes != pairs * 4) {
     throw_js(env, {true, "z or mask does not match the descriptor's shape"});
     return nullptr;
   }
-  const double t0 = now_ms();
-  DeviceBuf dz, dm, dp, dw, dws, dout;
-  if (!check(env, dz.alloc(zbytes), "triangle") || !check(env, dm.alloc(mask.bytes), "triangle") ||
-      !check(env, dp.alloc(packed.bytes), "triangle") || !check(env, dw.alloc(wbytes), "triangle") ||
-      !check(env, dws.alloc(wsbytes), "triangle") || !check(env, dout.alloc(pairs * d.c_z * 4), "triangle"))
-    return nullptr;
-  if (!check(env, afhip_buffer_write(dz.p, 0, z.data, zbytes), "triangle") ||
-      !check(env, afhip_buffer_write(dm.p, 0, mask.data, mask.bytes), "triangle") ||
-      !check(env, afhip_buffer_write(dp.p, 0, packed.data, packed.bytes), "triangle") ||
-      !check(env, afhip_triangle_prepare_weights(&d, (const float*)dp.p, dw.p, nullptr), "triangle") ||
-      !check(env, afhip_triangle_run(&d, dz.p, (const float*)dm.p, dw.p, dout.p, dws.p, wsbytes, nullptr),
-             "triangle"))
-    return nullptr;
-  std::vector<float> out(pairs * d.c_z);
-  if (!check(env, afhip_buffer_read(dout.p, 0, out.data(), out.size() * 4), "triangle")) return nullptr;
-  const double ms = now_ms() - t0;
-  const size_t peak = zbytes + mask.bytes + packed.bytes + wbytes + wsbytes + out.size() * 4;
-  return result_object(env, out, ms, peak);
+  j->ex = e->ex;
+  j->body = triangle_body;
+  return queue_job(env, j.release(), exh, "afhip.triangle");
 }
 
-// opmRun(desc, activations: Float32Array, mask: Float32Array, packed: Float32Array)
+// opmRun(execution, desc, activations: Float32Array, mask: Float32Array,
+// packed: Float32Array) -> Promise<...>
 napi_value OpmRun(napi_env env, napi_callback_info info) {
   Args a;
-  if (!get_args(env, info, a, 4)) return nullptr;
-  afhip_opm_desc d{};
+  if (!get_args(env, info, a, 5)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  if (!lookup_execution(env, a.argv[0], &exh, &e)) return nullptr;
+  std::unique_ptr<OperatorJob> j(new OperatorJob);
+  afhip_opm_desc& d = j->opm;
   int64_t v;
   double e1, e2;
-  napi_value o = a.argv[0];
+  napi_value o = a.argv[1];
   if (!prop_int(env, o, "sequences", 0, &v)) return nullptr;
   d.sequences = (int32_t)v;
   if (!prop_int(env, o, "length", 0, &v)) return nullptr;
@@ -1131,46 +1394,34 @@ napi_value OpmRun(napi_env env, napi_callback_info info) {
   d.normalization_epsilon = (float)e2;
   d.msa_dtype = AFHIP_F32;
   d.out_dtype = AFHIP_F32;
-  HostView act, mask, packed;
-  if (!get_view(env, a.argv[1], &act) || !get_view(env, a.argv[2], &mask) || !get_view(env, a.argv[3], &packed))
+  HostView act, mask;
+  if (!job_input(env, a.argv[2], *j, &act) || !job_input(env, a.argv[3], *j, &mask) || !job_input(env, a.argv[4], *j))
     return nullptr;
-  size_t wbytes = 0, wsbytes = 0;
-  if (!check(env, afhip_opm_weights_size(&d, &wbytes), "outerProductMean") ||
-      !check(env, afhip_opm_workspace_size(&d, &wsbytes), "outerProductMean"))
-    return nullptr;
+  size_t bytes = 0;
+  if (!check(env, afhip_opm_weights_size(&d, &bytes), "outerProductMean")) return nullptr;
   const size_t rows = (size_t)d.sequences * d.length;
   if (act.bytes != rows * d.c_m * 4 || mask.bytes != rows * 4) {
     throw_js(env, {true, "activations or mask do not match the descriptor's shape"});
     return nullptr;
   }
-  const size_t obytes = (size_t)d.length * d.length * d.c_z * 4;
-  const double t0 = now_ms();
-  DeviceBuf da, dm, dp, dw, dws, dout;
-  if (!check(env, da.alloc(act.bytes), "outerProductMean") || !check(env, dm.alloc(mask.bytes), "outerProductMean") ||
-      !check(env, dp.alloc(packed.bytes), "outerProductMean") || !check(env, dw.alloc(wbytes), "outerProductMean") ||
-      !check(env, dws.alloc(wsbytes), "outerProductMean") || !check(env, dout.alloc(obytes), "outerProductMean"))
-    return nullptr;
-  if (!check(env, afhip_buffer_write(da.p, 0, act.data, act.bytes), "outerProductMean") ||
-      !check(env, afhip_buffer_write(dm.p, 0, mask.data, mask.bytes), "outerProductMean") ||
-      !check(env, afhip_buffer_write(dp.p, 0, packed.data, packed.bytes), "outerProductMean") ||
-      !check(env, afhip_opm_prepare_weights(&d, (const float*)dp.p, dw.p, nullptr), "outerProductMean") ||
-      !check(env, afhip_opm_run(&d, da.p, (const float*)dm.p, dw.p, dout.p, dws.p, wsbytes, nullptr),
-             "outerProductMean"))
-    return nullptr;
-  std::vector<float> out(obytes / 4);
-  if (!check(env, afhip_buffer_read(dout.p, 0, out.data(), obytes), "outerProductMean")) return nullptr;
-  const double ms = now_ms() - t0;
-  return result_object(env, out, ms, act.bytes + mask.bytes + packed.bytes + wbytes + wsbytes + obytes);
+  j->ex = e->ex;
+  j->body = opm_body;
+  return queue_job(env, j.release(), exh, "afhip.outerProductMean");
 }
 
-// transitionRun(desc, activations: Float32Array, packed: Float32Array)
+// transitionRun(execution, desc, activations: Float32Array, packed:
+// Float32Array) -> Promise<...>
 napi_value TransitionRun(napi_env env, napi_callback_info info) {
   Args a;
-  if (!get_args(env, info, a, 3)) return nullptr;
-  afhip_transition_desc d{};
+  if (!get_args(env, info, a, 4)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  if (!lookup_execution(env, a.argv[0], &exh, &e)) return nullptr;
+  std::unique_ptr<OperatorJob> j(new OperatorJob);
+  afhip_transition_desc& d = j->tra;
   int64_t v;
   double eps;
-  napi_value o = a.argv[0];
+  napi_value o = a.argv[1];
   if (!prop_int(env, o, "rows", 0, &v)) return nullptr;
   d.rows = v;
   if (!prop_int(env, o, "channels", 0, &v)) return nullptr;
@@ -1183,45 +1434,35 @@ napi_value TransitionRun(napi_env env, napi_callback_info info) {
   d.epsilon = (float)eps;
   d.in_dtype = AFHIP_F32;
   d.out_dtype = AFHIP_F32;
-  HostView act, packed;
-  if (!get_view(env, a.argv[1], &act) || !get_view(env, a.argv[2], &packed)) return nullptr;
-  size_t wbytes = 0, wsbytes = 0;
-  if (!check(env, afhip_transition_weights_size(&d, &wbytes), "transition") ||
-      !check(env, afhip_transition_workspace_size(&d, &wsbytes), "transition"))
-    return nullptr;
+  HostView act;
+  if (!job_input(env, a.argv[2], *j, &act) || !job_input(env, a.argv[3], *j)) return nullptr;
+  size_t bytes = 0;
+  if (!check(env, afhip_transition_weights_size(&d, &bytes), "transition")) return nullptr;
   if (act.bytes != (size_t)d.rows * d.channels * 4) {
     throw_js(env, {true, "activations do not match the descriptor's shape"});
     return nullptr;
   }
-  const double t0 = now_ms();
-  DeviceBuf da, dp, dw, dws, dout;
-  if (!check(env, da.alloc(act.bytes), "transition") || !check(env, dp.alloc(packed.bytes), "transition") ||
-      !check(env, dw.alloc(wbytes), "transition") || !check(env, dws.alloc(wsbytes), "transition") ||
-      !check(env, dout.alloc(act.bytes), "transition"))
-    return nullptr;
-  if (!check(env, afhip_buffer_write(da.p, 0, act.data, act.bytes), "transition") ||
-      !check(env, afhip_buffer_write(dp.p, 0, packed.data, packed.bytes), "transition") ||
-      !check(env, afhip_transition_prepare_weights(&d, (const float*)dp.p, dw.p, nullptr), "transition") ||
-      !check(env, afhip_transition_run(&d, da.p, dw.p, dout.p, dws.p, wsbytes, nullptr), "transition"))
-    return nullptr;
-  std::vector<float> out(act.bytes / 4);
-  if (!check(env, afhip_buffer_read(dout.p, 0, out.data(), act.bytes), "transition")) return nullptr;
-  const double ms = now_ms() - t0;
-  return result_object(env, out, ms, act.bytes * 2 + packed.bytes + wbytes + wsbytes);
+  j->ex = e->ex;
+  j->body = transition_body;
+  return queue_job(env, j.release(), exh, "afhip.transition");
 }
 
-// attentionRun(desc {batch, queries, channels, heads, transpose, pairBias
-// (0 none, 1 normalized-input, 2 separate), pairChannels, precision,
-// epsilon}, activations: Float32Array, mask: Float32Array, pairActivations:
-// Float32Array | null, packed: Float32Array) -- AttentionGpu.run
-// (src/evoformer/attention.ts:1334-1452) over host arrays.
+// attentionRun(execution, desc {batch, queries, channels, heads, transpose,
+// pairBias (0 none, 1 normalized-input, 2 separate), pairChannels,
+// precision, epsilon}, activations: Float32Array, mask: Float32Array,
+// pairActivations: Float32Array | null, packed: Float32Array) ->
+// Promise<...>: AttentionGpu.run (src/evoformer/attention.ts:1334-1452).
 napi_value AttentionRun(napi_env env, napi_callback_info info) {
   Args a;
-  if (!get_args(env, info, a, 5)) return nullptr;
-  afhip_attention_desc d{};
+  if (!get_args(env, info, a, 6)) return nullptr;
+  uint32_t exh;
+  ExecutionEntry* e;
+  if (!lookup_execution(env, a.argv[0], &exh, &e)) return nullptr;
+  std::unique_ptr<OperatorJob> j(new OperatorJob);
+  afhip_attention_desc& d = j->att;
   int64_t v[8];
   double eps;
-  napi_value o = a.argv[0];
+  napi_value o = a.argv[1];
   const char* keys[8] = {"batch", "queries", "channels", "heads", "transpose", "pairBias", "pairChannels",
                          "precision"};
   const int64_t defaults[8] = {0, 0, 0, 0, 0, AFHIP_PAIR_BIAS_NONE, 0, AFHIP_PRECISION_F32};
@@ -1230,17 +1471,15 @@ napi_value AttentionRun(napi_env env, napi_callback_info info) {
   if (!prop_double(env, o, "epsilon", 1e-5, &eps)) return nullptr;
   d = {(int32_t)v[0], (int32_t)v[1], (int32_t)v[2], (int32_t)v[3], (int32_t)v[4], (int32_t)v[5], (int32_t)v[6],
        (int32_t)v[7], AFHIP_F32, AFHIP_F32, 0, (float)eps};
-  HostView act, mask, pair, packed;
   napi_valuetype pt;
-  napi_typeof(env, a.argv[3], &pt);
+  napi_typeof(env, a.argv[4], &pt);
   const bool has_pair = pt != napi_undefined && pt != napi_null;
-  if (!get_view(env, a.argv[1], &act) || !get_view(env, a.argv[2], &mask) ||
-      (has_pair && !get_view(env, a.argv[3], &pair)) || !get_view(env, a.argv[4], &packed))
+  HostView act, mask, pair;
+  if (!job_input(env, a.argv[2], *j, &act) || !job_input(env, a.argv[3], *j, &mask) || !job_input(env, a.argv[5], *j) ||
+      (has_pair && !job_input(env, a.argv[4], *j, &pair)))
     return nullptr;
-  size_t wbytes = 0, wsbytes = 0;
-  if (!check(env, afhip_attention_weights_size(&d, &wbytes), "attention") ||
-      !check(env, afhip_attention_workspace_size(&d, &wsbytes), "attention"))
-    return nullptr;
+  size_t bytes = 0;
+  if (!check(env, afhip_attention_weights_size(&d, &bytes), "attention")) return nullptr;
   const size_t rows = (size_t)d.batch * d.queries;
   if (act.bytes != rows * d.channels * 4 || mask.bytes != rows * 4) {
     throw_js(env, {true, "activations or mask do not match the descriptor's shape"});
@@ -1251,26 +1490,9 @@ napi_value AttentionRun(napi_env env, napi_callback_info info) {
     throw_js(env, {true, "a separate pair bias needs pair activations [queries][queries][pairChannels]"});
     return nullptr;
   }
-  const double t0 = now_ms();
-  DeviceBuf da, dm, dpair, dp, dw, dws, dout;
-  if (!check(env, da.alloc(act.bytes), "attention") || !check(env, dm.alloc(mask.bytes), "attention") ||
-      !check(env, dp.alloc(packed.bytes), "attention") || !check(env, dw.alloc(wbytes), "attention") ||
-      !check(env, dws.alloc(wsbytes), "attention") || !check(env, dout.alloc(act.bytes), "attention") ||
-      (has_pair && !check(env, dpair.alloc(pair.bytes), "attention")))
-    return nullptr;
-  if (!check(env, afhip_buffer_write(da.p, 0, act.data, act.bytes), "attention") ||
-      !check(env, afhip_buffer_write(dm.p, 0, mask.data, mask.bytes), "attention") ||
-      (has_pair && !check(env, afhip_buffer_write(dpair.p, 0, pair.data, pair.bytes), "attention")) ||
-      !check(env, afhip_buffer_write(dp.p, 0, packed.data, packed.bytes), "attention") ||
-      !check(env, afhip_attention_prepare_weights(&d, (const float*)dp.p, dw.p, nullptr), "attention") ||
-      !check(env, afhip_attention_run(&d, da.p, (const float*)dm.p, has_pair ? dpair.p : nullptr, dw.p, dout.p,
-                                      dws.p, wsbytes, nullptr),
-             "attention"))
-    return nullptr;
-  std::vector<float> out(act.bytes / 4);
-  if (!check(env, afhip_buffer_read(dout.p, 0, out.data(), act.bytes), "attention")) return nullptr;
-  const double ms = now_ms() - t0;
-  return result_object(env, out, ms, act.bytes * 2 + mask.bytes + pair.bytes + packed.bytes + wbytes + wsbytes);
+  j->ex = e->ex;
+  j->body = attention_body;
+  return queue_job(env, j.release(), exh, "afhip.attention");
 }
 
 // ---------------------------------------------------------------------------

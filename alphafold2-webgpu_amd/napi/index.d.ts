@@ -1,59 +1,92 @@
 // Types of the afhip Node-API shim (index.js), matching the reference's
 // operator signatures so TypeScript callers swap the class and nothing else:
-// src/triangle/webgpu.ts:9-23, src/triangle/types.ts:9-52,
-// src/evoformer/outer-product-mean.ts:21-40, src/evoformer/transition.ts:18-31.
+// src/triangle/webgpu.ts:9-23, :42-214, src/triangle/types.ts:1-40,
+// src/evoformer/outer-product-mean.ts:21-40, src/evoformer/transition.ts:18-31,
+// src/runtime/allocator.ts:8-29.
 
-export interface MemorySnapshot {
-  peakBytes: number;
+/** One label's share of the live working set (allocator.ts:8-12). */
+export interface AllocationShare {
+  readonly label: string;
+  readonly bytes: number;
+  readonly count: number;
 }
 
+/** AllocationSnapshot (src/runtime/allocator.ts:14-29). */
+export interface AllocationSnapshot {
+  readonly currentBytes: number;
+  readonly peakBytes: number;
+  readonly peakComposition: readonly AllocationShare[];
+  readonly residentBytes: number;
+  readonly peakResidentBytes: number;
+  readonly pooledBytes: number;
+  readonly allocationCount: number;
+  readonly bufferCount: number;
+}
+
+/** TriangleGpuResult, OuterProductMeanResult, TransitionResult, AttentionResult. */
 export interface OperatorResult {
-  output: Float32Array;
-  elapsedMilliseconds: number;
-  memory: MemorySnapshot;
+  readonly output: Float32Array;
+  readonly elapsedMilliseconds: number;
+  readonly memory: AllocationSnapshot;
 }
 
 export type Precision = "f32" | "f16";
 
+/** TriangleShape (src/triangle/types.ts:3-7). */
+export interface TriangleShape {
+  readonly length: number;
+  readonly cZ: number;
+  readonly cHidden: number;
+}
+
 export interface TriangleMultiplicationWeights {
-  layerNormInWeight: Float32Array;
-  layerNormInBias: Float32Array;
-  linearAPWeight: Float32Array;
-  linearAPBias: Float32Array;
-  linearAGWeight: Float32Array;
-  linearAGBias: Float32Array;
-  linearBPWeight: Float32Array;
-  linearBPBias: Float32Array;
-  linearBGWeight: Float32Array;
-  linearBGBias: Float32Array;
-  layerNormOutWeight: Float32Array;
-  layerNormOutBias: Float32Array;
-  linearZWeight: Float32Array;
-  linearZBias: Float32Array;
-  linearGWeight: Float32Array;
-  linearGBias: Float32Array;
+  readonly layerNormInWeight: Float32Array;
+  readonly layerNormInBias: Float32Array;
+  readonly linearAPWeight: Float32Array;
+  readonly linearAPBias: Float32Array;
+  readonly linearAGWeight: Float32Array;
+  readonly linearAGBias: Float32Array;
+  readonly linearBPWeight: Float32Array;
+  readonly linearBPBias: Float32Array;
+  readonly linearBGWeight: Float32Array;
+  readonly linearBGBias: Float32Array;
+  readonly layerNormOutWeight: Float32Array;
+  readonly layerNormOutBias: Float32Array;
+  readonly linearZWeight: Float32Array;
+  readonly linearZBias: Float32Array;
+  readonly linearGWeight: Float32Array;
+  readonly linearGBias: Float32Array;
 }
 
+/** TriangleMultiplicationInput (src/triangle/types.ts:28-34); z may also be
+ * f16 bit patterns in a Uint16Array (an addition). */
 export interface TriangleMultiplicationInput {
-  shape: readonly [length: number, cZ: number, cHidden: number];
-  /** [L][L][cZ] f32, or f16 bit patterns as a Uint16Array */
-  z: Float32Array | Uint16Array;
-  mask: Float32Array;
-  weights: TriangleMultiplicationWeights;
-  epsilon?: number;
+  readonly shape: TriangleShape;
+  readonly z: Float32Array | Uint16Array;
+  readonly mask: Float32Array;
+  readonly weights: TriangleMultiplicationWeights;
+  readonly epsilon?: number;
 }
 
+/** TriangleGpuOptions (src/triangle/webgpu.ts:9-16). */
 export interface TriangleGpuOptions {
-  precision?: Precision;
-  blockRows?: number;
+  readonly precision?: Precision;
+  readonly blockRows?: number;
 }
 
-export declare class TriangleMultiplicationOutgoingGpu {
-  run(input: TriangleMultiplicationInput, options?: TriangleGpuOptions): OperatorResult;
+/** Every operator owns its allocator; release() frees its pooled buffers. */
+declare class HipOperator {
+  release(): void;
 }
 
-export declare class TriangleMultiplicationIncomingGpu {
-  run(input: TriangleMultiplicationInput, options?: TriangleGpuOptions): OperatorResult;
+export declare class TriangleMultiplicationOutgoingGpu extends HipOperator {
+  constructor(device?: unknown);
+  run(input: TriangleMultiplicationInput, options?: TriangleGpuOptions): Promise<OperatorResult>;
+}
+
+export declare class TriangleMultiplicationIncomingGpu extends HipOperator {
+  constructor(device?: unknown);
+  run(input: TriangleMultiplicationInput, options?: TriangleGpuOptions): Promise<OperatorResult>;
 }
 
 export interface OuterProductMeanWeights {
@@ -67,17 +100,29 @@ export interface OuterProductMeanWeights {
   outputBias: Float32Array;
 }
 
+/** OuterProductMeanInput (src/evoformer/outer-product-mean.ts:21-34). */
 export interface OuterProductMeanInput {
-  shape: readonly [sequences: number, length: number, cM: number, cOuter: number, cZ: number];
-  activations: Float32Array;
-  mask: Float32Array;
-  weights: OuterProductMeanWeights;
-  layerNormEpsilon?: number;
-  normalizationEpsilon?: number;
+  readonly activations: Float32Array;
+  readonly mask: Float32Array;
+  readonly sequences: number;
+  readonly length: number;
+  readonly cM: number;
+  readonly cOuter: number;
+  readonly cZ: number;
+  readonly weights: OuterProductMeanWeights;
+  readonly layerNormEpsilon?: number;
+  readonly normalizationEpsilon?: number;
+  readonly rowBlockResidues?: number;
 }
 
-export declare class OuterProductMeanGpu {
-  run(input: OuterProductMeanInput, options?: { precision?: Precision; rowBlockResidues?: number }): OperatorResult;
+/** Additions: the arithmetic precision, from the constructor or a run. */
+export interface HipOperatorOptions {
+  readonly precision?: Precision;
+}
+
+export declare class OuterProductMeanGpu extends HipOperator {
+  constructor(device?: unknown, options?: HipOperatorOptions);
+  run(input: OuterProductMeanInput, options?: HipOperatorOptions): Promise<OperatorResult>;
 }
 
 export interface TransitionWeights {
@@ -89,15 +134,19 @@ export interface TransitionWeights {
   secondBias: Float32Array;
 }
 
+/** TransitionInput (src/evoformer/transition.ts:18-25). */
 export interface TransitionInput {
-  shape: readonly [rows: number, channels: number, hidden: number];
-  activations: Float32Array;
-  weights: TransitionWeights;
-  epsilon?: number;
+  readonly activations: Float32Array;
+  readonly rows: number;
+  readonly channels: number;
+  readonly hiddenChannels: number;
+  readonly weights: TransitionWeights;
+  readonly epsilon?: number;
 }
 
-export declare class TransitionGpu {
-  run(input: TransitionInput, options?: { precision?: Precision }): OperatorResult;
+export declare class TransitionGpu extends HipOperator {
+  constructor(device?: unknown, options?: HipOperatorOptions);
+  run(input: TransitionInput, options?: HipOperatorOptions): Promise<OperatorResult>;
 }
 
 /** Shape of the chained pair steps (include/afhip.h afhip_pair_stack_desc). */
@@ -171,8 +220,9 @@ export interface AttentionInput {
 }
 
 /** AttentionGpu (src/evoformer/attention.ts:1321-1452). */
-export declare class AttentionGpu {
-  run(input: AttentionInput, options?: { precision?: Precision }): OperatorResult;
+export declare class AttentionGpu extends HipOperator {
+  constructor(device?: unknown, options?: HipOperatorOptions);
+  run(input: AttentionInput, options?: HipOperatorOptions): Promise<OperatorResult>;
 }
 
 export declare function packAttentionWeights(weights: AttentionWeights, pairBias?: AttentionPairBias): Float32Array;
@@ -261,6 +311,10 @@ export interface GemmDesc {
   batchStrideA?: number;
   batchStrideW?: number;
   batchStrideC?: number;
+  /** 0: A[m][k] (sourceContiguous "k"); 1: A stored [k][m] (sourceContiguous "row", gemm.ts:308-360). */
+  aLayout?: 0 | 1;
+  /** 0: C[m][n]; 1: C stored [n][m] (a column-major matrixEpilogue, gemm.ts:268-285). */
+  cLayout?: 0 | 1;
 }
 
 /** GemmVariant (src/runtime/gemm.ts:150-206) as the library reports it. */
@@ -296,4 +350,8 @@ export declare const TRIANGLE_ORDER: readonly string[];
 export declare const DTYPE: { f32: 0; f16: 1; i8: 2 };
 export declare const PRECISION: { f32: 0; f16: 1 };
 export declare const KERNEL: { register: 0; lds_dma: 1; stream: 2 };
+export declare const SOURCE: { k: 0; row: 1 };
+export declare const OUTPUT: { row: 0; column: 1 };
+export declare function validateOuterProductMeanInput(input: OuterProductMeanInput): void;
+export declare function validateTransitionInput(input: TransitionInput): void;
 export declare const EPILOGUE: { scale: 1; bias: 2; attention: 4; relu: 8; residual: 16 };

@@ -13,8 +13,11 @@
 //   gemmGrid, the GEMM variant selection and its persisted calibration
 //     src/runtime/gemm.ts:213-228, :368-379; src/runtime/gemm-selection.ts:122-125, :560-660
 //
-// Inputs are the reference's (Float32Array tensors, weights by name, shape
-// tuples); results are {output: Float32Array, elapsedMilliseconds, memory}.
+// Inputs are the reference's own objects (TriangleMultiplicationInput with
+// its TriangleShape {length, cZ, cHidden}, OuterProductMeanInput and
+// TransitionInput with their flat dimension fields, AttentionInput); run()
+// returns a Promise of {output: Float32Array, elapsedMilliseconds, memory},
+// memory being the operator allocator's AllocationSnapshot.
 // The loader follows src/runtime/wgpu/backend.ts:80-99: require the addon
 // lazily and say how to build it when it is missing.
 //
@@ -40,6 +43,8 @@ function addon() {
 var F32 = 0, F16 = 1, I8 = 2;
 var PRECISION = { f32: 0, f16: 1 };
 var KERNEL = { register: 0, lds_dma: 1, stream: 2 };
+var SOURCE = { k: 0, row: 1 };
+var OUTPUT = { row: 0, column: 1 };
 var EPILOGUE = { scale: 1, bias: 2, attention: 4, relu: 8, residual: 16 };
 
 var opened = false;
@@ -83,18 +88,23 @@ function triangleWeightSizes(cZ, cHidden) {
   };
 }
 
-// validateTriangleInput (src/triangle/types.ts:54-89).
+// validateTriangleInput (src/triangle/types.ts:54-89): the reference's
+// TriangleShape {length, cZ, cHidden} and its checks and messages.
 function validateTriangleInput(input) {
-  var shape = input.shape;
-  positiveInteger("length", shape[0]);
-  positiveInteger("cZ", shape[1]);
-  positiveInteger("cHidden", shape[2]);
-  var pairs = shape[0] * shape[0];
-  expectLength("z", input.z, pairs * shape[1]);
+  var shape = input.shape || {};
+  var length = shape.length, cZ = shape.cZ, cHidden = shape.cHidden;
+  positiveInteger("length", length);
+  positiveInteger("cZ", cZ);
+  positiveInteger("cHidden", cHidden);
+  var pairs = length * length;
+  if (!Number.isSafeInteger(pairs * Math.max(cZ, cHidden))) {
+    throw new RangeError("tensor dimensions exceed JavaScript's safe integer range");
+  }
+  expectLength("z", input.z, pairs * cZ);
   expectLength("mask", input.mask, pairs);
-  var sizes = triangleWeightSizes(shape[1], shape[2]);
+  var sizes = triangleWeightSizes(cZ, cHidden);
   TRIANGLE_ORDER.forEach(function (name) { expectLength(name, input.weights[name], sizes[name]); });
-  if (input.epsilon !== undefined && !(input.epsilon > 0 && isFinite(input.epsilon))) {
+  if (input.epsilon !== undefined && (!(input.epsilon > 0) || !isFinite(input.epsilon))) {
     throw new RangeError("epsilon must be finite and positive; received " + input.epsilon);
   }
 }
@@ -109,32 +119,6 @@ function packTriangleWeights(weights) {
   return out;
 }
 
-function TriangleMultiplicationGpu(direction) {
-  this.direction = direction;
-}
-TriangleMultiplicationGpu.prototype.run = function (input, options) {
-  options = options || {};
-  validateTriangleInput(input);
-  var precision = options.precision === undefined ? "f32" : options.precision;
-  if (!(precision in PRECISION)) throw new RangeError("unknown precision " + precision);
-  requestHipDevice();
-  return addon().triangleRun({
-    length: input.shape[0], cZ: input.shape[1], cHidden: input.shape[2],
-    direction: this.direction === "incoming" ? 1 : 0,
-    precision: PRECISION[precision],
-    blockRows: options.blockRows === undefined ? 0 : options.blockRows,
-    epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
-  }, input.z, input.mask, packTriangleWeights(input.weights));
-};
-
-function TriangleMultiplicationOutgoingGpu() { TriangleMultiplicationGpu.call(this, "outgoing"); }
-TriangleMultiplicationOutgoingGpu.prototype = Object.create(TriangleMultiplicationGpu.prototype);
-function TriangleMultiplicationIncomingGpu() { TriangleMultiplicationGpu.call(this, "incoming"); }
-TriangleMultiplicationIncomingGpu.prototype = Object.create(TriangleMultiplicationGpu.prototype);
-
-var OPM_ORDER = ["layerNormScale", "layerNormOffset", "leftWeight", "leftBias", "rightWeight", "rightBias",
-  "outputWeight", "outputBias"];
-
 function packOrdered(weights, order) {
   var total = 0;
   order.forEach(function (n) { total += weights[n].length; });
@@ -144,44 +128,155 @@ function packOrdered(weights, order) {
   return out;
 }
 
-// OuterProductMeanGpu.run (src/evoformer/outer-product-mean.ts:549-646).
-// input: {shape: [sequences, length, cM, cOuter, cZ], activations, mask, weights}
-function OuterProductMeanGpu() {}
+function precisionOf(options, fallback) {
+  var precision = options && options.precision !== undefined ? options.precision : fallback;
+  if (!(precision in PRECISION)) throw new RangeError("unknown precision " + precision);
+  return precision;
+}
+
+// Every operator object owns one execution: its allocator
+// (GpuBufferAllocator, src/runtime/allocator.ts:168-388, one per operator as
+// the reference's constructors make one) pools device buffers across runs,
+// and `memory` in a result is that allocator's AllocationSnapshot
+// (allocator.ts:8-29), taken while the run's tensors are still live.
+function Operator(device, options) {
+  this.device = device;
+  this.options = options || {};
+}
+Operator.prototype._execution = function () {
+  if (this._handle === undefined) {
+    requestHipDevice();
+    this._handle = addon().executionCreate(0);
+  }
+  return this._handle;
+};
+// Starts fn, which validates, copies the host arrays and queues the device
+// work (runs of one operator take its execution's lock in turn on the
+// worker threads). A synchronous throw in fn (validation) rejects the
+// promise, as a throw inside the reference's async run() does.
+Operator.prototype._queue = function (fn) {
+  var started;
+  try {
+    started = fn();
+  } catch (err) {
+    return Promise.reject(err);
+  }
+  return started.then(function (r) {
+    return { output: r.output, elapsedMilliseconds: r.elapsedMilliseconds, memory: JSON.parse(r.memoryJson) };
+  });
+};
+// Frees the operator's pooled device memory (the allocator's destroy).
+Operator.prototype.release = function () {
+  if (this._handle !== undefined) {
+    addon().executionDestroy(this._handle);
+    this._handle = undefined;
+  }
+};
+
+// TriangleMultiplication{Outgoing,Incoming}Gpu (src/triangle/webgpu.ts:42-214).
+// run(input: TriangleMultiplicationInput, {precision, blockRows}) ->
+// Promise<{output, elapsedMilliseconds, memory}>.
+function TriangleMultiplicationGpu(device, direction) {
+  Operator.call(this, device);
+  this.direction = direction;
+}
+TriangleMultiplicationGpu.prototype = Object.create(Operator.prototype);
+TriangleMultiplicationGpu.prototype.run = function (input, options) {
+  var self = this;
+  return this._queue(function () {
+    options = options || {};
+    validateTriangleInput(input);
+    var precision = precisionOf(options, "f32");
+    if (options.blockRows !== undefined) positiveInteger("blockRows", options.blockRows);
+    return addon().triangleRun(self._execution(), {
+      length: input.shape.length, cZ: input.shape.cZ, cHidden: input.shape.cHidden,
+      direction: self.direction === "incoming" ? 1 : 0,
+      precision: PRECISION[precision],
+      blockRows: options.blockRows === undefined ? 0 : options.blockRows,
+      epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
+    }, input.z, input.mask, packTriangleWeights(input.weights));
+  });
+};
+
+function TriangleMultiplicationOutgoingGpu(device) { TriangleMultiplicationGpu.call(this, device, "outgoing"); }
+TriangleMultiplicationOutgoingGpu.prototype = Object.create(TriangleMultiplicationGpu.prototype);
+function TriangleMultiplicationIncomingGpu(device) { TriangleMultiplicationGpu.call(this, device, "incoming"); }
+TriangleMultiplicationIncomingGpu.prototype = Object.create(TriangleMultiplicationGpu.prototype);
+
+var OPM_ORDER = ["layerNormScale", "layerNormOffset", "leftWeight", "leftBias", "rightWeight", "rightBias",
+  "outputWeight", "outputBias"];
+
+// validate (src/evoformer/outer-product-mean.ts:45-64).
+function validateOuterProductMeanInput(input) {
+  var dims = [input.sequences, input.length, input.cM, input.cOuter, input.cZ];
+  if (!dims.every(function (v) { return Number.isSafeInteger(v) && v > 0; })) {
+    throw new RangeError("outer product mean dimensions must be positive safe integers");
+  }
+  var w = input.weights;
+  var S = input.sequences, L = input.length, cM = input.cM, co = input.cOuter, cZ = input.cZ;
+  [["activations", input.activations, S * L * cM], ["mask", input.mask, S * L],
+    ["layerNormScale", w.layerNormScale, cM], ["layerNormOffset", w.layerNormOffset, cM],
+    ["leftWeight", w.leftWeight, cM * co], ["leftBias", w.leftBias, co],
+    ["rightWeight", w.rightWeight, cM * co], ["rightBias", w.rightBias, co],
+    ["outputWeight", w.outputWeight, co * co * cZ], ["outputBias", w.outputBias, cZ]].forEach(function (e) {
+    expectLength(e[0], e[1], e[2]);
+  });
+  if (input.rowBlockResidues !== undefined) positiveInteger("rowBlockResidues", input.rowBlockResidues);
+}
+
+// OuterProductMeanGpu (src/evoformer/outer-product-mean.ts:538-646).
+// run(input: OuterProductMeanInput) with the reference's flat fields
+// (sequences, length, cM, cOuter, cZ, rowBlockResidues, layerNormEpsilon,
+// normalizationEpsilon; :21-34). Precision: options.precision of the
+// constructor or of run (an addition; "f32" by default).
+function OuterProductMeanGpu(device, options) { Operator.call(this, device, options); }
+OuterProductMeanGpu.prototype = Object.create(Operator.prototype);
 OuterProductMeanGpu.prototype.run = function (input, options) {
-  options = options || {};
-  var s = input.shape;
-  s.forEach(function (v, i) { positiveInteger(["sequences", "length", "cM", "cOuter", "cZ"][i], v); });
-  expectLength("activations", input.activations, s[0] * s[1] * s[2]);
-  expectLength("mask", input.mask, s[0] * s[1]);
-  var precision = options.precision === undefined ? "f32" : options.precision;
-  requestHipDevice();
-  return addon().opmRun({
-    sequences: s[0], length: s[1], cM: s[2], cOuter: s[3], cZ: s[4], precision: PRECISION[precision],
-    rowBlockResidues: options.rowBlockResidues === undefined ? 0 : options.rowBlockResidues,
-    layerNormEpsilon: input.layerNormEpsilon === undefined ? 1e-5 : input.layerNormEpsilon,
-    normalizationEpsilon: input.normalizationEpsilon === undefined ? 1e-3 : input.normalizationEpsilon,
-  }, input.activations, input.mask, packOrdered(input.weights, OPM_ORDER));
+  var self = this;
+  return this._queue(function () {
+    validateOuterProductMeanInput(input);
+    var precision = precisionOf(options, precisionOf(self.options, "f32"));
+    return addon().opmRun(self._execution(), {
+      sequences: input.sequences, length: input.length, cM: input.cM, cOuter: input.cOuter, cZ: input.cZ,
+      precision: PRECISION[precision],
+      rowBlockResidues: input.rowBlockResidues === undefined ? 0 : input.rowBlockResidues,
+      layerNormEpsilon: input.layerNormEpsilon === undefined ? 1e-5 : input.layerNormEpsilon,
+      normalizationEpsilon: input.normalizationEpsilon === undefined ? 1e-3 : input.normalizationEpsilon,
+    }, input.activations, input.mask, packOrdered(input.weights, OPM_ORDER));
+  });
 };
 
 var TRANSITION_ORDER = ["layerNormScale", "layerNormOffset", "firstWeight", "firstBias", "secondWeight",
   "secondBias"];
 
-// TransitionGpu.run (src/evoformer/transition.ts:264-361).
-// input: {shape: [rows, channels, hidden], activations, weights}
-function TransitionGpu() {}
+// validate (src/evoformer/transition.ts:140-157).
+function validateTransitionInput(input) {
+  var rows = input.rows, channels = input.channels, hidden = input.hiddenChannels;
+  if (![rows, channels, hidden].every(function (v) { return Number.isSafeInteger(v) && v > 0; })) {
+    throw new RangeError("transition dimensions must be positive safe integers");
+  }
+  var w = input.weights;
+  [["activations", input.activations, rows * channels], ["layerNormScale", w.layerNormScale, channels],
+    ["layerNormOffset", w.layerNormOffset, channels], ["firstWeight", w.firstWeight, channels * hidden],
+    ["firstBias", w.firstBias, hidden], ["secondWeight", w.secondWeight, hidden * channels],
+    ["secondBias", w.secondBias, channels]].forEach(function (e) { expectLength(e[0], e[1], e[2]); });
+}
+
+// TransitionGpu (src/evoformer/transition.ts:247-361). run(input:
+// TransitionInput) with {rows, channels, hiddenChannels, epsilon}
+// (:18-25).
+function TransitionGpu(device, options) { Operator.call(this, device, options); }
+TransitionGpu.prototype = Object.create(Operator.prototype);
 TransitionGpu.prototype.run = function (input, options) {
-  options = options || {};
-  var s = input.shape;
-  positiveInteger("rows", s[0]);
-  positiveInteger("channels", s[1]);
-  positiveInteger("hidden", s[2]);
-  expectLength("activations", input.activations, s[0] * s[1]);
-  var precision = options.precision === undefined ? "f32" : options.precision;
-  requestHipDevice();
-  return addon().transitionRun({
-    rows: s[0], channels: s[1], hidden: s[2], precision: PRECISION[precision],
-    epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
-  }, input.activations, packOrdered(input.weights, TRANSITION_ORDER));
+  var self = this;
+  return this._queue(function () {
+    validateTransitionInput(input);
+    var precision = precisionOf(options, precisionOf(self.options, "f32"));
+    return addon().transitionRun(self._execution(), {
+      rows: input.rows, channels: input.channels, hidden: input.hiddenChannels, precision: PRECISION[precision],
+      epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
+    }, input.activations, packOrdered(input.weights, TRANSITION_ORDER));
+  });
 };
 
 var ATTENTION_ORDER = ["queryNormScale", "queryNormOffset", "queryWeight", "keyWeight", "valueWeight",
@@ -212,45 +307,47 @@ function expectCount(name, value, size) {
   if (value.length !== size) throw new RangeError(name + " has " + value.length + " values; expected " + size);
 }
 
-// AttentionGpu.run (src/evoformer/attention.ts:1334-1452), with validate's
-// checks and messages (:102-141). input: the reference's AttentionInput.
-function AttentionGpu() {}
+// AttentionGpu (src/evoformer/attention.ts:1321-1452), with validate's
+// checks and messages (:102-141). run(input: AttentionInput).
+function AttentionGpu(device, options) { Operator.call(this, device, options); }
+AttentionGpu.prototype = Object.create(Operator.prototype);
 AttentionGpu.prototype.run = function (input, options) {
-  options = options || {};
-  var b = input.batch, q = input.queryLength, c = input.channels, h = input.heads;
-  [b, q, c, h].forEach(function (v) {
-    if (!Number.isSafeInteger(v) || v <= 0) throw new RangeError("attention dimensions must be positive safe integers");
+  var self = this;
+  return this._queue(function () {
+    var b = input.batch, q = input.queryLength, c = input.channels, h = input.heads;
+    [b, q, c, h].forEach(function (v) {
+      if (!Number.isSafeInteger(v) || v <= 0) throw new RangeError("attention dimensions must be positive safe integers");
+    });
+    if (c % h !== 0 || c / h > 32) {
+      throw new RangeError("the fused WebGPU attention path requires an integral head dimension no larger than 32");
+    }
+    var w = input.weights;
+    expectCount("activations", input.activations, b * q * c);
+    expectCount("mask", input.mask, b * q);
+    expectCount("queryNormScale", w.queryNormScale, c);
+    expectCount("queryNormOffset", w.queryNormOffset, c);
+    ["queryWeight", "keyWeight", "valueWeight", "gatingWeight"].forEach(function (n) { expectCount(n, w[n], c * c); });
+    expectCount("gatingBias", w.gatingBias, c);
+    expectCount("outputWeight", w.outputWeight, c * c);
+    expectCount("outputBias", w.outputBias, c);
+    var pair = input.pairBias;
+    var pairChannels = 0;
+    if (pair !== undefined && pair !== null && pair.source === "separate") {
+      pairChannels = pair.channels;
+      expectCount("pair activations", pair.activations, q * q * pairChannels);
+      expectCount("pair norm scale", pair.layerNormScale, pairChannels);
+      expectCount("pair norm offset", pair.layerNormOffset, pairChannels);
+      expectCount("pair projection", pair.projectionWeight, pairChannels * h);
+    } else if (pair !== undefined && pair !== null && pair.projectionWeight.length !== c * h) {
+      throw new RangeError("normalized-input pair projection has an invalid size");
+    }
+    var precision = precisionOf(options, precisionOf(self.options, "f32"));
+    return addon().attentionRun(self._execution(), {
+      batch: b, queries: q, channels: c, heads: h, transpose: input.transpose === true ? 1 : 0,
+      pairBias: pair === undefined || pair === null ? 0 : PAIR_BIAS[pair.source], pairChannels: pairChannels,
+      precision: PRECISION[precision], epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
+    }, input.activations, input.mask, pairChannels > 0 ? pair.activations : null, packAttentionWeights(w, pair));
   });
-  if (c % h !== 0 || c / h > 32) {
-    throw new RangeError("the fused WebGPU attention path requires an integral head dimension no larger than 32");
-  }
-  var w = input.weights;
-  expectCount("activations", input.activations, b * q * c);
-  expectCount("mask", input.mask, b * q);
-  expectCount("queryNormScale", w.queryNormScale, c);
-  expectCount("queryNormOffset", w.queryNormOffset, c);
-  ["queryWeight", "keyWeight", "valueWeight", "gatingWeight"].forEach(function (n) { expectCount(n, w[n], c * c); });
-  expectCount("gatingBias", w.gatingBias, c);
-  expectCount("outputWeight", w.outputWeight, c * c);
-  expectCount("outputBias", w.outputBias, c);
-  var pair = input.pairBias;
-  var pairChannels = 0;
-  if (pair !== undefined && pair !== null && pair.source === "separate") {
-    pairChannels = pair.channels;
-    expectCount("pair activations", pair.activations, q * q * pairChannels);
-    expectCount("pair norm scale", pair.layerNormScale, pairChannels);
-    expectCount("pair norm offset", pair.layerNormOffset, pairChannels);
-    expectCount("pair projection", pair.projectionWeight, pairChannels * h);
-  } else if (pair !== undefined && pair !== null && pair.projectionWeight.length !== c * h) {
-    throw new RangeError("normalized-input pair projection has an invalid size");
-  }
-  var precision = options.precision === undefined ? "f32" : options.precision;
-  requestHipDevice();
-  return addon().attentionRun({
-    batch: b, queries: q, channels: c, heads: h, transpose: input.transpose === true ? 1 : 0,
-    pairBias: pair === undefined || pair === null ? 0 : PAIR_BIAS[pair.source], pairChannels: pairChannels,
-    precision: PRECISION[precision], epsilon: input.epsilon === undefined ? 1e-5 : input.epsilon,
-  }, input.activations, input.mask, pairChannels > 0 ? pair.activations : null, packAttentionWeights(w, pair));
 };
 
 // gemmGrid (src/runtime/gemm.ts:368-379).
@@ -380,6 +477,8 @@ module.exports = {
   AttentionGpu: AttentionGpu,
   packAttentionWeights: packAttentionWeights,
   validateTriangleInput: validateTriangleInput,
+  validateOuterProductMeanInput: validateOuterProductMeanInput,
+  validateTransitionInput: validateTransitionInput,
   packTriangleWeights: packTriangleWeights,
   errorMetrics: errorMetrics,
   gemmGrid: gemmGrid,
@@ -397,5 +496,7 @@ module.exports = {
   DTYPE: { f32: F32, f16: F16, i8: I8 },
   PRECISION: PRECISION,
   KERNEL: KERNEL,
+  SOURCE: SOURCE,
+  OUTPUT: OUTPUT,
   EPILOGUE: EPILOGUE,
 };

@@ -11,8 +11,9 @@ openfold-triangle-small: OpenFold deterministic test weights (Apache-2.0).
 short-9: activations and parameters of AlphaFold model_3_ptm, block 0; the
 AlphaFold parameters are DeepMind's, under CC BY 4.0
 (https://github.com/google-deepmind/alphafold/blob/main/WEIGHTS_LICENSE).
-The two 59-residue fixtures (3.9 MB each) are not copied; the CPU tests read
-them in place when the reference checkout is present.
+model1-reference-59 (single sequence and a3m): AlphaFold model_1 block-0
+captures at 59 residues, same licence; 3.9 MB each, copied so the GPU tests
+can run them (test/triangle-multiplication-outgoing.gpu.test.ts:30-56).
 """
 import os
 import shutil
@@ -21,6 +22,8 @@ import sys
 FIXTURES = {
     "openfold-triangle-small": "test/fixtures/openfold-triangle-small",
     "alphafold-short-9": "test/fixtures/alphafold-single-sequence/short-9",
+    "alphafold-single-sequence-59": "test/fixtures/alphafold-single-sequence/model1-reference-59",
+    "alphafold-a3m-59": "test/fixtures/alphafold-a3m/model1-reference-59",
 }
 
 

@@ -1,6 +1,8 @@
 "use strict";
-// Reads a triangle reference bundle (manifest.json + float32 little-endian
-// tensors), as src/reference/node.ts:13-42 does.
+// loadTriangleReferenceBundleFromFiles (src/reference/node.ts:13-42): a
+// manifest.json plus float32 little-endian tensors; the input carries the
+// manifest's own TriangleShape {length, cZ, cHidden} and epsilon, as the
+// reference hands them to TriangleMultiplicationGpu.run.
 var fs = require("fs");
 var path = require("path");
 
@@ -10,32 +12,28 @@ var WEIGHTS = [
   "linearZWeight", "linearZBias", "linearGWeight", "linearGBias",
 ];
 
-function loadTriangleBundle(manifestPath) {
-  var manifest = JSON.parse(fs.readFileSync(manifestPath, "utf8"));
+async function loadTriangleReferenceBundleFromFiles(manifestPath) {
+  var manifest = JSON.parse(await fs.promises.readFile(manifestPath, "utf8"));
   if (manifest.formatVersion !== 1 || manifest.operator !== "TriangleMultiplicationOutgoing") {
     throw new Error("unsupported triangle reference manifest");
   }
   var dir = path.dirname(manifestPath);
-  function tensor(name) {
+  async function tensor(name) {
     var rec = manifest.tensors[name];
     if (!rec || rec.dtype !== "float32") throw new Error("missing float32 tensor " + name);
-    var buf = fs.readFileSync(path.join(dir, rec.file));
+    var bytes = await fs.promises.readFile(path.resolve(dir, rec.file));
     var count = rec.shape.reduce(function (a, b) { return a * b; }, 1);
-    if (buf.length !== count * 4) throw new Error("invalid byte length for tensor " + name);
-    var out = new Float32Array(count);
-    for (var i = 0; i < count; i++) out[i] = buf.readFloatLE(4 * i);
-    return out;
+    if (bytes.byteLength !== count * 4) throw new Error("invalid byte length for tensor " + name);
+    return new Float32Array(bytes.buffer.slice(bytes.byteOffset, bytes.byteOffset + bytes.byteLength));
   }
   var weights = {};
-  WEIGHTS.forEach(function (n) { weights[n] = tensor(n); });
+  await Promise.all(WEIGHTS.map(async function (n) { weights[n] = await tensor(n); }));
   return {
-    input: {
-      shape: [manifest.shape.length, manifest.shape.cZ, manifest.shape.cHidden],
-      epsilon: manifest.epsilon === undefined ? 1e-5 : manifest.epsilon,
-      z: tensor("z"), mask: tensor("mask"), weights: weights,
-    },
-    expected: tensor("expected"),
+    source: manifest.source,
+    input: { shape: manifest.shape, epsilon: manifest.epsilon, z: await tensor("z"), mask: await tensor("mask"),
+      weights: weights },
+    expected: await tensor("expected"),
   };
 }
 
-module.exports = { loadTriangleBundle: loadTriangleBundle };
+module.exports = { loadTriangleReferenceBundleFromFiles: loadTriangleReferenceBundleFromFiles };

@@ -1,15 +1,21 @@
 "use strict";
-// GPU parity through the Node-API addon, as the reference's own GPU tests
-// run it (test/triangle-multiplication-outgoing.gpu.test.ts:30-91,
-// test/evoformer-triangle-incoming.gpu.test.ts:42-106).
+// GPU parity through the Node-API addon, driven as the reference's own GPU
+// tests drive its operators: the reference's input objects, `await run()`,
+// the reference's tolerances (test/triangle-multiplication-outgoing.gpu.test.ts:30-91,
+// test/evoformer-triangle-incoming.gpu.test.ts:42-106,
+// test/outer-product-mean-reference.gpu.test.ts:100-135). The float64/f32
+// oracle's answers for the generated cases come from the Python test that
+// starts this script, in the directory AFHIP_NODE_EXPECTED.
 var assert = require("assert");
+var fs = require("fs");
 var path = require("path");
 var afhip = require("../../alphafold2-webgpu_amd/napi/index.js");
-var loadTriangleBundle = require("./fixtures.js").loadTriangleBundle;
+var loadTriangleReferenceBundleFromFiles = require("./fixtures.js").loadTriangleReferenceBundleFromFiles;
+var createDeterministicTriangleInput = require("./deterministic.js").createDeterministicTriangleInput;
 
 var golden = path.join(__dirname, "..", "golden");
+var expectedDir = process.env.AFHIP_NODE_EXPECTED;
 var report = { node: process.versions.node, cases: [] };
-afhip.requestHipDevice(0);
 
 function transposePairs(data, L, C) {
   var out = new Float32Array(data.length);
@@ -19,61 +25,137 @@ function transposePairs(data, L, C) {
   return out;
 }
 
-["openfold-triangle-small", "alphafold-short-9"].forEach(function (name) {
-  var b = loadTriangleBundle(path.join(golden, name, "manifest.json"));
-  var L = b.input.shape[0], C = b.input.shape[1];
-  var out = new afhip.TriangleMultiplicationOutgoingGpu().run(b.input, { precision: "f32" });
-  var m32 = afhip.errorMetrics(out.output, b.expected);
-  assert.ok(m32.meanAbsoluteError < 1e-5 && m32.maxAbsoluteError < 1e-4, name + " f32 " + JSON.stringify(m32));
-  assert.ok(out.elapsedMilliseconds > 0 && out.memory.peakBytes > 0);
-  var out16 = new afhip.TriangleMultiplicationOutgoingGpu().run(b.input, { precision: "f16" });
-  var m16 = afhip.errorMetrics(out16.output, b.expected);
-  assert.ok(m16.meanAbsoluteError < 1e-3 && m16.maxAbsoluteError < 1e-2, name + " f16 " + JSON.stringify(m16));
-  var blocked = new afhip.TriangleMultiplicationOutgoingGpu().run(b.input, { precision: "f32", blockRows: 2 });
-  assert.deepStrictEqual(Buffer.from(blocked.output.buffer), Buffer.from(out.output.buffer), name + " blocking");
-  // incoming(z) = T(outgoing(T(z))): the reference's kjc,kic->ijc (src/triangle/shaders.ts:452-495).
-  var t = { shape: b.input.shape, epsilon: b.input.epsilon, weights: b.input.weights,
-    z: transposePairs(b.input.z, L, C), mask: transposePairs(b.input.mask, L, 1) };
-  var incoming = new afhip.TriangleMultiplicationIncomingGpu().run(b.input, { precision: "f32" }).output;
-  var via = transposePairs(new afhip.TriangleMultiplicationOutgoingGpu().run(t, { precision: "f32" }).output, L, C);
-  var mi = afhip.errorMetrics(incoming, via);
-  assert.ok(mi.maxAbsoluteError <= 1e-6, name + " incoming " + JSON.stringify(mi));
-  report.cases.push({ fixture: name, f32: m32, f16: m16, incomingVsTransposed: mi });
-});
+function readF32(name) {
+  var bytes = fs.readFileSync(path.join(expectedDir, name));
+  return new Float32Array(bytes.buffer.slice(bytes.byteOffset, bytes.byteOffset + bytes.byteLength));
+}
 
-// Outer-product mean: the reference test's small case and closed form for an
-// all-ones mask with zero projections (count = S, rank-one outer product).
-(function () {
-  var S = 7, L = 5, cM = 6, cO = 4, cZ = 3;
-  function fill(n, f) { var a = new Float32Array(n); for (var i = 0; i < n; i++) a[i] = f(i); return a; }
-  var lb = fill(cO, function (i) { return 0.1 * (i + 1); });
-  var rb = fill(cO, function (i) { return -0.2 * (i + 1); });
-  var wo = fill(cO * cO * cZ, function (i) { return Math.sin(i + 1) * 0.3; });
-  var bo = fill(cZ, function (i) { return 0.05 * i; });
-  var input = { shape: [S, L, cM, cO, cZ], activations: fill(S * L * cM, function (i) { return Math.cos(i); }),
-    mask: fill(S * L, function () { return 1; }),
-    weights: { layerNormScale: fill(cM, function () { return 1; }), layerNormOffset: fill(cM, function () { return 0; }),
-      leftWeight: fill(cM * cO, function () { return 0; }), leftBias: lb,
-      rightWeight: fill(cM * cO, function () { return 0; }), rightBias: rb, outputWeight: wo, outputBias: bo } };
-  var out = new afhip.OuterProductMeanGpu().run(input, { precision: "f32" }).output;
-  var worst = 0;
-  for (var z = 0; z < cZ; z++) {
-    var e = bo[z];
-    for (var a = 0; a < cO; a++) for (var c = 0; c < cO; c++) e += S * lb[a] * rb[c] * wo[(a * cO + c) * cZ + z];
-    e /= 1e-3 + S;
-    for (var p = 0; p < L * L; p++) worst = Math.max(worst, Math.abs(out[p * cZ + z] - e) / Math.max(1, Math.abs(e)));
+function relativeMax(actual, expected) {
+  var worst = 0, largest = 0;
+  for (var i = 0; i < expected.length; i++) {
+    worst = Math.max(worst, Math.abs(actual[i] - expected[i]));
+    largest = Math.max(largest, Math.abs(expected[i]));
   }
-  assert.ok(worst < 1e-5, "opm closed form " + worst);
-  report.cases.push({ opmClosedFormMaxRelative: worst });
-})();
+  return worst / largest;
+}
 
+// The AllocationSnapshot fields (src/runtime/allocator.ts:8-29).
+function checkSnapshot(memory, labelPrefix) {
+  ["currentBytes", "peakBytes", "residentBytes", "peakResidentBytes", "pooledBytes", "allocationCount",
+    "bufferCount"].forEach(function (k) { assert.strictEqual(typeof memory[k], "number", k); });
+  assert.ok(Array.isArray(memory.peakComposition) && memory.peakComposition.length > 0);
+  memory.peakComposition.forEach(function (share) {
+    assert.ok(typeof share.label === "string" && share.bytes > 0 && share.count > 0);
+  });
+  assert.ok(memory.peakComposition.some(function (s) { return s.label.indexOf(labelPrefix) === 0; }));
+  assert.ok(memory.currentBytes > 0 && memory.peakBytes >= memory.currentBytes);
+  assert.ok(memory.residentBytes >= memory.currentBytes);
+}
+
+async function main() {
+  afhip.requestHipDevice(0);
+
+  // The reference's triangle fixtures, loaded as loadTriangleReferenceBundleFromFiles
+  // does, with their own TriangleShape objects.
+  var fixtures = ["openfold-triangle-small", "alphafold-short-9", "alphafold-single-sequence-59", "alphafold-a3m-59"];
+  for (var fi = 0; fi < fixtures.length; fi++) {
+    var name = fixtures[fi];
+    var b = await loadTriangleReferenceBundleFromFiles(path.join(golden, name, "manifest.json"));
+    var L = b.input.shape.length, C = b.input.shape.cZ;
+    var op = new afhip.TriangleMultiplicationOutgoingGpu(null);
+    var pending = op.run(b.input, { precision: "f32" });
+    assert.ok(pending instanceof Promise);
+    var out = await pending;
+    var m32 = afhip.errorMetrics(out.output, b.expected);
+    assert.ok(m32.meanAbsoluteError < 1e-5 && m32.maxAbsoluteError < 1e-4, name + " f32 " + JSON.stringify(m32));
+    assert.ok(out.elapsedMilliseconds > 0);
+    checkSnapshot(out.memory, "triangle.");
+    // A second run on the same operator reuses its pooled buffers.
+    var again = await op.run(b.input, { precision: "f32" });
+    assert.deepStrictEqual(Buffer.from(again.output.buffer), Buffer.from(out.output.buffer), name + " rerun");
+    assert.ok(again.memory.allocationCount > out.memory.allocationCount);
+    var out16 = await new afhip.TriangleMultiplicationOutgoingGpu(null).run(b.input, { precision: "f16" });
+    var r16 = relativeMax(out16.output, b.expected);
+    assert.ok(r16 <= 1e-2, name + " f16 " + r16);
+    var blocked = await op.run(b.input, { precision: "f32", blockRows: 2 });
+    assert.deepStrictEqual(Buffer.from(blocked.output.buffer), Buffer.from(out.output.buffer), name + " blocking");
+    op.release();
+    // incoming(z) = T(outgoing(T(z))): the reference's kjc,kic->ijc (src/triangle/shaders.ts:452-495).
+    var t = { shape: b.input.shape, epsilon: b.input.epsilon, weights: b.input.weights,
+      z: transposePairs(b.input.z, L, C), mask: transposePairs(b.input.mask, L, 1) };
+    var results = await Promise.all([new afhip.TriangleMultiplicationIncomingGpu(null).run(b.input),
+      new afhip.TriangleMultiplicationOutgoingGpu(null).run(t)]);
+    var mi = afhip.errorMetrics(results[0].output, transposePairs(results[1].output, L, C));
+    assert.ok(mi.maxAbsoluteError <= 1e-6, name + " incoming " + JSON.stringify(mi));
+    report.cases.push({ fixture: name, f32: m32, f16MaxRelative: r16, incomingVsTransposed: mi });
+  }
+
+  // createDeterministicTriangleInput, both directions, against the oracle;
+  // two runs queued on one operator without awaiting the first.
+  var det = JSON.parse(fs.readFileSync(path.join(expectedDir, "deterministic.json"), "utf8"));
+  var input = createDeterministicTriangleInput(det.shape, det.seed);
+  var directions = { outgoing: new afhip.TriangleMultiplicationOutgoingGpu(null),
+    incoming: new afhip.TriangleMultiplicationIncomingGpu(null) };
+  var detReport = {};
+  for (var dir in directions) {
+    var first = directions[dir].run(input), second = directions[dir].run(input, { blockRows: 5 });
+    var both = await Promise.all([first, second]);
+    var expect = readF32("deterministic_" + dir + ".f32");
+    var rd = relativeMax(both[0].output, expect);
+    assert.ok(rd <= 1e-5, "deterministic " + dir + " " + rd);
+    assert.deepStrictEqual(Buffer.from(both[1].output.buffer), Buffer.from(both[0].output.buffer));
+    detReport[dir] = rd;
+  }
+  report.cases.push({ deterministicInput: detReport });
+
+  // The reference test's outer-product-mean input literal
+  // (test/outer-product-mean-reference.gpu.test.ts:81-121) and tolerances.
+  await (async function () {
+    function spread(count, seed) {
+      var values = new Float32Array(count);
+      for (var index = 0; index < count; index += 1) values[index] = Math.sin((index + 1) * seed) * 0.7;
+      return values;
+    }
+    var sequences = 9, length = 8, cM = 12, cOuter = 32, cZ = 16;
+    var mask = new Float32Array(sequences * length).fill(1);
+    for (var index = 0; index < sequences * length; index += 3) mask[index] = 0;
+    var weights = {
+      layerNormScale: spread(cM, 0.31), layerNormOffset: spread(cM, 0.17),
+      leftWeight: spread(cM * cOuter, 0.11), leftBias: spread(cOuter, 0.23),
+      rightWeight: spread(cM * cOuter, 0.13), rightBias: spread(cOuter, 0.29),
+      outputWeight: spread(cOuter * cOuter * cZ, 0.07), outputBias: spread(cZ, 0.37),
+    };
+    var opmInput = {
+      activations: spread(sequences * length * cM, 0.19), mask: mask,
+      sequences: sequences, length: length, cM: cM, cOuter: cOuter, cZ: cZ, weights: weights,
+      layerNormEpsilon: 1e-5, normalizationEpsilon: 1e-3, rowBlockResidues: 3,
+    };
+    var actual = await new afhip.OuterProductMeanGpu(null).run(opmInput);
+    var error = afhip.errorMetrics(actual.output, readF32("opm_expected.f32"));
+    assert.ok(error.meanAbsoluteError < 2e-5 && error.maxAbsoluteError < 2e-4, "opm " + JSON.stringify(error));
+    checkSnapshot(actual.memory, "outer-product-mean.");
+    report.cases.push({ outerProductMeanReferenceCase: error });
+
+    // TransitionInput {rows, channels, hiddenChannels} (src/evoformer/transition.ts:18-25).
+    var rows = 37, channels = 16, hidden = 64;
+    var tInput = { rows: rows, channels: channels, hiddenChannels: hidden, activations: spread(rows * channels, 0.41),
+      weights: { layerNormScale: spread(channels, 0.53), layerNormOffset: spread(channels, 0.29),
+        firstWeight: spread(channels * hidden, 0.17), firstBias: spread(hidden, 0.23),
+        secondWeight: spread(hidden * channels, 0.07), secondBias: spread(channels, 0.31) } };
+    var tr = await new afhip.TransitionGpu(null).run(tInput);
+    var rt = relativeMax(tr.output, readF32("transition_expected.f32"));
+    assert.ok(rt <= 1e-5, "transition " + rt);
+    checkSnapshot(tr.memory, "transition.");
+    report.cases.push({ transitionMaxRelative: rt });
+  })();
+
+  var native = afhip.addon();
 // The bundle's mixed-q8 weight through device buffers, as a TypeScript host
 // holding the bundle would run it: packWeightQ8Block decodes it straight into
 // the packed operand W[n][k] (bit-exact against the decode of
 // src/reference/dtype.ts:66-99, value = code * f32(scale)), and an f32 plan
 // on that operand matches a double-precision product.
-(function () {
-  var native = afhip.addon();
+await (async function () {
   var K = 96, N = 80, M = 40, block = 64, start = 37;
   var total = start + K * N + 11;
   var codes = new Int8Array(total), scales = new Uint16Array(Math.ceil(total / block));
@@ -114,6 +196,13 @@ function transposePairs(data, L, C) {
     worst = Math.max(worst, Math.abs(out[r * N + c] - acc));
     largest = Math.max(largest, Math.abs(acc));
   }
+  // Operands smaller than the plan reads or writes are refused (WebGPU's
+  // binding-size validation).
+  var small = native.bufferCreate(16);
+  assert.throws(function () { native.gemmRun(plan, { a: small, w: bw, c: bo }); }, /buffer a holds 16 bytes/);
+  assert.throws(function () { native.gemmRun(plan, { a: ba, w: bw, c: small }); }, /buffer c holds 16 bytes/);
+  assert.throws(function () { native.gemmRun(plan, { a: ba, c: bo }); }, /needs operand w/);
+  native.bufferDestroy(small);
   native.gemmPlanDestroy(plan);
   [bc, bs, bw, ba, bo].forEach(function (b) { native.bufferDestroy(b); });
   assert.ok(worst <= 1e-5 * largest, "q8 gemm " + worst / largest);
@@ -123,7 +212,7 @@ function transposePairs(data, L, C) {
 // AttentionGpu with zero query and key weights and no bias: every key
 // weighs 1/Q, so row (b, q) is mean_k(v[b][k]) * g[b][q], then the output
 // projection -- computed here in float64 from the LayerNormed rows.
-(function () {
+await (async function () {
   var B = 3, Q = 5, C = 8, H = 2;
   function fill(n, f) { var a = new Float32Array(n); for (var i = 0; i < n; i++) a[i] = f(i); return a; }
   var x = fill(B * Q * C, function (i) { return Math.sin(1.3 * i) + 0.1 * (i % 5); });
@@ -134,8 +223,8 @@ function transposePairs(data, L, C) {
     gatingBias: fill(C, function (i) { return 0.1 * i; }),
     outputWeight: fill(C * C, function (i) { return 0.25 * Math.sin(0.9 * i + 1); }),
     outputBias: fill(C, function (i) { return 0.01 * i; }) };
-  var out = new afhip.AttentionGpu().run({ activations: x, mask: fill(B * Q, function () { return 1; }), batch: B,
-    queryLength: Q, channels: C, heads: H, weights: w }, { precision: "f32" }).output;
+  var out = (await new afhip.AttentionGpu().run({ activations: x, mask: fill(B * Q, function () { return 1; }), batch: B,
+    queryLength: Q, channels: C, heads: H, weights: w }, { precision: "f32" })).output;
   var worst = 0, largest = 0;
   for (var b = 0; b < B; b++) {
     var xn = [], vmean = new Array(C).fill(0);
@@ -170,7 +259,7 @@ function transposePairs(data, L, C) {
 // (HipExecution.pairStack) against the six operators run one by one through
 // their host-array entry points, the updates added on the host in the
 // block's order (src/evoformer/block.ts:1683-1750).
-(function () {
+await (async function () {
   var L = 12, S = 5, cM = 8, cO = 4, cZ = 16, cH = 16, hidden = 4 * cZ;
   function fill(n, f) { var a = new Float32Array(n); for (var i = 0; i < n; i++) a[i] = f(i); return a; }
   function wave(n, scale, phase, center) { return fill(n, function (i) { return (center || 0) + scale * Math.sin(0.7 * i + phase); }); }
@@ -211,20 +300,21 @@ function transposePairs(data, L, C) {
 
   var z = Float32Array.from(pair);
   function addInto(base, update) { for (var i = 0; i < base.length; i++) base[i] = Math.fround(base[i] + update[i]); }
-  addInto(z, new afhip.OuterProductMeanGpu().run({ shape: [S, L, cM, cO, cZ], activations: msa, mask: msaMask,
-    weights: weights.outerProductMean }).output);
-  addInto(z, new afhip.TriangleMultiplicationOutgoingGpu().run({ shape: [L, cZ, cH], z: z, mask: pairMask,
-    weights: weights.triangleMultiplicationOutgoing }).output);
-  addInto(z, new afhip.TriangleMultiplicationIncomingGpu().run({ shape: [L, cZ, cH], z: z, mask: pairMask,
-    weights: weights.triangleMultiplicationIncoming }).output);
-  [["triangleAttentionStarting", false], ["triangleAttentionEnding", true]].forEach(function (step) {
-    var a = weights[step[0]];
-    addInto(z, new afhip.AttentionGpu().run({ activations: z, mask: pairMask, batch: L, queryLength: L, channels: cZ,
-      heads: 2, transpose: step[1], weights: a.attention,
-      pairBias: { source: "normalized-input", projectionWeight: a.pairProjectionWeight } }).output);
-  });
-  addInto(z, new afhip.TransitionGpu().run({ shape: [L * L, cZ, hidden], activations: z,
-    weights: weights.pairTransition }).output);
+  addInto(z, (await new afhip.OuterProductMeanGpu().run({ sequences: S, length: L, cM: cM, cOuter: cO, cZ: cZ,
+    activations: msa, mask: msaMask, weights: weights.outerProductMean })).output);
+  addInto(z, (await new afhip.TriangleMultiplicationOutgoingGpu().run({ shape: { length: L, cZ: cZ, cHidden: cH },
+    z: z, mask: pairMask, weights: weights.triangleMultiplicationOutgoing })).output);
+  addInto(z, (await new afhip.TriangleMultiplicationIncomingGpu().run({ shape: { length: L, cZ: cZ, cHidden: cH },
+    z: z, mask: pairMask, weights: weights.triangleMultiplicationIncoming })).output);
+  var steps = [["triangleAttentionStarting", false], ["triangleAttentionEnding", true]];
+  for (var si = 0; si < steps.length; si++) {
+    var a = weights[steps[si][0]];
+    addInto(z, (await new afhip.AttentionGpu().run({ activations: z, mask: pairMask, batch: L, queryLength: L,
+      channels: cZ, heads: 2, transpose: steps[si][1], weights: a.attention,
+      pairBias: { source: "normalized-input", projectionWeight: a.pairProjectionWeight } })).output);
+  }
+  addInto(z, (await new afhip.TransitionGpu().run({ rows: L * L, channels: cZ, hiddenChannels: hidden,
+    activations: z, weights: weights.pairTransition })).output);
 
   var ex = new afhip.HipExecution();
   var shape = { length: L, sequences: S, cM: cM, cZ: cZ, cOuter: cO, cHidden: cH, transitionFactor: 4,
@@ -238,6 +328,20 @@ function transposePairs(data, L, C) {
   var largest = 0;
   for (var i = 0; i < z.length; i++) largest = Math.max(largest, Math.abs(z[i]));
   assert.ok(m.maxAbsoluteError <= 1e-5 * largest, "pair stack " + JSON.stringify(m));
+  // A prepared-weight handle of another kind, or a plain buffer, is refused
+  // before anything runs.
+  assert.throws(function () {
+    ex.pairStack(shape, { triangleOutgoing: prepared.triangleIncoming }, bPair, bMask);
+  }, /must come from executionPrepareWeights\("triangleOutgoing"\); handle \d+ was prepared as "triangleIncoming"/);
+  var plainBuffer = afhip.addon().bufferCreate(64);
+  assert.throws(function () { ex.pairStack(shape, { pairTransition: plainBuffer }, bPair, bMask); },
+    /was prepared as nothing/);
+  afhip.addon().bufferDestroy(plainBuffer);
+  // (prepared triangle weights pad c_hidden to 32 rows, so the larger shape
+  // is c_hidden 64)
+  var bigger = Object.assign({}, shape, { cHidden: 64 });
+  assert.throws(function () { ex.pairStack(bigger, { triangleOutgoing: prepared.triangleOutgoing }, bPair, bMask); },
+    /prepared weights for triangleOutgoing hold \d+ bytes; this shape needs \d+/);
   var snap = ex.snapshot();
   assert.ok(snap.peakComposition.length > 0 && snap.residentBytes >= snap.currentBytes);
   ex.release();
@@ -266,14 +370,14 @@ function transposePairs(data, L, C) {
   });
   var m2 = Float32Array.from(msa);
   var rw = msaW.msaRowAttention;
-  addInto(m2, new afhip.AttentionGpu().run({ activations: m2, mask: msaMask, batch: S, queryLength: L, channels: cM,
-    heads: 2, weights: rw.attention, pairBias: { source: "separate", activations: pair, channels: cZ,
+  addInto(m2, (await new afhip.AttentionGpu().run({ activations: m2, mask: msaMask, batch: S, queryLength: L,
+    channels: cM, heads: 2, weights: rw.attention, pairBias: { source: "separate", activations: pair, channels: cZ,
       layerNormScale: rw.pairLayerNormScale, layerNormOffset: rw.pairLayerNormOffset,
-      projectionWeight: rw.pairProjectionWeight } }).output);
-  addInto(m2, new afhip.AttentionGpu().run({ activations: m2, mask: msaMask, batch: L, queryLength: S, channels: cM,
-    heads: 2, transpose: true, weights: msaW.msaColumnAttention.attention }).output);
-  addInto(m2, new afhip.TransitionGpu().run({ shape: [S * L, cM, 4 * cM], activations: m2,
-    weights: msaW.msaTransition }).output);
+      projectionWeight: rw.pairProjectionWeight } })).output);
+  addInto(m2, (await new afhip.AttentionGpu().run({ activations: m2, mask: msaMask, batch: L, queryLength: S,
+    channels: cM, heads: 2, transpose: true, weights: msaW.msaColumnAttention.attention })).output);
+  addInto(m2, (await new afhip.TransitionGpu().run({ rows: S * L, channels: cM, hiddenChannels: 4 * cM,
+    activations: m2, weights: msaW.msaTransition })).output);
   var ex2 = new afhip.HipExecution();
   var ePair = ex2.upload("pair", pair), eMask = ex2.upload("pair-mask", pairMask);
   var eMsa = ex2.upload("msa", m2), eMsaMask = ex2.upload("msa-mask", msaMask);
@@ -295,4 +399,7 @@ function transposePairs(data, L, C) {
   report.cases.push({ evoformerBlockVsOperators: { msa: rm, pair: rz } });
 })();
 
-console.log(JSON.stringify(report));
+  console.log(JSON.stringify(report));
+}
+
+main().catch(function (err) { console.error(err); process.exit(1); });

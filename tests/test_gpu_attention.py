@@ -114,7 +114,7 @@ def test_attention_gpu_run_mirrors_the_reference_call(dev):
     res = attention.AttentionGpu().run(inp)
     expect = ref.attention(x, mask, w, B, Q, 16, 2, transpose=tr, pair_bias=pb)
     assert np.abs(res["output"] - expect).max() <= 1e-5 * np.abs(expect).max()
-    assert res["elapsedMilliseconds"] >= 0 and "allocatedBytes" in res["memory"]
+    assert res["elapsedMilliseconds"] >= 0 and res["memory"]["currentBytes"] > 0
     bad = dict(inp, heads=3)
     with pytest.raises(attention._lib.RangeError, match="integral head dimension"):
         attention.AttentionGpu().run(bad)

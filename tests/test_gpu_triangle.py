@@ -18,7 +18,7 @@ from conftest import GOLDEN
 
 pytestmark = pytest.mark.gpu
 
-FIXTURES = ["openfold-triangle-small", "alphafold-short-9"]
+FIXTURES = ["openfold-triangle-small", "alphafold-short-9", "alphafold-single-sequence-59", "alphafold-a3m-59"]
 
 
 @pytest.fixture(scope="module")
@@ -55,6 +55,15 @@ def test_outgoing_f32_matches_fixture(dev, name):
     m = ref.error_metrics(res["output"], b["expected"])
     assert m["meanAbsoluteError"] < 1e-5 and m["maxAbsoluteError"] < 1e-4
     assert res["elapsedMilliseconds"] > 0 and res["memory"]["peakBytes"] > 0
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_outgoing_f16_matches_fixture(dev, name):
+    # f16 operands with f32 accumulation against the official f32 capture:
+    # within the north star's 1e-2 of the largest value.
+    b = bundle(name)
+    out = gpu_class("outgoing")().run(b["input"], {"precision": "f16"})["output"]
+    assert rel_max(out, b["expected"]) <= 1e-2
 
 
 @pytest.mark.parametrize("name", FIXTURES)

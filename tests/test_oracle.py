@@ -11,12 +11,10 @@ import pytest
 
 from oracle import ref
 from afhip.reference import load_triangle_reference_bundle
-from conftest import GOLDEN, REFERENCE
+from afhip.triangle import triangle_shape
+from conftest import GOLDEN
 
-REFERENCE_59 = [
-    "test/fixtures/alphafold-single-sequence/model1-reference-59/manifest.json",
-    "test/fixtures/alphafold-a3m/model1-reference-59/manifest.json",
-]
+REFERENCE_59 = ["alphafold-single-sequence-59", "alphafold-a3m-59"]
 
 
 def golden(name):
@@ -140,7 +138,7 @@ def test_attention_project_closed_form():
 
 def _numpy_triangle(direction, inp):
     """Float64 restatement in AlphaFold's einsum form, independent of afref.c."""
-    L, cz, ch = inp["shape"]
+    L, cz, ch = triangle_shape(inp)
     w = {k: v.astype(np.float64) for k, v in inp["weights"].items()}
     z = inp["z"].astype(np.float64)
     eps = inp["epsilon"]
@@ -179,12 +177,11 @@ def test_triangle_outgoing_matches_alphafold_short9():
     assert m["meanAbsoluteError"] < 1e-5 and m["maxAbsoluteError"] < 1e-4
 
 
-@pytest.mark.parametrize("rel", REFERENCE_59)
-def test_triangle_outgoing_matches_alphafold_59(rel):
-    path = os.path.join(REFERENCE, rel)
-    if not os.path.exists(path):
-        pytest.skip("reference checkout not present")
-    bundle = load_triangle_reference_bundle(path)
+@pytest.mark.parametrize("name", REFERENCE_59)
+def test_triangle_outgoing_matches_alphafold_59(name):
+    # test/cpu-reference.test.ts:18-27's tolerances on the two AlphaFold
+    # 59-residue captures (copied under tests/golden by make_golden.py).
+    bundle = golden(name)
     inp = bundle["input"]
     out = ref.triangle("outgoing", inp["z"], inp["mask"], inp["weights"], inp["epsilon"])
     m = ref.error_metrics(out, bundle["expected"])
@@ -208,6 +205,43 @@ def test_triangle_matches_independent_float64_restatement(direction):
     out = ref.triangle(direction, inp["z"], inp["mask"], inp["weights"], inp["epsilon"])
     expect = _numpy_triangle(direction, inp)
     assert np.abs(out - expect).max() <= 2e-6 * max(1.0, np.abs(expect).max())
+
+
+def _generator_vectors():
+    import json
+    import os
+
+    from conftest import GOLDEN
+
+    with open(os.path.join(GOLDEN, "generators.json")) as f:
+        return json.load(f)
+
+
+def test_deterministic_input_matches_reference_generator():
+    # Vectors written by the reference's own createDeterministicTriangleInput
+    # (src/testing/deterministic-input.ts:7-51, run by
+    # tests/golden/make_generator_vectors.js): every tensor of the port equals
+    # them bit for bit, the mask's draw order and the default seed included.
+    g = _generator_vectors()
+    for case in g["createDeterministicTriangleInput"]:
+        s = case["shape"]
+        inp = ref.deterministic_triangle_input(s["length"], s["cZ"], s["cHidden"], seed=case["seed"])
+        assert np.array_equal(inp["z"].reshape(-1), np.asarray(case["z"], np.float32))
+        assert np.array_equal(inp["mask"].reshape(-1), np.asarray(case["mask"], np.float32))
+        for name in ref.TRIANGLE_ORDER:
+            assert np.array_equal(inp["weights"][name].reshape(-1), np.asarray(case["weights"][name], np.float32)), name
+    d = g["createDeterministicTriangleInputDefaultSeed"]
+    inp = ref.deterministic_triangle_input(2, 2, 2)
+    assert np.array_equal(inp["z"].reshape(-1), np.asarray(d["z"], np.float32))
+
+
+def test_lcg_values_match_reference_generators():
+    # test/gemm-half-precision.gpu.test.ts:44-50 and the calibration probes'
+    # probeValues (src/runtime/gemm-selection.ts:307-313, seed 0x1234567).
+    g = _generator_vectors()
+    for case in g["gemmTestValues"]:
+        assert np.array_equal(ref.lcg_values(case["seed"], case["count"]), np.asarray(case["values"], np.float32))
+    assert np.array_equal(ref.lcg_values(0x1234567, 12), np.asarray(g["probeValues"], np.float32))
 
 
 def test_deterministic_input_shape_and_mask_rate():
