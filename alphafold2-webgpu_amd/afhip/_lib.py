@@ -168,6 +168,8 @@ SIGNATURES = {
     "afhip_gemm_force_variant": [ctypes.POINTER(Variant)],
     "afhip_calibration_load": [ctypes.c_char_p],
     "afhip_calibration_save": [ctypes.c_char_p],
+    "afhip_calibration_clear": [],
+    "afhip_calibration_inject": [_i32, _i32, _i32, _i32],
     "afhip_pack_weight": [_vp, _i32, _i32, _i32, _vp, _i32, _vp],
     "afhip_dequant_q8_channel": [_vp, _vp, _i32, _i32, _vp, _vp],
     "afhip_dequant_q8_block": [_vp, _vp, _i32, _i64, _i64, _vp, _vp],

@@ -197,6 +197,23 @@ def calibration_save(path: str) -> None:
     _lib.call("afhip_calibration_save", path.encode())
 
 
+def calibration_clear() -> None:
+    """Forgets every calibrated answer this process holds."""
+    _lib.call("afhip_calibration_clear")
+
+
+CALIBRATION_FAULTS = {"none": 0, "run": 1, "result": 2}
+
+
+def calibration_inject(kernel: str, tile_rows: int, tile_columns: int, fault: str) -> None:
+    """Forces a fault on one calibration candidate from the host: "run" (it
+    counts as failing to run and is dropped), "result" (its result reads 5%
+    off and is refused) or "none"; kernel "all" with fault "none" clears
+    every fault. For tests of the calibration's failure handling."""
+    code = -1 if kernel == "all" else _KERNEL_CODES[kernel]
+    _lib.call("afhip_calibration_inject", code, tile_rows, tile_columns, CALIBRATION_FAULTS[fault])
+
+
 def pack_weight(w, precision: str = "f32"):
     """[K][N] device weight -> [N][K] in the precision's dtype (int8 stays int8):
     the counterpart of packWeights (src/triangle/weights.ts:20-34)."""

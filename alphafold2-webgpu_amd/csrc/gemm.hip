@@ -83,14 +83,20 @@ static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int6
   v.tile_inner = gemm_detail::kBK;
   v.vectorized = 1;
   v.source = 0;
-  if (t.precision == AFHIP_PRECISION_F16 && t.a_dtype == AFHIP_F16 && t.b_dtype == AFHIP_F16) {
+  // LDS_DMA takes f16 operands whose K is a multiple of 8 (its 16-byte
+  // chunks); anything else is staged through registers.
+  if (t.precision == AFHIP_PRECISION_F16 && t.a_dtype == AFHIP_F16 && t.b_dtype == AFHIP_F16 && K % 8 == 0) {
     v.kernel = AFHIP_KERNEL_LDS_DMA;
     dma_heuristic_tile(M, N, K, batch, &v.tile_rows, &v.tile_columns);
     return v;
   }
   v.kernel = AFHIP_KERNEL_REGISTER_STAGED;
-  // Prefer the largest tile that still gives every CU two workgroups.
-  const int64_t target = 2 * (int64_t)(device_cu_count() > 0 ? device_cu_count() : 256);
+  // Prefer the largest tile that still gives every CU two workgroups, or one
+  // when K is long enough for a tile's own k-loop to hide its latency
+  // (measured on the reference's opm-contract shape, 128 x 508 x 32000:
+  // 128 x 64 at 0.053 ms against 64 x 64 at 0.065 ms).
+  const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const int64_t target = K >= 384 ? cus : 2 * cus;
   const int shapes[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
   for (auto& s : shapes) {
     int64_t tiles = ceil_div(M, s[0]) * ceil_div(N, s[1]) * batch;
@@ -103,9 +109,12 @@ static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int6
 
 // Weight-stationary streaming for tall, bandwidth-bound projections (many
 // rows against a short K and at least 448 columns, so a slice's eight waves
-// are mostly busy); the tiled families otherwise.
+// are mostly busy); the tiled families otherwise. Measured on the
+// reference's SHAPES (tools/gemm-candidates.ts:637-669): STREAM wins from
+// ~16k rows (29,972 x 256 x 1,024: 0.026 ms against 0.028 for the best tile)
+// and loses below (8,192 x 128 x 512: 0.0083 against 0.0071).
 afhip_variant heuristic_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K, int batch) {
-  if (stream_shape_ok(t, M, N, K, batch) && M >= 4096 && N >= 448) {
+  if (stream_shape_ok(t, M, N, K, batch) && M >= 16384 && N >= 448) {
     afhip_variant v{};
     v.precision = t.precision;
     v.tile_rows = 64;

@@ -16,6 +16,7 @@
 #include <mutex>
 #include <sstream>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "gemm.h"
@@ -71,15 +72,19 @@ template <typename T> __global__ void fill_kernel(T* p, int64_t n, uint32_t seed
   else p[i] = (T)((float)(x & 0xffffu) / 65536.0f - 0.5f);
 }
 
-// The plain loop the candidates are checked against: one lane per output,
-// f32 accumulation over A[m][k] * W[n][k].
+// The plain loop the candidates are checked against: one lane per output of
+// the sampled rows, f32 accumulation over A[b][m][k] * W[b][n][k]; sample r
+// is row rows[r] of batch batches[r].
 template <typename TA, typename TB>
-__global__ void naive_kernel(const TA* a, const TB* b, float* c, int M, int N, int K) {
+__global__ void naive_kernel(const TA* a, const TB* b, float* c, const int* batches, const int* rows, int samples,
+                             int M, int N, int K) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)M * N) return;
-  int m = (int)(i / N), n = (int)(i % N);
+  if (i >= (int64_t)samples * N) return;
+  const int r = (int)(i / N), n = (int)(i % N);
+  const int64_t bb = batches[r], m = rows[r];
   float s = 0.0f;
-  for (int k = 0; k < K; k++) s += (float)a[(int64_t)m * K + k] * (float)b[(int64_t)n * K + k];
+  for (int k = 0; k < K; k++)
+    s += (float)a[(bb * M + m) * K + k] * (float)b[(bb * N + n) * K + k];
   c[i] = s;
 }
 
@@ -93,22 +98,30 @@ int fill_dtype(int dtype, void* p, int64_t n, uint32_t seed, hipStream_t s) {
   return fill<int8_t>(p, n, seed, s);
 }
 
-int naive(int ad, int bd, const void* a, const void* b, float* c, int M, int N, int K, hipStream_t s) {
-  dim3 grid((unsigned)ceil_div((int64_t)M * N, 256));
-  if (ad == AFHIP_F32 && bd == AFHIP_F32)
-    return launch("calibrate.check", naive_kernel<float, float>, grid, dim3(256), 0, s, (const float*)a,
-                  (const float*)b, c, M, N, K);
-  if (ad == AFHIP_F32 && bd == AFHIP_F16)
-    return launch("calibrate.check", naive_kernel<float, half_t>, grid, dim3(256), 0, s, (const float*)a,
-                  (const half_t*)b, c, M, N, K);
-  if (ad == AFHIP_F32)
-    return launch("calibrate.check", naive_kernel<float, int8_t>, grid, dim3(256), 0, s, (const float*)a,
-                  (const int8_t*)b, c, M, N, K);
-  if (bd == AFHIP_F16)
-    return launch("calibrate.check", naive_kernel<half_t, half_t>, grid, dim3(256), 0, s, (const half_t*)a,
-                  (const half_t*)b, c, M, N, K);
-  return launch("calibrate.check", naive_kernel<half_t, int8_t>, grid, dim3(256), 0, s, (const half_t*)a,
-                (const int8_t*)b, c, M, N, K);
+int naive(int ad, int bd, const void* a, const void* b, float* c, const int* batches, const int* rows, int samples,
+          int M, int N, int K, hipStream_t s) {
+  dim3 grid((unsigned)ceil_div((int64_t)samples * N, 256));
+#define AFHIP_NAIVE(TA, TB)                                                                                        \
+  return launch("calibrate.check", naive_kernel<TA, TB>, grid, dim3(256), 0, s, (const TA*)a, (const TB*)b, c,      \
+                batches, rows, samples, M, N, K)
+  if (ad == AFHIP_F32 && bd == AFHIP_F32) AFHIP_NAIVE(float, float);
+  if (ad == AFHIP_F32 && bd == AFHIP_F16) AFHIP_NAIVE(float, half_t);
+  if (ad == AFHIP_F32) AFHIP_NAIVE(float, int8_t);
+  if (bd == AFHIP_F16) AFHIP_NAIVE(half_t, half_t);
+  AFHIP_NAIVE(half_t, int8_t);
+#undef AFHIP_NAIVE
+}
+
+// Faults a test forces on chosen candidates from the host
+// (afhip_calibration_inject): the calibration's own failure handling is what
+// is under test, so no kernel is made to fail.
+std::mutex g_fault_mutex;
+std::map<std::tuple<int, int, int>, int> g_faults;
+
+int fault_of(const afhip_variant& v) {
+  std::lock_guard<std::mutex> lock(g_fault_mutex);
+  auto it = g_faults.find(std::make_tuple(v.kernel, v.tile_rows, v.tile_columns));
+  return it == g_faults.end() ? AFHIP_CALIBRATION_FAULT_NONE : it->second;
 }
 
 struct DeviceBuffer {
@@ -228,33 +241,58 @@ int afhip_gemm_calibrate(const afhip_gemm_desc* d, afhip_variant* out) {
   g.sc = (int64_t)M * N;
   g.batch = B;
 
-  // Correctness first, on the first 256 rows of the first batch.
-  const int cm = std::min(M, 256);
-  if (int s = ref.alloc(4 * (size_t)cm * N)) return s;
-  if (int s = naive(t.a_dtype, t.b_dtype, a.p, b.p, (float*)ref.p, cm, N, K, st)) return s;
-  std::vector<float> expect((size_t)cm * N);
+  // Correctness first, on up to 256 sampled rows spread over every batch
+  // (the first and last rows of each batch among them), so a candidate that
+  // is wrong only on later batches or rows cannot win.
+  const int samples = (int)std::min<int64_t>((int64_t)M * B, 256);
+  std::vector<int> sb(samples), sm(samples);
+  for (int r = 0; r < samples; r++) {
+    sb[r] = r % B;
+    const int k = r / B, per = (samples + B - 1) / B;
+    sm[r] = per <= 1 ? 0 : (int)((int64_t)k * (M - 1) / (per - 1));
+  }
+  DeviceBuffer rows_b, rows_m;
+  if (int s = ref.alloc(4 * (size_t)samples * N)) return s;
+  if (int s = rows_b.alloc(4 * (size_t)samples)) return s;
+  if (int s = rows_m.alloc(4 * (size_t)samples)) return s;
+  AFHIP_CHECK_HIP(hipMemcpy(rows_b.p, sb.data(), 4 * (size_t)samples, hipMemcpyHostToDevice));
+  AFHIP_CHECK_HIP(hipMemcpy(rows_m.p, sm.data(), 4 * (size_t)samples, hipMemcpyHostToDevice));
+  if (int s = naive(t.a_dtype, t.b_dtype, a.p, b.p, (float*)ref.p, (const int*)rows_b.p, (const int*)rows_m.p,
+                    samples, M, N, K, st))
+    return s;
+  std::vector<float> expect((size_t)samples * N);
   AFHIP_CHECK_HIP(hipMemcpy(expect.data(), ref.p, 4 * expect.size(), hipMemcpyDeviceToHost));
   double scale = 0.0;
   for (float v : expect) scale = std::max(scale, (double)std::fabs(v));
 
   std::vector<afhip_variant> cands = candidates(t.precision, dma_eligible(g, t), stream_eligible(g, t));
   std::vector<afhip_variant> usable;
-  std::vector<char> host((size_t)cm * N * ec);
+  std::vector<char> host((size_t)B * M * N * ec);
   for (auto& v : cands) {
-    if (run_gemm(g, t, v, "calibrate.candidate", st) != AFHIP_OK) continue;  // dropped, as :482-495
+    const int fault = fault_of(v);
+    // A candidate that does not run is dropped, not allowed to end the
+    // calibration (gemm-selection.ts:482-495).
+    if (fault == AFHIP_CALIBRATION_FAULT_RUN) continue;
+    if (run_gemm(g, t, v, "calibrate.candidate", st) != AFHIP_OK) continue;
     if (hipMemcpy(host.data(), c.p, host.size(), hipMemcpyDeviceToHost) != hipSuccess) continue;
     double worst = 0.0;
-    for (size_t i = 0; i < expect.size(); i++) {
-      double got = t.c_dtype == AFHIP_F32 ? (double)reinterpret_cast<float*>(host.data())[i]
-                                          : (double)(float)reinterpret_cast<_Float16*>(host.data())[i];
-      worst = std::max(worst, std::fabs(got - (double)expect[i]));
-    }
+    for (int r = 0; r < samples; r++)
+      for (int n = 0; n < N; n++) {
+        const size_t at = ((size_t)sb[r] * M + sm[r]) * N + n;
+        double got = t.c_dtype == AFHIP_F32 ? (double)reinterpret_cast<float*>(host.data())[at]
+                                            : (double)(float)reinterpret_cast<_Float16*>(host.data())[at];
+        if (fault == AFHIP_CALIBRATION_FAULT_RESULT) got += 0.05 * scale;
+        worst = std::max(worst, std::fabs(got - (double)expect[(size_t)r * N + n]));
+      }
     double rel = scale == 0.0 ? INFINITY : worst / scale;
-    if (rel <= kCheckTolerance) usable.push_back(v);
+    if (rel <= kCheckTolerance) usable.push_back(v);  // :584-586
   }
   if (usable.empty()) {
+    // Nothing reproduced the reference: the probe, not the arithmetic, is
+    // suspect, so nothing is installed and the heuristic stays
+    // (gemm-selection.ts:590-593, :653-656).
     *out = heuristic_variant(t, M, N, K, B);
-    return set_error(AFHIP_ERR_HIP, "no GEMM candidate reproduced the reference; keeping the heuristic");
+    return AFHIP_OK;
   }
 
   Events ev;
@@ -294,6 +332,25 @@ int afhip_gemm_calibrate(const afhip_gemm_desc* d, afhip_variant* out) {
   v.source = 1;
   install_calibrated(device_key() + "|" + shape_class(t, M, N, K, B), v);
   *out = v;
+  return AFHIP_OK;
+}
+
+int afhip_calibration_inject(int32_t kernel, int32_t tile_rows, int32_t tile_columns, int32_t fault) {
+  std::lock_guard<std::mutex> lock(g_fault_mutex);
+  if (fault == AFHIP_CALIBRATION_FAULT_NONE && kernel < 0) {
+    g_faults.clear();
+    return AFHIP_OK;
+  }
+  AFHIP_REQUIRE(fault >= AFHIP_CALIBRATION_FAULT_NONE && fault <= AFHIP_CALIBRATION_FAULT_RESULT,
+                "unknown calibration fault %d", fault);
+  const auto key = std::make_tuple((int)kernel, (int)tile_rows, (int)tile_columns);
+  if (fault == AFHIP_CALIBRATION_FAULT_NONE) g_faults.erase(key);
+  else g_faults[key] = fault;
+  return AFHIP_OK;
+}
+
+int afhip_calibration_clear(void) {
+  replace_calibrated({});
   return AFHIP_OK;
 }
 

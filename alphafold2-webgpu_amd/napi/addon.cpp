@@ -473,6 +473,24 @@ napi_value CalibrationLoad(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+napi_value CalibrationClear(napi_env env, napi_callback_info) {
+  check(env, afhip_calibration_clear(), "calibrationClear");
+  return nullptr;
+}
+
+// calibrationInject(kernel, tileRows, tileColumns, fault): a fault forced on
+// one calibration candidate, for tests of the calibration's failure handling.
+napi_value CalibrationInject(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a, 4)) return nullptr;
+  int64_t v[4];
+  for (int i = 0; i < 4; i++)
+    if (!get_int64(env, a.argv[i], &v[i])) return nullptr;
+  check(env, afhip_calibration_inject((int32_t)v[0], (int32_t)v[1], (int32_t)v[2], (int32_t)v[3]),
+        "calibrationInject");
+  return nullptr;
+}
+
 napi_value CalibrationSave(napi_env env, napi_callback_info info) {
   Args a;
   std::string path;
@@ -1530,7 +1548,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"bufferCreate", BufferCreate}, {"bufferDestroy", BufferDestroy}, {"bufferWrite", BufferWrite},
       {"bufferRead", BufferRead}, {"synchronize", Synchronize}, {"gemmGrid", GemmGrid}, {"gemmSelect", GemmSelect},
       {"gemmCalibrate", GemmCalibrate}, {"gemmForceVariant", GemmForceVariant}, {"calibrationLoad", CalibrationLoad},
-      {"calibrationSave", CalibrationSave}, {"gemmPlanCreate", GemmPlanCreate}, {"gemmPlanDestroy", GemmPlanDestroy},
+      {"calibrationSave", CalibrationSave}, {"calibrationClear", CalibrationClear},
+      {"calibrationInject", CalibrationInject}, {"gemmPlanCreate", GemmPlanCreate}, {"gemmPlanDestroy", GemmPlanDestroy},
       {"gemmWorkspaceSize", GemmWorkspaceSize}, {"gemmRun", GemmRun}, {"packWeightQ8Block", PackWeightQ8Block},
       {"executionCreate", ExecutionCreate}, {"executionDestroy", ExecutionDestroy},
       {"executionAllocate", ExecutionAllocate}, {"executionUpload", ExecutionUpload},

@@ -487,6 +487,7 @@ module.exports = {
   forceGemmVariant: function (variant) { addon().gemmForceVariant(variant === undefined ? null : variant); },
   calibrationLoad: function (file) { addon().calibrationLoad(file); },
   calibrationSave: function (file) { addon().calibrationSave(file); },
+  calibrationClear: function () { addon().calibrationClear(); },
   // The bundle's mixed-q8 weight (int8 codes and f16 scale bits, in device
   // buffers) decoded straight into a packed GEMM operand buffer.
   packWeightQ8Block: function (codes, scales, block, start, rowsK, columnsN, dst, dtype) {

@@ -16,8 +16,10 @@ the stream it is launched on (afhip_timing_*) during the same run;
 HBM bytes per launch from rocprofv3's FETCH_SIZE and WRITE_SIZE counters,
 scaled against a plain copy, as recorded in
 profiles/hbm_traffic_by_kernel.md. `configs` measures BASELINE's other
-configurations the same way. `cpu_baseline` is the CPU oracle
-(oracle/afref.c, one thread) on a bounded sample.
+configurations the same way. `cpu_baseline` is the reference's CPU path
+(cpu-reference.ts restated in plain JS, oracle/cpu_reference.js) under node
+on one thread, on a bounded sample, with the C oracle on one thread and on
+every core beside it.
 """
 from __future__ import annotations
 
@@ -87,23 +89,58 @@ def triangle_weights(seed: int, cz: int, ch: int) -> dict:
 
 
 def cpu_baseline() -> dict:
-    """The oracle (a restatement of src/triangle/cpu-reference.ts) on one
-    thread, timed on an L=128 outgoing triangle multiplication and reported
-    as its algorithmic TFLOP/s (the unit of `value`)."""
+    """The reference's CPU path timed on this host, a reported baseline.
+
+    Primary: oracle/cpu_reference.js, the reference's
+    triangleMultiplicationOutgoingReference (src/triangle/cpu-reference.ts:56-100)
+    in plain JavaScript, under this machine's node, one JS thread, on the
+    reference's deterministic input at L = 160 (a bounded sample, ~10-20 s).
+    Secondary: the C oracle (oracle/afref.c, -O2, no fast-math) on one thread
+    and on every core (OpenMP). Each is reported as the outgoing operator's
+    algorithmic TFLOP/s (the unit of `value`) and as the L = 384 step it
+    extrapolates to by FLOPs."""
+    import shutil
+    import subprocess
+
     from oracle import ref
 
-    length = 128
-    inp = ref.deterministic_triangle_input(length, CZ, CH, seed=11)
-    start = time.perf_counter()
-    ref.triangle("outgoing", inp["z"], inp["mask"], inp["weights"])
-    seconds = time.perf_counter() - start
-    flops = sum(triangle_flops(length, CZ, CH).values())
     full = 2 * sum(triangle_flops(L, CZ, CH).values())
-    return {"value": flops / seconds / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"one outgoing triangle multiplication at L={length}, c_z=c_h={CH} "
-                      f"({seconds:.2f} s, oracle/afref.c single-threaded -O2); a full step at L={L} "
-                      f"would take {full / (flops / seconds):.0f} s",
-            "ms_per_step_extrapolated": full / (flops / seconds) * 1e3}
+
+    def rate(length, seconds):
+        flops = sum(triangle_flops(length, CZ, CH).values())
+        return flops / seconds / 1e12, full / (flops / seconds) * 1e3
+
+    secondary = {}
+    for threads, length in ((1, 128), (ref.max_threads(), 256)):
+        inp = ref.deterministic_triangle_input(length, CZ, CH, seed=11)
+        ref.set_threads(threads)
+        start = time.perf_counter()
+        ref.triangle("outgoing", inp["z"], inp["mask"], inp["weights"])
+        seconds = time.perf_counter() - start
+        tflops, step_ms = rate(length, seconds)
+        secondary[f"c_oracle_{threads}_threads"] = {
+            "value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/afref.c, one outgoing triangle multiplication at L={length}, c_z=c_h={CH} "
+                      f"({seconds:.2f} s)", "ms_per_step_extrapolated": step_ms}
+    ref.set_threads(ref.max_threads())
+
+    node = shutil.which("node")
+    length = 160
+    if node is not None:
+        proc = subprocess.run([node, os.path.join(ROOT, "oracle", "cpu_reference.js"), str(length), str(CZ), str(CH),
+                               "11"], capture_output=True, text=True, timeout=600)
+        if proc.returncode == 0:
+            js = json.loads(proc.stdout.strip().splitlines()[-1])
+            tflops, step_ms = rate(length, js["seconds"])
+            return {"value": tflops, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                    "sample": f"the reference's cpu-reference.ts loops in plain JS (oracle/cpu_reference.js) under "
+                              f"node {js['node']}, one JS thread, on {js['cpus']} host CPUs ({js['cpuModel']}): one "
+                              f"outgoing triangle multiplication at L={length}, c_z=c_h={CH} ({js['seconds']:.1f} s); "
+                              f"a full L={L} step would take {step_ms / 1e3:.0f} s",
+                    "node": js["node"], "host_cpus": js["cpus"], "cpu_model": js["cpuModel"],
+                    "ms_per_step_extrapolated": step_ms, "secondary": secondary}
+    one = secondary["c_oracle_1_threads"]
+    return dict(one, secondary=secondary, note="node unavailable: the C oracle is the primary figure")
 
 
 def copy_probe(mib: int) -> None:
@@ -116,6 +153,84 @@ def copy_probe(mib: int) -> None:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_probe_bytes_each_way": n * 4, "launches": 10}))
+
+
+# tools/gemm-candidates.ts:637-669 (SHAPES): the model's projection and
+# contraction shapes, their 32-aligned twins and the calibration probe shapes.
+GEMM_SHAPES = [
+    ("opm-contract", 128, 508, 32000), ("opm-out", 4096, 1024, 128), ("opm-out2", 3000, 1024, 128),
+    ("project", 29972, 256, 1024), ("output", 29972, 256, 256), ("trans1", 29972, 256, 1024),
+    ("trans2", 29972, 1024, 256), ("extra1", 60416, 64, 256), ("project32", 29984, 256, 1024),
+    ("output32", 29984, 256, 256), ("trans2-32", 29984, 1024, 256), ("opmcon32", 128, 512, 32000),
+    ("probeA", 1024, 512, 512), ("probeB", 8192, 128, 512), ("probeC", 16384, 256, 256), ("probeD", 4096, 256, 512),
+]
+GEMM_CANDIDATES = [("register", 64, 64), ("register", 64, 128), ("register", 128, 64), ("register", 128, 128),
+                   ("lds_dma", 128, 128), ("lds_dma", 192, 192), ("lds_dma", 128, 256), ("lds_dma", 256, 256),
+                   ("stream", 64, 512)]
+
+
+def gemm_shapes(launches: int = 20) -> dict:
+    """The gemm-candidates benchmark (tools/gemm-candidates.ts:571-669,
+    tools/benchmark-gemm.ts:46-104) on MI355X: every candidate tile of the
+    f16 GEMM (f16 operands, f32 accumulation, f16 output, weight [N][K]) on
+    every shape of SHAPES, beside the variant the heuristic picks. A candidate
+    is timed only where its family takes the operands (LDS_DMA: K a multiple
+    of 8; STREAM: K of 64, 128 or 256 and N a multiple of 64), as the library
+    would otherwise run it on another family. ms is the average of
+    `launches` back-to-back launches between two events after three warm-up
+    launches."""
+    import torch
+
+    from afhip import device, gemm
+
+    device.open_device(0)
+    dev = device.device()
+    out = {"unit": "ms", "launches": launches, "shapes": []}
+    for name, M, K, N in GEMM_SHAPES:
+        a = torch.randn(M, K, device=dev).half()
+        w = (torch.randn(N, K, device=dev) / K ** 0.5).half()
+        c = torch.empty(M, N, device=dev, dtype=torch.float16)
+
+        def run(pin):
+            gemm.force_variant(pin)
+            try:
+                plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
+                                      out_dtype="f16")
+                chosen = plan.variant()
+                for _ in range(3):
+                    plan.run(a, w, out=c)
+                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                for _ in range(launches):
+                    plan.run(a, w, out=c)
+                stop.record()
+                stop.synchronize()
+                return chosen, start.elapsed_time(stop) / launches
+            finally:
+                gemm.force_variant(None)
+
+        flops = 2.0 * M * K * N
+        chosen, heuristic_ms = run(None)
+        entry = {"shape": name, "M": M, "K": K, "N": N,
+                 "heuristic": {"variant": chosen.name, "ms": round(heuristic_ms, 5),
+                               "tflops": round(flops / heuristic_ms / 1e9, 1)},
+                 "candidates": {}}
+        for kernel, tr, tc in GEMM_CANDIDATES:
+            if kernel == "lds_dma" and K % 8:
+                continue
+            if kernel == "stream" and (K not in (64, 128, 256) or N % 64):
+                continue
+            v = gemm.GemmVariant("f16", tr, tc, source="pinned", kernel=kernel)
+            _, ms = run(v)
+            entry["candidates"][v.name] = {"ms": round(ms, 5), "tflops": round(flops / ms / 1e9, 1)}
+        best = min(entry["candidates"].items(), key=lambda kv: kv[1]["ms"])
+        entry["best"] = {"variant": best[0], "ms": best[1]["ms"]}
+        entry["heuristic_over_best"] = round(heuristic_ms / best[1]["ms"], 3)
+        out["shapes"].append(entry)
+        print(f"gemm-shapes: {name} heuristic {chosen.name} {heuristic_ms:.4f} ms, best {best[0]} "
+              f"{best[1]['ms']:.4f} ms", file=sys.stderr, flush=True)
+        del a, w, c
+    return out
 
 
 def timed(fn, steps: int, warmup: int):
@@ -402,7 +517,13 @@ def main() -> None:
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                         help="only run a plain device-to-device copy of MIB MiB 10 times (the known-size kernel "
                              "rocprof's FETCH_SIZE / WRITE_SIZE readings are scaled by) and exit")
+    parser.add_argument("--gemm-shapes", action="store_true",
+                        help="only run the gemm-candidates benchmark (every candidate tile and the heuristic's "
+                             "choice on the reference's SHAPES) and print it as one JSON line")
     args = parser.parse_args()
+    if args.gemm_shapes:
+        print(json.dumps(gemm_shapes()))
+        return
     if args.copy_probe:
         copy_probe(args.copy_probe)
         return

@@ -225,9 +225,13 @@ typedef struct afhip_variant {
  * and gemmVariantCandidates (gemm-selection.ts:234-272). */
 AFHIP_API int afhip_gemm_select(const afhip_gemm_desc* desc, afhip_variant* out);
 /* Measures every candidate tile for the description's shape class on the
- * open device (correctness check first, then interleaved timing, as
- * measureGemmVariants does, gemm-selection.ts:471-531), installs and
- * returns the winner. Replaces calibrateGemmVariant (:560-660). */
+ * open device (correctness check first, on rows sampled from every batch,
+ * then interleaved timing, as measureGemmVariants does,
+ * gemm-selection.ts:471-531), installs and returns the winner. Replaces
+ * calibrateGemmVariant (:560-660). A candidate that fails to run is dropped
+ * and one whose error exceeds 0.02 of the largest reference value refused;
+ * when none is left, nothing is installed and the heuristic's variant is
+ * returned (source 0), as the reference keeps its f32 kernel. */
 AFHIP_API int afhip_gemm_calibrate(const afhip_gemm_desc* desc, afhip_variant* out);
 /* Pins a variant for every plan created afterwards (NULL unpins); the
  * counterpart of forceGemmVariant (gemm-selection.ts:122-125). */
@@ -238,6 +242,22 @@ AFHIP_API int afhip_gemm_force_variant(const afhip_variant* variant);
  * validation is ignored, as isGemmVariant rejects one (gemm-selection.ts:543-558). */
 AFHIP_API int afhip_calibration_load(const char* path);
 AFHIP_API int afhip_calibration_save(const char* path);
+/* Forgets every calibrated answer held in this process (the selection falls
+ * back to the heuristic until a calibration or a document installs one). */
+AFHIP_API int afhip_calibration_clear(void);
+
+/* Faults a test forces on one calibration candidate from the host, so the
+ * calibration's failure handling can be exercised without a failing kernel:
+ * RUN makes the candidate count as one that failed to run (dropped, as
+ * measureGemmVariants drops it, gemm-selection.ts:482-495); RESULT offsets
+ * the candidate's result by 5% of the reference's largest value as the check
+ * reads it (refused, :584-586). NONE clears the candidate's fault; NONE with
+ * kernel < 0 clears them all. No counterpart in the reference beyond those
+ * rules; for tests. */
+#define AFHIP_CALIBRATION_FAULT_NONE 0
+#define AFHIP_CALIBRATION_FAULT_RUN 1
+#define AFHIP_CALIBRATION_FAULT_RESULT 2
+AFHIP_API int afhip_calibration_inject(int32_t kernel, int32_t tile_rows, int32_t tile_columns, int32_t fault);
 
 /* Weight preparation for GEMM plans: W[k][n] -> W[n][k] (and f32 -> f16 when
  * dst_dtype is F16). Element types of src and dst given explicitly. */

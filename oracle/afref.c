@@ -16,6 +16,9 @@
  * Each function cites the reference file:line whose behaviour it restates
  * (paths relative to the alphafold2-webgpu checkout).
  */
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -260,6 +263,30 @@ EXPORT void afref_attention_project(const float* x, const float* w, const float*
 }
 
 /* ------------------------------------------------------------------------ */
+/* Threads                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* The triangle loops below split their outer (row or pair) loop over OpenMP
+ * threads. Every stored value is still computed by one thread in the
+ * reference's order, so any thread count gives the same bits; the count only
+ * matters to bench.py's CPU baseline (one thread, then all cores). */
+EXPORT void afref_set_threads(int threads) {
+#ifdef _OPENMP
+  omp_set_num_threads(threads > 0 ? threads : 1);
+#else
+  (void)threads;
+#endif
+}
+
+EXPORT int afref_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
 /* Triangle multiplication                                                   */
 /* ------------------------------------------------------------------------ */
 
@@ -268,6 +295,7 @@ static double sigmoid(double value) { return 1.0 / (1.0 + exp(-value)); }
 /* src/triangle/cpu-reference.ts:6-31 (normalizeRows). */
 static void normalize_rows(const float* input, size_t rows, int channels, const float* weight,
                            const float* bias, double epsilon, float* output) {
+#pragma omp parallel for schedule(static)
   for (size_t row = 0; row < rows; row++) {
     const float* x = input + row * (size_t)channels;
     double mean = 0.0;
@@ -288,6 +316,7 @@ static void normalize_rows(const float* input, size_t rows, int channels, const 
 /* src/triangle/cpu-reference.ts:33-54 (project): weight is [out][in]. */
 static void project(const float* input, size_t rows, int in_channels, int out_channels,
                     const float* weight, const float* bias, float* output) {
+#pragma omp parallel for schedule(static)
   for (size_t row = 0; row < rows; row++)
     for (int o = 0; o < out_channels; o++) {
       double value = (double)bias[o];
@@ -347,6 +376,7 @@ EXPORT void afref_triangle(int direction, int length, int cz, int ch, const floa
   project(zn, pairs, cz, ch, ag_w, ag_b, ag);
   project(zn, pairs, cz, ch, bp_w, bp_b, bp);
   project(zn, pairs, cz, ch, bg_w, bg_b, bg);
+#pragma omp parallel for schedule(static)
   for (size_t pair = 0; pair < pairs; pair++) {
     double m = (double)mask[pair];
     for (int h = 0; h < ch; h++) {
@@ -362,6 +392,7 @@ EXPORT void afref_triangle(int direction, int length, int cz, int ch, const floa
    * order of the sum are unchanged. */
   float* at = (float*)malloc(pairs * ch * sizeof(float));
   float* bt = (float*)malloc(pairs * ch * sizeof(float));
+#pragma omp parallel for schedule(static)
   for (size_t pair = 0; pair < pairs; pair++)
     for (int h = 0; h < ch; h++) {
       at[(size_t)h * pairs + pair] = ap[pair * ch + h];
@@ -371,6 +402,7 @@ EXPORT void afref_triangle(int direction, int length, int cz, int ch, const floa
   for (int h = 0; h < ch; h++) {
     const float* ah = at + (size_t)h * pairs;
     const float* bh = bt + (size_t)h * pairs;
+#pragma omp parallel for schedule(static)
     for (size_t i = 0; i < L; i++)
       for (size_t j = 0; j < L; j++) {
         double value = 0.0;
@@ -392,6 +424,7 @@ EXPORT void afref_triangle(int direction, int length, int cz, int ch, const floa
   project(normalized, pairs, ch, cz, z_w, z_b, out);
   float* gate = (float*)malloc(pairs * cz * sizeof(float));
   project(zn, pairs, cz, cz, g_w, g_b, gate);
+#pragma omp parallel for schedule(static)
   for (size_t index = 0; index < pairs * cz; index++)
     out[index] = (float)((double)out[index] * sigmoid((double)gate[index]));
   free(gate);

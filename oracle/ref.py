@@ -89,6 +89,17 @@ _opm = _sig("afref_opm", None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes
                                 _f32p, _f32p, ctypes.c_double, ctypes.c_double, _f32p])
 _transition = _sig("afref_transition", None, [_sz, ctypes.c_int, ctypes.c_int, _f32p, _f32p,
                                               ctypes.c_double, _f32p])
+_set_threads = _sig("afref_set_threads", None, [ctypes.c_int])
+_max_threads = _sig("afref_max_threads", ctypes.c_int, [])
+
+
+def set_threads(threads: int) -> None:
+    """OpenMP threads of the triangle's loops (same bits at any count)."""
+    _set_threads(int(threads))
+
+
+def max_threads() -> int:
+    return int(_max_threads())
 
 
 def _c32(x) -> np.ndarray:
@@ -232,6 +243,50 @@ def deterministic_triangle_input(length: int, cz: int, ch: int, seed: int = 7) -
     at += pairs
     z = (0 + (r[at:at + pairs * cz] * 2 - 1) * 1).astype(np.float32).reshape(length, length, cz)
     return {"shape": (length, cz, ch), "z": z, "mask": mask, "weights": weights, "epsilon": 1e-5}
+
+
+def triangle_pairs(direction: str, z, mask, weights: dict, pairs, epsilon: float = 1e-5) -> np.ndarray:
+    """out[i, j, :] of the triangle multiplication for the listed (i, j)
+    only, in float64: src/triangle/cpu-reference.ts:6-100 (LayerNorm with
+    the biased variance, weights [out][in], gate from the normalised pair),
+    the incoming direction contracting over the first index
+    (src/triangle/shaders.ts:452-495). Output pair (i, j) reads z's rows i and
+    j (outgoing: sum_k a[i,k] b[j,k]) or columns i and j (incoming:
+    sum_k a[k,j] b[k,i]) and z[i, j] itself, so a sample of pairs at full
+    size costs O(rows * L * c_z * c_h). Returns
+    [len(pairs)][c_z]."""
+    z64 = np.asarray(z, np.float64)
+    m64 = np.asarray(mask, np.float64)
+    w = {k: np.asarray(v, np.float64) for k, v in weights.items()}
+
+    def ln(x, g, b):
+        mean = x.mean(-1, keepdims=True)
+        var = ((x - mean) ** 2).mean(-1, keepdims=True)
+        return (x - mean) / np.sqrt(var + epsilon) * g + b
+
+    def sig(x):
+        return 1.0 / (1.0 + np.exp(-x))
+
+    projected = {}
+    for r in sorted({int(i) for i, _ in pairs} | {int(j) for _, j in pairs}):
+        line = z64[r] if direction == "outgoing" else z64[:, r]
+        keep = (m64[r] if direction == "outgoing" else m64[:, r])[:, None]
+        zn = ln(line, w["layerNormInWeight"], w["layerNormInBias"])
+        a = keep * (zn @ w["linearAPWeight"].T + w["linearAPBias"]) * sig(zn @ w["linearAGWeight"].T + w["linearAGBias"])
+        b = keep * (zn @ w["linearBPWeight"].T + w["linearBPBias"]) * sig(zn @ w["linearBGWeight"].T + w["linearBGBias"])
+        projected[r] = (a, b)
+    out = np.empty((len(pairs), z64.shape[2]))
+    for n, (i, j) in enumerate(pairs):
+        # outgoing ikc,jkc->ijc; incoming kjc,kic->ijc (a follows j, b follows i)
+        if direction == "outgoing":
+            x = (projected[int(i)][0] * projected[int(j)][1]).sum(0)
+        else:
+            x = (projected[int(j)][0] * projected[int(i)][1]).sum(0)
+        x = ln(x, w["layerNormOutWeight"], w["layerNormOutBias"])
+        gate = sig(ln(z64[i, j], w["layerNormInWeight"], w["layerNormInBias"]) @ w["linearGWeight"].T
+                   + w["linearGBias"])
+        out[n] = (x @ w["linearZWeight"].T + w["linearZBias"]) * gate
+    return out
 
 
 def pack_triangle_weights(weights: dict) -> np.ndarray:

@@ -27,7 +27,7 @@ async function main() {
     "executionCreate", "executionDestroy", "executionAllocate", "executionUpload", "executionRelease",
     "executionCheckpoint", "executionReleaseSince", "executionNoteSubmitted", "executionSnapshot",
     "executionAddInPlace", "executionPrepareWeights", "executionPairStack", "executionEvoformerBlock",
-    "setMemoryBudget", "memoryResident"];
+    "setMemoryBudget", "memoryResident", "calibrationClear", "calibrationInject"];
   expected.forEach(function (n) { assert.strictEqual(typeof native[n], "function", n); });
   assert.strictEqual(native.abiVersion(), 3);
 

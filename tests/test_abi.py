@@ -148,6 +148,15 @@ def test_variant_selection_without_device():
     assert (v.tile_rows, v.tile_columns) == (192, 192)
     v = gemm.select_variant(65536, 1024, 128, precision="f16", a_dtype="f16", w_dtype="f16")
     assert (v.tile_rows, v.tile_columns) == (128, 128)
+    # The reference's SHAPES (tools/gemm-candidates.ts:637-669), as measured
+    # by bench.py --gemm-shapes: STREAM from ~16k rows only; a K that is not a
+    # multiple of 8 (opm-contract, K = 508) is staged through registers, one
+    # tile a CU since K is long.
+    f16 = dict(precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f16")
+    assert gemm.select_variant(29972, 256, 1024, **f16).kernel == "stream"
+    assert gemm.select_variant(8192, 128, 512, **f16).kernel == "lds_dma"
+    v = gemm.select_variant(128, 508, 32000, **f16)
+    assert (v.kernel, v.tile_rows, v.tile_columns) == ("register", 128, 64)
 
 
 def test_calibration_document_round_trip(tmp_path):

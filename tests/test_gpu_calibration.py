@@ -1,0 +1,106 @@
+"""Per-device GEMM calibration on the GPU and its failure handling.
+
+The reference's rules (src/runtime/gemm-selection.ts): a candidate that fails
+to build or run is dropped, not allowed to end the calibration (:482-495);
+one whose relative error exceeds 0.02 is refused (:584-586); a remembered
+answer that does not validate is ignored (:543-558); when nothing usable is
+left the kernel in place stays (:590-593, :653-656). Faults are forced from
+the host (afhip_calibration_inject); no kernel is made to fail.
+"""
+import json
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SHAPE = dict(rows=200, inner=64, columns=136, batch=4, precision="f16", a_dtype="f16", w_dtype="f16",
+             out_dtype="f32")
+CANDIDATES = [("register", 64, 64), ("register", 64, 128), ("register", 128, 64), ("register", 128, 128),
+              ("lds_dma", 128, 128), ("lds_dma", 192, 192), ("lds_dma", 128, 256), ("lds_dma", 256, 256),
+              ("stream", 64, 512)]
+
+
+@pytest.fixture()
+def gemm():
+    from afhip import device, gemm
+
+    device.open_device(0)
+    gemm.calibration_clear()
+    gemm.calibration_inject("all", 0, 0, "none")
+    yield gemm
+    gemm.calibration_inject("all", 0, 0, "none")
+    gemm.calibration_clear()
+
+
+def select(gemm):
+    return gemm.select_variant(SHAPE["rows"], SHAPE["inner"], SHAPE["columns"], precision="f16", a_dtype="f16",
+                               w_dtype="f16", out_dtype="f32", batch=SHAPE["batch"])
+
+
+def calibrate(gemm):
+    return gemm.calibrate_variant(SHAPE["rows"], SHAPE["inner"], SHAPE["columns"], precision="f16", a_dtype="f16",
+                                  w_dtype="f16", out_dtype="f32", batch=SHAPE["batch"])
+
+
+def key(v):
+    return (v.kernel, v.tile_rows, v.tile_columns)
+
+
+def test_calibrate_persist_and_reload(gemm, tmp_path):
+    heuristic = select(gemm)
+    assert heuristic.source == "heuristic"
+    won = calibrate(gemm)
+    assert won.source == "calibrated" and key(won) in CANDIDATES
+    assert key(select(gemm)) == key(won) and select(gemm).source == "calibrated"
+    path = str(tmp_path / "calibration.json")
+    gemm.calibration_save(path)
+    doc = json.load(open(path))
+    assert doc["schema"] == 1 and len(doc["entries"]) == 1
+    gemm.calibration_clear()
+    assert select(gemm).source == "heuristic"
+    gemm.calibration_load(path)
+    again = select(gemm)
+    assert again.source == "calibrated" and key(again) == key(won)
+
+
+def test_failed_and_wrong_candidates_are_dropped(gemm):
+    first = calibrate(gemm)
+    # The winner fails to run: it is dropped and another candidate wins.
+    gemm.calibration_inject(first.kernel, first.tile_rows, first.tile_columns, "run")
+    second = calibrate(gemm)
+    assert second.source == "calibrated" and key(second) != key(first)
+    # The new winner reads 5% off the reference: refused as well.
+    gemm.calibration_inject(second.kernel, second.tile_rows, second.tile_columns, "result")
+    third = calibrate(gemm)
+    assert key(third) not in (key(first), key(second))
+    assert key(select(gemm)) == key(third)
+
+
+def test_nothing_usable_keeps_the_heuristic(gemm):
+    for kernel, tr, tc in CANDIDATES:
+        gemm.calibration_inject(kernel, tr, tc, "run" if tr == 64 else "result")
+    out = calibrate(gemm)
+    assert out.source == "heuristic"
+    assert key(out) == key(select(gemm)) and select(gemm).source == "heuristic"
+
+
+@pytest.mark.parametrize("corrupt", ["tile", "kernel", "schema", "garbage", "missing-field"])
+def test_corrupt_document_is_ignored(gemm, tmp_path, corrupt):
+    calibrate(gemm)
+    path = tmp_path / "calibration.json"
+    gemm.calibration_save(str(path))
+    doc = json.load(open(path))
+    entry = next(iter(doc["entries"].values()))
+    if corrupt == "tile":
+        entry["tile_rows"] = 100
+    elif corrupt == "kernel":
+        entry["kernel"] = 7
+    elif corrupt == "schema":
+        doc["schema"] = 2
+    elif corrupt == "missing-field":
+        del entry["tile_columns"]
+    text = "{not json" if corrupt == "garbage" else json.dumps(doc)
+    path.write_text(text)
+    gemm.calibration_clear()
+    gemm.calibration_load(str(path))
+    assert select(gemm).source == "heuristic"

@@ -27,7 +27,7 @@ def run_node(script, timeout=120, env=None):
 @needs_addon
 def test_addon_loads_and_validates_without_gpu():
     out = run_node("abi_check.js")
-    assert out["ok"] and out["exports"] == 42
+    assert out["ok"] and out["exports"] == 44
 
 
 def write_expected(directory):

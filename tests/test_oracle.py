@@ -188,6 +188,64 @@ def test_triangle_outgoing_matches_alphafold_59(name):
     assert m["meanAbsoluteError"] < 1e-5 and m["maxAbsoluteError"] < 1e-4
 
 
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("name", ["openfold-triangle-small", "alphafold-short-9", "alphafold-a3m-59"])
+def test_triangle_pairs_matches_the_whole_operator(name, direction):
+    # The sampled-pair restatement the full-size GPU tests use, against the
+    # oracle's whole operator on every pair of a fixture (the oracle stores
+    # f32 intermediates, this one keeps float64) and, outgoing, against the
+    # fixture's expected output at the reference's CPU tolerances.
+    bundle = golden(name)
+    inp = bundle["input"]
+    L = inp["z"].shape[0]
+    pairs = [(i, j) for i in range(L) for j in range(L)] if L <= 9 else \
+        [(i, j) for i in range(0, L, 7) for j in range(3, L, 5)]
+    got = ref.triangle_pairs(direction, inp["z"], inp["mask"], inp["weights"], pairs, inp["epsilon"])
+    whole = ref.triangle(direction, inp["z"], inp["mask"], inp["weights"], inp["epsilon"])
+    expect = np.stack([whole[i, j] for i, j in pairs])
+    assert np.abs(got - expect).max() <= 2e-6 * max(1.0, np.abs(expect).max())
+    if direction == "outgoing":
+        fixture = bundle["expected"].reshape(L, L, -1)
+        m = ref.error_metrics(got, np.stack([fixture[i, j] for i, j in pairs]))
+        assert m["meanAbsoluteError"] < 1e-6 and m["maxAbsoluteError"] < 1e-5
+
+
+def test_triangle_is_the_same_at_any_thread_count():
+    inp = ref.deterministic_triangle_input(20, 16, 8, seed=3)
+    outs = []
+    for threads in (1, 3, max(ref.max_threads(), 2)):
+        ref.set_threads(threads)
+        outs.append(ref.triangle("incoming", inp["z"], inp["mask"], inp["weights"]))
+    ref.set_threads(ref.max_threads())
+    assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs)
+
+
+def test_js_cpu_reference_matches_oracle(tmp_path):
+    # oracle/cpu_reference.js (bench.py's CPU baseline: the reference's
+    # cpu-reference.ts loops in plain JS) on the reference's deterministic
+    # input, against the C oracle: both accumulate in doubles and store f32
+    # per tensor, so they differ only where Math.exp and libm's exp round a
+    # double differently.
+    import shutil
+    import subprocess
+
+    node = shutil.which("node")
+    if node is None:
+        pytest.skip("no node executable")
+    from conftest import ROOT
+
+    out_file = tmp_path / "js.f32"
+    proc = subprocess.run([node, os.path.join(ROOT, "oracle", "cpu_reference.js"), "12", "16", "8", "7", "--output",
+                           str(out_file)], capture_output=True, text=True, timeout=60)
+    assert proc.returncode == 0, proc.stderr
+    report = __import__("json").loads(proc.stdout.strip().splitlines()[-1])
+    assert report["shape"] == {"length": 12, "cZ": 16, "cHidden": 8} and report["threads"] == 1
+    got = np.fromfile(out_file, dtype="<f4").reshape(12, 12, 16)
+    inp = ref.deterministic_triangle_input(12, 16, 8, seed=7)
+    expect = ref.triangle("outgoing", inp["z"], inp["mask"], inp["weights"])
+    assert np.abs(got - expect).max() <= 1e-6 * max(1.0, np.abs(expect).max())
+
+
 @pytest.mark.parametrize("name", ["openfold-triangle-small", "alphafold-short-9"])
 def test_triangle_incoming_is_transposed_outgoing(name):
     inp = golden(name)["input"]
