@@ -33,6 +33,9 @@ struct GemmArgs {
   int opm_length = 0;
   int opm_row0 = 0;
   float opm_eps = 0.0f;
+  // The fused contraction + output projection (run_opm_fused) only: the
+  // output weights in the order opm_fused_weight_index gives.
+  const void* opm_w = nullptr;
 };
 
 // Epilogue flags private to the library (beyond the public AFHIP_EPILOGUE_*).
@@ -62,6 +65,29 @@ bool dma_tile_supported(int tile_m, int tile_n);
 bool dma_eligible(const GemmArgs& args, const GemmTypes& types);
 void dma_heuristic_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int* tile_m, int* tile_n);
 int run_gemm_dma(const GemmArgs& args, int c_dtype, int tile_m, int tile_n, const char* label, hipStream_t stream);
+
+// The outer-product mean's contraction and output projection in one launch
+// (gemm_dma.hip), for f16 arithmetic with c_outer = 32 and c_z in (96, 128]:
+// A = left [L * 32][K], B = right [L * 32][K] (rows i * 32 + a, k-contiguous,
+// row stride lda = ldb), count [L][L], opm_w the permuted output weights,
+// bias [128], out [L][L][c_z] (row stride ldc = c_z) of dtype c_dtype, plus
+// the old contents when flags has AFHIP_EPILOGUE_RESIDUAL. Every pair (i, j)
+// computes
+//   outer[a][b] = f16(sum_s left[i * 32 + a][s] right[j * 32 + b][s] / (eps + count[i][j]))
+//   out[i][j][z] = sum_(a, b) outer[a][b] W[a * 32 + b][z] + bias[z] / (eps + count[i][j]).
+int run_opm_fused(const GemmArgs& args, int c_dtype, const char* label, hipStream_t stream);
+// Where W[k][z] (k = a * 32 + b, z < 128) sits in the fused kernel's
+// 128 x 1024 f16 weight array. The pair rows in LDS hold (a, b) at half
+// k' = 128 (b / 4) + 4 a + b % 4; an MFMA step reads 16-byte chunk
+// c = 8 Q + 4 h + t of a row (k' in [8 c, 8 c + 8)) in lane half h, so the
+// array is stored in the order the lanes load it, [z / 32][Q][t][h][z % 32]
+// [k' % 8]: every wave-level load of a step's B fragment is 1 KiB contiguous.
+__host__ __device__ inline int64_t opm_fused_weight_index(int k, int z) {
+  const int a = k >> 5, b = k & 31;
+  const int kp = 128 * (b >> 2) + 4 * a + (b & 3);
+  const int c = kp >> 3, Q = c >> 3, h = (c >> 2) & 1, t = c & 3;
+  return (((((int64_t)(z >> 5) * 16 + Q) * 4 + t) * 2 + h) * 32 + (z & 31)) * 8 + (kp & 7);
+}
 
 // The STREAM kernel (gemm_stream.hip): f16 activations and output, f16 or
 // int8 weights held in registers, K in {64, 128, 256}, N % 64 == 0.

@@ -49,7 +49,12 @@ constexpr int kRowBytes = 64;  // one row of a k-step stage
 
 __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
 
-template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC>
+// Epilogue families: GENERIC applies g.flags; OPM_FUSED is the outer-product
+// mean's output projection run on the finished contraction tile.
+constexpr int kEpiGeneric = 0;
+constexpr int kEpiOpmFused = 1;
+
+template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int EPI = kEpiGeneric>
 __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_kernel(gemm_detail::KernelArgs ka) {
   constexpr int WAVES = WM * WN;
   constexpr int kThreads = 64 * WAVES;
@@ -127,6 +132,41 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 #pragma unroll
   for (int s = 0; s < STAGES - 1; s++)
     if (s < nk) issue(s, s);
+
+  // The fused outer-product-mean epilogue (EPI == kEpiOpmFused): the tile is
+  // PI x PJ pairs (NPB blocks of 32); wave w computes output channels
+  // 32 (w % 4) + [0, 32) over part w / 4 of the KP parts of the 1024 k, in
+  // NG groups of 64. Its inputs that do not depend on the contraction load
+  // while it runs: the reciprocal of (eps + count) for the wave's pairs, the
+  // bias of its output channel, eps + count for one pair a thread and the
+  // first PRE groups of its weight fragments. (Extra vector-memory loads only
+  // make the waits on the stage loads stricter: loads complete in order.)
+  constexpr int PI = BM / 32, PJ = BN / 32, NPAIR = PI * PJ, NPB = NPAIR / 32;
+  constexpr int KP = WAVES / 4, NG = 16 / (KP > 0 ? KP : 1), PRE = 2, AHEAD = 6;
+  float rcpv[TM][TN] = {};
+  float bz = 0.0f, dval = 0.0f;
+  half8 wf[NG][4];
+  const half_t* wrow = nullptr;
+  if constexpr (EPI == kEpiOpmFused) {
+    static_assert(NPAIR % 32 == 0 && WAVES % 4 == 0 && (KP == 1 || (KP == 2 && NPB == 2)),
+                  "the fused epilogue's work split");
+    const int L = g.opm_length, ib = m0 >> 5, jb = n0 >> 5;
+    auto count_at = [&](int i, int j) { return i < L && j < L ? g.opm_count[(int64_t)i * L + j] : 0.0f; };
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+        rcpv[i][j] = 1.0f / (g.opm_eps + count_at(ib + (wm >> 5) + i, jb + (wn >> 5) + j));
+    if (threadIdx.x < NPAIR) dval = g.opm_eps + count_at(ib + threadIdx.x / PJ, jb + threadIdx.x % PJ);
+    bz = g.bias[32 * (wave & 3) + (lane & 31)];
+    // Fragment (Q, t) of output-channel block zb starts at half
+    // ((zb * 16 + Q) * 4 + t) * 512; the wave's part starts at Q = (16 / KP) kh.
+    wrow = reinterpret_cast<const half_t*>(g.opm_w) + ((wave & 3) * 16 + (16 / KP) * (wave >> 2)) * 2048 + 8 * lane;
+#pragma unroll
+    for (int q = 0; q < PRE; q++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) wf[q][t] = *reinterpret_cast<const half8*>(wrow + 2048 * q + 512 * t);
+  }
 
   const int frag_row = lane & 31;
   // Fragments of half kk (16 halves of k) of a stage: chunk 2 kk + lane / 32.
@@ -209,6 +249,123 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     asm volatile("" ::: "memory");
   }
 
+  if constexpr (EPI == kEpiOpmFused) {
+#pragma clang fp contract(off)
+    // The tile is the pair block i in [ib, ib + PI) x j in [jb, jb + PJ):
+    // acc[i][j] of wave (wm, wn) is pair p = PJ il + jl with il = wm / 32 + i,
+    // jl = wn / 32 + j, its row a = lane % 32 and columns
+    // b = 8 g4 + 4 (lane / 32) + [0, 4) in group g4.
+    //  1. outer / (eps + count) goes to LDS as f16, pair p in a row of its
+    //     own (PITCH bytes): (a, b) at half 128 (b / 4) + 4 a + b % 4, so
+    //     each wave-level write is 512 contiguous bytes.
+    //  2. out[p][z] = sum_k outer[p][k] W[k][z] on MFMA, every 32-pair block
+    //     against the wave's channels and k part: A fragments come from the
+    //     LDS rows (the 16-byte pad puts 16 consecutive rows on distinct
+    //     banks), B fragments from the weights in the same k order (an
+    //     L2-resident 256 KiB array stored in load order, so each
+    //     wave-level load is 1 KiB contiguous), PRE groups loaded during the
+    //     contraction, the rest AHEAD groups ahead of their MFMAs.
+    //  3. With two k parts they meet in LDS: wave part kh keeps pair block
+    //     kh and adds part 0 + part 1 in that order. Then bias / (eps +
+    //     count) (and the residual) is added and each row of 32 consecutive
+    //     channels is stored.
+    constexpr int PITCH = 2048 + 16;
+    constexpr int DEN = NPAIR * PITCH;
+    static_assert(DEN + NPAIR * 4 <= STAGES * STAGE_BYTES, "the pair rows fit the stage memory");
+    const int L = g.opm_length;
+    const int ib = m0 >> 5, jb = n0 >> 5;
+    const int a = lane & 31, h = lane >> 5;
+    float* const den = reinterpret_cast<float*>(smem + DEN);
+    block_barrier<false>();  // every wave is done reading the stages
+    if (threadIdx.x < NPAIR) den[threadIdx.x] = dval;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int il = (wm >> 5) + i;
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int jl = (wn >> 5) + j;
+        unsigned char* row = smem + (PJ * il + jl) * PITCH;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+          half4 v;
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[e] = (half_t)(acc[i][j][4 * g4 + e] * rcpv[i][j]);
+          *reinterpret_cast<half4*>(row + (((2 * g4 + h) * 32 + a) << 3)) = v;
+        }
+      }
+    }
+    // Group q of the wave's part: chunks (16 bytes) (128 / KP) kh + 8 q + 4 h
+    // + t, t = 0..3, of the pair rows, against the same chunks of weight row
+    // z, which the array holds in load order (opm_fused_weight_index).
+    auto load_group = [&](int q) {
+#pragma unroll
+      for (int t = 0; t < 4; t++) wf[q][t] = *reinterpret_cast<const half8*>(wrow + 2048 * q + 512 * t);
+    };
+#pragma unroll
+    for (int q = PRE; q < PRE + AHEAD; q++)
+      if (q < NG) load_group(q);
+    block_barrier();
+    const int zb = wave & 3, kh = wave >> 2;
+    const int z = 32 * zb + a;
+    const unsigned char* arow = smem + a * PITCH + 16 * ((128 / KP) * kh + 4 * h);
+    floatx16 part[NPB];
+#pragma unroll
+    for (int pb = 0; pb < NPB; pb++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) part[pb][v] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NG; q++) {
+      if (q + PRE + AHEAD < NG) load_group(q + PRE + AHEAD);
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int pb = 0; pb < NPB; pb++) {
+          const half8 af = *reinterpret_cast<const half8*>(arow + 32 * pb * PITCH + 16 * (8 * q + t));
+          part[pb] = mfma_f16(af, wf[q][t], part[pb]);
+        }
+      }
+    }
+    // part[pb][r] = this wave's part of out[p][z], p = 32 pb + 8 (r / 4) + 4 h + r % 4.
+    float y[NPB][16];
+    if constexpr (KP == 2) {
+      block_barrier<false>();  // every wave is done reading the pair rows
+      float* xfer = reinterpret_cast<float*>(smem);
+      const int give = 1 - kh;
+#pragma unroll
+      for (int r = 0; r < 16; r++) xfer[((zb * 2 + give) * 16 + r) * 64 + lane] = kh ? part[0][r] : part[1][r];
+      block_barrier();
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float other = xfer[((zb * 2 + kh) * 16 + r) * 64 + lane];
+        const float mine = kh ? part[1][r] : part[0][r];
+        y[0][r] = kh ? other + mine : mine + other;
+      }
+    } else {
+#pragma unroll
+      for (int pb = 0; pb < NPB; pb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) y[pb][r] = part[pb][r];
+    }
+    constexpr int FIN = KP == 2 ? 1 : NPB;  // pair blocks this wave stores
+    const bool residual = (g.flags & AFHIP_EPILOGUE_RESIDUAL) != 0;
+    TC* C = reinterpret_cast<TC*>(g.c);
+#pragma unroll
+    for (int f = 0; f < FIN; f++) {
+      const int pb = KP == 2 ? kh : f;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int p = 32 * pb + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int i = ib + p / PJ, j = jb + p % PJ;
+        float v = y[f][r] + bz / den[p];
+        if (i < L && j < L && z < g.ldc) {
+          const int64_t at = ((int64_t)i * L + j) * g.ldc + z;
+          if (residual) v += (float)C[at];
+          C[at] = (TC)v;
+        }
+      }
+    }
+    return;
+  }
   if constexpr (sizeof(TC) == 2) {
     if (g.flags == 0 && (g.ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(g.c) & 15) == 0 && (g.sc & 7) == 0) {
       // Plain f16 store (the contraction's case), staged through the stage
@@ -383,6 +540,27 @@ int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(64 * WM * WN), shared, s, ka);
 }
 
+template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC>
+int launch_opm_fused(const GemmArgs& g, const char* label, hipStream_t s) {
+  gemm_detail::KernelArgs ka;
+  ka.g = g;
+  ka.tiles_m = (int)ceil_div(g.M, BM);
+  ka.tiles_n = (int)ceil_div(g.N, BN);
+  ka.total_tiles = ka.tiles_m * ka.tiles_n;
+  ka.per_xcd = (int)ceil_div(ka.total_tiles, 8);
+  const size_t shared = (size_t)STAGES * (BM + BN) * kRowBytes;
+  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC, kEpiOpmFused>;
+  if (int st = allow_lds((const void*)kernel, shared)) return st;
+  return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(64 * WM * WN), shared, s, ka);
+}
+
+// The 256 x 256 tile (64 pairs, one workgroup a CU). Measured at N_seq = 512,
+// N_res = 256 (f32 out): 106 us against 109 us for 128 x 256 tiles (32 pairs,
+// two workgroups a CU, twice the weight traffic).
+template <typename TC> int launch_opm_fused_tile(const GemmArgs& g, const char* label, hipStream_t s) {
+  return launch_opm_fused<256, 256, 5, 2, 4, true, TC>(g, label, s);
+}
+
 template <typename TC> int launch_typed(const GemmArgs& g, int tm, int tn, const char* label, hipStream_t s) {
   if (tm == 192 && tn == 192) return launch_tile<192, 192, 3, 2, 2, false, TC>(g, label, s);
   if (tm == 128 && tn == 128) return launch_tile<128, 128, 4, 2, 2, false, TC>(g, label, s);
@@ -442,6 +620,16 @@ void dma_heuristic_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int* tm,
     return;
   }
   *tm = *tn = 128;
+}
+
+int run_opm_fused(const GemmArgs& g, int c_dtype, const char* label, hipStream_t s) {
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (g.M != 32 * g.opm_length || g.N != g.M || g.K <= 0 || g.K % 8 || g.lda % 8 || g.ldb % 8 || g.lda < g.K ||
+      g.ldb < g.K || !al16(g.a) || !al16(g.b) || !al16(g.opm_w) || g.ldc <= 96 || g.ldc > 128 ||
+      (int64_t)256 * std::max(g.lda, g.ldb) * 2 >= (int64_t)kOutOfRange || (int64_t)g.opm_length * 32 > (1 << 24))
+    return set_error(AFHIP_ERR_INVALID_ARGUMENT, "fused outer-product-mean launch outside its shape");
+  if (c_dtype == AFHIP_F16) return launch_opm_fused_tile<half_t>(g, label, s);
+  return launch_opm_fused_tile<float>(g, label, s);
 }
 
 int run_gemm_dma(const GemmArgs& g, int c_dtype, int tm, int tn, const char* label, hipStream_t s) {

@@ -23,6 +23,12 @@
 //     divided in its epilogue as the reference's contraction does
 //     (:350-417), then the output projection through the shared GEMM with
 //     the bias scaled by the same 1/(eps + count) (:433-481).
+//     Under f16 arithmetic with c_outer = 32 and c_z in (96, 128] (the
+//     model's shapes) both run in one launch instead (run_opm_fused): each
+//     256 x 256 contraction tile is an 8 x 8 block of pairs whose outer
+//     blocks go through LDS straight into the output projection, so outer
+//     never reaches memory and the residue blocking has nothing left to
+//     bound (the same arithmetic, the same f16 rounding of outer).
 #include <algorithm>
 #include <cmath>
 
@@ -33,6 +39,11 @@ namespace afhip {
 namespace {
 
 constexpr int kRows = 64;
+
+// The single-launch contraction + output projection applies.
+bool fused_ok(const afhip_opm_desc& d) {
+  return d.precision == AFHIP_PRECISION_F16 && d.c_outer == 32 && d.c_z > 96 && d.c_z <= 128;
+}
 
 struct OpmWeights {
   size_t ln_scale, ln_offset, w_lr, b_lr, w_out, b_out, total;
@@ -83,7 +94,7 @@ OpmWorkspace opm_workspace(const afhip_opm_desc& d) {
   const size_t rows = (size_t)d.length * d.c_outer;
   w.left = take(es * rows * w.sp);
   w.right = take(es * rows * w.sp);
-  w.outer = take(es * (size_t)w.row_block * d.length * d.c_outer * d.c_outer);
+  w.outer = take(fused_ok(d) ? 0 : es * (size_t)w.row_block * d.length * d.c_outer * d.c_outer);
   w.count = take(4 * (size_t)d.length * d.length);
   w.total = at;
   return w;
@@ -402,6 +413,19 @@ __global__ __launch_bounds__(kFastThreads, 2) void opm_project_fast_kernel(Proje
   }
 }
 
+// Zeros sequences [S, sp) of every left and right row (the fast projection
+// writes them itself): the fused contraction reads whole 8-sequence chunks.
+__global__ void opm_zero_tail_kernel(half_t* __restrict__ left, half_t* __restrict__ right, int64_t rows, int64_t sp,
+                                     int S) {
+  const int pad = (int)(sp - S);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < 2 * rows * pad;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / pad;
+    half_t* dst = r < rows ? left : right;
+    dst[(r < rows ? r : r - rows) * sp + S + (int)(i - r * pad)] = (half_t)0.0f;
+  }
+}
+
 bool project_fast_ok(const afhip_opm_desc& d) {
   return d.precision == AFHIP_PRECISION_F16 && d.c_outer == 32 && (d.c_m == 64 || d.c_m == 128 || d.c_m == 256);
 }
@@ -426,7 +450,8 @@ template <typename MT> int launch_fast_cm(const ProjectArgs& pa, hipStream_t s) 
 template <typename CT>
 __global__ void opm_prepare_kernel(const float* __restrict__ packed, int cm, int co, int cz, int cmp, int cop, int czp,
                                    CT* __restrict__ w_lr, float* __restrict__ b_lr, CT* __restrict__ w_out,
-                                   float* __restrict__ b_out, float* __restrict__ ln_s, float* __restrict__ ln_o) {
+                                   float* __restrict__ b_out, float* __restrict__ ln_s, float* __restrict__ ln_o,
+                                   bool fused) {
   const float* ln_scale = packed;
   const float* ln_offset = ln_scale + cm;
   const float* left_w = ln_offset + cm;
@@ -447,7 +472,9 @@ __global__ void opm_prepare_kernel(const float* __restrict__ packed, int cm, int
     } else if (i < n_lr + n_out) {  // [czp][co*co] <- out [co*co][cz] transposed
       const int64_t j = i - n_lr;
       const int n = (int)(j / (co * co)), k = (int)(j % (co * co));
-      w_out[j] = (CT)(n < cz ? out_w[(size_t)k * cz + n] : 0.0f);
+      // The fused kernel reads them in its fragment order.
+      const int64_t at = fused ? opm_fused_weight_index(k, n) : j;
+      w_out[at] = (CT)(n < cz ? out_w[(size_t)k * cz + n] : 0.0f);
     } else if (i < n_lr + n_out + cop) {
       const int n = (int)(i - n_lr - n_out);
       b_lr[n] = n < co ? left_b[n] : (n < 2 * co ? right_b[n - co] : 0.0f);
@@ -518,12 +545,12 @@ int afhip_opm_prepare_weights(const afhip_opm_desc* desc, const float* packed, v
   if (d.precision == AFHIP_PRECISION_F16) {
     if (int s = launch("opm.prepare", opm_prepare_kernel<half_t>, grid, block, 0, st, packed, d.c_m, d.c_outer, d.c_z,
                        w.cmp, w.cop, w.czp, (half_t*)(base + w.w_lr), (float*)(base + w.b_lr),
-                       (half_t*)(base + w.w_out), (float*)(base + w.b_out), ln_s, ln_o))
+                       (half_t*)(base + w.w_out), (float*)(base + w.b_out), ln_s, ln_o, fused_ok(d)))
       return s;
   } else {
     if (int s = launch("opm.prepare", opm_prepare_kernel<float>, grid, block, 0, st, packed, d.c_m, d.c_outer, d.c_z,
                        w.cmp, w.cop, w.czp, (float*)(base + w.w_lr), (float*)(base + w.b_lr),
-                       (float*)(base + w.w_out), (float*)(base + w.b_out), ln_s, ln_o))
+                       (float*)(base + w.w_out), (float*)(base + w.b_out), ln_s, ln_o, false))
       return s;
   }
   return AFHIP_OK;
@@ -565,7 +592,8 @@ int afhip_opm_run(const afhip_opm_desc* desc, const void* activations, const flo
   size_t psh = round_up((int64_t)w.cmp * (kRows + 1) * 4, 16) +
                (f16 ? round_up((int64_t)kRows * (w.cmp + 8) * 2, 16) : 0) + (size_t)64 * (kRows + 8) * (f16 ? 2 : 4);
   int s;
-  if (project_fast_ok(d) && (reinterpret_cast<uintptr_t>(activations) & 15) == 0)
+  const bool fast = project_fast_ok(d) && (reinterpret_cast<uintptr_t>(activations) & 15) == 0;
+  if (fast)
     s = d.msa_dtype == AFHIP_F32 ? launch_fast_cm<float>(pa, st) : launch_fast_cm<half_t>(pa, st);
   else if (f16)
     s = d.msa_dtype == AFHIP_F32 ? launch_project<float, true>(pa, psh, st) : launch_project<half_t, true>(pa, psh, st);
@@ -581,6 +609,29 @@ int afhip_opm_run(const afhip_opm_desc* desc, const void* activations, const flo
       return s;
   }
 
+  if (fused_ok(d)) {
+    if (!fast && ws.sp > S) {
+      const int64_t rows = (int64_t)L * co, n = 2 * rows * (ws.sp - S);
+      if ((s = launch("opm.zero_tail", opm_zero_tail_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 1024)),
+                      dim3(256), 0, st, (half_t*)(wsb + ws.left), (half_t*)(wsb + ws.right), rows, ws.sp, S)))
+        return s;
+    }
+    GemmArgs g;
+    g.a = wsb + ws.left;
+    g.b = wsb + ws.right;
+    g.c = out;
+    g.bias = (const float*)(wb + w.b_out);
+    g.opm_w = wb + w.w_out;
+    g.M = g.N = L * co;
+    g.K = (int)ws.sp;  // sequences [S, sp) are zeros
+    g.lda = g.ldb = ws.sp;
+    g.ldc = d.c_z;
+    g.flags = d.residual ? AFHIP_EPILOGUE_RESIDUAL : 0u;
+    g.opm_count = count;
+    g.opm_length = L;
+    g.opm_eps = d.normalization_epsilon;
+    return run_opm_fused(g, d.out_dtype, "opm.fused", st);
+  }
   const int ct = f16 ? AFHIP_F16 : AFHIP_F32;
   const size_t es = f16 ? 2 : 4;
   for (int i0 = 0; i0 < L; i0 += ws.row_block) {

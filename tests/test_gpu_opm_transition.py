@@ -116,6 +116,61 @@ def test_opm_f16_fast_projection(dev, S, L, cm, msa_dtype):
     assert np.abs(out - expect).max() <= 1e-2 * scale
 
 
+def fused_case(S, L, cm, cz, seed):
+    co = 32
+    act = ref.round_f16(ref.normal(seed, (S, L, cm)))
+    mask = (ref.uniform(seed + 1, (S, L), 0, 1) > 0.2).astype(np.float32)
+    mask[:, L // 2] = 0.0  # residue L / 2 never aligned: its pairs count 0 (bias / eps)
+    w = {"layerNormScale": ref.normal(seed + 2, (cm,), 0.1, 1.0), "layerNormOffset": ref.normal(seed + 3, (cm,), 0.1),
+         "leftWeight": ref.normal(seed + 4, (cm, co), 1 / cm), "leftBias": ref.normal(seed + 5, (co,), 0.02),
+         "rightWeight": ref.normal(seed + 6, (cm, co), 1 / cm), "rightBias": ref.normal(seed + 7, (co,), 0.02),
+         "outputWeight": ref.normal(seed + 8, (co * co, cz), 1 / (co * co)),
+         "outputBias": ref.normal(seed + 9, (cz,), 0.02)}
+    return act, mask, w
+
+
+@pytest.mark.parametrize("S,L,cm,cz,out_dtype,residual", [(64, 13, 64, 128, "f32", False),
+                                                          (40, 45, 64, 100, "f16", True),
+                                                          (512, 8, 256, 128, "f32", True),
+                                                          (7, 70, 40, 128, "f16", False)])
+def test_opm_fused_contraction_output(dev, S, L, cm, cz, out_dtype, residual):
+    # The single-launch contraction + output projection (f16, c_outer 32,
+    # c_z in (96, 128]): residue counts off the 8-residue pair blocks, a
+    # c_z below the 128 the weights are padded to, an all-masked residue,
+    # f16 and f32 output, the residual added to the output's old contents,
+    # a sequence count off the 8-sequence chunks after the general
+    # projection (c_m 40); against the f64 oracle within the f16 tolerance,
+    # and bit-identical whatever the residue blocking.
+    import torch
+
+    from afhip import opm
+
+    act, mask, w = fused_case(S, L, cm, cz, 100 + L)
+    expect = ref.opm(act, mask, w).astype(np.float64)
+    old = ref.normal(7 * L, (L, L, cz)) if residual else np.zeros((L, L, cz))
+    if out_dtype == "f16":
+        old = ref.round_f16(old)
+    tdt = torch.float16 if out_dtype == "f16" else torch.float32
+    outs = []
+    for rb in (0, 3):
+        op = opm.OuterProductMean(S, L, cm, 32, cz, precision="f16", msa_dtype="f16", out_dtype=out_dtype,
+                                  row_block=rb, residual=residual)
+        op.prepare(w)
+        out = torch.from_numpy(old).to(dev, tdt)
+        op(torch.from_numpy(act).to(dev, torch.float16), torch.from_numpy(mask).to(dev), out)
+        outs.append(out.float().cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    want = expect + old
+    scale = max(1.0, float(np.abs(want).max()))
+    err = np.abs(outs[0] - want)
+    print(f"fused S={S} L={L} cz={cz} {out_dtype}: max|d| {err.max():.3e} scale {scale:.3f}", flush=True)
+    assert err.max() <= 1e-2 * scale
+    # The never-aligned residue: row and column L / 2 are bias / eps exactly
+    # up to the output rounding.
+    r = L // 2
+    assert np.allclose(outs[0][r] - old[r], w["outputBias"] / 1e-3, rtol=2e-3, atol=1e-2)
+
+
 def test_opm_all_masked_row_gives_bias_over_eps(dev):
     from afhip import opm
 
