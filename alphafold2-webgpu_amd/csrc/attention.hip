@@ -30,6 +30,7 @@
 // a one-thread-per-query kernel in f32 on the natural units.
 #include <algorithm>
 #include <cmath>
+#include <cstddef>
 #include <utility>
 
 #include "gemm.h"
@@ -486,6 +487,9 @@ constexpr int kFlashQueryWaves = 4;
 constexpr int kFlashThreads = 64 * kFlashBatch * kFlashQueryWaves;
 constexpr float kLogitBound = 30000.0f;
 constexpr float kSlack = 8.0f;
+// Base-2 distance below the row maximum past which exp2 gives 0 in f32
+// (below 2^-149) and therefore in f16.
+constexpr float kClampReach = 160.0f;
 
 struct FlashTile {
   half_t k[kFlashBatch][32][40];   // [bi][key][channel], rows padded to 80 bytes
@@ -516,7 +520,7 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   // holding row c / 8, keys 4 (c % 8)..).
   const half_t* tile_src;
   int64_t tile_step;  // elements per key block
-  half_t* tile_dst[2];
+  uint32_t tile_dst;  // byte offset in tiles[0]; tiles[1] is sizeof(FlashTile) further
   {
     const int part = tid >> 7;
     const int u = tid & 127;
@@ -529,18 +533,18 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
       tile_src = a.vt + (be * a.H + h) * a.key_blocks * 1024 + u * 8;
       tile_step = 1024;
     }
-    for (int t = 0; t < 2; t++)
-      tile_dst[t] = part < 2 ? &tiles[t].k[e][u >> 2][8 * (u & 3)] : &tiles[t].vt[e][u >> 2][8 * (u & 3)];
+    const uint32_t at = 2u * (uint32_t)((e * 32 + (u >> 2)) * 40 + 8 * (u & 3));
+    tile_dst = (uint32_t)(part < 2 ? offsetof(FlashTile, k) : offsetof(FlashTile, vt)) + at;
   }
   const float* bias_src[2] = {nullptr, nullptr};
-  float* bias_dst[2][2] = {};
+  uint32_t bias_dst[2] = {};
   if (BIAS) {
     for (int i = 0; i < 2; i++) {
       const int c = tid + kFlashThreads * i;
       const int r = c >> 3;
       const int q = min(qbase + r, Q - 1);
       bias_src[i] = a.bias + ((int64_t)h * Q + q) * a.stride + 4 * (c & 7);
-      for (int t = 0; t < 2; t++) bias_dst[t][i] = &tiles[t].bias[r][4 * (c & 7)];
+      bias_dst[i] = (uint32_t)offsetof(FlashTile, bias) + 4u * (uint32_t)(r * 36 + 4 * (c & 7));
     }
   }
   static_assert(2 * kFlashThreads * 4 == 32 * kFlashQueryWaves * 32, "two bias pieces a lane cover the tile");
@@ -556,11 +560,15 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
       staged[2] = *reinterpret_cast<const uint4*>(bias_src[1] + k0);
     }
   };
+  // Byte offsets into the __shared__ array (not generic pointers), so the
+  // writes are LDS stores.
+  unsigned char* const lds_tiles = reinterpret_cast<unsigned char*>(tiles);
   auto stash = [&](int t) {
-    *reinterpret_cast<uint4*>(tile_dst[t]) = staged[0];
+    unsigned char* const tb = lds_tiles + t * (uint32_t)sizeof(FlashTile);
+    *reinterpret_cast<uint4*>(tb + tile_dst) = staged[0];
     if (BIAS) {
-      *reinterpret_cast<uint4*>(bias_dst[t][0]) = staged[1];
-      *reinterpret_cast<uint4*>(bias_dst[t][1]) = staged[2];
+      *reinterpret_cast<uint4*>(tb + bias_dst[0]) = staged[1];
+      *reinterpret_cast<uint4*>(tb + bias_dst[1]) = staged[2];
     }
   };
 
@@ -603,17 +611,30 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
     sc = __builtin_amdgcn_mfma_f32_32x32x8f16(am, bm_frag, sc, 0, 0, 0);
     float x[16];
 #pragma unroll
-    for (int v = 0; v < 16; v++) x[v] = __builtin_amdgcn_fmed3f(sc[v], lo, up);
-    if (k0 + 32 > Q) {  // the last block: keys past the end take no weight
+    for (int v = 0; v < 16; v++) x[v] = sc[v];
+    const bool last = k0 + 32 > Q;
+    auto drop_past_end = [&]() {  // the last block: keys past the end take no weight
 #pragma unroll
       for (int g = 0; g < 4; g++)
 #pragma unroll
         for (int i = 0; i < 4; i++)
           if (k0 + 8 * g + 4 * hi + i >= Q) x[4 * g + i] = -INFINITY;
-    }
+    };
+    if (last) drop_past_end();
     float bm = x[0];
 #pragma unroll
     for (int v = 1; v < 16; v++) bm = fmaxf(bm, x[v]);
+    // The clamp to [lo, up] changes a probability only where the block's
+    // largest logit is above up or within kClampReach of lo: otherwise
+    // every logit below lo, clamped or not, is more than kClampReach under
+    // the row's maximum and its probability underflows to 0 in f32 and f16
+    // alike. So it runs (exactly) only for such blocks.
+    if (__builtin_amdgcn_ballot_w64(bm > up || bm < lo + kClampReach)) {
+#pragma unroll
+      for (int v = 0; v < 16; v++) x[v] = __builtin_amdgcn_fmed3f(x[v], lo, up);
+      if (last) drop_past_end();
+      bm = __builtin_amdgcn_fmed3f(bm, lo, up);
+    }
     if (first || __builtin_amdgcn_ballot_w64(bm > kSlack)) {
       // Move m to the pair's maximum, rounded to the nearest f16: the first
       // block sets it, a later one only raises it. Within [-kLogitBound,
