@@ -138,13 +138,13 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   // 32 (w % 4) + [0, 32) over part w / 4 of the KP parts of the 1024 k, in
   // NG groups of 64. Its inputs that do not depend on the contraction load
   // while it runs: the reciprocal of (eps + count) for the wave's pairs, the
-  // bias of its output channel, eps + count for one pair a thread and the
-  // first PRE groups of its weight fragments. (Extra vector-memory loads only
+  // bias of its output channel and the first PRE groups of its weight
+  // fragments. (Extra vector-memory loads only
   // make the waits on the stage loads stricter: loads complete in order.)
   constexpr int PI = BM / 32, PJ = BN / 32, NPAIR = PI * PJ, NPB = NPAIR / 32;
   constexpr int KP = WAVES / 4, NG = 16 / (KP > 0 ? KP : 1), PRE = 2, AHEAD = 6;
   float rcpv[TM][TN] = {};
-  float bz = 0.0f, dval = 0.0f;
+  float bz = 0.0f;
   half8 wf[NG][4];
   const half_t* wrow = nullptr;
   if constexpr (EPI == kEpiOpmFused) {
@@ -157,7 +157,6 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 #pragma unroll
       for (int j = 0; j < TN; j++)
         rcpv[i][j] = 1.0f / (g.opm_eps + count_at(ib + (wm >> 5) + i, jb + (wn >> 5) + j));
-    if (threadIdx.x < NPAIR) dval = g.opm_eps + count_at(ib + threadIdx.x / PJ, jb + threadIdx.x % PJ);
     bz = g.bias[32 * (wave & 3) + (lane & 31)];
     // Fragment (Q, t) of output-channel block zb starts at half
     // ((zb * 16 + Q) * 4 + t) * 512; the wave's part starts at Q = (16 / KP) kh.
@@ -255,42 +254,44 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     // acc[i][j] of wave (wm, wn) is pair p = PJ il + jl with il = wm / 32 + i,
     // jl = wn / 32 + j, its row a = lane % 32 and columns
     // b = 8 g4 + 4 (lane / 32) + [0, 4) in group g4.
-    //  1. outer / (eps + count) goes to LDS as f16, pair p in a row of its
-    //     own (PITCH bytes): (a, b) at half 128 (b / 4) + 4 a + b % 4, so
-    //     each wave-level write is 512 contiguous bytes.
+    //  1. outer / (eps + count) goes to LDS as f16, pair p in a 2 KiB row
+    //     of its own: (a, b) at half k' = 128 (b / 4) + 4 a + b % 4, whose
+    //     16-byte chunk c = k' / 8 sits at slot c ^ (p % 16), so each
+    //     wave-level write is 512 contiguous bytes and the 16 rows a 16-lane
+    //     group of a fragment read covers fall on distinct banks.
     //  2. out[p][z] = sum_k outer[p][k] W[k][z] on MFMA, every 32-pair block
-    //     against the wave's channels and k part: A fragments come from the
-    //     LDS rows (the 16-byte pad puts 16 consecutive rows on distinct
-    //     banks), B fragments from the weights in the same k order (an
+    //     against the wave's channels and k part: A fragments from the LDS
+    //     rows, B fragments from the weights in the same k order (an
     //     L2-resident 256 KiB array stored in load order, so each
     //     wave-level load is 1 KiB contiguous), PRE groups loaded during the
     //     contraction, the rest AHEAD groups ahead of their MFMAs.
-    //  3. With two k parts they meet in LDS: wave part kh keeps pair block
-    //     kh and adds part 0 + part 1 in that order. Then bias / (eps +
-    //     count) (and the residual) is added and each row of 32 consecutive
-    //     channels is stored.
-    constexpr int PITCH = 2048 + 16;
-    constexpr int DEN = NPAIR * PITCH;
-    static_assert(DEN + NPAIR * 4 <= STAGES * STAGE_BYTES, "the pair rows fit the stage memory");
+    //  3. With two k parts they meet in LDS past the pair rows: wave part kh
+    //     keeps pair block kh and adds part 0 + part 1 in that order. Then
+    //     bias / (eps + count) (and the residual) is added and each row of 32
+    //     consecutive channels is stored.
+    constexpr int ROW = 2048;
+    constexpr int XFER = NPAIR * ROW;
+    static_assert(XFER + (KP == 2 ? WAVES * 16 * 64 * 4 : 0) <= STAGES * STAGE_BYTES,
+                  "the pair rows and the exchange fit the stage memory");
     const int L = g.opm_length;
     const int ib = m0 >> 5, jb = n0 >> 5;
     const int a = lane & 31, h = lane >> 5;
-    float* const den = reinterpret_cast<float*>(smem + DEN);
     block_barrier<false>();  // every wave is done reading the stages
-    if (threadIdx.x < NPAIR) den[threadIdx.x] = dval;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int il = (wm >> 5) + i;
 #pragma unroll
       for (int j = 0; j < TN; j++) {
         const int jl = (wn >> 5) + j;
-        unsigned char* row = smem + (PJ * il + jl) * PITCH;
+        const int p = PJ * il + jl;
+        unsigned char* row = smem + p * ROW + 8 * (a & 1);
 #pragma unroll
         for (int g4 = 0; g4 < 4; g4++) {
           half4 v;
 #pragma unroll
           for (int e = 0; e < 4; e++) v[e] = (half_t)(acc[i][j][4 * g4 + e] * rcpv[i][j]);
-          *reinterpret_cast<half4*>(row + (((2 * g4 + h) * 32 + a) << 3)) = v;
+          const int c = (2 * g4 + h) * 16 + (a >> 1);
+          *reinterpret_cast<half4*>(row + 16 * (c ^ (p & 15))) = v;
         }
       }
     }
@@ -307,48 +308,10 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     block_barrier();
     const int zb = wave & 3, kh = wave >> 2;
     const int z = 32 * zb + a;
-    const unsigned char* arow = smem + a * PITCH + 16 * ((128 / KP) * kh + 4 * h);
-    floatx16 part[NPB];
-#pragma unroll
-    for (int pb = 0; pb < NPB; pb++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) part[pb][v] = 0.0f;
-#pragma unroll
-    for (int q = 0; q < NG; q++) {
-      if (q + PRE + AHEAD < NG) load_group(q + PRE + AHEAD);
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-#pragma unroll
-        for (int pb = 0; pb < NPB; pb++) {
-          const half8 af = *reinterpret_cast<const half8*>(arow + 32 * pb * PITCH + 16 * (8 * q + t));
-          part[pb] = mfma_f16(af, wf[q][t], part[pb]);
-        }
-      }
-    }
-    // part[pb][r] = this wave's part of out[p][z], p = 32 pb + 8 (r / 4) + 4 h + r % 4.
-    float y[NPB][16];
-    if constexpr (KP == 2) {
-      block_barrier<false>();  // every wave is done reading the pair rows
-      float* xfer = reinterpret_cast<float*>(smem);
-      const int give = 1 - kh;
-#pragma unroll
-      for (int r = 0; r < 16; r++) xfer[((zb * 2 + give) * 16 + r) * 64 + lane] = kh ? part[0][r] : part[1][r];
-      block_barrier();
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float other = xfer[((zb * 2 + kh) * 16 + r) * 64 + lane];
-        const float mine = kh ? part[1][r] : part[0][r];
-        y[0][r] = kh ? other + mine : mine + other;
-      }
-    } else {
-#pragma unroll
-      for (int pb = 0; pb < NPB; pb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) y[pb][r] = part[pb][r];
-    }
     constexpr int FIN = KP == 2 ? 1 : NPB;  // pair blocks this wave stores
-    const bool residual = (g.flags & AFHIP_EPILOGUE_RESIDUAL) != 0;
-    TC* C = reinterpret_cast<TC*>(g.c);
+    // eps + count of the pairs this lane stores, p = 32 pb + 8 (r / 4) + 4 h
+    // + r % 4, read while the MFMAs run.
+    float dnv[FIN][16];
 #pragma unroll
     for (int f = 0; f < FIN; f++) {
       const int pb = KP == 2 ? kh : f;
@@ -356,12 +319,96 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
       for (int r = 0; r < 16; r++) {
         const int p = 32 * pb + 8 * (r >> 2) + 4 * h + (r & 3);
         const int i = ib + p / PJ, j = jb + p % PJ;
-        float v = y[f][r] + bz / den[p];
-        if (i < L && j < L && z < g.ldc) {
-          const int64_t at = ((int64_t)i * L + j) * g.ldc + z;
-          if (residual) v += (float)C[at];
-          C[at] = (TC)v;
+        dnv[f][r] = g.opm_eps + (i < L && j < L ? g.opm_count[(int64_t)i * L + j] : 0.0f);
+      }
+    }
+    const unsigned char* arow = smem + a * ROW;
+    const int aswz = a & 15;  // the rows 32 pb + a share their low four bits
+    floatx16 part[NPB];
+#pragma unroll
+    for (int pb = 0; pb < NPB; pb++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) part[pb][v] = 0.0f;
+    float bterm[FIN][16];  // bias / (eps + count), computed among the MFMAs
+#pragma unroll
+    for (int q = 0; q < NG; q++) {
+      if (q + PRE + AHEAD < NG) load_group(q + PRE + AHEAD);
+      if (q == NG / 2) {
+#pragma unroll
+        for (int f = 0; f < FIN; f++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) bterm[f][r] = bz / dnv[f][r];
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int c = (128 / KP) * kh + 8 * q + 4 * h + t;
+#pragma unroll
+        for (int pb = 0; pb < NPB; pb++) {
+          const half8 af = *reinterpret_cast<const half8*>(arow + 32 * pb * ROW + 16 * (c ^ aswz));
+          part[pb] = mfma_f16(af, wf[q][t], part[pb]);
         }
+      }
+    }
+    // part[pb][r] = this wave's part of out[p][z], p = 32 pb + 8 (r / 4) + 4 h + r % 4.
+    float y[NPB][16];
+    if constexpr (KP == 2) {
+      // The exchange area lies past the pair rows, so no wave waits for the
+      // others to finish reading them.
+      // Slot (zb, pair block) holds each lane's 16 values as four 16-byte
+      // chunks, chunk c of lane l at l * 64 + 16 (c ^ (l / 4 % 4)): the 16
+      // lanes of an access fall on distinct banks.
+      unsigned char* const xfer = smem + XFER;
+      const int give = 1 - kh;
+      const int xs = (lane >> 2) & 3;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        floatx4 v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = kh ? part[0][4 * c + e] : part[1][4 * c + e];
+        *reinterpret_cast<floatx4*>(xfer + (zb * 2 + give) * 4096 + lane * 64 + 16 * (c ^ xs)) = v;
+      }
+      block_barrier();
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const floatx4 other = *reinterpret_cast<const floatx4*>(xfer + (zb * 2 + kh) * 4096 + lane * 64 + 16 * (c ^ xs));
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float mine = kh ? part[1][4 * c + e] : part[0][4 * c + e];
+          y[0][4 * c + e] = kh ? other[e] + mine : mine + other[e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int pb = 0; pb < NPB; pb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) y[pb][r] = part[pb][r];
+    }
+    const bool residual = (g.flags & AFHIP_EPILOGUE_RESIDUAL) != 0;
+    TC* C = reinterpret_cast<TC*>(g.c);
+#pragma unroll
+    for (int f = 0; f < FIN; f++) {
+      const int pb = KP == 2 ? kh : f;
+      int64_t at[16];
+      bool on[16];
+      float old[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int p = 32 * pb + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int i = ib + p / PJ, j = jb + p % PJ;
+        on[r] = i < L && j < L && z < g.ldc;
+        at[r] = ((int64_t)i * L + j) * g.ldc + z;
+        old[r] = 0.0f;
+      }
+      if (residual) {  // every old value in flight before the first store
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          if (on[r]) old[r] = (float)C[at[r]];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        float v = y[f][r] + bterm[f][r];
+        if (residual) v += old[r];
+        if (on[r]) C[at[r]] = (TC)v;
       }
     }
     return;

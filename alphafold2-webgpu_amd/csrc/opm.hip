@@ -17,7 +17,8 @@
 //     weights resident in VGPRs, and 128-byte channel-major stores.
 //  2. pair count: count[i][j] = sum_s mask[s][i] mask[s][j] (:317-332), as an
 //     f32 GEMM of the transposed mask with itself (exact for 0/1 masks, whose
-//     partial sums are small integers).
+//     partial sums are small integers). With the fast projection its tiles
+//     are extra workgroups of the projection's launch.
 //  3. per residue block, the contraction through the shared GEMM,
 //     outer[i][j][a][b] = sum_s left[s][i][a] right[s][j][b] / (eps + count),
 //     divided in its epilogue as the reference's contraction does
@@ -216,27 +217,27 @@ __global__ __launch_bounds__(256) void opm_project_kernel(ProjectArgs a) {
 }
 
 // Pair counts count[i][j] = sum_s mask[s][i] mask[s][j] (the masked
-// sequence count per pair, outer-product-mean.ts:317-332): one 32 x 32 tile
-// of counts per workgroup. Its sixteen waves take interleaved two-sequence
-// steps of the f32 MFMA, both operands read straight from the [S][L] mask
-// (A = mask[s][i0 + m], B = mask[s][j0 + n]), then sum their partial tiles in
-// LDS in wave order, so the result does not depend on timing.
-constexpr int kCountWaves = 16;
-__global__ __launch_bounds__(64 * kCountWaves) void opm_pair_count_kernel(const float* __restrict__ mask, int S, int L,
-                                                                          float* __restrict__ count) {
-  __shared__ float part[kCountWaves][16][64];
+// sequence count per pair, outer-product-mean.ts:317-332) of one 32 x 32
+// tile, by the WAVES waves of the calling workgroup: they take interleaved
+// two-sequence steps of the f32 MFMA, both operands read straight from the
+// [S][L] mask (A = mask[s][i0 + m], B = mask[s][j0 + n]), then sum their
+// partial tiles in LDS (`part`, WAVES x 4 KiB) in wave order, so the result
+// does not depend on timing.
+template <int WAVES>
+__device__ __forceinline__ void pair_count_tile(const float* __restrict__ mask, int S, int L, float* __restrict__ count,
+                                                int tile, float* part) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tiles = (L + 31) / 32;
-  const int i0 = (blockIdx.x / tiles) * 32, j0 = (blockIdx.x % tiles) * 32;
+  const int i0 = (tile / tiles) * 32, j0 = (tile % tiles) * 32;
   const int col = lane & 31, hi = lane >> 5;
   const bool in_i = i0 + col < L, in_j = j0 + col < L;
   floatx16 acc = {};
   // Four steps' loads go out together before their MFMAs.
-  for (int s0 = 2 * wave; s0 < S; s0 += 8 * kCountWaves) {
+  for (int s0 = 2 * wave; s0 < S; s0 += 8 * WAVES) {
     float a[4], b[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      const int s = s0 + 2 * kCountWaves * u + hi;
+      const int s = s0 + 2 * WAVES * u + hi;
       a[u] = s < S && in_i ? mask[(int64_t)s * L + i0 + col] : 0.0f;
       b[u] = s < S && in_j ? mask[(int64_t)s * L + j0 + col] : 0.0f;
     }
@@ -244,16 +245,26 @@ __global__ __launch_bounds__(64 * kCountWaves) void opm_pair_count_kernel(const 
     for (int u = 0; u < 4; u++) acc = mfma_f32(a[u], b[u], acc);
   }
 #pragma unroll
-  for (int v = 0; v < 16; v++) part[wave][v][lane] = acc[v];
+  for (int v = 0; v < 16; v++) part[(wave * 16 + v) * 64 + lane] = acc[v];
   __syncthreads();
   // Element (m, n) of the tile sits at row v = 4 (m / 8) + m % 4 of lane
   // n + 32 ((m / 4) % 2).
-  const int m = threadIdx.x >> 5, n = threadIdx.x & 31;
-  const int v = 4 * (m >> 3) + (m & 3), l = n + 32 * ((m >> 2) & 1);
-  float sum = 0.0f;
+  for (int e = threadIdx.x; e < 1024; e += 64 * WAVES) {
+    const int m = e >> 5, n = e & 31;
+    const int v = 4 * (m >> 3) + (m & 3), l = n + 32 * ((m >> 2) & 1);
+    float sum = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kCountWaves; w++) sum += part[w][v][l];
-  if (i0 + m < L && j0 + n < L) count[(int64_t)(i0 + m) * L + j0 + n] = sum;
+    for (int w = 0; w < WAVES; w++) sum += part[(w * 16 + v) * 64 + l];
+    if (i0 + m < L && j0 + n < L) count[(int64_t)(i0 + m) * L + j0 + n] = sum;
+  }
+}
+
+// The pair counts on their own: one 32 x 32 tile per sixteen-wave workgroup.
+constexpr int kCountWaves = 16;
+__global__ __launch_bounds__(64 * kCountWaves) void opm_pair_count_kernel(const float* __restrict__ mask, int S, int L,
+                                                                          float* __restrict__ count) {
+  __shared__ float part[kCountWaves * 16 * 64];
+  pair_count_tile<kCountWaves>(mask, S, L, count, blockIdx.x, part);
 }
 
 // ---------------------------------------------------------------------------
@@ -300,9 +311,13 @@ template <> struct RowChunk<float> {
 // LPR = CM / 8 lanes per row, 8 channels per lane. The projection is
 // x_hat [64 x CM] (A operand, from LDS) times W^T (B operand, VGPRs): wave w
 // computes rows 32 (w & 1) and output columns 32 (w >> 1) (left, then right).
+// The first count_blocks workgroups of the launch compute the pair counts
+// instead (one 32 x 32 tile each, pair_count_tile), so they need no launch
+// of their own; they come first so they are dispatched first.
 template <int CM, typename MT>
 __global__ __launch_bounds__(kFastThreads, 2) void opm_project_fast_kernel(ProjectArgs a, int ntiles,
-                                                                          int tiles_per_res) {
+                                                                          int tiles_per_res, int count_blocks,
+                                                                          float* __restrict__ count) {
   using Lay = FastLayout<CM>;
   constexpr int LPR = CM / 8;             // lanes per row
   constexpr int RPL = 64 / LPR;           // rows per wave-level load
@@ -345,10 +360,15 @@ __global__ __launch_bounds__(kFastThreads, 2) void opm_project_fast_kernel(Proje
     if (tid < kFastRows) mval = s0 + tid < a.S ? a.mask[(int64_t)(s0 + tid) * a.L + res] : 0.0f;
   };
 
-  int t = blockIdx.x;
+  if ((int)blockIdx.x < count_blocks) {
+    pair_count_tile<kFastThreads / 64>(a.mask, a.S, a.L, count, blockIdx.x, reinterpret_cast<float*>(smem));
+    return;
+  }
+  const int G = (int)gridDim.x - count_blocks;
+  int t = (int)blockIdx.x - count_blocks;
   if (t >= ntiles) return;
   fetch(t);
-  for (; t < ntiles; t += gridDim.x) {
+  for (; t < ntiles; t += G) {
     const int res = t / tiles_per_res, s0 = (t - res * tiles_per_res) * kFastRows;
     // LayerNorm: two-pass mean and biased variance in f32, eps inside the
     // root (outer-product-mean.ts:221-261), the affine applied per channel.
@@ -374,7 +394,7 @@ __global__ __launch_bounds__(kFastThreads, 2) void opm_project_fast_kernel(Proje
       *reinterpret_cast<half8*>(xhat + row * Lay::APITCH + c0) = h;
     }
     if (tid < kFastRows) mbuf[tid] = mval;
-    if (t + (int)gridDim.x < ntiles) fetch(t + gridDim.x);  // lands while this tile computes
+    if (t + G < ntiles) fetch(t + G);  // lands while this tile computes
     __syncthreads();
 
     floatx16 acc;
@@ -430,21 +450,27 @@ bool project_fast_ok(const afhip_opm_desc& d) {
   return d.precision == AFHIP_PRECISION_F16 && d.c_outer == 32 && (d.c_m == 64 || d.c_m == 128 || d.c_m == 256);
 }
 
-template <int CM, typename MT> int launch_fast(const ProjectArgs& pa, hipStream_t s) {
+// Three workgroups a CU (their VGPRs allow it at every c_m): 21.6 us
+// against 23.5 us for two at N_seq = 512, N_res = 256, c_m = 256.
+template <int CM, typename MT> int launch_fast(const ProjectArgs& pa, float* count, hipStream_t s) {
   auto k = opm_project_fast_kernel<CM, MT>;
   constexpr size_t bytes = FastLayout<CM>::BYTES;
+  static_assert(bytes >= (size_t)(kFastThreads / 64) * 16 * 64 * 4, "the pair-count partials fit");
   if (int st = allow_lds((const void*)k, bytes)) return st;
   const int tiles_per_res = (int)ceil_div(pa.S, kFastRows);
   const int ntiles = tiles_per_res * pa.L;
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  const int grid = std::min(ntiles, 2 * cus);
-  return launch("opm.project", k, dim3((unsigned)grid), dim3(kFastThreads), bytes, s, pa, ntiles, tiles_per_res);
+  const int grid = std::min(ntiles, 3 * cus);
+  const int64_t count_tiles = ceil_div(pa.L, 32) * ceil_div(pa.L, 32);
+  AFHIP_REQUIRE(grid + count_tiles < ((int64_t)1 << 31), "too many residues");
+  return launch("opm.project", k, dim3((unsigned)(grid + count_tiles)), dim3(kFastThreads), bytes, s, pa, ntiles,
+                tiles_per_res, (int)count_tiles, count);
 }
 
-template <typename MT> int launch_fast_cm(const ProjectArgs& pa, hipStream_t s) {
-  if (pa.cm == 64) return launch_fast<64, MT>(pa, s);
-  if (pa.cm == 128) return launch_fast<128, MT>(pa, s);
-  return launch_fast<256, MT>(pa, s);
+template <typename MT> int launch_fast_cm(const ProjectArgs& pa, float* count, hipStream_t s) {
+  if (pa.cm == 64) return launch_fast<64, MT>(pa, count, s);
+  if (pa.cm == 128) return launch_fast<128, MT>(pa, count, s);
+  return launch_fast<256, MT>(pa, count, s);
 }
 
 template <typename CT>
@@ -592,17 +618,18 @@ int afhip_opm_run(const afhip_opm_desc* desc, const void* activations, const flo
   size_t psh = round_up((int64_t)w.cmp * (kRows + 1) * 4, 16) +
                (f16 ? round_up((int64_t)kRows * (w.cmp + 8) * 2, 16) : 0) + (size_t)64 * (kRows + 8) * (f16 ? 2 : 4);
   int s;
+  float* count = (float*)(wsb + ws.count);
+  // The fast projection computes the pair counts in the same launch.
   const bool fast = project_fast_ok(d) && (reinterpret_cast<uintptr_t>(activations) & 15) == 0;
   if (fast)
-    s = d.msa_dtype == AFHIP_F32 ? launch_fast_cm<float>(pa, st) : launch_fast_cm<half_t>(pa, st);
+    s = d.msa_dtype == AFHIP_F32 ? launch_fast_cm<float>(pa, count, st) : launch_fast_cm<half_t>(pa, count, st);
   else if (f16)
     s = d.msa_dtype == AFHIP_F32 ? launch_project<float, true>(pa, psh, st) : launch_project<half_t, true>(pa, psh, st);
   else
     s = d.msa_dtype == AFHIP_F32 ? launch_project<float, false>(pa, psh, st) : launch_project<half_t, false>(pa, psh, st);
   if (s) return s;
 
-  float* count = (float*)(wsb + ws.count);
-  {
+  if (!fast) {
     const int64_t tiles = ceil_div(L, 32);
     if ((s = launch("opm.pair_count", opm_pair_count_kernel, dim3((unsigned)(tiles * tiles)), dim3(64 * kCountWaves),
                     0, st, mask, S, L, count)))
