@@ -341,7 +341,11 @@ typedef struct afhip_opm_desc {
   int32_t precision;  /* AFHIP_PRECISION_* */
   int32_t msa_dtype;  /* activations: AFHIP_F32 | AFHIP_F16 */
   int32_t out_dtype;  /* AFHIP_F32 | AFHIP_F16 */
-  int32_t row_block;  /* residues per contraction block; 0 = all (rowBlockResidues) */
+  int32_t row_block;  /* residues per contraction block; 0 = all (rowBlockResidues). It
+                       * bounds the f16/f32 `outer` block in the workspace; at f16
+                       * precision with c_outer 32 and c_z in (96, 128] the contraction
+                       * and output projection run fused with no `outer` at all, and
+                       * row_block changes nothing. Results never depend on it. */
   int32_t residual;   /* out += result */
   float layer_norm_epsilon;    /* 1e-5 */
   float normalization_epsilon; /* 1e-3 */
