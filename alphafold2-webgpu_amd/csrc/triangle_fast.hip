@@ -570,6 +570,256 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
   if (wave >= kLoaderWaves) store_tile(tile - G);
 }
 
+// ---------------------------------------------------------------------------
+// Output, software-pipelined (f16 z)
+// ---------------------------------------------------------------------------
+//
+// The same arithmetic as tri_output_f16_kernel in the same order, so the
+// results are bit-identical, but tile t's hidden statistics and z LayerNorm
+// run in one straight-line block with tile t-1's MFMAs and gate epilogue, so
+// the matrix and vector pipes overlap (the sequential kernel spent ~6.4k
+// cycles a tile, its phases one after another behind three barriers). The
+// normalised tiles (hn, gn) are double-buffered, which the LDS budget allows
+// only by giving up the output staging: each wave stores its accumulator
+// rows itself (four consecutive channels a lane, 16 bytes in f32), through a
+// buffer resource over [pair0, pair0 + pairs) so ragged pairs are dropped and
+// every wave issues the same number of vector-memory instructions, which
+// keeps the loader waves' vmcnt waits exact. Two barriers a tile:
+//   B1: tile t's stage has landed; hn[t-1] (and gn[t-1]) complete.
+//   B2: tile t's partial statistics and gn[t] complete; stage t is dead.
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+struct PipeLayout {
+  static constexpr int ZROW = kC * 2;
+  static constexpr int XBYTES = kC * kTile * 2;  // contraction tile, [128 channels][64 pairs] f16
+  static constexpr int ZBYTES = kTile * ZROW;
+  static constexpr int STAGE = XBYTES + ZBYTES;
+  static constexpr int STAGES = 2;
+  static constexpr int XLOADS = XBYTES / 1024;
+  static constexpr int ZLOADS = ZBYTES / 1024;
+  static constexpr int LPW = (XLOADS + ZLOADS) / kLoaderWaves;
+  static constexpr int ZROWS_PER_LOAD = 1024 / ZROW;
+  static constexpr int ZLANES_PER_ROW = 64 / ZROWS_PER_LOAD;
+  static constexpr int NBUF = kTile * kPitch * 2;  // one normalised tile
+  static constexpr int GN = STAGES * STAGE;         // two z x_hat tiles
+  static constexpr int HN = GN + 2 * NBUF;          // two hidden x_hat tiles
+  static constexpr int PART = HN + 2 * NBUF;        // [8 waves][64 pairs] x (mean, m2)
+  static constexpr int BYTES = PART + 8 * kTile * 2 * 4;
+};
+static_assert(PipeLayout::BYTES <= 160 * 1024, "LDS budget");
+
+template <typename OT>
+__global__ __launch_bounds__(kThreads, 1) void tri_output_pipe_kernel(FastOutputArgs a, int ntiles) {
+  using Lay = PipeLayout;
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  float2* part = reinterpret_cast<float2*>(smem + Lay::PART);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nt = 32 * (wave & 3), rh = 32 * (wave >> 2);
+  const int G = gridDim.x;
+
+  const half_t* wz = a.w_z + (size_t)(nt + (lane & 31)) * kC + 8 * (lane >> 5);
+  const half_t* wgp = a.w_g + (size_t)(nt + (lane & 31)) * kC + 8 * (lane >> 5);
+  half8 fz[8], fg[8];
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    fz[s] = *reinterpret_cast<const half8*>(wz + 16 * s);
+    fg[s] = *reinterpret_cast<const half8*>(wgp + 16 * s);
+  }
+  float bzv[16], bgv[16];
+#pragma unroll
+  for (int v = 0; v < 16; v++) {
+    bzv[v] = a.b_z[nt + mfma_row(v, lane)];
+    bgv[v] = a.b_g[nt + mfma_row(v, lane)];
+  }
+  wait_vmcnt<0>();  // weights in hand before the tile loads queue up behind them
+
+  const int32x4_t rx = make_rsrc(a.contracted, (uint32_t)((int64_t)kC * a.bstride * 2));
+  const int32x4_t rz = make_rsrc(reinterpret_cast<const unsigned char*>(a.z) + (size_t)a.pair0 * Lay::ZROW,
+                                 (uint32_t)((int64_t)a.pairs * Lay::ZROW));
+  constexpr int OROW = kC * (int)sizeof(OT);
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<unsigned char*>(a.out) + (size_t)a.pair0 * OROW, 0, (int)((int64_t)a.pairs * OROW), 0x00020000);
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+  auto issue = [&](int tile, int stage) {  // loader waves only
+    const uint32_t base = lds0 + stage * Lay::STAGE;
+    const int q0 = tile * kTile;
+#pragma unroll
+    for (int i = 0; i < Lay::LPW; i++) {
+      const int q = wave + kLoaderWaves * i;
+      uint32_t off;
+      if (q < Lay::XLOADS) {  // channel rows 8q + lane / 8, pairs q0 + 8 (lane % 8) ..
+        const int c = 8 * q + (lane >> 3);
+        const int p = q0 + 8 * (lane & 7);
+        off = p < a.pairs ? (uint32_t)(((int64_t)c * a.bstride + p) * 2) : kOutOfRange;
+        dma16(rx, base + q * 1024, off);
+      } else {
+        const int zq = q - Lay::XLOADS;
+        const int row = zq * Lay::ZROWS_PER_LOAD + lane / Lay::ZLANES_PER_ROW;
+        const int chunk = lane % Lay::ZLANES_PER_ROW;
+        const int p = q0 + row;
+        off = p < a.pairs ? (uint32_t)p * Lay::ZROW + 16u * chunk : kOutOfRange;
+        dma16(rz, base + q * 1024, off);
+      }
+    }
+  };
+
+  // Tile t's partial hidden statistics (wave w holds channels [16 w, +16)
+  // of pair `lane`) and z's x_hat into gn[buf].
+  float xh[16];
+  auto stats_and_zln = [&](int stage, int buf) {
+    const unsigned char* st = smem + stage * Lay::STAGE;
+    const half_t* xs = reinterpret_cast<const half_t*>(st);
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      xh[e] = (float)xs[(16 * wave + e) * kTile + lane];
+      s += xh[e];
+    }
+    const float mean = s * (1.0f / 16);
+    float m2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const float d = xh[e] - mean;
+      m2 += d * d;
+    }
+    part[wave * kTile + lane] = make_float2(mean, m2);
+    half_t* gn = reinterpret_cast<half_t*>(smem + Lay::GN + buf * Lay::NBUF);
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+      const int row = pass * 32 + (tid >> 4);
+      const int c0 = (tid & 15) * 8;
+      float x[8];
+      read8<half_t>(st + Lay::XBYTES + row * Lay::ZROW + c0 * 2, x);
+      normalize16(x, a.eps, gn + row * kPitch + c0);
+    }
+  };
+  // Chan et al.: merge eight (mean, M2) over 16 channels each; x_hat of the
+  // wave's 16 channels of pair `lane` into hn[buf].
+  auto merge = [&](int buf) {
+    float mean = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 8; w++) mean += part[w * kTile + lane].x;
+    mean *= 1.0f / 8;
+    float m2 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+      const float2 pw = part[w * kTile + lane];
+      const float d = pw.x - mean;
+      m2 += pw.y + 16.0f * d * d;
+    }
+    const float rstd = fast_rsqrt(m2 * (1.0f / kC) + a.eps);
+    const float shift = -mean * rstd;
+    half8 h0, h1;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      h0[e] = (half_t)fmaf(xh[e], rstd, shift);
+      h1[e] = (half_t)fmaf(xh[e + 8], rstd, shift);
+    }
+    half_t* dst = reinterpret_cast<half_t*>(smem + Lay::HN + buf * Lay::NBUF) + lane * kPitch + 16 * wave;
+    reinterpret_cast<half8*>(dst)[0] = h0;
+    reinterpret_cast<half8*>(dst)[1] = h1;
+  };
+  // W (A operand) x x_hat^T (B operand) for tile `t` from buffers `buf`: the
+  // accumulator's column is the pair rh + lane % 32, its rows four
+  // consecutive output channels per group; out = p sigmoid(g) (+ the old
+  // value, read first). Stores past the tile's valid pairs fall outside the
+  // resource and are dropped.
+  auto project_store = [&](int t, int buf, bool residual) {
+    // The product, its rounding to OT and the residual add each round on
+    // their own (no fused multiply-add, no mixed-precision fused forms): f32
+    // outputs equal the staged kernel's bit for bit, and f16 outputs round
+    // the f32 product (the staged kernel let the compiler fuse that
+    // conversion, one ulp apart at most).
+#pragma clang fp contract(off)
+    const uint32_t orow = (uint32_t)(t * kTile + rh + (lane & 31)) * OROW;
+    typedef OT ot4 __attribute__((ext_vector_type(4)));
+    ot4 old[4];
+    if (residual) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; g4++) {
+        const uint32_t off = orow + (uint32_t)(nt + 8 * g4 + 4 * (lane >> 5)) * (uint32_t)sizeof(OT);
+        if constexpr (sizeof(OT) == 4)
+          old[g4] = __builtin_bit_cast(ot4, __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, 0));
+        else
+          old[g4] = __builtin_bit_cast(ot4, __builtin_amdgcn_raw_buffer_load_b64(ro, off, 0, 0));
+      }
+    }
+    floatx16 accz, accg;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      accz[v] = bzv[v];
+      accg[v] = bgv[v];
+    }
+    const half_t* hrow =
+        reinterpret_cast<const half_t*>(smem + Lay::HN + buf * Lay::NBUF) + (rh + (lane & 31)) * kPitch + 8 * (lane >> 5);
+    const half_t* grow =
+        reinterpret_cast<const half_t*>(smem + Lay::GN + buf * Lay::NBUF) + (rh + (lane & 31)) * kPitch + 8 * (lane >> 5);
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+      accz = mfma_f16(fz[s], *reinterpret_cast<const half8*>(hrow + 16 * s), accz);
+      accg = mfma_f16(fg[s], *reinterpret_cast<const half8*>(grow + 16 * s), accg);
+    }
+#pragma unroll
+    for (int g4 = 0; g4 < 4; g4++) {
+      const uint32_t off = orow + (uint32_t)(nt + 8 * g4 + 4 * (lane >> 5)) * (uint32_t)sizeof(OT);
+      ot4 y;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        y[e] = (OT)(accz[4 * g4 + e] * gate_of(accg[4 * g4 + e]));
+        if (residual) y[e] = (OT)((float)y[e] + (float)old[g4][e]);
+      }
+      if constexpr (sizeof(OT) == 4)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, off, 0, 0);
+      else
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, y), ro, off, 0, 0);
+    }
+  };
+  const bool residual = a.residual != 0;
+  // A loader's tile has landed once at most the vector-memory instructions
+  // it issued after that tile's loads are outstanding: the previous tile's
+  // residual reads and stores (four each), or none on the first pass.
+  auto wait_tile = [&](bool after_stores) {
+    if (!after_stores) wait_vmcnt<0>();
+    else if (residual) wait_vmcnt<8>();
+    else wait_vmcnt<4>();
+  };
+
+  const int t0 = blockIdx.x;
+  if (t0 >= ntiles) return;
+  if (wave < kLoaderWaves) issue(t0, 0);
+  // First tile: statistics only.
+  if (wave < kLoaderWaves) wait_tile(false);
+  block_barrier();  // B1
+  if (wave < kLoaderWaves && t0 + G < ntiles) issue(t0 + G, 1);
+  stats_and_zln(0, 0);
+  block_barrier();  // B2
+  merge(0);
+  int it = 1;
+  for (int tile = t0 + G; tile < ntiles; it++, tile += G) {
+    const int buf = it & 1;
+    if (wave < kLoaderWaves) wait_tile(it > 1);
+    block_barrier();  // B1: stage `buf` landed, hn[buf ^ 1] complete
+    if (wave < kLoaderWaves && tile + G < ntiles) issue(tile + G, buf ^ 1);
+    // Tile it-1's MFMAs and epilogue beside tile it's statistics: one block.
+    project_store(tile - G, buf ^ 1, residual);
+    stats_and_zln(buf, buf);
+    // One MFMA, then fourteen VALU (the block's ~180 vector instructions
+    // spread over its 16 MFMAs). Measured at L = 384: 33.4 us against 33.8
+    // for twelve, 34.3 for eighteen, 34.6 for six and 34.8 with no hint.
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
+    }
+    block_barrier();  // B2: partial statistics and gn[buf] complete; stage buf is dead
+    merge(buf);
+  }
+  block_barrier();  // hn of the last tile complete
+  project_store(t0 + (it - 1) * G, (it - 1) & 1, residual);
+}
+
 int grid_for(int tiles) {
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   return std::max(1, std::min(tiles, cus));
@@ -604,6 +854,14 @@ int launch_triangle_project_f16(const FastProjectArgs& a, int pair_dtype, hipStr
 
 template <typename ZT, typename OT> int launch_output(const FastOutputArgs& a, hipStream_t s) {
   const int tiles = (int)ceil_div(a.pairs, kTile);
+  if constexpr (sizeof(ZT) == 2) {  // the pipelined kernel (its double buffers fit with f16 z)
+    AFHIP_REQUIRE((int64_t)a.pairs * kC * (int64_t)sizeof(OT) < ((int64_t)1 << 31),
+                  "triangle of %d pairs exceeds the output kernel's 2 GiB bound", a.pairs);
+    auto k = tri_output_pipe_kernel<OT>;
+    constexpr int bytes = PipeLayout::BYTES;
+    if (int st = prepare_lds(k, bytes)) return st;
+    return launch("triangle.output", k, dim3(grid_for(tiles)), dim3(kThreads), bytes, s, a, tiles);
+  }
   auto k = tri_output_f16_kernel<ZT, OT>;
   constexpr int bytes = OutputLayout<ZT, OT>::BYTES;
   if (int st = prepare_lds(k, bytes)) return st;
