@@ -529,6 +529,57 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     auto aligned4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & (4 * sizeof(TC) - 1)) == 0; };
     const bool vec4 = (g.ldc & 3) == 0 && (g.sc & 3) == 0 && aligned4(g.c) &&
                       (!(g.flags & AFHIP_EPILOGUE_RESIDUAL) || aligned4(g.residual));
+    if (!(g.flags & (AFHIP_EPILOGUE_SCALE | EPILOGUE_OPM_OUTPUT)) && vec4 && m0 + BM <= g.M && n0 + BN <= g.N) {
+      // A whole tile with bias, ReLU and residual at most: no global read
+      // waits behind a store. The output may alias the residual (and, as
+      // far as the compiler knows, the bias), so it keeps such a read after
+      // any earlier store; interleaved, that was one memory round trip per
+      // four outputs. Here the tile's bias goes to LDS once (the stages are
+      // idle), and the residual values of each 32-row block are read before
+      // its first store: a lane reads only the elements it later writes.
+      // The arithmetic is epilogue_row4's, step for step.
+#pragma clang fp contract(off)
+      typedef TC tc4 __attribute__((ext_vector_type(4)));
+      const uint32_t flags = g.flags;
+      float* const bl = reinterpret_cast<float*>(smem);
+      if (flags & AFHIP_EPILOGUE_BIAS) {
+        block_barrier<false>();  // every wave is done reading the stages
+        for (int c = threadIdx.x; c < BN; c += kThreads) bl[c] = g.bias[n0 + c];
+        block_barrier();
+      }
+      const TC* R = reinterpret_cast<const TC*>(g.residual) + (int64_t)bt * g.sc;
+      TC* C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int row = m0 + wm + 32 * i + (lane & 31);
+        tc4 res[TN][4];
+        if (flags & AFHIP_EPILOGUE_RESIDUAL) {
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++)
+              res[j][g4] = *reinterpret_cast<const tc4*>(R + (int64_t)row * g.ldc + n0 + wn + 32 * j + 8 * g4 +
+                                                         4 * (lane >> 5));
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; g4++) {
+            const int col = n0 + wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+            tc4 v;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              float y = acc[i][j][4 * g4 + e];
+              if (flags & AFHIP_EPILOGUE_BIAS) y += bl[wn + 32 * j + 8 * g4 + 4 * (lane >> 5) + e];
+              if (flags & AFHIP_EPILOGUE_RELU) y = fmaxf(y, 0.0f);
+              if (flags & AFHIP_EPILOGUE_RESIDUAL) y += (float)res[j][g4][e];
+              v[e] = (TC)y;
+            }
+            *reinterpret_cast<tc4*>(C + (int64_t)row * g.ldc + col) = v;
+          }
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int row = m0 + wm + 32 * i + (lane & 31);

@@ -351,6 +351,55 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(KernelArgs ka) {
     __syncthreads();
   }
 
+  if ((g.flags & ~(AFHIP_EPILOGUE_SCALE | AFHIP_EPILOGUE_BIAS | AFHIP_EPILOGUE_RELU | AFHIP_EPILOGUE_RESIDUAL)) == 0) {
+    // Scale, bias, ReLU and residual only: epilogue_store's steps in its
+    // order, with every global read issued before the stores it would
+    // otherwise wait behind (the output may alias the residual and, as far
+    // as the compiler knows, the scale and bias, so it keeps such a read
+    // after any earlier store: one memory round trip per element). A lane's
+    // column is fixed per 32 x 32 tile, so its scale and bias are read once;
+    // the tile's residual values are read before its first store, and a
+    // lane reads only the elements it later writes.
+#pragma clang fp contract(off)
+    const uint32_t flags = g.flags;
+    float sc_[TN], bi_[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int col = n0 + wn + 32 * j + (lane & 31);
+      sc_[j] = (flags & AFHIP_EPILOGUE_SCALE) && col < g.N ? g.scale[col] : 1.0f;
+      bi_[j] = (flags & AFHIP_EPILOGUE_BIAS) && col < g.N ? g.bias[col] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int col = n0 + wn + 32 * j + (lane & 31);
+        if (col >= g.N) continue;
+        auto at_of = [&](int row) {
+          return (int64_t)b * g.sc + (g.c_column_major ? (int64_t)col * g.ldc + row : (int64_t)row * g.ldc + col);
+        };
+        float r[16];
+        if (flags & AFHIP_EPILOGUE_RESIDUAL) {
+#pragma unroll
+          for (int v = 0; v < 16; v++) {
+            const int row = m0 + wm + 32 * i + mfma_row(v, lane);
+            r[v] = row < g.M ? (float)reinterpret_cast<const TC*>(g.residual)[at_of(row)] : 0.0f;
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int row = m0 + wm + 32 * i + mfma_row(v, lane);
+          if (row >= g.M) continue;
+          float y = acc[i][j][v];
+          if (flags & AFHIP_EPILOGUE_SCALE) y *= sc_[j];
+          if (flags & AFHIP_EPILOGUE_BIAS) y += bi_[j];
+          if (flags & AFHIP_EPILOGUE_RELU) y = fmaxf(y, 0.0f);
+          if (flags & AFHIP_EPILOGUE_RESIDUAL) y += r[v];
+          reinterpret_cast<TC*>(g.c)[at_of(row)] = (TC)y;
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
