@@ -278,6 +278,15 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
     __syncthreads();
   }
   const int j = threadIdx.x % LANES;
+  // The LayerNorm affine of this lane's channels, read once (inside the
+  // loop each read would wait behind the previous row's stores, which the
+  // compiler cannot prove do not alias it).
+  float sc[8], of[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    sc[e] = a.scale[8 * j + e];
+    of[e] = a.offset[8 * j + e];
+  }
   for (int64_t r0 = (int64_t)blockIdx.x * kRows; r0 < a.rows; r0 += (int64_t)gridDim.x * kRows) {
     const int64_t r = r0 + threadIdx.x / LANES;
     const bool live = r < a.rows;
@@ -298,7 +307,7 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
     }
     const float rstd = 1.0f / sqrtf(lane_sum<LANES>(var) / (float)C + a.eps);
 #pragma unroll
-    for (int e = 0; e < 8; e++) v[e] = (v[e] - mean) * rstd * a.scale[8 * j + e] + a.offset[8 * j + e];
+    for (int e = 0; e < 8; e++) v[e] = (v[e] - mean) * rstd * sc[e] + of[e];
     if (a.out && live) store8(reinterpret_cast<OT*>(a.out) + rr * C + 8 * j, v);
     if (a.mask && live && j == 0) key_bias_store(a, b * a.stride + q, a.mask[src]);
     if (a.w) {
@@ -690,14 +699,22 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   const half_t* gr = base + (row0 + myq) * ld4 + 3 * a.C + h * a.d;
   const int64_t src = a.transpose ? (int64_t)myq * a.B + b : row0 + myq;
   half_t* out = reinterpret_cast<half_t*>(a.weighted) + src * a.C + h * a.d;
+  // The gate values are all read before the first store, which the
+  // compiler could not move a read above (out and the gates may alias as
+  // far as it knows): otherwise each read waits for a memory round trip.
+  half4 gv[4];
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const int c0 = 8 * g + 4 * hi;
+    if (c0 < a.d) gv[g] = *reinterpret_cast<const half4*>(gr + c0);
+  }
 #pragma unroll
   for (int g = 0; g < 4; g++) {
     const int c0 = 8 * g + 4 * hi;
     if (c0 >= a.d) break;
-    const half4 gv = *reinterpret_cast<const half4*>(gr + c0);
     half4 r;
 #pragma unroll
-    for (int i = 0; i < 4; i++) r[i] = (half_t)(o[4 * g + i] * inv * (float)gv[i]);
+    for (int i = 0; i < 4; i++) r[i] = (half_t)(o[4 * g + i] * inv * (float)gv[g][i]);
     *reinterpret_cast<half4*>(out + c0) = r;
   }
 }
