@@ -7,10 +7,11 @@ L = 1024 with f16 output. Output pair (i, j) reads only rows (outgoing) or
 columns (incoming) i and j of z and z[i, j], so a few hundred sampled pairs are
 checked against a float64 restatement (oracle/ref.py triangle_pairs, pinned in
 tests/test_oracle.py against the whole oracle and the fixtures). Config 4: the
-outer-product mean at S = 512, L = 256, c_m = 256; out[i, j] reads only MSA
-columns i and j, so the oracle on the two-residue slice (i, j) is exact for
-that pair. Inputs are bench.py's own (same generators and seeds). Tolerance:
-the north star's 1e-2 of the largest reference value for the f16 paths.
+outer-product mean at S = 512, L = 256, c_m = 256 through the fused
+contraction + output projection; out[i, j] reads only MSA columns i and j,
+so the oracle on the two-residue slice (i, j) is exact for that pair. Inputs
+are bench.py's own (same generators and seeds). Tolerance: the north star's
+1e-2 of the largest reference value for the f16 paths.
 """
 import numpy as np
 import pytest
@@ -116,7 +117,7 @@ def test_config4_outer_product_mean_full_size(dev):
     import torch
 
     import bench
-    from afhip import gemm, opm
+    from afhip import device, opm
 
     s = bench.SEED + 3
     S, L, CM, CO, CZ = 512, 256, 256, 32, 128
@@ -126,13 +127,18 @@ def test_config4_outer_product_mean_full_size(dev):
          "leftWeight": ref.normal(s + 3, (CM, CO), 1 / CM), "leftBias": ref.normal(s + 4, (CO,), 0.02),
          "rightWeight": ref.normal(s + 5, (CM, CO), 1 / CM), "rightBias": ref.normal(s + 6, (CO,), 0.02),
          "outputWeight": ref.normal(s + 7, (CO * CO, CZ), 1 / (CO * CO)), "outputBias": ref.normal(s + 8, (CZ,), 0.02)}
-    # The contraction runs the tile the bench's run uses (192 x 192 with the
-    # divide-by-count epilogue).
-    v = gemm.select_variant(L * CO, S, L * CO, precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f16")
-    assert (v.kernel, v.tile_rows, v.tile_columns) == ("lds_dma", 192, 192)
+    # The run goes through the launches bench.py times: the projection (with
+    # the pair counts) and the fused contraction + output projection.
     op = opm.OuterProductMean(S, L, CM, CO, CZ, precision="f16", msa_dtype="f16", out_dtype="f32")
     op.prepare(w)
-    out = op(torch.from_numpy(act).half().to(dev), torch.from_numpy(mask).to(dev)).cpu().numpy()
+    device.timing_reset()
+    device.timing_enable(True)
+    try:
+        out = op(torch.from_numpy(act).half().to(dev), torch.from_numpy(mask).to(dev)).cpu().numpy()
+        labels = set(device.timing_report())
+    finally:
+        device.timing_enable(False)
+    assert labels == {"opm.project", "opm.fused"}, labels
     got, expect = [], []
     for i, j in sample_pairs(L, 7, 7):
         cols = [i] if i == j else [i, j]
