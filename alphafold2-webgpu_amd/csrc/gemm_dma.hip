@@ -46,6 +46,13 @@ namespace {
 
 constexpr int kBK = 32;        // halves per k-step
 constexpr int kRowBytes = 64;  // one row of a k-step stage
+// Tiles of one batch entry are visited in runs of kTileGroup tile rows,
+// column by column within a run, so the tiles resident at once on an XCD
+// (consecutive indices) form a block that shares few A and B panels: on the
+// outer-product mean's 32 x 32 tiles of 256, an XCD's 32 concurrent tiles
+// read 8 A and 4 B panels (3 MiB, within its 4 MiB L2) instead of 1 A and
+// 32 B panels (8.25 MiB). Measured there: 109.5 us against 114.4 us.
+constexpr int kTileGroup = 8;
 
 __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
 
@@ -77,8 +84,11 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   const int per_batch = ka.tiles_m * ka.tiles_n;
   const int bt = t / per_batch;
   const int rt = t - bt * per_batch;
-  const int m0 = (rt / ka.tiles_n) * BM;
-  const int n0 = (rt % ka.tiles_n) * BN;
+  const int run = rt / (kTileGroup * ka.tiles_n);
+  const int run_rows = min(ka.tiles_m - run * kTileGroup, kTileGroup);
+  const int in_run = rt - run * kTileGroup * ka.tiles_n;
+  const int m0 = (run * kTileGroup + in_run % run_rows) * BM;
+  const int n0 = (in_run / run_rows) * BN;
 
   const int lane = threadIdx.x & 63;
   // Wave-uniform by construction; readfirstlane lets the compiler keep the
