@@ -79,8 +79,9 @@ AttentionWeights weights_layout(const afhip_attention_desc& d) {
 // Workspace. The key bias [B][stride] and the pair bias [H][Q][stride] rows
 // are padded to a multiple of four keys, so the flash kernels read them as
 // float4; the padding is never used as a live key. On the fast path the
-// flash kernel reads one key block ahead of the one it computes, up to 63
-// keys past the last, so the tensors it reads end in that much padding.
+// flash kernel reads whole blocks of 32 keys (its read-ahead stops at the
+// last block), up to 31 keys past the last, so the tensors it reads end in
+// at least that much padding.
 struct AttentionWorkspace {
   size_t normalized, key_bias, key_mask, qkvg, bias, vt, weighted, total;
   int stride, key_blocks;
@@ -487,10 +488,10 @@ __global__ __launch_bounds__(256) void attention_vt_kernel(const half_t* __restr
 // wave (bi, qi) taking queries 32 qi.. of batch entry bi. Each key block's
 // K and V^T tiles (shared by a batch entry's four query waves) and pair-bias
 // tile (shared by both batch entries) pass through LDS, double-buffered:
-// every lane holds its share of block j + 1 in registers while block j is
-// computed, stores it to LDS after, and after the block's one barrier loads
-// its share of block j + 2. Loads past the last key land in the workspace's
-// padding, and those keys are masked.
+// every lane holds its share of blocks j + 1 and j + 2 in registers while
+// block j is computed, stores block j + 1 to LDS after, and after the
+// block's one barrier loads its share of block j + 3. Keys past the end of
+// the last block are masked.
 constexpr int kFlashBatch = 2;
 constexpr int kFlashQueryWaves = 4;
 constexpr int kFlashThreads = 64 * kFlashBatch * kFlashQueryWaves;
@@ -504,6 +505,7 @@ struct FlashTile {
   half_t k[kFlashBatch][32][40];   // [bi][key][channel], rows padded to 80 bytes
   half_t vt[kFlashBatch][32][40];  // [bi][channel][position]
   float bias[32 * kFlashQueryWaves][36];  // [query][key], rows padded to 144 bytes
+  half_t code[kFlashBatch * kFlashQueryWaves][32];  // [wave][key]: each wave's own copy of its keys' mask codes
 };
 
 template <bool BIAS>
@@ -557,29 +559,6 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
     }
   }
   static_assert(2 * kFlashThreads * 4 == 32 * kFlashQueryWaves * 32, "two bias pieces a lane cover the tile");
-  // K channels past the head dimension are zero (their loads, kept for a
-  // uniform count, read the row's next columns).
-  const bool tile_zero = (tid >> 7) < 2 && 8 * (tid & 3) >= a.d;
-  uint4 staged[3];
-  auto fetch = [&](int k0) {
-    staged[0] = *reinterpret_cast<const uint4*>(tile_src + (k0 >> 5) * tile_step);
-    if (tile_zero) staged[0] = uint4{0u, 0u, 0u, 0u};
-    if (BIAS) {
-      staged[1] = *reinterpret_cast<const uint4*>(bias_src[0] + k0);
-      staged[2] = *reinterpret_cast<const uint4*>(bias_src[1] + k0);
-    }
-  };
-  // Byte offsets into the __shared__ array (not generic pointers), so the
-  // writes are LDS stores.
-  unsigned char* const lds_tiles = reinterpret_cast<unsigned char*>(tiles);
-  auto stash = [&](int t) {
-    unsigned char* const tb = lds_tiles + t * (uint32_t)sizeof(FlashTile);
-    *reinterpret_cast<uint4*>(tb + tile_dst) = staged[0];
-    if (BIAS) {
-      *reinterpret_cast<uint4*>(tb + bias_dst[0]) = staged[1];
-      *reinterpret_cast<uint4*>(tb + bias_dst[1]) = staged[2];
-    }
-  };
 
   // This wave's batch entry and queries.
   const int64_t b = b0 + bi;
@@ -604,7 +583,8 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   half4 bm_frag = hi ? half4{} : half4{(half_t)kMaskScale, (half_t)0.0f, (half_t)0.0f, (half_t)0.0f};
   const half_t one = (half_t)1.0f;
 
-  auto step = [&](const FlashTile& tl, half_t code, int k0, bool first) {
+  auto step = [&](const FlashTile& tl, int k0, bool first) {
+    const half_t code = tl.code[wave][col];
     floatx16 sc = {};
     if constexpr (BIAS) {
 #pragma unroll
@@ -679,19 +659,71 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
       o = mfma_f16(*reinterpret_cast<const half8*>(&tl.vt[bi][col][16 * s + 8 * hi]), pf[s], o);
   };
 
-  fetch(0);
-  half_t code = cp[0];
-  stash(0);
+  // K channels past the head dimension are zero (their loads, kept for a
+  // uniform count, read the row's next columns); the zeros go in at the LDS
+  // store, so no wait for the load sits at the fetch.
+  const unsigned tile_keep = (tid >> 7) < 2 && 8 * (tid & 3) >= a.d ? 0u : ~0u;
+  // A block's share of the loads, two sets in flight, each with the mask
+  // code of the lane's key in that block. Blocks past the last one fetch the
+  // last one again (and are never stored).
+  const int last_k0 = ((Q - 1) >> 5) << 5;
+  struct Staged {
+    uint4 v[3];
+    half_t code;
+  };
+  auto fetch = [&](int k0, Staged& st) {
+    k0 = min(k0, last_k0);
+    st.v[0] = *reinterpret_cast<const uint4*>(tile_src + (k0 >> 5) * tile_step);
+    if (BIAS) {
+      st.v[1] = *reinterpret_cast<const uint4*>(bias_src[0] + k0);
+      st.v[2] = *reinterpret_cast<const uint4*>(bias_src[1] + k0);
+    }
+    st.code = cp[k0];
+  };
+  // Byte offsets into the __shared__ array (not generic pointers), so the
+  // writes are LDS stores. The mask code goes through LDS too (the wave
+  // reads back its own), so no register with a load in flight is live
+  // across the loop's back edge, where a copy of it would wait for every
+  // load.
+  unsigned char* const lds_tiles = reinterpret_cast<unsigned char*>(tiles);
+  const uint32_t code_dst = (uint32_t)offsetof(FlashTile, code) + 2u * (uint32_t)(wave * 32 + col);
+  auto stash = [&](int t, const Staged& st) {
+    unsigned char* const tb = lds_tiles + t * (uint32_t)sizeof(FlashTile);
+    const uint4 tv = st.v[0];
+    *reinterpret_cast<uint4*>(tb + tile_dst) =
+        uint4{tv.x & tile_keep, tv.y & tile_keep, tv.z & tile_keep, tv.w & tile_keep};
+    if (BIAS) {
+      *reinterpret_cast<uint4*>(tb + bias_dst[0]) = st.v[1];
+      *reinterpret_cast<uint4*>(tb + bias_dst[1]) = st.v[2];
+    }
+    *reinterpret_cast<half_t*>(tb + code_dst) = st.code;
+  };
+  // Block j computes from LDS buffer j % 2 while the lane holds blocks j + 1
+  // and j + 2 in registers (sets alternating, so the loop is unrolled by
+  // two): after the compute it stores block j + 1, and after the barrier it
+  // loads block j + 3 into the set just stored. A load has two blocks of
+  // compute to land.
+  Staged sa, sb;
+  fetch(0, sa);
+  stash(0, sa);
   __syncthreads();
-  fetch(32);  // in the padding when there is one block
-  for (int k0 = 0, t = 0; k0 < Q; k0 += 32, t ^= 1) {
-    const half_t next_code = cp[k0 + 32];
-    if (active) step(tiles[t], code, k0, k0 == 0);
-    code = next_code;
-    if (k0 + 32 >= Q) break;
-    stash(t ^ 1);
+  fetch(32, sb);
+  fetch(64, sa);
+  if (active) step(tiles[0], 0, true);
+  for (int k0 = 32, t = 1; k0 < Q;) {
+    stash(t, sb);
     __syncthreads();
-    fetch(k0 + 64);
+    fetch(k0 + 64, sb);
+    if (active) step(tiles[t], k0, false);
+    k0 += 32;
+    t ^= 1;
+    if (k0 >= Q) break;
+    stash(t, sa);
+    __syncthreads();
+    fetch(k0 + 64, sa);
+    if (active) step(tiles[t], k0, false);
+    k0 += 32;
+    t ^= 1;
   }
   run_sum += __shfl_xor(run_sum, 32);
   if (!active || myq >= Q) return;
