@@ -4,11 +4,13 @@
 // Both are persistent (one 512-lane workgroup per CU walking 64-pair tiles)
 // and split their eight waves by role:
 //  - waves 0-3 issue the tile loads, straight into a ring of LDS stages
-//    (buffer_load ... lds) several tiles ahead. They issue no other
-//    vector-memory instruction, so the s_waitcnt vmcnt that says "this tile
-//    has landed" is exact.
-//  - waves 4-7 write the finished tile back from an LDS staging area with
-//    16-byte stores that cover whole 128-byte lines.
+//    (buffer_load ... lds) several tiles ahead. Besides those they issue
+//    only a fixed number of stores a tile, so the s_waitcnt vmcnt that says
+//    "this tile has landed" is exact.
+//  - the finished tile goes back to HBM with 16-byte stores that cover
+//    whole 128-byte lines: from an LDS staging area (the projection: each
+//    wave stores the rows it wrote, right after writing them) or straight
+//    from the accumulators (the pipelined output kernel).
 //  - all eight compute, with the weights held in VGPRs for the whole kernel
 //    (2 x 8 half8 fragments = 64 VGPRs per wave).
 //
@@ -25,7 +27,7 @@
 // contraction's channel-major operand rows) as 8-byte writes. The loop is
 // software-pipelined: tile t's MFMAs and tile t+1's LayerNorm are one
 // straight-line block (two zn buffers), so the matrix and vector pipes
-// overlap, with two barriers per tile.
+// overlap, with one barrier per tile.
 //
 // tri_output: the contraction tile arrives channel-major; its LayerNorm over
 // the 128 hidden channels is computed as per-wave partial statistics (each
@@ -99,6 +101,16 @@ __device__ __forceinline__ float gate_of(float acc) { return fast_rcp(1.0f + __b
 template <int LATER> __device__ __forceinline__ void wait_stage(bool later_issued) {
   if (later_issued) wait_vmcnt<LATER>();
   else wait_vmcnt<0>();
+}
+
+// wait_vmcnt<BASE + STEP * min(k, KMAX)>() for a wave-uniform k.
+template <int BASE, int STEP, int KMAX> __device__ __forceinline__ void wait_vmcnt_by(int k) {
+  if constexpr (KMAX == 0) {
+    wait_vmcnt<BASE>();
+  } else {
+    if (k >= KMAX) wait_vmcnt<BASE + STEP * KMAX>();
+    else wait_vmcnt_by<BASE, STEP, KMAX - 1>(k);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -209,16 +221,23 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       }
     }
   };
-  // Loader waves: the tile issued `later_tiles` tiles before the newest has
-  // landed (when all of those were issued; otherwise wait for everything).
-  auto wait_tile = [&](bool later_issued, bool all_stages_later) {
-    if (all_stages_later) {
-      if (wave == 0) wait_stage<(S - 1) * (Lay::LPW + 1)>(later_issued);
-      else wait_stage<(S - 1) * Lay::LPW>(later_issued);
-    } else {
-      if (wave == 0) wait_stage<(S - 2) * (Lay::LPW + 1)>(later_issued);
-      else wait_stage<(S - 2) * Lay::LPW>(later_issued);
-    }
+  // Loader waves. Before the loop: tile 0 has landed once the S - 1 tiles
+  // issued after it are all that may be pending. In pass `it`: tile it + 1
+  // has landed once what was issued after its loads is all that may be
+  // pending: the loads of tiles it + 2 .. it + S - 1 and, since every wave
+  // stores its rows of each finished tile (kStores instructions a pass), the
+  // stores of the min(it, S - 1) passes since. Vector-memory instructions
+  // complete in issue order, loads and stores alike. When a later tile was
+  // not issued (the end of the range), wait for everything.
+  constexpr int kStores = 2 * kC * kTile * 2 / 1024 / (kThreads / 64);  // a wave's 32 rows of 64 pairs, 1 KiB a store
+  auto wait_first = [&](bool later_issued) {
+    if (wave == 0) wait_stage<(S - 1) * (Lay::LPW + 1)>(later_issued);
+    else wait_stage<(S - 1) * Lay::LPW>(later_issued);
+  };
+  auto wait_next = [&](int it, bool later_issued) {
+    if (!later_issued) wait_vmcnt<0>();
+    else if (wave == 0) wait_vmcnt_by<(S - 2) * (Lay::LPW + 1), kStores, S - 1>(it);
+    else wait_vmcnt_by<(S - 2) * Lay::LPW, kStores, S - 1>(it);
   };
   // x_hat of the tile in `stage` into zn; the tile's mask into mdst (the
   // stage is refilled before the tile's epilogue runs).
@@ -237,29 +256,35 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
     mdst[lane] = reinterpret_cast<const float*>(st + Lay::ZBYTES)[lane];
   };
 
-  const int t4 = tid - kLoaderWaves * 64;
-  const int srow = t4 >> 3, schunk = t4 & 7;
-  uint32_t svof[4];
+  // A wave's stores: its 32 channel rows of the staged tile, store k
+  // covering rows 8 k + lane / 8, 16-byte chunk lane % 8 (pairs 8 (lane % 8)
+  // ..), so each instruction writes eight whole 128-byte row pieces. The
+  // lane's offsets are fixed, the tile's base rides in the scalar offset.
+  static_assert(kStores == 4, "32 rows, eight a store");
+  const int srow = lane >> 3, schunk = lane & 7;
+  const half_t* const sown = ost + (o * kC + hb + srow) * kOutPitch + schunk * 8;
+  uint32_t svof[kStores];
 #pragma unroll
-  for (int k = 0; k < 4; k++) svof[k] = (uint32_t)(((int64_t)(srow + 32 * k) * a.cstride + schunk * 8) * 2);
+  for (int k = 0; k < kStores; k++)
+    svof[k] = (uint32_t)(((int64_t)(hb + srow + 8 * k) * a.cstride + schunk * 8) * 2);
   const int obytes = (int)((int64_t)kC * a.cstride * 2);
-  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(a.out_a, 0, obytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(a.out_b, 0, obytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rso =
+      __builtin_amdgcn_make_buffer_rsrc(o == 0 ? a.out_a : a.out_b, 0, obytes, 0x00020000);
 
   if (t0 >= ntiles) return;
   if (wave < kLoaderWaves) {
 #pragma unroll
     for (int s = 0; s < S; s++)
       if (t0 + s * G < ntiles) issue(t0 + s * G, s);
-    wait_tile(t0 + (S - 1) * G < ntiles, true);
+    wait_first(t0 + (S - 1) * G < ntiles);
   }
   block_barrier();  // the first tile has landed
   layer_norm_tile(0, zn_base, mask_base);
 
   for (int it = 0, tile = t0; tile < ntiles; it++, tile += G) {
     // Tiles it + 2 .. it + S - 1 may still be in flight; tile it + 1 must be in.
-    if (wave < kLoaderWaves) wait_tile(tile + (S - 1) * G < ntiles, false);
-    block_barrier();  // B1: zn[it % 2] complete, the next tile landed, staging free
+    if (wave < kLoaderWaves) wait_next(it, tile + (S - 1) * G < ntiles);
+    block_barrier();  // zn[it % 2] complete, the next tile landed
     if (wave < kLoaderWaves && tile + S * G < ntiles) issue(tile + S * G, it % S);
 
     const half_t* zn = zn_base + (it & 1) * kTile * kPitch;
@@ -310,24 +335,19 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then four VALU (five measured 3% slower)
     }
-    block_barrier();  // B2: the staged tile and zn[(it + 1) % 2] are complete
-
-    if (wave >= kLoaderWaves) {
-      // 256 channel rows x 64 pairs: eight 16-byte chunks per row; store k
-      // writes row (t4 >> 3) + 32 k (a's rows, then b's). The lane's offsets
-      // are fixed, the tile's base rides in the scalar offset. Pairs past P
-      // land in the operand's padding (its rows are cstride >= 64 * ntiles
-      // long), which the contraction never reads.
+    // The wave's own rows go out as soon as it has written them (LDS
+    // accesses of one wave complete in order), so no barrier waits for the
+    // whole staged tile; the next pass's barrier covers zn[(it + 1) % 2].
+    // Pairs past P land in the operand's padding (its rows are cstride >=
+    // 64 * ntiles long), which the contraction never reads.
+    {
+      u32x4 v[kStores];
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        u32x4 v[4];
+      for (int k = 0; k < kStores; k++) v[k] = *reinterpret_cast<const u32x4*>(sown + 8 * k * kOutPitch);
 #pragma unroll
-        for (int k = 0; k < 4; k++) v[k] = *reinterpret_cast<const u32x4*>(ost + (srow + 32 * (4 * h + k)) * kOutPitch + schunk * 8);
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-          __builtin_amdgcn_raw_buffer_store_b128(v[k], h == 0 ? rsa : rsb, svof[k], (uint32_t)tile * kTile * 2, 0);
-        stores_read(v[0], v[1], v[2], v[3]);
-      }
+      for (int k = 0; k < kStores; k++)
+        __builtin_amdgcn_raw_buffer_store_b128(v[k], rso, svof[k], (uint32_t)tile * kTile * 2, 0);
+      stores_read(v[0], v[1], v[2], v[3]);
     }
   }
 }
