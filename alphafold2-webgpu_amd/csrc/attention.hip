@@ -22,8 +22,9 @@
 // 16 keys and the same query's output for 16 channels, so the running maximum,
 // sum and rescale stay inside the lane (one exchange with the lane 32 away),
 // and the probabilities feed the second MFMA from the registers they were
-// computed in. V^T comes from a pre-pass that lays each 32-key block out in
-// the key order of those registers, so every fragment is one 16-byte load.
+// computed in. V stays in its natural [key][channel] layout: the V^T
+// fragments come from gfx950's transposing LDS read (ds_read_b64_tr_b16),
+// which hands each lane its channel's keys in the order of those registers.
 // Its logits are kept in base-2 units (q, the key bias and the pair bias
 // carry a factor log2(e)), which changes nothing but the rounding:
 // exp2(log2(e) x) = exp(x). Any other head dimension, or f32 precision, runs
@@ -83,8 +84,8 @@ AttentionWeights weights_layout(const afhip_attention_desc& d) {
 // last block), up to 31 keys past the last, so the tensors it reads end in
 // at least that much padding.
 struct AttentionWorkspace {
-  size_t normalized, key_bias, key_mask, qkvg, bias, vt, weighted, total;
-  int stride, key_blocks;
+  size_t normalized, key_bias, key_mask, qkvg, bias, weighted, total;
+  int stride;
 };
 
 constexpr int kReadAhead = 64;  // keys
@@ -101,15 +102,12 @@ AttentionWorkspace workspace_layout(const afhip_attention_desc& d) {
     return here;
   };
   w.stride = (int)round_up(d.queries, 4);
-  w.key_blocks = (int)ceil_div(d.queries, 32);
   w.normalized = take(es * rows * C);
   w.key_bias = take(fast ? 0 : 4 * (size_t)d.batch * w.stride);
   // f16 key mask codes [B][stride] (fast path)
   w.key_mask = take(fast ? 2 * ((size_t)d.batch * w.stride + kReadAhead) : 0);
   w.qkvg = take(es * (rows + (fast ? kReadAhead : 0)) * 4 * C);
   w.bias = take(d.pair_bias ? 4 * ((size_t)d.heads * d.queries * w.stride + (fast ? kReadAhead : 0)) : 0);
-  // V^T blocks [B][H][key block][32 channels][32 keys] (fast path), and two spare blocks
-  w.vt = take(fast ? 2 * ((size_t)d.batch * d.heads * w.key_blocks + 2) * 1024 : 0);
   w.weighted = take(es * rows * C);
   w.total = at;
   return w;
@@ -372,9 +370,8 @@ struct FlashArgs {
   const float* key_bias;  // [B][stride] (general kernel)
   const half_t* key_mask; // [B][stride] codes (f16 kernel)
   const float* bias;      // [H][Q][stride] or null
-  const half_t* vt;       // V^T blocks (f16 path)
   void* weighted;         // [B Q][C] in source order
-  int B, Q, C, H, d, transpose, stride, key_blocks;
+  int B, Q, C, H, d, transpose, stride;
   float clamp;
 };
 
@@ -430,47 +427,12 @@ int launch_flash_generic(const FlashArgs& fa, hipStream_t st, std::integer_seque
   return launch("attention.flash", table[fa.d - 1], dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, st, fa);
 }
 
-// V^T blocks for the f16 flash kernel: block (b, h, kb) is [32 channels][32
-// positions], position 16 s + 8 hi + e holding key 32 kb + 16 s + 8 (e / 4) +
-// 4 hi + e % 4 (zero past the last key): the keys a lane's probabilities
-// cover, in the order they fill the second MFMA's B operand.
-__global__ __launch_bounds__(256) void attention_vt_kernel(const half_t* __restrict__ qkvg, int B, int Q, int C,
-                                                           int H, int D, int key_blocks, half_t* __restrict__ vt) {
-  // Two blocks a workgroup: 128 lanes load one block's 32 keys x 32
-  // channels as 16-byte row pieces into LDS, then write its [channel][position]
-  // rows as 16-byte pieces.
-  __shared__ __attribute__((aligned(16))) half_t tile[2][32][40];
-  const int sub = threadIdx.x >> 7, u = threadIdx.x & 127;
-  const int64_t t = (int64_t)blockIdx.x * 2 + sub;
-  const bool live = t < (int64_t)B * H * key_blocks;
-  int64_t b = 0;
-  int h = 0, kb = 0;
-  if (live) {
-    kb = (int)(t % key_blocks);
-    const int64_t bh = t / key_blocks;
-    h = (int)(bh % H);
-    b = bh / H;
-    const int key = 32 * kb + (u >> 2);
-    half8 v = {};
-    if (key < Q && 8 * (u & 3) < D)  // channels past the head dimension are zero
-      v = *reinterpret_cast<const half8*>(qkvg + (b * Q + key) * 4 * (int64_t)C + 2 * C + h * D + 8 * (u & 3));
-    *reinterpret_cast<half8*>(&tile[sub][u >> 2][8 * (u & 3)]) = v;
-  }
-  __syncthreads();
-  if (!live) return;
-  const int d = u >> 2, s = (u >> 1) & 1, hi = u & 1;
-  half8 o;
-#pragma unroll
-  for (int e = 0; e < 8; e++) o[e] = tile[sub][16 * s + 8 * (e >> 2) + 4 * hi + (e & 3)][d];
-  *reinterpret_cast<half8*>(vt + t * 1024 + d * 32 + 16 * s + 8 * hi) = o;
-}
-
 // f16 operands, head_dim 32: one wave per 32 queries of one (b, h), keys in
 // blocks of 32. S^T = K Q^T: A = K [key][d] straight from the projection
 // output, B = Q^T (the wave's queries, held for the whole loop); the result
 // gives lane l query l % 32 and keys 8 (v / 4) + 4 (l / 32) + v % 4. The
 // probabilities, packed to f16 in that key order, are the B operand of
-// O^T = V^T P^T, whose A operand is the V^T block in the same order.
+// O^T = V^T P^T, whose A operand holds V^T in the same key order.
 //
 // The MFMA does the per-logit additions: the accumulator starts from the pair
 // bias (loaded in the accumulator's own layout), and a 32x32x8 step adds
@@ -486,7 +448,7 @@ __global__ __launch_bounds__(256) void attention_vt_kernel(const half_t* __restr
 //
 // A workgroup is two batch entries by 128 queries of one head: eight waves,
 // wave (bi, qi) taking queries 32 qi.. of batch entry bi. Each key block's
-// K and V^T tiles (shared by a batch entry's four query waves) and pair-bias
+// K and V tiles (shared by a batch entry's four query waves) and pair-bias
 // tile (shared by both batch entries) pass through LDS, double-buffered:
 // every lane holds its share of blocks j + 1 and j + 2 in registers while
 // block j is computed, stores block j + 1 to LDS after, and after the
@@ -501,9 +463,13 @@ constexpr float kSlack = 8.0f;
 // (below 2^-149) and therefore in f16.
 constexpr float kClampReach = 160.0f;
 
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef short short8v __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
 struct FlashTile {
   half_t k[kFlashBatch][32][40];   // [bi][key][channel], rows padded to 80 bytes
-  half_t vt[kFlashBatch][32][40];  // [bi][channel][position]
+  half_t v[kFlashBatch][32][32];   // [bi][key][channel], read transposed (ds_read_b64_tr_b16)
   float bias[32 * kFlashQueryWaves][36];  // [query][key], rows padded to 144 bytes
   half_t code[kFlashBatch * kFlashQueryWaves][32];  // [wave][key]: each wave's own copy of its keys' mask codes
 };
@@ -526,9 +492,10 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
 
   // This lane's share of a block's loads, at key block 0; block k0 adds
   // uniform offsets: one 16-byte piece of a tile (lanes 0-127 and 128-255 the
-  // K tiles of batch entries 0 and 1, lanes 256-383 and 384-511 their V^T
-  // tiles) and two of the bias tile (lane t: pieces t and t + 512, piece c
-  // holding row c / 8, keys 4 (c % 8)..).
+  // K tiles of batch entries 0 and 1, lanes 256-383 and 384-511 their V
+  // tiles; piece u of a tile holds key u / 4, channels 8 (u % 4)..) and two
+  // of the bias tile (lane t: pieces t and t + 512, piece c holding row c / 8,
+  // keys 4 (c % 8)..).
   const half_t* tile_src;
   int64_t tile_step;  // elements per key block
   uint32_t tile_dst;  // byte offset in tiles[0]; tiles[1] is sizeof(FlashTile) further
@@ -537,15 +504,12 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
     const int u = tid & 127;
     const int e = part & 1;
     const int64_t be = min(b0 + e, (int64_t)a.B - 1);
-    if (part < 2) {
-      tile_src = base + (be * Q + (u >> 2)) * ld4 + a.C + h * a.d + 8 * (u & 3);
-      tile_step = 32 * ld4;
-    } else {
-      tile_src = a.vt + (be * a.H + h) * a.key_blocks * 1024 + u * 8;
-      tile_step = 1024;
-    }
-    const uint32_t at = 2u * (uint32_t)((e * 32 + (u >> 2)) * 40 + 8 * (u & 3));
-    tile_dst = (uint32_t)(part < 2 ? offsetof(FlashTile, k) : offsetof(FlashTile, vt)) + at;
+    tile_src = base + (be * Q + (u >> 2)) * ld4 + (part < 2 ? 1 : 2) * a.C + h * a.d + 8 * (u & 3);
+    tile_step = 32 * ld4;
+    // K rows are padded to 80 bytes for the fragment reads; V rows are 64
+    // bytes, which keeps the transposing reads free of bank conflicts.
+    tile_dst = part < 2 ? (uint32_t)offsetof(FlashTile, k) + 2u * (uint32_t)((e * 32 + (u >> 2)) * 40 + 8 * (u & 3))
+                        : (uint32_t)offsetof(FlashTile, v) + 2u * (uint32_t)((e * 32 + (u >> 2)) * 32 + 8 * (u & 3));
   }
   const float* bias_src[2] = {nullptr, nullptr};
   uint32_t bias_dst[2] = {};
@@ -583,6 +547,14 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   half4 bm_frag = hi ? half4{} : half4{(half_t)kMaskScale, (half_t)0.0f, (half_t)0.0f, (half_t)0.0f};
   const half_t one = (half_t)1.0f;
 
+  // V^T fragments of O^T = V^T P^T from the [key][channel] tile with the
+  // transposing LDS read: within each 16-lane group, output lane i gets, as
+  // its element j, element i % 4 of the 8 bytes lane 4 j + i / 4 addressed.
+  // Lane 16 g + m addresses key 16 s + 4 (lane / 32) + m / 4 (+ 8 for the
+  // second read), channels 16 (g % 2) + 4 (m % 4).., so lane (channel c, hi)
+  // receives keys 16 s + 8 (e / 4) + 4 hi + e % 4 of channel c: the order the
+  // probabilities take in the MFMA's other operand.
+  const int tr_key = 4 * hi + ((lane & 15) >> 2), tr_ch = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   auto step = [&](const FlashTile& tl, int k0, bool first) {
     const half_t code = tl.code[wave][col];
     floatx16 sc = {};
@@ -655,14 +627,21 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
       pf[v >> 3][(v & 7) + 1] = pp[1];
     }
 #pragma unroll
-    for (int s = 0; s < 2; s++)
-      o = mfma_f16(*reinterpret_cast<const half8*>(&tl.vt[bi][col][16 * s + 8 * hi]), pf[s], o);
+    for (int s = 0; s < 2; s++) {
+      const half_t* vp = &tl.v[bi][16 * s + tr_key][tr_ch];
+      const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)vp);
+      const short4v up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(vp + 8 * 32));
+      o = mfma_f16(__builtin_bit_cast(half8, short8v{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]}), pf[s], o);
+    }
   };
 
-  // K channels past the head dimension are zero (their loads, kept for a
-  // uniform count, read the row's next columns); the zeros go in at the LDS
-  // store, so no wait for the load sits at the fetch.
-  const unsigned tile_keep = (tid >> 7) < 2 && 8 * (tid & 3) >= a.d ? 0u : ~0u;
+  // K and V channels past the head dimension are zero (their loads, kept
+  // for a uniform count, read the row's next columns), and so are keys past
+  // the last (whose loads read the next rows or the tensor's padding: a
+  // probability of 0 times a non-finite value would not be 0). The zeros go
+  // in at the LDS store, so no wait for the load sits at the fetch.
+  const unsigned tile_keep = 8 * (tid & 3) >= a.d ? 0u : ~0u;
+  const int tile_key = (tid & 127) >> 2;
   // A block's share of the loads, two sets in flight, each with the mask
   // code of the lane's key in that block. Blocks past the last one fetch the
   // last one again (and are never stored).
@@ -687,11 +666,11 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   // load.
   unsigned char* const lds_tiles = reinterpret_cast<unsigned char*>(tiles);
   const uint32_t code_dst = (uint32_t)offsetof(FlashTile, code) + 2u * (uint32_t)(wave * 32 + col);
-  auto stash = [&](int t, const Staged& st) {
+  auto stash = [&](int t, const Staged& st, int k0) {
     unsigned char* const tb = lds_tiles + t * (uint32_t)sizeof(FlashTile);
     const uint4 tv = st.v[0];
-    *reinterpret_cast<uint4*>(tb + tile_dst) =
-        uint4{tv.x & tile_keep, tv.y & tile_keep, tv.z & tile_keep, tv.w & tile_keep};
+    const unsigned keep = k0 + tile_key < Q ? tile_keep : 0u;
+    *reinterpret_cast<uint4*>(tb + tile_dst) = uint4{tv.x & keep, tv.y & keep, tv.z & keep, tv.w & keep};
     if (BIAS) {
       *reinterpret_cast<uint4*>(tb + bias_dst[0]) = st.v[1];
       *reinterpret_cast<uint4*>(tb + bias_dst[1]) = st.v[2];
@@ -705,20 +684,20 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   // compute to land.
   Staged sa, sb;
   fetch(0, sa);
-  stash(0, sa);
+  stash(0, sa, 0);
   __syncthreads();
   fetch(32, sb);
   fetch(64, sa);
   if (active) step(tiles[0], 0, true);
   for (int k0 = 32, t = 1; k0 < Q;) {
-    stash(t, sb);
+    stash(t, sb, k0);
     __syncthreads();
     fetch(k0 + 64, sb);
     if (active) step(tiles[t], k0, false);
     k0 += 32;
     t ^= 1;
     if (k0 >= Q) break;
-    stash(t, sa);
+    stash(t, sa, k0);
     __syncthreads();
     fetch(k0 + 64, sa);
     if (active) step(tiles[t], k0, false);
@@ -928,7 +907,6 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
     fa.key_bias = (const float*)(wsb + ws.key_bias);
     fa.key_mask = (const half_t*)(wsb + ws.key_mask);
     fa.bias = bias;
-    fa.vt = (const half_t*)(wsb + ws.vt);
     fa.weighted = wsb + ws.weighted;
     fa.B = B;
     fa.Q = Q;
@@ -937,15 +915,8 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
     fa.d = C / H;
     fa.transpose = d.transpose;
     fa.stride = ws.stride;
-    fa.key_blocks = ws.key_blocks;
     fa.clamp = 1e8f;
     if (fast) {
-      const int64_t vt_blocks = (int64_t)B * H * ws.key_blocks;
-      AFHIP_REQUIRE(ceil_div(vt_blocks, 2) < ((int64_t)1 << 31), "attention grid too large");
-      if ((s = launch("attention.vt", attention_vt_kernel, dim3((unsigned)ceil_div(vt_blocks, 2)), dim3(256), 0,
-                      st, (const half_t*)(wsb + ws.qkvg), B, Q, C, H, C / H, ws.key_blocks,
-                      (half_t*)(wsb + ws.vt))))
-        return s;
       const int64_t groups = ceil_div(B, kFlashBatch) * H * ceil_div(Q, 32 * kFlashQueryWaves);
       AFHIP_REQUIRE(groups < ((int64_t)1 << 31), "attention grid too large");
       s = bias ? launch("attention.flash", attention_flash_f16_kernel<true>, dim3((unsigned)groups),
