@@ -261,21 +261,25 @@ template <typename T> __device__ __forceinline__ void store8(T* p, const float (
 
 // Vectorised rows: LANES lanes a row, eight channels a lane (C = 8 LANES);
 // a workgroup walks 256 / LANES rows at a time through the tensor, the head
-// weights (zero past H, H <= 8) staged once in LDS.
-template <typename IT, typename OT, int LANES>
+// weights (zero past H, H <= HB, HB 4 or 8) staged once in LDS. Rows are
+// fewer than 2^24, so a row's (b, q) comes from an f32 reciprocal of Q and
+// one correction instead of a 64-bit division.
+template <typename IT, typename OT, int LANES, int HB>
 __global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
   constexpr int C = 8 * LANES;
   constexpr int kRows = 256 / LANES;
-  __shared__ __attribute__((aligned(16))) float wl[C * 8];
+  static_assert(HB == 4 || HB == 8, "head bound");
+  __shared__ __attribute__((aligned(16))) float wl[C * HB];
   if (a.w) {
-    // channel c = 8 j + e at [e][j][8]: the lanes of a row read adjacent
-    // 32-byte pieces for each e
-    for (int i = threadIdx.x; i < C * 8; i += 256) {
-      const int c = i >> 3, h = i & 7;
-      wl[((c & 7) * LANES + (c >> 3)) * 8 + h] = h < a.H ? a.w[c * a.H + h] : 0.0f;
+    // channel c = 8 j + e at [e][j][HB]: the lanes of a row read adjacent
+    // 4 HB-byte pieces for each e
+    for (int i = threadIdx.x; i < C * HB; i += 256) {
+      const int c = i / HB, h = i % HB;
+      wl[((c & 7) * LANES + (c >> 3)) * HB + h] = h < a.H ? a.w[c * a.H + h] : 0.0f;
     }
     __syncthreads();
   }
+  const float inv_q = 1.0f / (float)a.Q;
   const int j = threadIdx.x % LANES;
   // The LayerNorm affine of this lane's channels, read once (inside the
   // loop each read would wait behind the previous row's stores, which the
@@ -290,7 +294,18 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
     const int64_t r = r0 + threadIdx.x / LANES;
     const bool live = r < a.rows;
     const int64_t rr = live ? r : a.rows - 1;  // past the end: recompute the last row, store nothing
-    const int64_t b = rr / a.Q, q = rr % a.Q;
+    // floor(rr / Q) to within one from the f32 product (rr < 2^24 converts
+    // exactly; the product is off by less than one), then corrected.
+    int bi = (int)((float)(int)rr * inv_q);
+    int qi = (int)rr - bi * a.Q;
+    if (qi < 0) {
+      bi -= 1;
+      qi += a.Q;
+    } else if (qi >= a.Q) {
+      bi += 1;
+      qi -= a.Q;
+    }
+    const int64_t b = bi, q = qi;
     const int64_t src = a.transpose ? q * a.B + b : rr;
     float v[8];
     load8(reinterpret_cast<const IT*>(a.x) + src * C + 8 * j, v);
@@ -310,17 +325,18 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
     if (a.out && live) store8(reinterpret_cast<OT*>(a.out) + rr * C + 8 * j, v);
     if (a.mask && live && j == 0) key_bias_store(a, b * a.stride + q, a.mask[src]);
     if (a.w) {
-      float acc[8] = {};
+      float acc[HB] = {};
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        const float4 w0 = *reinterpret_cast<const float4*>(&wl[(e * LANES + j) * 8]);
-        const float4 w1 = *reinterpret_cast<const float4*>(&wl[(e * LANES + j) * 8 + 4]);
-        acc[0] += v[e] * w0.x, acc[1] += v[e] * w0.y, acc[2] += v[e] * w0.z, acc[3] += v[e] * w0.w;
-        acc[4] += v[e] * w1.x, acc[5] += v[e] * w1.y, acc[6] += v[e] * w1.z, acc[7] += v[e] * w1.w;
+#pragma unroll
+        for (int h4 = 0; h4 < HB; h4 += 4) {
+          const float4 w4 = *reinterpret_cast<const float4*>(&wl[(e * LANES + j) * HB + h4]);
+          acc[h4] += v[e] * w4.x, acc[h4 + 1] += v[e] * w4.y, acc[h4 + 2] += v[e] * w4.z, acc[h4 + 3] += v[e] * w4.w;
+        }
       }
       float mine = 0.0f;
 #pragma unroll
-      for (int h = 0; h < 8; h++) {
+      for (int h = 0; h < HB; h++) {
         const float t = lane_sum<LANES>(acc[h]);
         if (h == j) mine = t;
       }
@@ -751,13 +767,18 @@ int launch_rows_typed(const RowsArgs& r, const char* label, hipStream_t st) {
   const bool vec = (reinterpret_cast<uintptr_t>(r.x) & 15) == 0 &&
                    (!r.out || (reinterpret_cast<uintptr_t>(r.out) & 15) == 0);
   const dim3 block(256);
-  const bool heads_ok = !r.w || r.H <= 8;
-  if (vec && heads_ok && r.C == 64)
-    return launch(label, attention_rows_kernel<IT, OT, 8>, dim3((unsigned)std::min<int64_t>(ceil_div(r.rows, 32), 4096)), block, 0, st, r);
-  if (vec && heads_ok && r.C == 128)
-    return launch(label, attention_rows_kernel<IT, OT, 16>, dim3((unsigned)std::min<int64_t>(ceil_div(r.rows, 16), 4096)), block, 0, st, r);
-  if (vec && heads_ok && r.C == 256)
-    return launch(label, attention_rows_kernel<IT, OT, 32>, dim3((unsigned)std::min<int64_t>(ceil_div(r.rows, 8), 4096)), block, 0, st, r);
+  const bool fits = (!r.w || r.H <= 8) && r.rows < ((int64_t)1 << 24);
+  const bool four = !r.w || r.H <= 4;
+  auto grid = [&](int per_block) { return dim3((unsigned)std::min<int64_t>(ceil_div(r.rows, per_block), 4096)); };
+  if (vec && fits && r.C == 64)
+    return four ? launch(label, attention_rows_kernel<IT, OT, 8, 4>, grid(32), block, 0, st, r)
+                : launch(label, attention_rows_kernel<IT, OT, 8, 8>, grid(32), block, 0, st, r);
+  if (vec && fits && r.C == 128)
+    return four ? launch(label, attention_rows_kernel<IT, OT, 16, 4>, grid(16), block, 0, st, r)
+                : launch(label, attention_rows_kernel<IT, OT, 16, 8>, grid(16), block, 0, st, r);
+  if (vec && fits && r.C == 256)
+    return four ? launch(label, attention_rows_kernel<IT, OT, 32, 4>, grid(8), block, 0, st, r)
+                : launch(label, attention_rows_kernel<IT, OT, 32, 8>, grid(8), block, 0, st, r);
   return launch(label, attention_rows_any_kernel<IT, OT>, dim3((unsigned)ceil_div(r.rows, 4)), block, 0, st, r);
 }
 
