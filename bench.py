@@ -233,13 +233,29 @@ def gemm_shapes(launches: int = 20) -> dict:
     return out
 
 
+# Untimed clock settle before each measurement's warm-up steps. From a cold
+# start the headline step runs ~20% slow for its first ~20 ms of continuous
+# work while the GPU's clocks ramp (0.118 ms an operation, then 0.0955 from
+# ~20 ms on, measured on one MI355X), so a short timed region would measure
+# the ramp. `--settle-ms 0` turns it off.
+SETTLE_MS = 60.0
+
+
 def timed(fn, steps: int, warmup: int):
     """(ms per call by wall clock around synchronised loops, per-kernel
-    average ms from the library's hipEvents)."""
+    average ms from the library's hipEvents). The calls run for SETTLE_MS of
+    wall time first (untimed), then `warmup` untimed calls, then the timed
+    ones."""
     import torch
 
     from afhip import device
 
+    if SETTLE_MS > 0:
+        start = time.perf_counter()
+        while (time.perf_counter() - start) * 1e3 < SETTLE_MS:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -507,12 +523,16 @@ def measure_attention(steps: int, warmup: int) -> dict:
 
 
 def main() -> None:
+    global SETTLE_MS
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
     # A headline step is ~0.2 ms: 100 steps keep the timed region short while
     # averaging past the first steps' clock ramp.
     parser.add_argument("--steps", type=int, default=100)
     parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                        help="untimed run time before each measurement's warm-up steps, so the timed steps run at "
+                             "settled clocks (0: none)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--headline-only", action="store_true", help="skip BASELINE configs 1, 2, 4 and 5")
     parser.add_argument("--configs", default="1,2,4,5,attention,block",
@@ -525,6 +545,7 @@ def main() -> None:
                         help="only run the gemm-candidates benchmark (every candidate tile and the heuristic's "
                              "choice on the reference's SHAPES) and print it as one JSON line")
     args = parser.parse_args()
+    SETTLE_MS = args.settle_ms
     if args.gemm_shapes:
         print(json.dumps(gemm_shapes()))
         return
@@ -585,6 +606,7 @@ def main() -> None:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
