@@ -552,24 +552,36 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
       typedef TC tc4 __attribute__((ext_vector_type(4)));
       const uint32_t flags = g.flags;
       float* const bl = reinterpret_cast<float*>(smem);
+      const TC* R = reinterpret_cast<const TC*>(g.residual) + (int64_t)bt * g.sc;
+      TC* C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
+      auto load_res = [&](int i, tc4(&res)[TN][4]) {
+        const int row = m0 + wm + 32 * i + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; g4++)
+            res[j][g4] = *reinterpret_cast<const tc4*>(R + (int64_t)row * g.ldc + n0 + wn + 32 * j + 8 * g4 +
+                                                       4 * (lane >> 5));
+      };
+      // With f16 outputs the residual reads run one row block ahead of the
+      // stores (block 0's before the bias staging), so their round trips
+      // overlap the stores instead of preceding them; f32 has no registers
+      // to spare for the second block.
+      constexpr bool kAhead = sizeof(TC) == 2;
+      tc4 res_a[TN][4], res_b[TN][4];
+      if (kAhead && (flags & AFHIP_EPILOGUE_RESIDUAL)) load_res(0, res_a);
       if (flags & AFHIP_EPILOGUE_BIAS) {
         block_barrier<false>();  // every wave is done reading the stages
         for (int c = threadIdx.x; c < BN; c += kThreads) bl[c] = g.bias[n0 + c];
         block_barrier();
       }
-      const TC* R = reinterpret_cast<const TC*>(g.residual) + (int64_t)bt * g.sc;
-      TC* C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
 #pragma unroll
       for (int i = 0; i < TM; i++) {
         const int row = m0 + wm + 32 * i + (lane & 31);
-        tc4 res[TN][4];
+        tc4(&res)[TN][4] = (!kAhead || i % 2 == 0) ? res_a : res_b;
         if (flags & AFHIP_EPILOGUE_RESIDUAL) {
-#pragma unroll
-          for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int g4 = 0; g4 < 4; g4++)
-              res[j][g4] = *reinterpret_cast<const tc4*>(R + (int64_t)row * g.ldc + n0 + wn + 32 * j + 8 * g4 +
-                                                         4 * (lane >> 5));
+          if (!kAhead) load_res(i, res);
+          else if (i + 1 < TM) load_res(i + 1, i % 2 == 0 ? res_b : res_a);
         }
 #pragma unroll
         for (int j = 0; j < TN; j++)
