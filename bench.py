@@ -554,7 +554,8 @@ def main() -> None:
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the path runs on one device and bench.py "
-                                   "--gpus N>1 is not supported (see DESIGN.md for how it would shard)"}))
+                                   "--gpus N>1 is not supported: every GPU box here has one GPU; the path would shard on "
+                                   "output rows i, one process per GPU, with one all-gather of b"}))
         sys.exit(2)
 
     import numpy as np
