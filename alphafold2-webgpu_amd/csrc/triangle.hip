@@ -383,9 +383,9 @@ __global__ __launch_bounds__(256) void tri_output_kernel(OutputArgs a) {
 //   W' = s W diag(gamma),  b' = s (b + W beta),
 // gamma, beta the LayerNorm feeding the matrix and s = -log2(e) for the two
 // gates (their sigmoid then reads 1 / (1 + 2^acc)). Matrices, in order:
-// AP, AG, BP, BG (LayerNorm-in), Z (LayerNorm-out), G (LayerNorm-in), all
-// [out][in]; every product and the bias sum are taken in double and rounded
-// once (weights to f16, biases to f32).
+// AP, AG, BP, BG (LayerNorm-in), Z (LayerNorm-out), G (LayerNorm-in), each
+// 128 x 128 in MFMA fragment order (fold_index); every product and the bias
+// sum are taken in double and rounded once (weights to f16, biases to f32).
 struct FoldSources {
   const float* w[kFoldMatrices];
   const float* b[kFoldMatrices];
@@ -404,7 +404,7 @@ __global__ void fold_weights_kernel(FoldSources src, int n_out, int n_in, half_t
   double bias = src.b[m][n];
   for (int k = 0; k < n_in; k++) {
     bias += (double)w[k] * (double)src.beta[m][k];
-    w_out[((size_t)m * n_out + n) * n_in + k] = (half_t)(s * (double)w[k] * (double)src.gamma[m][k]);
+    w_out[fold_index(m, n, k)] = (half_t)(s * (double)w[k] * (double)src.gamma[m][k]);
   }
   b_out[(size_t)m * n_out + n] = (float)(s * bias);
 }

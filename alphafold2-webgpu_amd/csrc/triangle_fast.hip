@@ -149,19 +149,19 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
   const int t0 = blockIdx.x;
 
   // Weight fragments (the B operand): W[n][k] with n = hb + lane % 32,
-  // k = 16 s + 8 (lane / 32); the biases of this lane's channel.
+  // k = 16 s + 8 (lane / 32); the biases of this lane's channel. They are
+  // waited for together with the first two tiles, below.
   const int ch = hb + (lane & 31);
-  const half_t* wp = a.w_proj + (size_t)(2 * o) * kC * kC + (size_t)ch * kC + 8 * (lane >> 5);
+  const half_t* wp = a.w_proj + (size_t)(2 * o) * kC * kC;
   const half_t* wg = wp + (size_t)kC * kC;
   half8 fp[8], fg[8];
 #pragma unroll
   for (int s = 0; s < 8; s++) {
-    fp[s] = *reinterpret_cast<const half8*>(wp + 16 * s);
-    fg[s] = *reinterpret_cast<const half8*>(wg + 16 * s);
+    fp[s] = fold_fragment(wp, wave & 3, s, lane);
+    fg[s] = fold_fragment(wg, wave & 3, s, lane);
   }
   const float bp = a.b_proj[(2 * o) * kC + ch];
   const float bg = a.b_proj[(2 * o + 1) * kC + ch];
-  wait_vmcnt<0>();  // weights in hand before the tile loads queue up behind them
 
   const int32x4_t rz = make_rsrc(a.z, (uint32_t)((int64_t)a.P * Lay::ZROW));
   const int32x4_t rm = make_rsrc(a.mask, (uint32_t)((int64_t)a.P * 4));
@@ -221,8 +221,9 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       }
     }
   };
-  // Loader waves. Before the loop: tile 0 has landed once the S - 1 tiles
-  // issued after it are all that may be pending. In pass `it`: tile it + 1
+  // Loader waves. Before the loop the weights and the first two tiles are
+  // waited for together (the compiler's own wait for the weights, which
+  // follows the untracked tile loads, would drain them anyway). In pass `it`: tile it + 1
   // has landed once what was issued after its loads is all that may be
   // pending: the loads of tiles it + 2 .. it + S - 1 and, since every wave
   // stores its rows of each finished tile (kStores instructions a pass), the
@@ -230,10 +231,6 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
   // complete in issue order, loads and stores alike. When a later tile was
   // not issued (the end of the range), wait for everything.
   constexpr int kStores = 2 * kC * kTile * 2 / 1024 / (kThreads / 64);  // a wave's 32 rows of 64 pairs, 1 KiB a store
-  auto wait_first = [&](bool later_issued) {
-    if (wave == 0) wait_stage<(S - 1) * (Lay::LPW + 1)>(later_issued);
-    else wait_stage<(S - 1) * Lay::LPW>(later_issued);
-  };
   auto wait_next = [&](int it, bool later_issued) {
     if (!later_issued) wait_vmcnt<0>();
     else if (wave == 0) wait_vmcnt_by<(S - 2) * (Lay::LPW + 1), kStores, S - 1>(it);
@@ -272,11 +269,18 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       __builtin_amdgcn_make_buffer_rsrc(o == 0 ? a.out_a : a.out_b, 0, obytes, 0x00020000);
 
   if (t0 >= ntiles) return;
+  // The weights and the first two tiles load at once; the other stages are
+  // filled once they have landed.
+  static_assert(S >= 2, "two tiles in the first wait");
+  if (wave < kLoaderWaves) {
+    issue(t0, 0);
+    if (t0 + G < ntiles) issue(t0 + G, 1);
+  }
+  wait_vmcnt<0>();
   if (wave < kLoaderWaves) {
 #pragma unroll
-    for (int s = 0; s < S; s++)
+    for (int s = 2; s < S; s++)
       if (t0 + s * G < ntiles) issue(t0 + s * G, s);
-    wait_first(t0 + (S - 1) * G < ntiles);
   }
   block_barrier();  // the first tile has landed
   layer_norm_tile(0, zn_base, mask_base);
@@ -398,19 +402,23 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_f16_kernel(FastOutputA
 
   // Weight fragments (the A operand): W[n][k] with n = nt + lane % 32; the
   // biases of this lane's accumulator rows n = nt + mfma_row(v).
-  const half_t* wz = a.w_z + (size_t)(nt + (lane & 31)) * kC + 8 * (lane >> 5);
-  const half_t* wgp = a.w_g + (size_t)(nt + (lane & 31)) * kC + 8 * (lane >> 5);
   half8 fz[8], fg[8];
 #pragma unroll
   for (int s = 0; s < 8; s++) {
-    fz[s] = *reinterpret_cast<const half8*>(wz + 16 * s);
-    fg[s] = *reinterpret_cast<const half8*>(wgp + 16 * s);
+    fz[s] = fold_fragment(a.w_z, wave & 3, s, lane);
+    fg[s] = fold_fragment(a.w_g, wave & 3, s, lane);
   }
+  // Rows mfma_row(v, lane) come in runs of four: 8 (v / 4) + 4 (lane / 32) ..
   float bzv[16], bgv[16];
 #pragma unroll
-  for (int v = 0; v < 16; v++) {
-    bzv[v] = a.b_z[nt + mfma_row(v, lane)];
-    bgv[v] = a.b_g[nt + mfma_row(v, lane)];
+  for (int g4 = 0; g4 < 4; g4++) {
+    const floatx4 z4 = *reinterpret_cast<const floatx4*>(a.b_z + nt + 8 * g4 + 4 * (lane >> 5));
+    const floatx4 q4 = *reinterpret_cast<const floatx4*>(a.b_g + nt + 8 * g4 + 4 * (lane >> 5));
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      bzv[4 * g4 + e] = z4[e];
+      bgv[4 * g4 + e] = q4[e];
+    }
   }
   wait_vmcnt<0>();  // weights in hand before the tile loads queue up behind them
 
@@ -639,21 +647,25 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_pipe_kernel(FastOutput
   const int nt = 32 * (wave & 3), rh = 32 * (wave >> 2);
   const int G = gridDim.x;
 
-  const half_t* wz = a.w_z + (size_t)(nt + (lane & 31)) * kC + 8 * (lane >> 5);
-  const half_t* wgp = a.w_g + (size_t)(nt + (lane & 31)) * kC + 8 * (lane >> 5);
   half8 fz[8], fg[8];
 #pragma unroll
   for (int s = 0; s < 8; s++) {
-    fz[s] = *reinterpret_cast<const half8*>(wz + 16 * s);
-    fg[s] = *reinterpret_cast<const half8*>(wgp + 16 * s);
+    fz[s] = fold_fragment(a.w_z, wave & 3, s, lane);
+    fg[s] = fold_fragment(a.w_g, wave & 3, s, lane);
   }
+  // Rows mfma_row(v, lane) come in runs of four: 8 (v / 4) + 4 (lane / 32) ..
   float bzv[16], bgv[16];
 #pragma unroll
-  for (int v = 0; v < 16; v++) {
-    bzv[v] = a.b_z[nt + mfma_row(v, lane)];
-    bgv[v] = a.b_g[nt + mfma_row(v, lane)];
+  for (int g4 = 0; g4 < 4; g4++) {
+    const floatx4 z4 = *reinterpret_cast<const floatx4*>(a.b_z + nt + 8 * g4 + 4 * (lane >> 5));
+    const floatx4 q4 = *reinterpret_cast<const floatx4*>(a.b_g + nt + 8 * g4 + 4 * (lane >> 5));
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      bzv[4 * g4 + e] = z4[e];
+      bgv[4 * g4 + e] = q4[e];
+    }
   }
-  wait_vmcnt<0>();  // weights in hand before the tile loads queue up behind them
+  // The weights are waited for together with the first tile, below.
 
   const int32x4_t rx = make_rsrc(a.contracted, (uint32_t)((int64_t)kC * a.bstride * 2));
   const int32x4_t rz = make_rsrc(reinterpret_cast<const unsigned char*>(a.z) + (size_t)a.pair0 * Lay::ZROW,
@@ -809,8 +821,8 @@ __global__ __launch_bounds__(kThreads, 1) void tri_output_pipe_kernel(FastOutput
   const int t0 = blockIdx.x;
   if (t0 >= ntiles) return;
   if (wave < kLoaderWaves) issue(t0, 0);
-  // First tile: statistics only.
-  if (wave < kLoaderWaves) wait_tile(false);
+  // First tile: statistics only. Every wave's weights have landed too.
+  wait_vmcnt<0>();
   block_barrier();  // B1
   if (wave < kLoaderWaves && t0 + G < ntiles) issue(t0 + G, 1);
   stats_and_zln(0, 0);
