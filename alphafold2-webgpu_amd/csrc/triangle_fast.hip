@@ -36,6 +36,7 @@
 // out = p sigmoid(g) (+ out when accumulating) is written along the pair's
 // 128 channels.
 #include <algorithm>
+#include <type_traits>
 
 #include "dma.h"
 #include "triangle_fast.h"
@@ -249,8 +250,11 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       normalize16(x, a.eps, zn + row * kPitch + c0);
     }
     // Every wave copies the same 64 values (no branch, so this stays in the
-    // straight-line block the MFMAs are scheduled with).
-    mdst[lane] = reinterpret_cast<const float*>(st + Lay::ZBYTES)[lane];
+    // straight-line block the MFMAs are scheduled with) and learns whether
+    // they are all 1.
+    const float mv = reinterpret_cast<const float*>(st + Lay::ZBYTES)[lane];
+    mdst[lane] = mv;
+    return __builtin_amdgcn_ballot_w64(mv == 1.0f) == ~0ull;
   };
 
   // A wave's stores: its 32 channel rows of the staged tile, store k
@@ -283,14 +287,14 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       if (t0 + s * G < ntiles) issue(t0 + s * G, s);
   }
   block_barrier();  // the first tile has landed
-  layer_norm_tile(0, zn_base, mask_base);
+  bool ones = layer_norm_tile(0, zn_base, mask_base);
 
-  for (int it = 0, tile = t0; tile < ntiles; it++, tile += G) {
-    // Tiles it + 2 .. it + S - 1 may still be in flight; tile it + 1 must be in.
-    if (wave < kLoaderWaves) wait_next(it, tile + (S - 1) * G < ntiles);
-    block_barrier();  // zn[it % 2] complete, the next tile landed
-    if (wave < kLoaderWaves && tile + S * G < ntiles) issue(tile + S * G, it % S);
-
+  // One pass; MASKED false (every mask value of the tile 1) leaves out the
+  // multiplication by the mask, which would not change a bit.
+  int it = 0, tile = t0;
+  auto pass = [&](auto masked) -> bool {
+    constexpr bool MASKED = decltype(masked)::value;
+    bool ones_next;
     const half_t* zn = zn_base + (it & 1) * kTile * kPitch;
     const float* mk = mask_base + (it & 1) * kTile;
     half_t* orow = ost + (o * kC + ch) * kOutPitch;
@@ -316,11 +320,16 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       for (int g4 = 0; g4 < 4; g4++) {
         // rows 4 g4 .. 4 g4 + 3 of the accumulator: pairs p0 .. p0 + 3
         const int p0 = sub * 32 + 8 * g4 + 4 * (lane >> 5);
-        const floatx4 m4 = *reinterpret_cast<const floatx4*>(mk + p0);
         half4 h;
+        if constexpr (MASKED) {
+          const floatx4 m4 = *reinterpret_cast<const floatx4*>(mk + p0);
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-          h[e] = (half_t)(m4[e] * accp[sub][4 * g4 + e] * gate_of(accg[sub][4 * g4 + e]));
+          for (int e = 0; e < 4; e++)
+            h[e] = (half_t)(m4[e] * accp[sub][4 * g4 + e] * gate_of(accg[sub][4 * g4 + e]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++) h[e] = (half_t)(accp[sub][4 * g4 + e] * gate_of(accg[sub][4 * g4 + e]));
+        }
         *reinterpret_cast<half4*>(orow + p0) = h;
       }
     };
@@ -330,7 +339,8 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
     // the compiler to interleave each MFMA with vector work instead of
     // issuing them back to back.
     mfma_sub(0);
-    layer_norm_tile((it + 1) % S, zn_base + ((it + 1) & 1) * kTile * kPitch, mask_base + ((it + 1) & 1) * kTile);
+    ones_next =
+        layer_norm_tile((it + 1) % S, zn_base + ((it + 1) & 1) * kTile * kPitch, mask_base + ((it + 1) & 1) * kTile);
     mfma_sub(1);
     epilogue_sub(0);
     epilogue_sub(1);
@@ -353,6 +363,14 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
         __builtin_amdgcn_raw_buffer_store_b128(v[k], rso, svof[k], (uint32_t)tile * kTile * 2, 0);
       stores_read(v[0], v[1], v[2], v[3]);
     }
+    return ones_next;
+  };
+  for (; tile < ntiles; it++, tile += G) {
+    // Tiles it + 2 .. it + S - 1 may still be in flight; tile it + 1 must be in.
+    if (wave < kLoaderWaves) wait_next(it, tile + (S - 1) * G < ntiles);
+    block_barrier();  // zn[it % 2] complete, the next tile landed
+    if (wave < kLoaderWaves && tile + S * G < ntiles) issue(tile + S * G, it % S);
+    ones = ones ? pass(std::false_type{}) : pass(std::true_type{});
   }
 }
 
