@@ -202,7 +202,7 @@ def calibration_clear() -> None:
     _lib.call("afhip_calibration_clear")
 
 
-CALIBRATION_FAULTS = {"none": 0, "run": 1, "result": 2}
+CALIBRATION_FAULTS = {"none": 0, "run": 1, "result": 2, "last-batch": 3}
 
 
 def calibration_inject(kernel: str, tile_rows: int, tile_columns: int, fault: str) -> None:

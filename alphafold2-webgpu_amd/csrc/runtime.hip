@@ -1,4 +1,5 @@
 // Context, errors, buffers, device report and kernel timing.
+#include <atomic>
 #include <cstdarg>
 #include <cstring>
 #include <map>
@@ -12,15 +13,19 @@ namespace afhip {
 namespace {
 thread_local std::string g_last_error = "no error";
 std::mutex g_mutex;
-int g_device = -1;
-int g_cu_count = 0;
+// Read without the lock by every entry point (require_open, the launch paths),
+// possibly on other threads than the one that opens or closes the context
+// (the Node addon runs operators on its worker threads).
+std::atomic<int> g_device{-1};
+std::atomic<int> g_cu_count{0};
 
 struct TimingRecord {
   hipEvent_t start, stop;
   std::string label;
 };
-bool g_timing = false;
+std::atomic<bool> g_timing{false};
 thread_local int g_timing_off = 0;
+std::mutex g_timing_mutex;  // guards g_pending and g_totals
 std::vector<TimingRecord> g_pending;
 std::map<std::string, std::pair<long, double>> g_totals;
 }  // namespace
@@ -40,21 +45,22 @@ int hip_status(hipError_t err, const char* what) {
   return set_error(AFHIP_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
 }
 
-bool is_open() { return g_device >= 0; }
+bool is_open() { return g_device.load(std::memory_order_relaxed) >= 0; }
 
 int require_open() {
-  if (g_device < 0) return set_error(AFHIP_ERR_NOT_OPEN, "afhip_open has not been called");
+  if (g_device.load(std::memory_order_relaxed) < 0)
+    return set_error(AFHIP_ERR_NOT_OPEN, "afhip_open has not been called");
   return AFHIP_OK;
 }
 
-int device_cu_count() { return g_cu_count; }
+int device_cu_count() { return g_cu_count.load(std::memory_order_relaxed); }
 
 bool timing_enabled() { return g_timing && g_timing_off == 0; }
 
 TimingOff::TimingOff() { g_timing_off++; }
 TimingOff::~TimingOff() { g_timing_off--; }
 
-int current_device() { return g_device; }
+int current_device() { return g_device.load(std::memory_order_relaxed); }
 
 int allow_lds(const void* kernel, size_t bytes) {
   if (bytes <= 65536) return AFHIP_OK;
@@ -77,8 +83,12 @@ bool timing_events(hipEvent_t* start, hipEvent_t* stop) {
   return true;
 }
 
-void timing_record(const char* label, hipEvent_t start, hipEvent_t stop) { g_pending.push_back({start, stop, label}); }
+void timing_record(const char* label, hipEvent_t start, hipEvent_t stop) {
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
+  g_pending.push_back({start, stop, label});
+}
 
+// Callers hold g_timing_mutex.
 static void timing_drain() {
   for (auto& r : g_pending) {
     (void)hipEventSynchronize(r.stop);
@@ -132,7 +142,7 @@ int afhip_device_report(char* json, size_t capacity) {
   if (int s = require_open()) return s;
   AFHIP_REQUIRE(json != nullptr && capacity > 0, "report buffer is empty");
   hipDeviceProp_t prop;
-  AFHIP_CHECK_HIP(hipGetDeviceProperties(&prop, g_device));
+  AFHIP_CHECK_HIP(hipGetDeviceProperties(&prop, current_device()));
   int driver = 0, runtime = 0;
   (void)hipDriverGetVersion(&driver);
   (void)hipRuntimeGetVersion(&runtime);
@@ -188,14 +198,14 @@ int afhip_timing_enable(int enable) {
 }
 
 int afhip_timing_reset(void) {
-  std::lock_guard<std::mutex> lock(g_mutex);
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
   timing_drain();
   g_totals.clear();
   return AFHIP_OK;
 }
 
 int afhip_timing_report(char* json, size_t capacity) {
-  std::lock_guard<std::mutex> lock(g_mutex);
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
   AFHIP_REQUIRE(json != nullptr && capacity > 0, "report buffer is empty");
   timing_drain();
   std::string out = "{";

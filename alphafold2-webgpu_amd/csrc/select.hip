@@ -241,10 +241,11 @@ int afhip_gemm_calibrate(const afhip_gemm_desc* d, afhip_variant* out) {
   g.sc = (int64_t)M * N;
   g.batch = B;
 
-  // Correctness first, on up to 256 sampled rows spread over every batch
-  // (the first and last rows of each batch among them), so a candidate that
-  // is wrong only on later batches or rows cannot win.
-  const int samples = (int)std::min<int64_t>((int64_t)M * B, 256);
+  // Correctness first, on sampled rows spread over every batch (the first
+  // and last rows of each batch among them), so a candidate that is wrong
+  // only on later batches or rows cannot win: 256 rows, or one row of every
+  // batch when there are more batches than that.
+  const int samples = (int)std::min<int64_t>((int64_t)M * B, std::max<int64_t>(256, B));
   std::vector<int> sb(samples), sm(samples);
   for (int r = 0; r < samples; r++) {
     sb[r] = r % B;
@@ -281,7 +282,8 @@ int afhip_gemm_calibrate(const afhip_gemm_desc* d, afhip_variant* out) {
         const size_t at = ((size_t)sb[r] * M + sm[r]) * N + n;
         double got = t.c_dtype == AFHIP_F32 ? (double)reinterpret_cast<float*>(host.data())[at]
                                             : (double)(float)reinterpret_cast<_Float16*>(host.data())[at];
-        if (fault == AFHIP_CALIBRATION_FAULT_RESULT) got += 0.05 * scale;
+        if (fault == AFHIP_CALIBRATION_FAULT_RESULT || (fault == AFHIP_CALIBRATION_FAULT_LAST_BATCH && sb[r] == B - 1))
+          got += 0.05 * scale;
         worst = std::max(worst, std::fabs(got - (double)expect[(size_t)r * N + n]));
       }
     double rel = scale == 0.0 ? INFINITY : worst / scale;
@@ -341,7 +343,7 @@ int afhip_calibration_inject(int32_t kernel, int32_t tile_rows, int32_t tile_col
     g_faults.clear();
     return AFHIP_OK;
   }
-  AFHIP_REQUIRE(fault >= AFHIP_CALIBRATION_FAULT_NONE && fault <= AFHIP_CALIBRATION_FAULT_RESULT,
+  AFHIP_REQUIRE(fault >= AFHIP_CALIBRATION_FAULT_NONE && fault <= AFHIP_CALIBRATION_FAULT_LAST_BATCH,
                 "unknown calibration fault %d", fault);
   const auto key = std::make_tuple((int)kernel, (int)tile_rows, (int)tile_columns);
   if (fault == AFHIP_CALIBRATION_FAULT_NONE) g_faults.erase(key);

@@ -202,6 +202,12 @@ struct ExecutionEntry {
   // (allocation index in the execution, buffer handle) of each tensor this
   // addon handed out, so release_since can retire the handles it frees.
   std::vector<std::pair<uint64_t, uint32_t>> handles;
+  // Operator runs queued on this execution whose completion has not run yet
+  // (counted on the JS thread only). A destroy requested while some are
+  // pending marks the entry released: no new work may name it, and the last
+  // completion frees it, since its worker may still be using the memory.
+  int pending = 0;
+  bool released = false;
 };
 
 struct Registry {
@@ -234,6 +240,10 @@ double now_ms() {
 // ---------------------------------------------------------------------------
 
 int g_ordinal = 0;  // the device Open selected; each worker thread selects it too
+// Set by Close while operator runs are still queued: the context is closed by
+// the last of their completions instead (a worker re-selects the device and
+// uses the execution's memory until its job ends).
+bool g_close_deferred = false;
 
 napi_value Open(napi_env env, napi_callback_info info) {
   Args a;
@@ -242,18 +252,37 @@ napi_value Open(napi_env env, napi_callback_info info) {
   if (a.argc > 0 && !get_int64(env, a.argv[0], &ordinal)) return nullptr;
   if (!check(env, afhip_open((int)ordinal), "open")) return nullptr;
   g_ordinal = (int)ordinal;
+  g_close_deferred = false;  // opened again before the pending runs ended: stay open
   return nullptr;
+}
+
+bool runs_pending() {
+  for (auto& kv : g_reg.executions)
+    if (kv.second.pending > 0) return true;
+  return false;
 }
 
 napi_value Close(napi_env env, napi_callback_info) {
   for (auto& kv : g_reg.buffers)
     if (!g_reg.owner.count(kv.first)) afhip_buffer_destroy(kv.second.first);
-  for (auto& kv : g_reg.executions) afhip_execution_destroy(kv.second.ex);
+  for (auto it = g_reg.executions.begin(); it != g_reg.executions.end();) {
+    if (it->second.pending > 0) {
+      it->second.released = true;
+      ++it;
+    } else {
+      afhip_execution_destroy(it->second.ex);
+      it = g_reg.executions.erase(it);
+    }
+  }
   for (auto& kv : g_reg.plans) afhip_gemm_plan_destroy(kv.second);
   g_reg.buffers.clear();
   g_reg.plans.clear();
-  g_reg.executions.clear();
   g_reg.owner.clear();
+  g_reg.prepared.clear();
+  if (runs_pending()) {
+    g_close_deferred = true;
+    return nullptr;
+  }
   if (!check(env, afhip_close(), "close")) return nullptr;
   return nullptr;
 }
@@ -660,7 +689,7 @@ bool lookup_execution(napi_env env, napi_value v, uint32_t* handle, ExecutionEnt
   int64_t h;
   if (!get_int64(env, v, &h)) return false;
   auto it = g_reg.executions.find((uint32_t)h);
-  if (it == g_reg.executions.end()) {
+  if (it == g_reg.executions.end() || it->second.released) {
     throw_js(env, {true, "unknown execution handle " + std::to_string(h)});
     return false;
   }
@@ -732,6 +761,11 @@ napi_value ExecutionDestroy(napi_env env, napi_callback_info info) {
   ExecutionEntry* e;
   if (!lookup_execution(env, a.argv[0], &exh, &e)) return nullptr;
   for (auto& ih : e->handles) forget_buffer(ih.second);
+  e->handles.clear();
+  if (e->pending > 0) {
+    e->released = true;  // the last pending run's completion destroys it
+    return nullptr;
+  }
   afhip_execution_destroy(e->ex);
   g_reg.executions.erase(exh);
   return nullptr;
@@ -1157,6 +1191,7 @@ struct OperatorJob {
   napi_async_work work = nullptr;
   napi_deferred deferred = nullptr;
   afhip_execution* ex = nullptr;
+  uint32_t exh = 0;  // the execution's handle, for its pending count
   std::mutex* lock = nullptr;
   std::vector<std::vector<char>> inputs;  // host copies, in the order the body uploads them
   int (*body)(OperatorJob&) = nullptr;
@@ -1303,7 +1338,18 @@ void job_complete(napi_env env, napi_status, void* data) {
     napi_reject_deferred(env, j->deferred, err);
   }
   napi_delete_async_work(env, j->work);
+  // The worker is done with the execution: free it if a destroy (or Close)
+  // came while this run was pending, and finish a deferred Close.
+  auto it = g_reg.executions.find(j->exh);
+  if (it != g_reg.executions.end() && --it->second.pending == 0 && it->second.released) {
+    afhip_execution_destroy(it->second.ex);
+    g_reg.executions.erase(it);
+  }
   delete j;
+  if (g_close_deferred && !runs_pending()) {
+    g_close_deferred = false;
+    (void)afhip_close();
+  }
 }
 
 std::mutex& execution_lock(uint32_t handle) {
@@ -1325,6 +1371,8 @@ bool job_input(napi_env env, napi_value v, OperatorJob& j, HostView* view = null
 
 napi_value queue_job(napi_env env, OperatorJob* j, uint32_t exh, const char* name) {
   j->lock = &execution_lock(exh);
+  j->exh = exh;
+  g_reg.executions[exh].pending++;
   napi_value promise, resource;
   napi_create_promise(env, &j->deferred, &promise);
   napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &resource);

@@ -72,9 +72,14 @@ export interface TriangleMultiplicationInput {
 export interface TriangleGpuOptions {
   readonly precision?: Precision;
   readonly blockRows?: number;
+  /** Accepted for compatibility; the operands are stored in the precision's
+   * dtype, and a value that differs is reported once as a Node warning
+   * (code AFHIP_OPTION). Values other than "f32" / "f16" throw RangeError. */
+  readonly wholeStorage?: "f32" | "f16";
 }
 
-/** Every operator owns its allocator; release() frees its pooled buffers. */
+/** Every operator owns its allocator; release() frees its pooled buffers
+ * (after any run still pending on it has finished). */
 declare class HipOperator {
   release(): void;
 }

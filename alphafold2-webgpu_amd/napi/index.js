@@ -173,9 +173,41 @@ Operator.prototype.release = function () {
   }
 };
 
+// Options of the reference that this backend takes with another meaning are
+// reported once per process as a Node warning (code AFHIP_OPTION), so a
+// caller switching backends learns of them without its runs failing.
+var warned = {};
+function warnOnce(key, message) {
+  if (warned[key]) return;
+  warned[key] = true;
+  process.emitWarning(message, { code: "AFHIP_OPTION" });
+}
+
+// The triangle options with no exact counterpart (src/triangle/webgpu.ts:9-15):
+// wholeStorage picks the reference's storage of the whole projection; here
+// the a/b operands are always stored in the precision's dtype. precision
+// "f16" is the reference's f16 weights over an f32 pair; here f16 MFMA
+// operands with f32 accumulation.
+function triangleOptionNotes(options, precision) {
+  if (options.wholeStorage !== undefined) {
+    if (options.wholeStorage !== "f32" && options.wholeStorage !== "f16") {
+      throw new RangeError("unknown wholeStorage " + options.wholeStorage);
+    }
+    if (options.wholeStorage !== precision) {
+      warnOnce("wholeStorage", "wholeStorage \"" + options.wholeStorage + "\" has no effect on the HIP backend: " +
+        "the triangle operands are stored as " + precision + ", the precision's dtype");
+    }
+  }
+  if (precision === "f16") {
+    warnOnce("precision-f16", "precision \"f16\" on the HIP backend runs f16 MFMA operands (weights, normalised " +
+      "activations and the a/b projections) with f32 accumulation, where the WebGPU backend keeps an f32 pair " +
+      "with f16 weights");
+  }
+}
+
 // TriangleMultiplication{Outgoing,Incoming}Gpu (src/triangle/webgpu.ts:42-214).
-// run(input: TriangleMultiplicationInput, {precision, blockRows}) ->
-// Promise<{output, elapsedMilliseconds, memory}>.
+// run(input: TriangleMultiplicationInput, {precision, blockRows, wholeStorage})
+// -> Promise<{output, elapsedMilliseconds, memory}>.
 function TriangleMultiplicationGpu(device, direction) {
   Operator.call(this, device);
   this.direction = direction;
@@ -188,6 +220,7 @@ TriangleMultiplicationGpu.prototype.run = function (input, options) {
     validateTriangleInput(input);
     var precision = precisionOf(options, "f32");
     if (options.blockRows !== undefined) positiveInteger("blockRows", options.blockRows);
+    triangleOptionNotes(options, precision);
     return addon().triangleRun(self._execution(), {
       length: input.shape.length, cZ: input.shape.cZ, cHidden: input.shape.cHidden,
       direction: self.direction === "incoming" ? 1 : 0,

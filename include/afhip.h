@@ -251,12 +251,15 @@ AFHIP_API int afhip_calibration_clear(void);
  * RUN makes the candidate count as one that failed to run (dropped, as
  * measureGemmVariants drops it, gemm-selection.ts:482-495); RESULT offsets
  * the candidate's result by 5% of the reference's largest value as the check
- * reads it (refused, :584-586). NONE clears the candidate's fault; NONE with
- * kernel < 0 clears them all. No counterpart in the reference beyond those
- * rules; for tests. */
+ * reads it (refused, :584-586); LAST_BATCH does the same to the rows of
+ * the shape's last batch entry only, so a check that sampled fewer batches
+ * would let the candidate through. NONE clears the candidate's fault; NONE
+ * with kernel < 0 clears them all. No counterpart in the reference beyond
+ * those rules; for tests. */
 #define AFHIP_CALIBRATION_FAULT_NONE 0
 #define AFHIP_CALIBRATION_FAULT_RUN 1
 #define AFHIP_CALIBRATION_FAULT_RESULT 2
+#define AFHIP_CALIBRATION_FAULT_LAST_BATCH 3
 AFHIP_API int afhip_calibration_inject(int32_t kernel, int32_t tile_rows, int32_t tile_columns, int32_t fault);
 
 /* Weight preparation for GEMM plans: W[k][n] -> W[n][k] (and f32 -> f16 when

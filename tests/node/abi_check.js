@@ -66,6 +66,19 @@ async function main() {
     /cZ must be a positive safe integer; received undefined/);
   assert.throws(function () { afhip.validateTriangleInput({ shape: { length: 0, cZ: 3, cHidden: 4 } }); },
     RangeError);
+  // The reference's wholeStorage option: an unknown value is refused before
+  // any device work; one the backend does not apply is reported once as a
+  // Node warning (the run itself then needs the device).
+  var valid = createDeterministicTriangleInput({ length: 4, cZ: 8, cHidden: 4 }, 3);
+  await rejects(new afhip.TriangleMultiplicationOutgoingGpu().run(valid, { wholeStorage: "f64" }),
+    /unknown wholeStorage f64/);
+  var warnings = [];
+  process.on("warning", function (w) { if (w.code === "AFHIP_OPTION") warnings.push(w.message); });
+  try { await new afhip.TriangleMultiplicationOutgoingGpu().run(valid, { wholeStorage: "f16" }); } catch (e) { /* no device */ }
+  try { await new afhip.TriangleMultiplicationOutgoingGpu().run(valid, { wholeStorage: "f16" }); } catch (e) { /* no device */ }
+  await new Promise(function (resolve) { setImmediate(resolve); });
+  assert.strictEqual(warnings.length, 1, JSON.stringify(warnings));
+  assert.ok(/wholeStorage "f16" has no effect/.test(warnings[0]), warnings[0]);
   await rejects(new afhip.OuterProductMeanGpu().run({ sequences: 2, length: 0, cM: 4, cOuter: 2, cZ: 3 }),
     /outer product mean dimensions must be positive safe integers/);
   await rejects(new afhip.OuterProductMeanGpu().run({ sequences: 2, length: 3, cM: 4, cOuter: 2, cZ: 3,

@@ -10,10 +10,8 @@ var assert = require("assert");
 var fs = require("fs");
 var path = require("path");
 var afhip = require("../../alphafold2-webgpu_amd/napi/index.js");
-var loadTriangleReferenceBundleFromFiles = require("./fixtures.js").loadTriangleReferenceBundleFromFiles;
 var createDeterministicTriangleInput = require("./deterministic.js").createDeterministicTriangleInput;
 
-var golden = path.join(__dirname, "..", "golden");
 var expectedDir = process.env.AFHIP_NODE_EXPECTED;
 var report = { node: process.versions.node, cases: [] };
 
@@ -28,6 +26,25 @@ function transposePairs(data, L, C) {
 function readF32(name) {
   var bytes = fs.readFileSync(path.join(expectedDir, name));
   return new Float32Array(bytes.buffer.slice(bytes.byteOffset, bytes.byteOffset + bytes.byteLength));
+}
+
+// A triangle fixture as the Python side hands it over: <name>.json lists the
+// arrays (name, element count) in the order they are packed into <name>.f32,
+// plus the shape and epsilon; the result is the reference's operator input
+// and the expected output.
+function readTriangleFixture(name) {
+  var index = JSON.parse(fs.readFileSync(path.join(expectedDir, name + ".json"), "utf8"));
+  var data = readF32(name + ".f32");
+  var arrays = {}, at = 0;
+  index.arrays.forEach(function (entry) {
+    arrays[entry[0]] = data.subarray(at, at + entry[1]);
+    at += entry[1];
+  });
+  assert.strictEqual(at, data.length, name + " holds " + data.length + " values, its index " + at);
+  var weights = {};
+  index.weights.forEach(function (n) { weights[n] = arrays[n]; });
+  return { input: { shape: index.shape, epsilon: index.epsilon, z: arrays.z, mask: arrays.mask, weights: weights },
+    expected: arrays.expected };
 }
 
 function relativeMax(actual, expected) {
@@ -55,12 +72,11 @@ function checkSnapshot(memory, labelPrefix) {
 async function main() {
   afhip.requestHipDevice(0);
 
-  // The reference's triangle fixtures, loaded as loadTriangleReferenceBundleFromFiles
-  // does, with their own TriangleShape objects.
+  // The reference's triangle fixtures, with their own TriangleShape objects.
   var fixtures = ["openfold-triangle-small", "alphafold-short-9", "alphafold-single-sequence-59", "alphafold-a3m-59"];
   for (var fi = 0; fi < fixtures.length; fi++) {
     var name = fixtures[fi];
-    var b = await loadTriangleReferenceBundleFromFiles(path.join(golden, name, "manifest.json"));
+    var b = readTriangleFixture(name);
     var L = b.input.shape.length, C = b.input.shape.cZ;
     var op = new afhip.TriangleMultiplicationOutgoingGpu(null);
     var pending = op.run(b.input, { precision: "f32" });
@@ -89,6 +105,33 @@ async function main() {
     assert.ok(mi.maxAbsoluteError <= 1e-6, name + " incoming " + JSON.stringify(mi));
     report.cases.push({ fixture: name, f32: m32, f16MaxRelative: r16, incomingVsTransposed: mi });
   }
+
+  // release() right after run(), before the run is awaited: the pending run
+  // still resolves (its device memory is freed when it has finished), and
+  // the operator's next run makes a new execution.
+  await (async function () {
+    var first = readTriangleFixture(fixtures[0]);
+    var op = new afhip.TriangleMultiplicationOutgoingGpu(null);
+    var pending = op.run(first.input);
+    op.release();
+    var done = await pending;
+    var m = afhip.errorMetrics(done.output, first.expected);
+    assert.ok(m.maxAbsoluteError < 1e-4, "run resolved after release " + JSON.stringify(m));
+    var again = await op.run(first.input);
+    assert.deepStrictEqual(Buffer.from(again.output.buffer), Buffer.from(done.output.buffer));
+    op.release();
+    // Two runs pending on two operators while the context closes: both
+    // resolve, and the context closes when the second has finished.
+    var ops = [new afhip.TriangleMultiplicationOutgoingGpu(null), new afhip.TriangleMultiplicationOutgoingGpu(null)];
+    var runs = ops.map(function (o) { return o.run(first.input); });
+    afhip.addon().close();
+    var both = await Promise.all(runs);
+    both.forEach(function (r) {
+      assert.deepStrictEqual(Buffer.from(r.output.buffer), Buffer.from(done.output.buffer));
+    });
+    afhip.addon().open(0);
+    report.cases.push({ releaseWhilePending: m });
+  })();
 
   // createDeterministicTriangleInput, both directions, against the oracle;
   // two runs queued on one operator without awaiting the first.

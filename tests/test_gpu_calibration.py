@@ -104,3 +104,15 @@ def test_corrupt_document_is_ignored(gemm, tmp_path, corrupt):
     gemm.calibration_clear()
     gemm.calibration_load(str(path))
     assert select(gemm).source == "heuristic"
+
+
+def test_every_batch_is_checked(gemm):
+    # 300 batch entries of 8 x 32 x 40: more batches than the check's 256
+    # sampled rows. A winner whose results are off only in the last batch
+    # entry is refused, and the next calibration picks another candidate.
+    shape = dict(precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f32", batch=300)
+    first = gemm.calibrate_variant(8, 32, 40, **shape)
+    assert first.source == "calibrated"
+    gemm.calibration_inject(first.kernel, first.tile_rows, first.tile_columns, "last-batch")
+    second = gemm.calibrate_variant(8, 32, 40, **shape)
+    assert key(second) != key(first)

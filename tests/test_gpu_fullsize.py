@@ -39,11 +39,48 @@ def sample_pairs(length, count, seed):
     return [(i, j) for i in idx for j in jdx]
 
 
-def check(got, expect, what):
+def check(got, expect, what, tolerance=1e-2):
     scale = float(np.abs(expect).max())
     err = np.abs(np.asarray(got, np.float64) - expect)
     print(f"{what}: max|d| {err.max():.3e} mean|d| {err.mean():.3e} max|ref| {scale:.3f}", flush=True)
-    assert err.max() <= 1e-2 * scale, what
+    assert err.max() <= tolerance * scale, what
+
+
+def run_f32_triangle(dev, length, direction, seed, count, pair_seed):
+    # The f32 path (precision f32, f32 pair in and out) at full size, on
+    # sampled pairs against float64: the north star's 1e-5 of the largest
+    # reference value (max|d| / max|ref|, test/gemm-half-precision.gpu.test.ts:193-201).
+    import torch
+
+    import bench
+    from afhip import triangle
+
+    CZ, CH = bench.CZ, bench.CH
+    z = ref.normal(seed, (length, length, CZ))
+    mask = (ref.uniform(seed + 1, (length, length), 0, 1) > 0.15).astype(np.float32)
+    weights = bench.triangle_weights(seed, CZ, CH)
+    op = triangle.TriangleMultiplication(length, CZ, CH, direction=direction, precision="f32", pair_dtype="f32",
+                                         out_dtype="f32")
+    op.prepare(weights)
+    zd = torch.from_numpy(z).to(dev)
+    out = op(zd, torch.from_numpy(mask).to(dev)).cpu().numpy()
+    del zd, op
+    pairs = sample_pairs(length, count, pair_seed)
+    check(np.stack([out[i, j] for i, j in pairs]), ref.triangle_pairs(direction, z, mask, weights, pairs),
+          f"f32 {direction} L={length}", tolerance=1e-5)
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_config3_triangle_l384_f32_precision(dev, direction):
+    import bench
+
+    run_f32_triangle(dev, bench.L, direction, bench.SEED + 22, 14, 8 if direction == "outgoing" else 9)
+
+
+def test_config5_incoming_l1024_f32_precision(dev):
+    import bench
+
+    run_f32_triangle(dev, 1024, "incoming", bench.SEED + 24, 10, 10)
 
 
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])

@@ -378,13 +378,30 @@ def test_config2_mixed_q8_attention_projection(dev, rows):
     x, q, s = _config2_inputs(rows)
     xd = to_dev(x.astype(np.float16), dev)
     outs = gemm.attention_project(xd, to_dev(q, dev), heads=8, head_dim=32, scale=to_dev(s, dev))
-    check = np.arange(0, rows, max(1, rows // 2048))
+    got = [o.float().cpu().numpy() for o in outs]
     wq = ref.q8_channel_decode(q, s)
-    expect = ref.attention_project(x[check], wq, None, heads=8, head_dim=32)
-    for got, exp in zip(outs, expect):
-        g = got.float().cpu().numpy()[check]
+
+    def close(g, exp, what):
         err = np.abs(g - exp)
-        assert np.all(err <= 1e-2 * np.maximum(1.0, np.abs(exp))), float(err.max())
+        assert np.all(err <= 1e-2 * np.maximum(1.0, np.abs(exp))), (what, float(err.max()))
+
+    # Every row against a float64 product with the oracle-decoded weight
+    # (columns [q | k | v | g], q scaled by 1/sqrt(32), g through the
+    # sigmoid), in blocks of rows.
+    w64 = wq.astype(np.float64)
+    for r0 in range(0, rows, 8192):
+        y = x[r0:r0 + 8192].astype(np.float64) @ w64
+        exp = (y[:, :256] / np.sqrt(32.0), y[:, 256:512], y[:, 512:768], 1.0 / (1.0 + np.exp(-y[:, 768:])))
+        for i, (g, e) in enumerate(zip(got, exp)):
+            close(g[r0:r0 + 8192], e, ("qkvg"[i], r0))
+    # The oracle's own epilogue on seeded rows that cover every position in
+    # a 32-row activation tile, tiles of both parities and the last tile.
+    rng = np.random.default_rng(0xAF2001)
+    check = np.unique(np.concatenate([rng.choice(rows, 512, replace=False), np.arange(64), np.arange(rows - 64, rows)]))
+    assert set(check % 32) == set(range(32)) and set((check // 32) % 2) == {0, 1}
+    expect = ref.attention_project(x[check], wq, None, heads=8, head_dim=32)
+    for i, (g, exp) in enumerate(zip(got, expect)):
+        close(g[check], exp, ("qkvg"[i], "oracle rows"))
 
 
 def test_attention_gate_bias_and_f32_path(dev):

@@ -37,7 +37,20 @@ def write_expected(directory):
     generated here exactly as the Node script generates it."""
     import numpy as np
 
+    from afhip import reference
     from oracle import ref
+
+    # The reference's triangle fixtures, read here (manifest.json + f32
+    # tensors) and handed over as one packed f32 file each with its index.
+    for name in ("openfold-triangle-small", "alphafold-short-9", "alphafold-single-sequence-59", "alphafold-a3m-59"):
+        bundle = reference.load_triangle_reference_bundle(os.path.join(ROOT, "tests", "golden", name, "manifest.json"))
+        inp = bundle["input"]
+        arrays = [("z", inp["z"]), ("mask", inp["mask"])] + [(n, inp["weights"][n]) for n in reference.WEIGHT_NAMES]
+        arrays.append(("expected", bundle["expected"]))
+        with open(os.path.join(directory, name + ".json"), "w") as f:
+            json.dump({"shape": inp["shape"], "epsilon": inp["epsilon"], "weights": list(reference.WEIGHT_NAMES),
+                       "arrays": [[n, int(a.size)] for n, a in arrays]}, f)
+        np.concatenate([a.reshape(-1).astype("<f4") for _, a in arrays]).tofile(os.path.join(directory, name + ".f32"))
 
     shape = {"length": 24, "cZ": 32, "cHidden": 16}
     with open(os.path.join(directory, "deterministic.json"), "w") as f:
@@ -75,4 +88,4 @@ def write_expected(directory):
 def test_addon_parity_on_gpu(tmp_path):
     write_expected(str(tmp_path))
     out = run_node("gpu_parity.js", timeout=300, env={"AFHIP_NODE_EXPECTED": str(tmp_path)})
-    assert len(out["cases"]) == 11
+    assert len(out["cases"]) == 12
