@@ -176,6 +176,7 @@ SIGNATURES = {
     "afhip_pack_weight_q8_block": [_vp, _vp, _i32, _i64, _i32, _i32, _vp, _i32, _vp],
     "afhip_triangle_weights_size": [ctypes.POINTER(TriangleDesc), _szp],
     "afhip_triangle_workspace_size": [ctypes.POINTER(TriangleDesc), _szp],
+    "afhip_triangle_fast_path": [ctypes.POINTER(TriangleDesc), ctypes.POINTER(ctypes.c_int32)],
     "afhip_triangle_prepare_weights": [ctypes.POINTER(TriangleDesc), _vp, _vp, _vp],
     "afhip_triangle_run": [ctypes.POINTER(TriangleDesc), _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "afhip_opm_weights_size": [ctypes.POINTER(OpmDesc), _szp],

@@ -81,6 +81,10 @@ TriWorkspace tri_workspace(const afhip_triangle_desc& d) {
   size_t es = d.precision == AFHIP_PRECISION_F16 ? 2 : 4;
   int64_t L = d.length, P = L * L;
   w.block_rows = d.block_rows > 0 ? std::min(d.block_rows, d.length) : d.length;
+  // The fast output kernels address a block's z, contracted values and
+  // output with 32-bit buffer offsets: at long lengths the block shrinks to
+  // what they reach (the result does not depend on the block).
+  if (triangle_fast_eligible(d)) w.block_rows = std::min(w.block_rows, triangle_fast_block_rows(d));
   w.cstride = round_up(P, 64);
   w.bstride = round_up((int64_t)w.block_rows * L, 64);
   size_t at = 0;
@@ -494,6 +498,13 @@ int afhip_triangle_weights_size(const afhip_triangle_desc* desc, size_t* bytes) 
   if (int s = validate(desc)) return s;
   AFHIP_REQUIRE(bytes != nullptr, "output is NULL");
   *bytes = tri_layout(*desc).total;
+  return AFHIP_OK;
+}
+
+int afhip_triangle_fast_path(const afhip_triangle_desc* desc, int32_t* fast) {
+  if (int s = validate(desc)) return s;
+  AFHIP_REQUIRE(fast != nullptr, "output is NULL");
+  *fast = triangle_fast_eligible(*desc) ? 1 : 0;
   return AFHIP_OK;
 }
 

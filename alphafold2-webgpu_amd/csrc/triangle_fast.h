@@ -52,6 +52,9 @@ struct FastOutputArgs {
 };
 
 bool triangle_fast_eligible(const afhip_triangle_desc& d);
+// The most output rows one block of the fast output kernels takes (their
+// per-block buffer offsets stay below 2 GiB).
+int triangle_fast_block_rows(const afhip_triangle_desc& d);
 int launch_triangle_project_f16(const FastProjectArgs& a, int pair_dtype, hipStream_t s);
 int launch_triangle_output_f16(const FastOutputArgs& a, int pair_dtype, int out_dtype, hipStream_t s);
 

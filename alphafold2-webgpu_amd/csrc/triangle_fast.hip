@@ -164,28 +164,29 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
   const float bp = a.b_proj[(2 * o) * kC + ch];
   const float bg = a.b_proj[(2 * o + 1) * kC + ch];
 
-  const int32x4_t rz = make_rsrc(a.z, (uint32_t)((int64_t)a.P * Lay::ZROW));
+  // Incoming lanes read z (and the mask) at their own offsets into the whole
+  // tensor (triangle_fast_eligible keeps it within 32 bits); outgoing tiles
+  // are consecutive pairs, addressed through a resource based at the tile.
+  const int32x4_t rz = make_rsrc(a.z, (uint32_t)std::min<int64_t>((int64_t)a.P * Lay::ZROW, UINT32_MAX));
   const int32x4_t rm = make_rsrc(a.mask, (uint32_t)((int64_t)a.P * 4));
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
   // Load geometry: load i of a loader wave fills stage row
   // row_i = (wave + 4 i) * ROWS_PER_LOAD + lane / LANES_PER_ROW, 16-byte chunk
   // lane % LANES_PER_ROW; wave 0 also loads the tile's 64 mask values.
   // Outgoing pairs are consecutive rows of z: the lane's offset within the
-  // tile is fixed and the tile's base rides in the instruction's scalar
-  // offset; rows past P read as zeros. Incoming pairs are z
+  // tile is fixed and the tile's base is the base of the tile's resource;
+  // rows past P read as zeros. Incoming pairs are z
   // transposed: row r of the tile stream is pair (r % L) * L + r / L, whose
   // coordinates (r / L, r % L) each lane advances by G * 64 rows per issued
   // tile instead of dividing.
   constexpr int NL = Lay::LPW + 1;  // the loads, then the mask (wave 0)
   uint32_t vofs[NL];
-  int vrow[NL];        // the tile row the lane fills
   int ci[NL], ck[NL];  // incoming: r / L and r % L of the lane's next row
   const int dq = (G * kTile) / a.L, dr = (G * kTile) % a.L;
 #pragma unroll
   for (int i = 0; i < NL; i++) {
     const int row = i < Lay::LPW ? (wave + kLoaderWaves * i) * Lay::ROWS_PER_LOAD + lane / Lay::LANES_PER_ROW : lane;
     const int chunk = i < Lay::LPW ? lane % Lay::LANES_PER_ROW : 0;
-    vrow[i] = row;
     if constexpr (INCOMING) {
       const int r = t0 * kTile + row;
       ci[i] = r / a.L;
@@ -203,7 +204,9 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
       const uint32_t lds = i < Lay::LPW ? base + (wave + kLoaderWaves * i) * 1024 : base + Lay::ZBYTES;
       const uint32_t esz = i < Lay::LPW ? (uint32_t)Lay::ZROW : 4u;
       if constexpr (INCOMING) {
-        const uint32_t off = ci[i] < a.L ? (uint32_t)(ck[i] * a.L + ci[i]) * esz + vofs[i] : kOutOfRange;
+        // Rows past P read pair 0: their results land in the operands'
+        // padding, which the contraction never reads.
+        const uint32_t off = ci[i] < a.L ? (uint32_t)(ck[i] * a.L + ci[i]) * esz + vofs[i] : vofs[i];
         if (i < Lay::LPW) dma16(rz, lds, off);
         else dma4(rm, lds, off);
         ck[i] += dr;
@@ -213,12 +216,16 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
           ci[i] += 1;
         }
       } else {
-        // Rows past P take an out-of-range vector offset (the scalar offset
-        // alone is not range-checked on every generation).
-        const uint32_t so = (uint32_t)tile * kTile * esz;
-        const uint32_t off = vrow[i] < a.P - tile * kTile ? vofs[i] : kOutOfRange;
-        if (i < Lay::LPW) dma16_so(rz, lds, off, so);
-        else dma4_so(rm, lds, off, so);
+        // A resource based at the tile's first pair and ending at P (or past
+        // the tile): rows past P read as zeros.
+        const int64_t first = (int64_t)tile * kTile;
+        const int rows = min(kTile, a.P - tile * kTile);
+        const int32x4_t rt = i < Lay::LPW
+                                 ? make_rsrc(reinterpret_cast<const unsigned char*>(a.z) + first * Lay::ZROW,
+                                             (uint32_t)(rows * Lay::ZROW))
+                                 : make_rsrc(a.mask + first, (uint32_t)(rows * 4));
+        if (i < Lay::LPW) dma16(rt, lds, vofs[i]);
+        else dma4(rt, lds, vofs[i]);
       }
     }
   };
@@ -264,13 +271,13 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
   static_assert(kStores == 4, "32 rows, eight a store");
   const int srow = lane >> 3, schunk = lane & 7;
   const half_t* const sown = ost + (o * kC + hb + srow) * kOutPitch + schunk * 8;
+  // The store resource covers the wave's own 32 channels.
   uint32_t svof[kStores];
 #pragma unroll
-  for (int k = 0; k < kStores; k++)
-    svof[k] = (uint32_t)(((int64_t)(hb + srow + 8 * k) * a.cstride + schunk * 8) * 2);
-  const int obytes = (int)((int64_t)kC * a.cstride * 2);
+  for (int k = 0; k < kStores; k++) svof[k] = (uint32_t)(((int64_t)(srow + 8 * k) * a.cstride + schunk * 8) * 2);
+  const int obytes = (int)((int64_t)32 * a.cstride * 2);
   const __amdgpu_buffer_rsrc_t rso =
-      __builtin_amdgcn_make_buffer_rsrc(o == 0 ? a.out_a : a.out_b, 0, obytes, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((o == 0 ? a.out_a : a.out_b) + (int64_t)hb * a.cstride, 0, obytes, 0x00020000);
 
   if (t0 >= ntiles) return;
   // The weights and the first two tiles load at once; the other stages are
@@ -881,9 +888,24 @@ template <typename K> int prepare_lds(K kernel, int bytes) { return allow_lds((c
 
 bool triangle_fast_eligible(const afhip_triangle_desc& d) {
   if (d.precision != AFHIP_PRECISION_F16 || d.c_z != kC || d.c_hidden != kC) return false;
-  // Byte offsets into z (and the mask) must stay below the out-of-range marker.
   const int64_t P = (int64_t)d.length * d.length;
-  return P * kC * (d.pair_dtype == AFHIP_F32 ? 4 : 2) < (int64_t)kOutOfRange;
+  // The incoming projection reads z transposed, each lane at its own 32-bit
+  // byte offset into all of z; every other access is rebased per tile, per
+  // wave or per block of output rows. Operand channels of 32 stay below 2 GiB.
+  const int64_t zrow = (int64_t)kC * (d.pair_dtype == AFHIP_F32 ? 4 : 2);
+  if (d.direction == AFHIP_TRIANGLE_INCOMING && P * zrow > (int64_t)UINT32_MAX) return false;
+  return P <= ((int64_t)1 << 26) && 32 * (P + 64) * 2 < ((int64_t)1 << 31);
+}
+
+int triangle_fast_block_rows(const afhip_triangle_desc& d) {
+  // Per block of B rows (B L pairs): z and the output take B L rows of
+  // 128 channels, the contracted values 128 channels of round_up(B L, 64).
+  const int64_t widest = std::max<int64_t>(d.pair_dtype == AFHIP_F32 ? 4 : 2, d.out_dtype == AFHIP_F32 ? 4 : 2);
+  const int64_t pairs = (((int64_t)1 << 31) - 1) / (kC * widest) - 64;
+  const int64_t most = std::max<int64_t>(1, std::min<int64_t>(d.length, pairs / d.length));
+  // As many blocks as that takes, of equal size (no short last block).
+  const int64_t blocks = ceil_div(d.length, most);
+  return (int)ceil_div(d.length, blocks);
 }
 
 template <typename ZT, bool INCOMING> int launch_project(const FastProjectArgs& a, hipStream_t s) {
@@ -895,8 +917,9 @@ template <typename ZT, bool INCOMING> int launch_project(const FastProjectArgs& 
 
 int launch_triangle_project_f16(const FastProjectArgs& a, int pair_dtype, hipStream_t s) {
   // Buffer offsets are 32-bit: the operands' 128 rows and z must stay below 2 GiB.
-  AFHIP_REQUIRE((int64_t)kC * a.cstride * 2 < ((int64_t)1 << 31) && (int64_t)a.P * kC * 4 < ((int64_t)1 << 31),
-                "triangle of %d pairs exceeds the projection kernel's 2 GiB operand bound", a.P);
+  const int64_t zrow = (int64_t)kC * (pair_dtype == AFHIP_F32 ? 4 : 2);
+  AFHIP_REQUIRE((int64_t)32 * a.cstride * 2 < ((int64_t)1 << 31) && (!a.incoming || (int64_t)a.P * zrow <= UINT32_MAX),
+                "triangle of %d pairs exceeds the projection kernel's buffer offsets", a.P);
   if (pair_dtype == AFHIP_F16)
     return a.incoming ? launch_project<half_t, true>(a, s) : launch_project<half_t, false>(a, s);
   return a.incoming ? launch_project<float, true>(a, s) : launch_project<float, false>(a, s);

@@ -324,6 +324,12 @@ AFHIP_API int afhip_triangle_workspace_size(const afhip_triangle_desc* desc, siz
  * (ORDER), weights [out][in], as packWeights lays them out (weights.ts:20-34). */
 AFHIP_API int afhip_triangle_prepare_weights(const afhip_triangle_desc* desc, const float* packed, void* prepared,
                                    void* stream);
+/* Which kernels a run of this descriptor takes: *fast = 1 for the persistent
+ * f16 kernels (c_z = c_hidden = 128, f16 precision, z 16-byte aligned, and an
+ * incoming z of at most 4 GiB), 0 for the general ones; results agree within
+ * the precision's tolerance either way. The counterpart of afhip_gemm_select
+ * for this operator (the reference has one kernel set, src/triangle/shaders.ts). */
+AFHIP_API int afhip_triangle_fast_path(const afhip_triangle_desc* desc, int32_t* fast);
 /* z [L][L][c_z]; mask [L][L] f32; out [L][L][c_z]. */
 AFHIP_API int afhip_triangle_run(const afhip_triangle_desc* desc, const void* z, const float* mask,
                        const void* prepared, void* out, void* workspace, size_t workspace_bytes,

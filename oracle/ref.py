@@ -255,7 +255,8 @@ def triangle_pairs(direction: str, z, mask, weights: dict, pairs, epsilon: float
     sum_k a[k,j] b[k,i]) and z[i, j] itself, so a sample of pairs at full
     size costs O(rows * L * c_z * c_h). Returns
     [len(pairs)][c_z]."""
-    z64 = np.asarray(z, np.float64)
+    # Only the rows (outgoing) or columns (incoming) the pairs read are
+    # widened to float64, so z may be any size that fits in memory as given.
     m64 = np.asarray(mask, np.float64)
     w = {k: np.asarray(v, np.float64) for k, v in weights.items()}
 
@@ -269,13 +270,13 @@ def triangle_pairs(direction: str, z, mask, weights: dict, pairs, epsilon: float
 
     projected = {}
     for r in sorted({int(i) for i, _ in pairs} | {int(j) for _, j in pairs}):
-        line = z64[r] if direction == "outgoing" else z64[:, r]
+        line = np.asarray(z[r] if direction == "outgoing" else z[:, r], np.float64)
         keep = (m64[r] if direction == "outgoing" else m64[:, r])[:, None]
         zn = ln(line, w["layerNormInWeight"], w["layerNormInBias"])
         a = keep * (zn @ w["linearAPWeight"].T + w["linearAPBias"]) * sig(zn @ w["linearAGWeight"].T + w["linearAGBias"])
         b = keep * (zn @ w["linearBPWeight"].T + w["linearBPBias"]) * sig(zn @ w["linearBGWeight"].T + w["linearBGBias"])
         projected[r] = (a, b)
-    out = np.empty((len(pairs), z64.shape[2]))
+    out = np.empty((len(pairs), z.shape[2]))
     for n, (i, j) in enumerate(pairs):
         # outgoing ikc,jkc->ijc; incoming kjc,kic->ijc (a follows j, b follows i)
         if direction == "outgoing":
@@ -283,7 +284,7 @@ def triangle_pairs(direction: str, z, mask, weights: dict, pairs, epsilon: float
         else:
             x = (projected[int(j)][0] * projected[int(i)][1]).sum(0)
         x = ln(x, w["layerNormOutWeight"], w["layerNormOutBias"])
-        gate = sig(ln(z64[i, j], w["layerNormInWeight"], w["layerNormInBias"]) @ w["linearGWeight"].T
+        gate = sig(ln(np.asarray(z[i, j], np.float64), w["layerNormInWeight"], w["layerNormInBias"]) @ w["linearGWeight"].T
                    + w["linearGBias"])
         out[n] = (x @ w["linearZWeight"].T + w["linearZBias"]) * gate
     return out

@@ -76,6 +76,36 @@ def test_gemm_grid_matches_reference():
             gemm.gemm_grid(*bad)
 
 
+def test_triangle_fast_path_bounds():
+    # Which triangle shapes take the persistent f16 kernels, decided on the
+    # host: AlphaFold's widths at f16 precision, any length whose operands
+    # fit, except an incoming z past 4 GiB (read with 32-bit lane offsets).
+    import ctypes
+
+    from afhip import _lib
+
+    lib = _lib.library()
+
+    def fast(length, direction=0, pair=1, cz=128, precision=1):
+        flag = ctypes.c_int32(-1)
+        desc = _lib.TriangleDesc(length, cz, 128, direction, precision, pair, 0, 0, 0, 1e-5)
+        assert lib.afhip_triangle_fast_path(ctypes.byref(desc), ctypes.byref(flag)) == _lib.OK
+        return flag.value
+
+    assert fast(384) == 1 and fast(384, direction=1) == 1
+    assert fast(3072) == 1 and fast(3072, direction=1) == 1 and fast(3300, direction=1) == 1
+    assert fast(4095, direction=1) == 1 and fast(4096, direction=1) == 0 and fast(4096) == 1
+    assert fast(3072, pair=0) == 1 and fast(3072, direction=1, pair=0) == 0 and fast(2896, direction=1, pair=0) == 1
+    assert fast(384, cz=64) == 0 and fast(384, precision=0) == 0
+    # At L = 3072 the output kernels' blocks of rows shrink so their buffer
+    # offsets stay below 2 GiB: the contracted block is smaller than all rows.
+    size = ctypes.c_size_t()
+    desc = _lib.TriangleDesc(3072, 128, 128, 0, 1, 1, 0, 0, 0, 1e-5)
+    assert lib.afhip_triangle_workspace_size(ctypes.byref(desc), ctypes.byref(size)) == _lib.OK
+    full = 128 * 3072 * 3072 * 2
+    assert 2 * full <= size.value < 3 * full
+
+
 def test_descriptor_validation_is_host_side():
     import ctypes
 
@@ -170,5 +200,9 @@ def test_calibration_document_round_trip(tmp_path):
     path.write_text('{"schema": 1, "entries": {"x|y": {"precision": 1, "tile_rows": 96, '
                     '"tile_columns": 128, "tile_inner": 32}}}')
     gemm.calibration_load(str(path))
+    shape = dict(precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f16", batch=1)
+    assert gemm.select_variant(200, 96, 128, **shape).source == "heuristic"
     path.write_text("not json at all")
     gemm.calibration_load(str(path))
+    assert gemm.select_variant(200, 96, 128, **shape).source == "heuristic"
+    assert gemm.select_variant(384, 384, 384, **dict(shape, batch=128)).tile_rows == 192

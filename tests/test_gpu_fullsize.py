@@ -183,3 +183,41 @@ def test_config4_outer_product_mean_full_size(dev):
         got.append(out[i, j])
         expect.append(sl[0, 0] if i == j else sl[0, 1])
     check(np.stack(got), np.stack(expect).astype(np.float64), "config 4 outer-product mean")
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_long_complex_l3072_fast_path(dev, direction):
+    # Past the length where an f16 pair outgrows 2 GiB (L = 2,896): the
+    # persistent f16 kernels at L = 3072, f16 z (2.4 GB) with the 15%-zero
+    # mask, f32 out. z is drawn on the device (seeded); the oracle reads the
+    # sampled pairs' rows or columns from a host copy.
+    import ctypes
+
+    import torch
+
+    import bench
+    from afhip import _lib, triangle
+
+    L, CZ, CH = 3072, bench.CZ, bench.CH
+    desc = _lib.TriangleDesc(L, CZ, CH, 0 if direction == "outgoing" else 1, 1, 1, 0, 0, 0, 1e-5)
+    flag = ctypes.c_int32(-1)
+    _lib.call("afhip_triangle_fast_path", ctypes.byref(desc), ctypes.byref(flag))
+    assert flag.value == 1
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xAF2005)
+    zd = torch.randn((L, L, CZ), generator=gen, device=dev).half()
+    mask = (ref.uniform(bench.SEED + 25, (L, L), 0, 1) > 0.15).astype(np.float32)
+    weights = bench.triangle_weights(bench.SEED + 26, CZ, CH)
+    op = triangle.TriangleMultiplication(L, CZ, CH, direction=direction, precision="f16", pair_dtype="f16",
+                                         out_dtype="f32")
+    op.prepare(weights)
+    out = op(zd, torch.from_numpy(mask).to(dev))
+    pairs = sample_pairs(L, 10, 11 if direction == "outgoing" else 12)
+    ii = torch.tensor([i for i, _ in pairs], device=dev)
+    jj = torch.tensor([j for _, j in pairs], device=dev)
+    got = out[ii, jj].cpu().numpy()
+    del out, op
+    z = zd.cpu().numpy()
+    del zd
+    torch.cuda.empty_cache()
+    check(got, ref.triangle_pairs(direction, z, mask, weights, pairs), f"f16 {direction} L={L} fast path")
