@@ -83,9 +83,11 @@ static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int6
   v.tile_inner = gemm_detail::kBK;
   v.vectorized = 1;
   v.source = 0;
-  // LDS_DMA takes f16 operands whose K is a multiple of 8 (its 16-byte
-  // chunks); anything else is staged through registers.
-  if (t.precision == AFHIP_PRECISION_F16 && t.a_dtype == AFHIP_F16 && t.b_dtype == AFHIP_F16 && K % 8 == 0) {
+  // LDS_DMA takes f16 operands with an even K (16-byte loads when K is a
+  // multiple of 8, 4-byte loads otherwise), and int8 weights that a plan
+  // widens to f16 first (exact); anything else is staged through registers.
+  if (t.precision == AFHIP_PRECISION_F16 && t.a_dtype == AFHIP_F16 &&
+      (t.b_dtype == AFHIP_F16 || t.b_dtype == AFHIP_I8) && K % 2 == 0) {
     v.kernel = AFHIP_KERNEL_LDS_DMA;
     dma_heuristic_tile(M, N, K, batch, &v.tile_rows, &v.tile_columns);
     return v;
@@ -147,6 +149,31 @@ __global__ void pack_transpose_kernel(const TS* __restrict__ src, int K, int N, 
   for (int r = ty; r < 32; r += 8) {
     int n = n0 + r, k = k0 + tx;
     if (n < N && k < K) dst[(int64_t)n * ld_dst + k] = (TD)tile[tx][r];
+  }
+}
+
+// int8 rows [rows][cols] (leading dimension ld_src) widened to f16 rows of
+// cols halves; exact, |q| <= 127. Eight columns a lane (one 8-byte read, one
+// 16-byte write where both are aligned), rows along y.
+__global__ void widen_rows_kernel(const int8_t* __restrict__ src, int rows, int cols, int64_t ld_src,
+                                  half_t* __restrict__ dst) {
+  const int c = 8 * (blockIdx.x * blockDim.x + threadIdx.x);
+  if (c >= cols) return;
+  for (int r = blockIdx.y; r < rows; r += gridDim.y) {
+    const int8_t* s = src + (int64_t)r * ld_src + c;
+    half_t* d = dst + (int64_t)r * cols + c;
+    if (c + 8 <= cols && (reinterpret_cast<uintptr_t>(s) & 7) == 0 && (reinterpret_cast<uintptr_t>(d) & 15) == 0) {
+      const uint2 v = *reinterpret_cast<const uint2*>(s);
+      half8 h;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        h[e] = (half_t)(float)(int8_t)(v.x >> (8 * e));
+        h[4 + e] = (half_t)(float)(int8_t)(v.y >> (8 * e));
+      }
+      *reinterpret_cast<half8*>(d) = h;
+    } else {
+      for (int e = 0; e < 8 && c + e < cols; e++) d[e] = (half_t)(float)s[e];
+    }
   }
 }
 
@@ -228,7 +255,8 @@ int pack_dispatch(const TS* src, int K, int N, int64_t ld_src, void* dst, int ds
 int pack_transpose(const void* src, int src_dtype, int K, int N, int64_t ld_src, void* dst, int dst_dtype,
                    int64_t ld_dst, hipStream_t s) {
   AFHIP_REQUIRE(src && dst && K > 0 && N > 0, "invalid weight pack arguments");
-  AFHIP_REQUIRE(src_dtype != AFHIP_I8 || dst_dtype == AFHIP_I8, "int8 weights pack to int8 only");
+  AFHIP_REQUIRE(src_dtype != AFHIP_I8 || dst_dtype == AFHIP_I8 || dst_dtype == AFHIP_F16,
+                "int8 weights pack to int8 or (exactly) to f16");
   if (src_dtype == AFHIP_F32) return pack_dispatch((const float*)src, K, N, ld_src, dst, dst_dtype, ld_dst, s);
   if (src_dtype == AFHIP_F16) return pack_dispatch((const half_t*)src, K, N, ld_src, dst, dst_dtype, ld_dst, s);
   return pack_dispatch((const int8_t*)src, K, N, ld_src, dst, dst_dtype, ld_dst, s);
@@ -433,24 +461,30 @@ int afhip_gemm_plan_destroy(afhip_gemm_plan* plan) {
 }
 
 // The weight dtype the kernels read for a precision: f16 (or int8) under f16
-// arithmetic, f32 under f32 arithmetic.
-static int kernel_w_dtype(const afhip_gemm_desc& d) {
-  if (d.precision == AFHIP_PRECISION_F16) return d.w_dtype == AFHIP_I8 ? AFHIP_I8 : AFHIP_F16;
-  return AFHIP_F32;
+// arithmetic, f32 under f32 arithmetic. An int8 weight stays int8 for the
+// families that widen it themselves (STREAM, REGISTER_STAGED) and is widened
+// to f16 (exactly) for LDS_DMA, whose stages take f16 rows; the per-column
+// scale is applied to the f32 accumulator either way.
+static int kernel_w_dtype(const afhip_gemm_plan& p) {
+  const auto& d = p.desc;
+  if (d.precision != AFHIP_PRECISION_F16) return AFHIP_F32;
+  if (d.w_dtype != AFHIP_I8) return AFHIP_F16;
+  return p.variant.kernel == AFHIP_KERNEL_LDS_DMA ? AFHIP_F16 : AFHIP_I8;
 }
 
-// Only a column-contiguous weight is rewritten per run (transposed, and
-// converted to the kernel's dtype on the way); a k-contiguous one must
-// already be in that dtype, which plan creation checks.
-static bool needs_weight_workspace(const afhip_gemm_desc& d) {
-  return d.w_layout == AFHIP_WEIGHT_COLUMN_CONTIGUOUS;
+// A column-contiguous weight is rewritten per run (transposed, and converted
+// to the kernel's dtype on the way); a k-contiguous one must already be in
+// that dtype, which plan creation checks, except an int8 one widened for
+// LDS_DMA.
+static bool needs_weight_workspace(const afhip_gemm_plan& p) {
+  return p.desc.w_layout == AFHIP_WEIGHT_COLUMN_CONTIGUOUS || kernel_w_dtype(p) != p.desc.w_dtype;
 }
 
 int afhip_gemm_workspace_size(const afhip_gemm_plan* plan, size_t* bytes) {
   AFHIP_REQUIRE(plan && bytes, "NULL plan or output");
   const auto& d = plan->desc;
-  if (needs_weight_workspace(d)) {
-    size_t one = (size_t)d.inner * d.columns * dtype_size(kernel_w_dtype(d));
+  if (needs_weight_workspace(*plan)) {
+    size_t one = (size_t)d.inner * d.columns * dtype_size(kernel_w_dtype(*plan));
     size_t n = d.batch_stride_w == 0 ? 1 : (size_t)d.batch;
     *bytes = round_up((int64_t)(one * n), 256);
   } else {
@@ -500,19 +534,27 @@ int afhip::run_gemm_plan(const afhip_gemm_plan* plan, const void* a, const void*
     g.q_scale = (float)(1.0 / std::sqrt((double)d.head_dim));
   }
   GemmTypes types = plan->types;
-  if (needs_weight_workspace(d)) {
+  if (needs_weight_workspace(*plan)) {
     size_t need = 0;
     afhip_gemm_workspace_size(plan, &need);
     AFHIP_REQUIRE(workspace != nullptr && workspace_bytes >= need,
                   "these weights need a %zu-byte workspace to be laid out for the kernel", need);
     AFHIP_REQUIRE(w != nullptr, "weight is NULL");
-    const int kd = kernel_w_dtype(d);
+    const int kd = kernel_w_dtype(*plan);
     int nb = d.batch_stride_w == 0 ? 1 : d.batch;
     size_t es = dtype_size(d.w_dtype), kes = dtype_size(kd);
     for (int b = 0; b < nb; b++) {
       const char* src = (const char*)w + (size_t)b * d.batch_stride_w * es;
       char* dst = (char*)workspace + (size_t)b * d.inner * d.columns * kes;
-      if (int s = pack_transpose(src, d.w_dtype, d.inner, d.columns, plan->ldw, dst, kd, d.inner, st)) return s;
+      if (d.w_layout == AFHIP_WEIGHT_COLUMN_CONTIGUOUS) {
+        if (int s = pack_transpose(src, d.w_dtype, d.inner, d.columns, plan->ldw, dst, kd, d.inner, st)) return s;
+      } else {
+        // A k-contiguous int8 weight [N][K], widened in place of the layout.
+        const dim3 grid((unsigned)ceil_div(d.inner, 8 * 256), (unsigned)std::min(d.columns, 65535));
+        if (int s = launch("widen_int8", widen_rows_kernel, grid, dim3(256), 0, st, (const int8_t*)src, d.columns,
+                           d.inner, plan->ldw, (half_t*)dst))
+          return s;
+      }
     }
     g.b = workspace;
     g.ldb = d.inner;

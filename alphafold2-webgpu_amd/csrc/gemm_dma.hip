@@ -14,7 +14,10 @@
 //  - Operands travel global -> LDS without passing through VGPRs
 //    (buffer_load_dwordx4 ... lds). A k-step stage is (BM + BN) rows of
 //    64 bytes; each wave-level load instruction fills 16 rows (1 KiB of LDS,
-//    lane l -> row l/4, 16-byte slot l%4). STAGES stages are in flight, so the
+//    lane l -> row l/4, 16-byte slot l%4). Rows that are only 4-byte aligned
+//    (K or a leading dimension not a multiple of 8 halves) load with
+//    buffer_load_dword ... lds instead: 4 rows an instruction, 16 lanes a row,
+//    into the same stage layout. STAGES stages are in flight, so the
 //    loads for step k + STAGES - 1 are issued while step k computes, and one
 //    barrier per k-step both publishes a stage and retires the one to refill.
 //  - Bank conflicts: a row's four 16-byte chunks are stored XOR-swizzled,
@@ -61,7 +64,7 @@ __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
 constexpr int kEpiGeneric = 0;
 constexpr int kEpiOpmFused = 1;
 
-template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int EPI = kEpiGeneric>
+template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int EPI = kEpiGeneric, int LW = 16>
 __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_kernel(gemm_detail::KernelArgs ka) {
   constexpr int WAVES = WM * WN;
   constexpr int kThreads = 64 * WAVES;
@@ -69,10 +72,13 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int ROWS = BM + BN;
   constexpr int STAGE_BYTES = ROWS * kRowBytes;
-  constexpr int LOADS = ROWS / 16;    // wave-level load instructions per stage
+  static_assert(LW == 16 || LW == 4, "16- or 4-byte loads");
+  constexpr int RPL = LW;             // stage rows a wave-level load fills (64 lanes x LW bytes)
+  constexpr int LPR = 64 / LW;        // lanes a row
+  constexpr int LOADS = ROWS / RPL;   // wave-level load instructions per stage
   constexpr int LPW = LOADS / WAVES;  // per wave
   static_assert(WTM % 32 == 0 && WTN % 32 == 0 && LOADS % WAVES == 0, "tile shape");
-  static_assert(BM % 16 == 0, "a load instruction fills rows of one operand");
+  static_assert(BM % RPL == 0, "a load instruction fills rows of one operand");
   static_assert((STAGES - 2) * LPW < 64, "vmcnt holds at most 63 outstanding loads");
   static_assert(!PIPE || STAGES >= 4, "the pipelined schedule keeps STAGES - 2 steps in flight");
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
@@ -105,18 +111,22 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   const int32x4_t rb = make_rsrc(B, (uint32_t)((int64_t)rows_b * g.ldb * 2));
 
   // This lane's part of each of the wave's load instructions: instruction
-  // q = wave + WAVES i fills stage rows [16 q, 16 q + 16); the lane fills slot
-  // lane % 4 of row 16 q + lane / 4 with global chunk slot ^ swizzle(row).
+  // q = wave + WAVES i fills stage rows [RPL q, RPL q + RPL); the lane fills
+  // bytes [LW s, LW s + LW) of row RPL q + lane / LPR, s = lane % LPR, which
+  // lie in 16-byte slot LW s / 16: it loads the same bytes of global chunk
+  // slot ^ swizzle(row).
   uint32_t base_off[LPW];
-  int chunk_k[LPW];
+  int chunk_k[LPW];  // the first k the lane's bytes hold
 #pragma unroll
   for (int i = 0; i < LPW; i++) {
     const int q = wave + WAVES * i;
-    const int row = 16 * q + (lane >> 2);
-    const int chunk = (lane & 3) ^ swizzle(row);
-    chunk_k[i] = 8 * chunk;
-    if (16 * q < BM) base_off[i] = (uint32_t)((int64_t)row * g.lda * 2 + 16 * chunk);
-    else base_off[i] = (uint32_t)((int64_t)(row - BM) * g.ldb * 2 + 16 * chunk);
+    const int row = RPL * q + lane / LPR;
+    const int byte = LW * (lane % LPR);
+    const int chunk = (byte >> 4) ^ swizzle(row);
+    const int inner = 16 * chunk + (byte & 15);
+    chunk_k[i] = inner / 2;
+    if (RPL * q < BM) base_off[i] = (uint32_t)((int64_t)row * g.lda * 2 + inner);
+    else base_off[i] = (uint32_t)((int64_t)(row - BM) * g.ldb * 2 + inner);
   }
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
 
@@ -126,7 +136,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     for (int i = 0; i < LPW; i++) {
       const int q = wave + WAVES * i;
       const uint32_t off = k0 + chunk_k[i] < g.K ? base_off[i] + 2u * k0 : kOutOfRange;
-      dma16(16 * q < BM ? ra : rb, lds0 + stage * STAGE_BYTES + q * 1024, off);
+      if constexpr (LW == 16) dma16(RPL * q < BM ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
+      else dma4(RPL * q < BM ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
     }
   };
 
@@ -539,19 +550,20 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     auto aligned4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & (4 * sizeof(TC) - 1)) == 0; };
     const bool vec4 = (g.ldc & 3) == 0 && (g.sc & 3) == 0 && aligned4(g.c) &&
                       (!(g.flags & AFHIP_EPILOGUE_RESIDUAL) || aligned4(g.residual));
-    if (!(g.flags & (AFHIP_EPILOGUE_SCALE | EPILOGUE_OPM_OUTPUT)) && vec4 && m0 + BM <= g.M && n0 + BN <= g.N) {
-      // A whole tile with bias, ReLU and residual at most: no global read
-      // waits behind a store. The output may alias the residual (and, as
-      // far as the compiler knows, the bias), so it keeps such a read after
-      // any earlier store; interleaved, that was one memory round trip per
-      // four outputs. Here the tile's bias goes to LDS once (the stages are
-      // idle), and the residual values of each 32-row block are read before
-      // its first store: a lane reads only the elements it later writes.
-      // The arithmetic is epilogue_row4's, step for step.
+    if (!(g.flags & EPILOGUE_OPM_OUTPUT) && vec4 && m0 + BM <= g.M && n0 + BN <= g.N) {
+      // A whole tile with scale, bias, ReLU and residual at most: no global
+      // read waits behind a store. The output may alias the residual (and,
+      // as far as the compiler knows, the scale and bias), so it keeps such a
+      // read after any earlier store; interleaved, that was one memory round
+      // trip per four outputs. Here the tile's scale and bias go to LDS once
+      // (the stages are idle), and the residual values of each 32-row block
+      // are read before its first store: a lane reads only the elements it
+      // later writes. The arithmetic is epilogue_row4's, step for step.
 #pragma clang fp contract(off)
       typedef TC tc4 __attribute__((ext_vector_type(4)));
       const uint32_t flags = g.flags;
       float* const bl = reinterpret_cast<float*>(smem);
+      float* const sl = bl + BN;
       const TC* R = reinterpret_cast<const TC*>(g.residual) + (int64_t)bt * g.sc;
       TC* C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
       auto load_res = [&](int i, tc4(&res)[TN][4]) {
@@ -570,9 +582,12 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
       constexpr bool kAhead = sizeof(TC) == 2;
       tc4 res_a[TN][4], res_b[TN][4];
       if (kAhead && (flags & AFHIP_EPILOGUE_RESIDUAL)) load_res(0, res_a);
-      if (flags & AFHIP_EPILOGUE_BIAS) {
+      if (flags & (AFHIP_EPILOGUE_BIAS | AFHIP_EPILOGUE_SCALE)) {
         block_barrier<false>();  // every wave is done reading the stages
-        for (int c = threadIdx.x; c < BN; c += kThreads) bl[c] = g.bias[n0 + c];
+        for (int c = threadIdx.x; c < BN; c += kThreads) {
+          if (flags & AFHIP_EPILOGUE_BIAS) bl[c] = g.bias[n0 + c];
+          if (flags & AFHIP_EPILOGUE_SCALE) sl[c] = g.scale[n0 + c];
+        }
         block_barrier();
       }
 #pragma unroll
@@ -592,6 +607,7 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 #pragma unroll
             for (int e = 0; e < 4; e++) {
               float y = acc[i][j][4 * g4 + e];
+              if (flags & AFHIP_EPILOGUE_SCALE) y *= sl[wn + 32 * j + 8 * g4 + 4 * (lane >> 5) + e];
               if (flags & AFHIP_EPILOGUE_BIAS) y += bl[wn + 32 * j + 8 * g4 + 4 * (lane >> 5) + e];
               if (flags & AFHIP_EPILOGUE_RELU) y = fmaxf(y, 0.0f);
               if (flags & AFHIP_EPILOGUE_RESIDUAL) y += (float)res[j][g4][e];
@@ -644,7 +660,7 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     }
 }
 
-template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC>
+template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int LW = 16>
 int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   gemm_detail::KernelArgs ka;
   ka.g = g;
@@ -655,7 +671,7 @@ int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   ka.total_tiles = (int)total;
   ka.per_xcd = (int)ceil_div(total, 8);
   const size_t shared = (size_t)STAGES * (BM + BN) * kRowBytes;
-  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC>;
+  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC, kEpiGeneric, LW>;
   if (int st = allow_lds((const void*)kernel, shared)) return st;
   return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(64 * WM * WN), shared, s, ka);
 }
@@ -681,7 +697,18 @@ template <typename TC> int launch_opm_fused_tile(const GemmArgs& g, const char* 
   return launch_opm_fused<256, 256, 5, 2, 4, true, TC>(g, label, s);
 }
 
+// Operand rows whose k-runs are 16-byte aligned load 16 bytes a lane;
+// otherwise (4-byte aligned, dma_eligible) 4 bytes a lane.
+bool dma_wide(const GemmArgs& g) {
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return al16(g.a) && al16(g.b) && g.K % 8 == 0 && g.lda % 8 == 0 && g.ldb % 8 == 0 && g.sa % 8 == 0 && g.sb % 8 == 0;
+}
+
 template <typename TC> int launch_typed(const GemmArgs& g, int tm, int tn, const char* label, hipStream_t s) {
+  // 4-byte loads take four times the instructions; the 128 x 128 tile (five
+  // stages of 16 loads a wave, three in flight) keeps them within vmcnt's
+  // range.
+  if (!dma_wide(g)) return launch_tile<128, 128, 5, 2, 2, false, TC, 4>(g, label, s);
   if (tm == 192 && tn == 192) return launch_tile<192, 192, 3, 2, 2, false, TC>(g, label, s);
   if (tm == 128 && tn == 128) return launch_tile<128, 128, 4, 2, 2, false, TC>(g, label, s);
   if (tm == 128 && tn == 256) return launch_tile<128, 256, 3, 2, 2, false, TC>(g, label, s);
@@ -696,12 +723,14 @@ bool dma_tile_supported(int tm, int tn) {
 }
 
 bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
-  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
   if (t.precision != AFHIP_PRECISION_F16 || t.a_dtype != AFHIP_F16 || t.b_dtype != AFHIP_F16) return false;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return false;
   if (g.a_row_contiguous || g.c_column_major) return false;
-  if (!al16(g.a) || !al16(g.b)) return false;
-  if (g.K % 8 || g.lda % 8 || g.ldb % 8 || g.sa % 8 || g.sb % 8) return false;
+  // 16-byte loads (dma_wide) or, for rows that are only 4-byte aligned,
+  // 4-byte loads, which need K and the strides even.
+  if (!al4(g.a) || !al4(g.b)) return false;
+  if (g.K % 2 || g.lda % 2 || g.ldb % 2 || g.sa % 2 || g.sb % 2) return false;
   if (g.lda < g.K || g.ldb < g.K) return false;
   // Byte offsets within a 256-row panel stay below the out-of-range marker.
   return (int64_t)256 * std::max(g.lda, g.ldb) * 2 < (int64_t)kOutOfRange;

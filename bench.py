@@ -163,6 +163,9 @@ GEMM_SHAPES = [
     ("trans2", 29972, 1024, 256), ("extra1", 60416, 64, 256), ("project32", 29984, 256, 1024),
     ("output32", 29984, 256, 256), ("trans2-32", 29984, 1024, 256), ("opmcon32", 128, 512, 32000),
     ("probeA", 1024, 512, 512), ("probeB", 8192, 128, 512), ("probeC", 16384, 256, 256), ("probeD", 4096, 256, 512),
+    # trans2 with the bundle's mixed-q8 weight: int8 [N][K], per-column f32 scales
+    # (tools/quantize-web-model.ts:98-119 quantises every weight of the bundle).
+    ("trans2-q8", 29972, 1024, 256, "i8"),
 ]
 GEMM_CANDIDATES = [("register", 64, 64), ("register", 64, 128), ("register", 128, 64), ("register", 128, 128),
                    ("lds_dma", 128, 128), ("lds_dma", 192, 192), ("lds_dma", 128, 256), ("lds_dma", 256, 256),
@@ -173,12 +176,13 @@ def gemm_shapes(launches: int = 20) -> dict:
     """The gemm-candidates benchmark (tools/gemm-candidates.ts:571-669,
     tools/benchmark-gemm.ts:46-104) on MI355X: every candidate tile of the
     f16 GEMM (f16 operands, f32 accumulation, f16 output, weight [N][K]) on
-    every shape of SHAPES, beside the variant the heuristic picks. A candidate
-    is timed only where its family takes the operands (LDS_DMA: K a multiple
-    of 8; STREAM: K of 64, 128 or 256 and N a multiple of 64), as the library
-    would otherwise run it on another family. ms is the average of
-    `launches` back-to-back launches between two events after three warm-up
-    launches."""
+    every shape of SHAPES, beside the variant the heuristic picks; a shape
+    marked i8 has an int8 weight with per-column scales (the plan widens it
+    to f16 for LDS_DMA, inside the timed run). A candidate is timed only
+    where its family takes the operands (LDS_DMA: K even; STREAM: K of 64,
+    128 or 256 and N a multiple of 64), as the library would otherwise run it
+    on another family. ms is the average of `launches` back-to-back launches
+    between two events after three warm-up launches."""
     import torch
 
     from afhip import device, gemm
@@ -186,23 +190,29 @@ def gemm_shapes(launches: int = 20) -> dict:
     device.open_device(0)
     dev = device.device()
     out = {"unit": "ms", "launches": launches, "shapes": []}
-    for name, M, K, N in GEMM_SHAPES:
+    for name, M, K, N, *kind in GEMM_SHAPES:
+        wdt = kind[0] if kind else "f16"
         a = torch.randn(M, K, device=dev).half()
-        w = (torch.randn(N, K, device=dev) / K ** 0.5).half()
+        if wdt == "i8":
+            w = torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8)
+            scale = torch.rand(N, device=dev) * 9e-3 + 1e-3
+        else:
+            w = (torch.randn(N, K, device=dev) / K ** 0.5).half()
+            scale = None
         c = torch.empty(M, N, device=dev, dtype=torch.float16)
 
         def run(pin):
             gemm.force_variant(pin)
             try:
-                plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
-                                      out_dtype="f16")
+                plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype=wdt, w_layout="k",
+                                      out_dtype="f16", epilogue=("scale",) if scale is not None else ())
                 chosen = plan.variant()
                 for _ in range(3):
-                    plan.run(a, w, out=c)
+                    plan.run(a, w, scale=scale, out=c)
                 start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 start.record()
                 for _ in range(launches):
-                    plan.run(a, w, out=c)
+                    plan.run(a, w, scale=scale, out=c)
                 stop.record()
                 stop.synchronize()
                 return chosen, start.elapsed_time(stop) / launches
@@ -211,12 +221,12 @@ def gemm_shapes(launches: int = 20) -> dict:
 
         flops = 2.0 * M * K * N
         chosen, heuristic_ms = run(None)
-        entry = {"shape": name, "M": M, "K": K, "N": N,
+        entry = {"shape": name, "M": M, "K": K, "N": N, "weight": wdt,
                  "heuristic": {"variant": chosen.name, "ms": round(heuristic_ms, 5),
                                "tflops": round(flops / heuristic_ms / 1e9, 1)},
                  "candidates": {}}
         for kernel, tr, tc in GEMM_CANDIDATES:
-            if kernel == "lds_dma" and K % 8:
+            if kernel == "lds_dma" and K % 2:
                 continue
             if kernel == "stream" and (K not in (64, 128, 256) or N % 64):
                 continue

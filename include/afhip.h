@@ -206,9 +206,11 @@ typedef struct afhip_variant {
  * REGISTER_STAGED: operands pass through VGPRs into double-buffered LDS; any
  *   operand dtype (f32, f16, int8 weights), tiles 64 or 128 on each side.
  * LDS_DMA: operands go global -> LDS directly (buffer loads into LDS), several
- *   k-steps in flight; f16 operands, K a multiple of 8; tiles 128x128,
- *   192x192 or 128x256. The counterpart of the reference's matrix kernel with
- *   deeper k-staging (src/runtime/gemm.ts:470-479).
+ *   k-steps in flight; f16 operands (an int8 weight is widened to f16 by the
+ *   plan first, exactly) with an even K: 16-byte loads when K and the leading
+ *   dimensions are multiples of 8, 4-byte loads (128x128 tiles) otherwise;
+ *   tiles 128x128, 192x192, 128x256 or 256x256. The counterpart of the
+ *   reference's matrix kernel with deeper k-staging (src/runtime/gemm.ts:470-479).
  * STREAM: weight-stationary: the weight stays in registers and 64-row tiles of
  *   the activations stream past it, each byte read and written once; f16
  *   activations and output, f16 or int8 weights, K of 64, 128 or 256, columns

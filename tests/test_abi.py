@@ -149,14 +149,18 @@ def test_variant_selection_without_device():
     from afhip import gemm
 
     # BASELINE config 2 (tall, K = 256, int8 weights, f16 out) streams past
-    # register-resident weights; with an f32 output it stays on the register-
-    # staged kernel.
+    # register-resident weights; with an f32 output it takes the LDS_DMA
+    # family, its plan widening the int8 weight to f16 first; so does the
+    # reference's trans2 shape (K = 1024) with int8 weights.
     v = gemm.select_variant(131072, 256, 1024, precision="f16", a_dtype="f16", w_dtype="i8", out_dtype="f16")
     assert (v.kernel, v.tile_rows, v.tile_columns, v.source) == ("stream", 64, 512, "heuristic")
     assert v.name == "mfma-stream-f16-64x512k32"
     v = gemm.select_variant(131072, 256, 1024, precision="f16", a_dtype="f16", w_dtype="i8", out_dtype="f32")
-    assert v.tile_rows in (64, 128) and v.tile_columns in (64, 128) and v.source == "heuristic"
-    assert v.kernel == "register" and v.name.startswith("mfma-register-f16-")
+    assert v.kernel == "lds_dma" and v.source == "heuristic"
+    assert gemm.select_variant(29972, 1024, 256, precision="f16", a_dtype="f16", w_dtype="i8",
+                               out_dtype="f16").kernel == "lds_dma"
+    # An odd K stays on the register-staged kernel (no 4-byte chunk holds it).
+    assert gemm.select_variant(100, 33, 64, precision="f16", a_dtype="f16", w_dtype="f16").kernel == "register"
     # f16 operands on both sides take the LDS_DMA family; the triangle
     # contraction at L = 384 (128 channels) tiles 192 x 192, two per CU.
     v = gemm.select_variant(384, 384, 384, precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f16",
@@ -179,14 +183,14 @@ def test_variant_selection_without_device():
     v = gemm.select_variant(65536, 1024, 128, precision="f16", a_dtype="f16", w_dtype="f16")
     assert (v.tile_rows, v.tile_columns) == (128, 128)
     # The reference's SHAPES (tools/gemm-candidates.ts:637-669), as measured
-    # by bench.py --gemm-shapes: STREAM from ~16k rows only; a K that is not a
-    # multiple of 8 (opm-contract, K = 508) is staged through registers, one
-    # tile a CU since K is long.
+    # by bench.py --gemm-shapes: STREAM from ~16k rows only; a K that is even
+    # but not a multiple of 8 (opm-contract, K = 508) takes LDS_DMA with
+    # 4-byte loads, on 128 x 128 tiles.
     f16 = dict(precision="f16", a_dtype="f16", w_dtype="f16", out_dtype="f16")
     assert gemm.select_variant(29972, 256, 1024, **f16).kernel == "stream"
     assert gemm.select_variant(8192, 128, 512, **f16).kernel == "lds_dma"
     v = gemm.select_variant(128, 508, 32000, **f16)
-    assert (v.kernel, v.tile_rows, v.tile_columns) == ("register", 128, 64)
+    assert v.kernel == "lds_dma"
 
 
 def test_calibration_document_round_trip(tmp_path):

@@ -101,11 +101,15 @@ def _batched_f16_plan(gemm, B, M, N, K, out_dtype, lda=0):
 
 
 @pytest.mark.parametrize("out_dtype", ["f16", "f32"])
-@pytest.mark.parametrize("shape", [(3, 200, 136, 104, 0), (2, 64, 448, 40, 56), (1, 385, 193, 392, 0)])
+@pytest.mark.parametrize("shape", [(3, 200, 136, 104, 0), (2, 64, 448, 40, 56), (1, 385, 193, 392, 0),
+                                   (2, 200, 300, 508, 0), (1, 130, 257, 98, 102), (3, 65, 70, 30, 34)])
 def test_lds_dma_tiles_match_register_kernel_bitwise(dev, out_dtype, shape):
     # Both kernel families walk K in the same 32-deep steps of two 16-deep
     # MFMAs, so they accumulate in one order: every tile gives the register-
     # staged kernel's result bit for bit, ragged M, N and K tails included.
+    # The last three shapes have rows that are only 4-byte aligned (K or lda
+    # not a multiple of 8, as the reference's opm-contract K = 508): LDS_DMA
+    # loads them 4 bytes a lane.
     from afhip import gemm
 
     B, M, N, K, lda = shape
@@ -128,6 +132,39 @@ def test_lds_dma_tiles_match_register_kernel_bitwise(dev, out_dtype, shape):
     assert rel_max(base, expect) <= 2e-3
     for key, got in results.items():
         assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), key
+
+
+@pytest.mark.parametrize("out_dtype", ["f16", "f32"])
+@pytest.mark.parametrize("w_layout", ["column", "k"])
+def test_int8_weights_on_lds_dma_match_register_kernel(dev, out_dtype, w_layout):
+    # The reference's trans2 shape class with mixed-q8 weights (K = 1024):
+    # a plan on the LDS_DMA family widens the int8 weight to f16 (exact) and
+    # applies the per-column scale to the f32 accumulator, as the register-
+    # staged kernel does inside its loader: the same bits. Against float64
+    # with the oracle-decoded weight within the q8 path's 1e-2.
+    from afhip import gemm
+
+    M, K, N = 500, 1024, 256
+    x = ref.round_f16(ref.normal(51, (M, K)))
+    q = ref.uniform_i8(52, (K, N))
+    s = ref.uniform(53, (N,), 1e-3, 1e-2)
+    w = q if w_layout == "column" else np.ascontiguousarray(q.T)
+    xd, wd, sd = to_dev(x, dev).half(), to_dev(w, dev), to_dev(s, dev)
+    results = {}
+    for pin in (gemm.GemmVariant("f16", 128, 128, source="pinned", kernel="register"), None):
+        gemm.force_variant(pin)
+        try:
+            plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype="i8", w_layout=w_layout,
+                                  out_dtype=out_dtype, epilogue=("scale",))
+            kernel = plan.variant().kernel
+            results[kernel] = plan.run(xd, wd, scale=sd).float().cpu().numpy()
+        finally:
+            gemm.force_variant(None)
+    assert set(results) == {"register", "lds_dma"}
+    assert np.array_equal(results["lds_dma"].view(np.uint32), results["register"].view(np.uint32))
+    expect = x.astype(np.float64) @ ref.q8_channel_decode(q, s).astype(np.float64)
+    err = np.abs(results["lds_dma"] - expect)
+    assert np.all(err <= 1e-2 * np.maximum(1.0, np.abs(expect))), float(err.max())
 
 
 @pytest.mark.parametrize("out_dtype", ["f16", "f32"])
