@@ -1,7 +1,9 @@
 // Transition for gfx950: LayerNorm, linear channels -> hidden + bias + ReLU,
 // linear hidden -> channels + bias (src/evoformer/transition.ts:179-234,
 // :264-361). At f16 precision with 128 channels and hidden 512 (the pair
-// transition) one fused kernel does all three steps (transition_fused.hip).
+// transition) one fused kernel does all three steps (transition_fused.hip);
+// so does another at 256 channels and hidden 1024 (the MSA transition,
+// transition_msa.hip), from its own folded copy of the weights.
 // Otherwise the LayerNorm writes the normalised rows in the GEMM's operand
 // dtype (rows spread over lane groups with 16-byte accesses for the f16 path
 // at 64, 128 or 256 channels, one wave per row otherwise) and both linears run
@@ -17,7 +19,7 @@ namespace afhip {
 namespace {
 
 struct TransitionWeights {
-  size_t scale, offset, w1, b1, w2, b2, total;
+  size_t scale, offset, w1, b1, w2, b2, msa, total;
 };
 
 TransitionWeights layout(const afhip_transition_desc& d) {
@@ -35,6 +37,7 @@ TransitionWeights layout(const afhip_transition_desc& d) {
   w.b1 = take(4 * (size_t)d.hidden);
   w.w2 = take(es * (size_t)d.channels * d.hidden);  // [C][H]
   w.b2 = take(4 * (size_t)d.channels);
+  w.msa = transition_msa_shape(d) ? take(transition_msa_weight_bytes()) : 0;
   w.total = at;
   return w;
 }
@@ -235,8 +238,8 @@ int afhip_transition_weights_size(const afhip_transition_desc* desc, size_t* byt
 int afhip_transition_workspace_size(const afhip_transition_desc* desc, size_t* bytes) {
   if (int s = validate(desc)) return s;
   AFHIP_REQUIRE(bytes != nullptr, "output is NULL");
-  // The fused kernel keeps the normalised rows and the hidden activation on chip.
-  *bytes = transition_fused_shape(*desc) ? 0 : workspace(*desc).total;
+  // The fused kernels keep the normalised rows and the hidden activation on chip.
+  *bytes = transition_fused_shape(*desc) || transition_msa_shape(*desc) ? 0 : workspace(*desc).total;
   return AFHIP_OK;
 }
 
@@ -249,10 +252,14 @@ int afhip_transition_prepare_weights(const afhip_transition_desc* desc, const fl
   const TransitionWeights w = layout(d);
   char* b = (char*)prepared;
   hipStream_t st = (hipStream_t)stream;
-  if (d.precision == AFHIP_PRECISION_F16)
-    return launch("transition.prepare", transition_prepare_kernel<half_t>, dim3(1024), dim3(256), 0, st, packed,
-                  d.channels, d.hidden, (float*)(b + w.scale), (float*)(b + w.offset), (half_t*)(b + w.w1),
-                  (float*)(b + w.b1), (half_t*)(b + w.w2), (float*)(b + w.b2));
+  if (d.precision == AFHIP_PRECISION_F16) {
+    if (int s = launch("transition.prepare", transition_prepare_kernel<half_t>, dim3(1024), dim3(256), 0, st, packed,
+                       d.channels, d.hidden, (float*)(b + w.scale), (float*)(b + w.offset), (half_t*)(b + w.w1),
+                       (float*)(b + w.b1), (half_t*)(b + w.w2), (float*)(b + w.b2)))
+      return s;
+    if (transition_msa_shape(d)) return prepare_transition_msa(packed, b + w.msa, st);
+    return AFHIP_OK;
+  }
   return launch("transition.prepare", transition_prepare_kernel<float>, dim3(1024), dim3(256), 0, st, packed,
                 d.channels, d.hidden, (float*)(b + w.scale), (float*)(b + w.offset), (float*)(b + w.w1),
                 (float*)(b + w.b1), (float*)(b + w.w2), (float*)(b + w.b2));
@@ -285,7 +292,19 @@ int afhip_transition_run(const afhip_transition_desc* desc, const void* activati
     f.b2 = (const float*)(wb + w.b2);
     return launch_transition_fused(f, d.in_dtype, d.out_dtype, st);
   }
-  AFHIP_REQUIRE(!transition_fused_shape(d) || workspace_bytes >= ws.total,
+  if (transition_msa_eligible(d, activations, out)) {
+    MsaTransitionArgs m{};
+    m.x = (const half_t*)activations;
+    m.out = out;
+    m.rows = d.rows;
+    m.residual = d.residual;
+    m.eps = d.epsilon;
+    m.blocks = wb + w.msa;
+    m.b1 = (const float*)(wb + w.msa + transition_msa_weight_bytes() - 4 * (size_t)(d.hidden + d.channels));
+    m.b2 = m.b1 + d.hidden;
+    return launch_transition_msa(m, d.out_dtype, st);
+  }
+  AFHIP_REQUIRE(!(transition_fused_shape(d) || transition_msa_shape(d)) || workspace_bytes >= ws.total,
                 "this transition shape runs fused and needs activations and output 16-byte aligned");
   AFHIP_REQUIRE(workspace_ptr != nullptr && workspace_bytes >= ws.total, "workspace of %zu bytes is smaller than %zu",
                 workspace_bytes, ws.total);

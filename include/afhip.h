@@ -397,6 +397,10 @@ AFHIP_API int afhip_transition_workspace_size(const afhip_transition_desc* desc,
  * secondWeight [H][C], secondBias [C]. */
 AFHIP_API int afhip_transition_prepare_weights(const afhip_transition_desc* desc, const float* packed, void* prepared,
                                      void* stream);
+/* At f16 precision, channels 128 with hidden 512 (the pair transition) and
+ * channels 256 with hidden 1024 and f16 activations (the MSA transition) run
+ * as one fused kernel: the workspace size is 0, and activations and out must
+ * be 16-byte aligned. activations == out is allowed (in place). */
 AFHIP_API int afhip_transition_run(const afhip_transition_desc* desc, const void* activations, const void* prepared,
                          void* out, void* workspace, size_t workspace_bytes, void* stream);
 

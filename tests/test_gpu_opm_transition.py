@@ -271,6 +271,62 @@ def test_transition_fused_in_place_full_size(dev):
     assert err <= 1e-2 * max(1.0, expect.abs().max().item())
 
 
+@pytest.mark.parametrize("rows,out_dt,residual", [
+    (1, "f16", False), (37, "f32", True), (300, "f16", True), (515, "f32", False), (4099, "f16", True)])
+def test_transition_fused_msa(dev, rows, out_dt, residual):
+    """The MSA transition at f16 precision, channels 256 and hidden 1024
+    (src/evoformer/block.ts:1713-1716), runs as one fused kernel that streams
+    the weights in blocks of 32 hidden units: f16 rows in, f16 or f32 out, the
+    residual added into the output, and row counts off the 256-row tiles and
+    32-row waves."""
+    import ctypes
+
+    import torch
+
+    from afhip import _lib, transition
+
+    c, h = 256, 1024
+    inp = transition_case(rows, c, h, 5 * rows + 1)
+    x = ref.round_f16(inp["activations"])
+    base = ref.normal(rows + 13, (rows, c))
+    base = base if out_dt == "f32" else ref.round_f16(base)
+    expect = ref.transition(x, inp["weights"]) + (base if residual else 0.0)
+    op = transition.Transition(rows, c, h, precision="f16", in_dtype="f16", out_dtype=out_dt, residual=residual)
+    size = ctypes.c_size_t()
+    _lib.call("afhip_transition_workspace_size", ctypes.byref(op.desc), ctypes.byref(size))
+    assert size.value == 0  # no normalised rows and no hidden activation in HBM
+    op.prepare(inp["weights"])
+    tdt = {"f32": torch.float32, "f16": torch.float16}
+    out = torch.from_numpy(base).to(tdt[out_dt]).to(dev)
+    op(torch.from_numpy(x).half().to(dev), out=out)
+    got = out.float().cpu().numpy()
+    assert np.abs(got - expect).max() <= 1e-2 * max(1.0, np.abs(expect).max())
+
+
+def test_transition_fused_msa_in_place_full_size(dev):
+    """m += transition(m) in place over BASELINE config 4's MSA (512
+    sequences x 256 residues, 131,072 rows of 256 channels), against the
+    oracle on seeded rows that cover every row of a 32-row wave and the last
+    tile."""
+    import torch
+
+    from afhip import transition
+
+    rows, c, h = 512 * 256, 256, 1024
+    inp = transition_case(64, c, h, 9)
+    m = ref.round_f16(ref.normal(0xAF2007, (rows, c)))
+    md = torch.from_numpy(m).half().to(dev)
+    op = transition.Transition(rows, c, h, precision="f16", in_dtype="f16", out_dtype="f16", residual=True)
+    op.prepare(inp["weights"])
+    op(md, out=md)
+    got = md.float().cpu().numpy()
+    rng = np.random.default_rng(7)
+    check = np.unique(np.concatenate([rng.choice(rows, 480, replace=False), np.arange(32), np.arange(rows - 32, rows)]))
+    expect = m[check].astype(np.float64) + ref.transition(m[check], inp["weights"])
+    err = np.abs(got[check] - expect)
+    assert err.max() <= 1e-2 * max(1.0, np.abs(expect).max()), float(err.max())
+
+
 def test_invalid_opm_and_transition_raise(dev):
     from afhip import _lib, opm, transition
 
