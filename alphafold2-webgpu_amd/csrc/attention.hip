@@ -34,6 +34,7 @@
 #include <cstddef>
 #include <utility>
 
+#include "dma.h"
 #include "gemm.h"
 
 namespace afhip {
@@ -85,7 +86,7 @@ AttentionWeights weights_layout(const afhip_attention_desc& d) {
 // at least that much padding.
 struct AttentionWorkspace {
   size_t normalized, key_bias, key_mask, qkvg, bias, weighted, total;
-  int stride;
+  int stride, code_stride;
 };
 
 constexpr int kReadAhead = 64;  // keys
@@ -102,10 +103,11 @@ AttentionWorkspace workspace_layout(const afhip_attention_desc& d) {
     return here;
   };
   w.stride = (int)round_up(d.queries, 4);
+  w.code_stride = (int)round_up(d.queries, 32);
   w.normalized = take(es * rows * C);
   w.key_bias = take(fast ? 0 : 4 * (size_t)d.batch * w.stride);
-  // f16 key mask codes [B][stride] (fast path)
-  w.key_mask = take(fast ? 2 * ((size_t)d.batch * w.stride + kReadAhead) : 0);
+  // f16 key mask codes [B][code_stride] (fast path)
+  w.key_mask = take(fast ? 2 * (size_t)d.batch * w.code_stride : 0);
   w.qkvg = take(es * (rows + (fast ? kReadAhead : 0)) * 4 * C);
   w.bias = take(d.pair_bias ? 4 * ((size_t)d.heads * d.queries * w.stride + (fast ? kReadAhead : 0)) : 0);
   w.weighted = take(es * rows * C);
@@ -217,12 +219,13 @@ struct RowsArgs {
   const float* mask;        // source order, or null (no key bias)
   float* key_bias;          // [B][stride] f32, or null
   float key_scale;
-  half_t* key_mask;         // [B][stride] f16 codes (mask - 1) kMaskCode, or null
+  half_t* key_mask;         // [B][code_stride] f16 codes (mask - 1) kMaskCode, or null
   const float* w;           // [C][H], or null (no pair bias)
   int H;
   float bias_scale;
   float* bias;              // [H][Q][stride]
   int stride;
+  int code_stride;          // Q rounded up to 32: keys Q.. of a code row hold -inf
 };
 
 // The key mask code of the fast path: (mask - 1) 32768 in f16 (exact for a
@@ -231,9 +234,26 @@ struct RowsArgs {
 constexpr float kMaskCode = 32768.0f;
 constexpr float kMaskScale = 44032.0f;
 
-__device__ __forceinline__ void key_bias_store(const RowsArgs& a, int64_t at, float mask) {
-  if (a.key_bias) a.key_bias[at] = a.key_scale * (mask - 1.0f);
-  if (a.key_mask) a.key_mask[at] = (half_t)((mask - 1.0f) * kMaskCode);
+// Key (b, q)'s bias or code. The last key of a code row also fills the row's
+// padding with -inf codes: past the last key a key block's mask step then
+// gives -inf logits.
+__device__ __forceinline__ void key_bias_store(const RowsArgs& a, int64_t b, int64_t q, float mask) {
+  if (a.key_bias) a.key_bias[b * a.stride + q] = a.key_scale * (mask - 1.0f);
+  if (a.key_mask) {
+    half_t* row = a.key_mask + b * a.code_stride;
+    row[q] = (half_t)((mask - 1.0f) * kMaskCode);
+    if (q == a.Q - 1)
+      for (int k = a.Q; k < a.code_stride; k++) row[k] = (half_t)(-INFINITY);
+  }
+}
+
+// Pair bias (h, query b, key q); the last key of a row also zeroes the row's
+// padding up to the stride, which the fast kernels read as keys past the end.
+__device__ __forceinline__ void pair_bias_store(const RowsArgs& a, int h, int64_t b, int64_t q, float v) {
+  float* row = a.bias + ((int64_t)h * a.Q + b) * a.stride;
+  row[q] = a.bias_scale * v;
+  if (q == a.Q - 1)
+    for (int k = a.Q; k < a.stride; k++) row[k] = 0.0f;
 }
 
 template <typename T> __device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
@@ -323,7 +343,7 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; e++) v[e] = (v[e] - mean) * rstd * sc[e] + of[e];
     if (a.out && live) store8(reinterpret_cast<OT*>(a.out) + rr * C + 8 * j, v);
-    if (a.mask && live && j == 0) key_bias_store(a, b * a.stride + q, a.mask[src]);
+    if (a.mask && live && j == 0) key_bias_store(a, b, q, a.mask[src]);
     if (a.w) {
       float acc[HB] = {};
 #pragma unroll
@@ -340,7 +360,7 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(RowsArgs a) {
         const float t = lane_sum<LANES>(acc[h]);
         if (h == j) mine = t;
       }
-      if (live && j < a.H) a.bias[((int64_t)j * a.Q + b) * a.stride + q] = a.bias_scale * mine;
+      if (live && j < a.H) pair_bias_store(a, j, b, q, mine);
     }
   }
 }
@@ -369,14 +389,14 @@ __global__ __launch_bounds__(256) void attention_rows_any_kernel(RowsArgs a) {
   if (a.out)
     for (int c = lane; c < C; c += 64)
       reinterpret_cast<OT*>(a.out)[r * C + c] = (OT)((ld(xr, c) - mean) * rstd * a.scale[c] + a.offset[c]);
-  if (a.mask && lane == 0) key_bias_store(a, b * a.stride + q, a.mask[src]);
+  if (a.mask && lane == 0) key_bias_store(a, b, q, a.mask[src]);
   if (a.w) {
     for (int h = 0; h < a.H; h++) {
       float acc = 0.0f;
       for (int c = lane; c < C; c += 64)
         acc += ((ld(xr, c) - mean) * rstd * a.scale[c] + a.offset[c]) * a.w[(int64_t)c * a.H + h];
       for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-      if (lane == 0) a.bias[((int64_t)h * a.Q + b) * a.stride + q] = a.bias_scale * acc;
+      if (lane == 0) pair_bias_store(a, h, b, q, acc);
     }
   }
 }
@@ -384,10 +404,10 @@ __global__ __launch_bounds__(256) void attention_rows_any_kernel(RowsArgs a) {
 struct FlashArgs {
   const void* qkvg;       // [B Q][4C]: q (scaled), k, v, g (sigmoid)
   const float* key_bias;  // [B][stride] (general kernel)
-  const half_t* key_mask; // [B][stride] codes (f16 kernel)
+  const half_t* key_mask; // [B][code_stride] codes (f16 kernels)
   const float* bias;      // [H][Q][stride] or null
   void* weighted;         // [B Q][C] in source order
-  int B, Q, C, H, d, transpose, stride;
+  int B, Q, C, H, d, transpose, stride, code_stride;
   float clamp;
 };
 
@@ -554,7 +574,7 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
     if (8 * hi < a.d) qf[0] = *reinterpret_cast<const half8*>(qr);
     if (16 + 8 * hi < a.d) qf[1] = *reinterpret_cast<const half8*>(qr + 16);
   }
-  const half_t* cp = a.key_mask + bc * a.stride + col;
+  const half_t* cp = a.key_mask + bc * a.code_stride + col;
 
   floatx16 o = {};       // O^T: lane holds query myq, channels 8 (v / 4) + 4 hi + v % 4
   float run_sum = 0.0f;  // over this lane's keys; the lane 32 away holds the rest
@@ -746,6 +766,311 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
   }
 }
 
+// The same attention at head dimension 32 (every Evoformer attention), with
+// more independent work a wave and no staging registers:
+//  - a wave takes 64 queries of one (b, h), as two 32-query tiles against
+//    each key block, so the K and V^T fragments it reads from LDS feed two
+//    MFMAs each and the two tiles' softmax and MFMAs interleave;
+//  - a workgroup is two batch entries by two such waves (128 queries of one
+//    head per entry), four waves meeting at one barrier a key block;
+//  - K, V, the pair-bias tile and the mask codes of a key block arrive by
+//    DMA (buffer_load ... lds) in a ring of three LDS buffers, two blocks
+//    ahead. A resource per batch entry ends at the entry's last row, so keys
+//    past the end load as zeros; their logits are then set to -inf.
+//  - a block's softmax first takes the probabilities at the current offset
+//    m. When the tile's clamp bounds are far from m and every lane's 16
+//    probabilities sum below 2^7 (so each is below 2^7), the exact path
+//    would neither clamp (its clamped logits underflow to 0 either way) nor
+//    move m, and would compute the same probabilities: they are kept. The
+//    first block, the last and any other block run the exact path of the
+//    kernel above.
+// LDS buffer: K [entry][16-byte channel granule][key]; V [entry][key][channel]
+// (64-byte rows for the transposing reads); mask codes, a 256-byte slot a
+// wave (its first 32 bytes loaded); pair bias [query][key] f32, the eight
+// 16-byte granules of row q stored at granule ^ (q mod 8).
+constexpr int kF2Entries = 2;
+constexpr int kF2QueryWaves = 2;
+constexpr int kF2Tiles = 2;
+constexpr int kF2Threads = 64 * kF2Entries * kF2QueryWaves;
+constexpr int kF2Queries = 32 * kF2Tiles * kF2QueryWaves;  // of each entry
+constexpr int kF2Buffers = 3;
+constexpr int kF2K = 0, kF2V = 4096, kF2Code = 8192, kF2Bias = 9216;
+constexpr int kF2BufBias = kF2Bias + kF2Queries * 128;
+constexpr int kF2BufNoBias = kF2Bias;
+constexpr float kF2FastSum = 128.0f;
+
+template <bool BIAS>
+__global__ __launch_bounds__(kF2Threads, BIAS ? 2 : 4) void attention_flash2_kernel(FlashArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  constexpr int BUF = BIAS ? kF2BufBias : kF2BufNoBias;
+  constexpr int kIssue = BIAS ? 7 : 3;  // DMA instructions a wave issues a block
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, hi = lane >> 5;
+  const int bi = wave / kF2QueryWaves, qi = wave % kF2QueryWaves;
+  const int Q = a.Q, C = a.C;
+  const int qblocks = (Q + kF2Queries - 1) / kF2Queries;
+  // Workgroups run on the XCDs in turn; renumbered so that each XCD takes a
+  // contiguous range: the workgroups of one batch pair (its query blocks and
+  // heads) then share that XCD's L2.
+  const unsigned G = gridDim.x;
+  const unsigned vid = (G % 8 == 0) ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+  const int qb = (int)(vid % qblocks);
+  const int h = (int)((vid / qblocks) % a.H);
+  const int64_t b0 = (int64_t)(vid / qblocks / a.H) * kF2Entries;
+  const int qbase = qb * kF2Queries;
+  const half_t* base = reinterpret_cast<const half_t*>(a.qkvg);
+  const int64_t ld4 = 4 * (int64_t)C;
+  const uint32_t row_bytes = (uint32_t)(2 * ld4);
+
+  // This wave's batch entry; an entry past the last loads the last one's rows
+  // (never used).
+  const int64_t b = b0 + bi;
+  const int64_t be = b < a.B ? b : a.B - 1;
+  const int32x4_t kv_rsrc = make_rsrc(base + be * Q * ld4, (uint32_t)Q * row_bytes);
+  const int32x4_t code_rsrc = make_rsrc(a.key_mask + be * a.code_stride, 2u * (uint32_t)a.code_stride);
+  int32x4_t bias_rsrc{};
+  if (BIAS) bias_rsrc = make_rsrc(a.bias + (int64_t)h * Q * a.stride, 4u * (uint32_t)Q * (uint32_t)a.stride);
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+  // Per-lane parts of the block's DMA offsets (block k0 adds k0 rows or keys).
+  const uint32_t k_off = (uint32_t)(2 * (C + 32 * h) + 16 * (2 * qi + hi));
+  const uint32_t v_off = (uint32_t)(2 * (2 * C + 32 * h) + 16 * (lane & 3));
+  const int v_key = 16 * qi + (lane >> 2);
+  const uint32_t b_gran = (uint32_t)(16 * ((lane & 7) ^ (lane >> 3)));
+  auto issue = [&](int j) {
+    const uint32_t buf = lds0 + (uint32_t)((j % kF2Buffers) * BUF);
+    const int k0 = 32 * j;
+    dma16(kv_rsrc, buf + kF2K + 2048 * bi + 1024 * qi, (uint32_t)(k0 + col) * row_bytes + k_off);
+    dma16(kv_rsrc, buf + kF2V + 2048 * bi + 1024 * qi, (uint32_t)(k0 + v_key) * row_bytes + v_off);
+    dma4(code_rsrc, buf + kF2Code + 256 * wave, lane < 8 ? 2u * (uint32_t)(k0 + 16 * qi + 2 * lane) : kOutOfRange);
+    if (BIAS) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int n = 4 * wave + i;  // bias rows 8 n .. 8 n + 7 of the workgroup's 128
+        dma16(bias_rsrc, buf + kF2Bias + 1024 * n,
+              4u * ((uint32_t)(qbase + 8 * n + (lane >> 3)) * (uint32_t)a.stride + (uint32_t)k0) + b_gran);
+      }
+    }
+  };
+  const int nblk = (Q + 31) >> 5;
+  issue(0);
+  if (nblk > 1) issue(1);
+
+  // This wave's queries: tile t holds qbase + 32 (2 qi + t) + col.
+  const bool active = b < a.B && qbase + 64 * qi < Q;  // idle waves still load and meet every barrier
+  const int64_t row0 = be * Q;
+  half8 qf[kF2Tiles][2];
+#pragma unroll
+  for (int t = 0; t < kF2Tiles; t++) {
+    const int q = min(qbase + 32 * (2 * qi + t) + col, Q - 1);
+    const half_t* qr = base + (row0 + q) * ld4 + 32 * h + 8 * hi;
+    qf[t][0] = *reinterpret_cast<const half8*>(qr);
+    qf[t][1] = *reinterpret_cast<const half8*>(qr + 16);
+  }
+  // Everything in flight, the query fragments included, lands here: the
+  // compiler then knows no load of its own is outstanding in the loop, where
+  // its wait for one would also wait for every DMA issued after it.
+  wait_vmcnt<0>();
+
+  floatx16 o[kF2Tiles];
+  float run_sum[kF2Tiles], lo[kF2Tiles], up[kF2Tiles];
+  // How far the clamp bounds are from m beyond what the fast softmax needs
+  // (up >= kSlack + 1, lo <= -kClampReach); negative before the first block.
+  float margin[kF2Tiles];
+  half4 bm_frag[kF2Tiles];
+  const half_t one = (half_t)1.0f;
+#pragma unroll
+  for (int t = 0; t < kF2Tiles; t++) {
+    o[t] = floatx16{};
+    run_sum[t] = 0.0f;
+    lo[t] = -kLogitBound;
+    up[t] = kLogitBound;
+    margin[t] = -1.0f;
+    // The mask step's B operand, (kMaskScale, -m) per query: every lane holds
+    // it (the A operand is zero on lanes 32-63), so m reads back from it.
+    bm_frag[t] = half4{(half_t)kMaskScale, (half_t)0.0f, (half_t)0.0f, (half_t)0.0f};
+  }
+  const int tr_key = 4 * hi + ((lane & 15) >> 2), tr_ch = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  // The exact softmax step of one tile (the kernel above): the clamp where it
+  // can matter, m moved, then the probabilities. Keys past the end come with
+  // -inf logits (their mask codes), which the clamp leaves alone. (The
+  // variant without a pair bias sets them again in the last block, as the
+  // kernel above does: its registers then fit four waves a SIMD.)
+  auto exact = [&](int t, floatx16& x, bool first, bool last, int k0, half8 (&pf)[2]) {
+    auto drop_past_end = [&]() {
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (k0 + 8 * g + 4 * hi + i >= Q) x[4 * g + i] = -INFINITY;
+    };
+    if (!BIAS && last) drop_past_end();
+    float bm = x[0];
+#pragma unroll
+    for (int v = 1; v < 16; v++) bm = fmaxf(bm, x[v]);
+    if (__builtin_amdgcn_ballot_w64(bm > up[t] || bm < lo[t] + kClampReach)) {
+#pragma unroll
+      for (int v = 0; v < 16; v++)
+        x[v] = x[v] == -INFINITY ? x[v] : __builtin_amdgcn_fmed3f(x[v], lo[t], up[t]);
+      if (!BIAS && last) drop_past_end();
+      bm = __builtin_amdgcn_fmed3f(bm, lo[t], up[t]);
+    }
+    if (first || __builtin_amdgcn_ballot_w64(bm > kSlack)) {
+      const float m = -(float)bm_frag[t][1];
+      const float pm = fmaxf(bm, __shfl_xor(bm, 32));
+      const float want = first ? pm : m + fmaxf(pm, 0.0f);
+      const float mn = (float)(half_t)want;
+      const float delta = mn - m;
+#pragma unroll
+      for (int v = 0; v < 16; v++) x[v] -= delta;
+      lo[t] -= delta;
+      up[t] -= delta;
+      if (!first) {
+        const float f = __builtin_amdgcn_exp2f(-delta);
+        run_sum[t] *= f;
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[t][v] *= f;
+      }
+      bm_frag[t][1] = (half_t)(-mn);
+    }
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      const half2v pp = half2v{(half_t)__builtin_amdgcn_exp2f(x[v]), (half_t)__builtin_amdgcn_exp2f(x[v + 1])};
+      run_sum[t] = __builtin_amdgcn_fdot2(pp, half2v{one, one}, run_sum[t], false);
+      pf[v >> 3][v & 7] = pp[0];
+      pf[v >> 3][(v & 7) + 1] = pp[1];
+    }
+    margin[t] = fminf(up[t] - (kSlack + 1.0f), -kClampReach - lo[t]);
+  };
+
+  for (int j = 0; j < nblk; j++) {
+    // Block j has landed once at most block j + 1's loads are outstanding;
+    // the barrier publishes it and retires buffer (j + 2) % 3, whose block
+    // j - 1 every wave has finished.
+    if (j + 1 < nblk) wait_vmcnt<kIssue>();
+    else wait_vmcnt<0>();
+    block_barrier<false>();
+    if (j + 2 < nblk) issue(j + 2);
+    if (!active) continue;
+    const unsigned char* bp = smem + (j % kF2Buffers) * BUF;
+    const bool first = j == 0;
+    const unsigned char* kp = bp + kF2K + 2048 * bi + 16 * col;
+    const half8 kf0 = *reinterpret_cast<const half8*>(kp + 512 * hi);
+    const half8 kf1 = *reinterpret_cast<const half8*>(kp + 512 * (2 + hi));
+    const half_t code = *reinterpret_cast<const half_t*>(bp + kF2Code + 256 * (2 * bi + (col >> 4)) + 2 * (col & 15));
+    const half4 am = hi ? half4{} : half4{code, one, (half_t)0.0f, (half_t)0.0f};
+    floatx16 sc[kF2Tiles];
+#pragma unroll
+    for (int t = 0; t < kF2Tiles; t++) {
+      sc[t] = floatx16{};
+      if constexpr (BIAS) {
+        const unsigned char* brow = bp + kF2Bias + 128 * (32 * (2 * qi + t) + col);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4 v = *reinterpret_cast<const float4*>(brow + 16 * ((2 * g + hi) ^ (col & 7)));
+          sc[t][4 * g] = v.x, sc[t][4 * g + 1] = v.y, sc[t][4 * g + 2] = v.z, sc[t][4 * g + 3] = v.w;
+        }
+      }
+      sc[t] = mfma_f16(kf0, qf[t][0], sc[t]);
+      sc[t] = mfma_f16(kf1, qf[t][1], sc[t]);
+      sc[t] = __builtin_amdgcn_mfma_f32_32x32x8f16(am, bm_frag[t], sc[t], 0, 0, 0);
+    }
+    const unsigned char* vp = bp + kF2V + 2048 * bi + 64 * tr_key + 2 * tr_ch;
+    auto read_v = [&](int s) {
+      const short4v l4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(vp + 1024 * s));
+      const short4v u4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(vp + 1024 * s + 512));
+      return __builtin_bit_cast(half8, short8v{l4[0], l4[1], l4[2], l4[3], u4[0], u4[1], u4[2], u4[3]});
+    };
+    // A tile's probabilities at the current offset and their sum; whether
+    // the exact step must redo them.
+    half8 pf[kF2Tiles][2];
+    float bs[kF2Tiles];
+    auto fast = [&](int t) {
+      bs[t] = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const half2v pp =
+            half2v{(half_t)__builtin_amdgcn_exp2f(sc[t][v]), (half_t)__builtin_amdgcn_exp2f(sc[t][v + 1])};
+        bs[t] = __builtin_amdgcn_fdot2(pp, half2v{one, one}, bs[t], false);
+        pf[t][v >> 3][v & 7] = pp[0];
+        pf[t][v >> 3][(v & 7) + 1] = pp[1];
+      }
+      return __builtin_amdgcn_ballot_w64(!(bs[t] < kF2FastSum) || margin[t] < 0.0f);
+    };
+    if constexpr (BIAS) {
+      // Both tiles in one straight-line block, the V^T fragments read first
+      // so their latency overlaps the softmax (two waves a SIMD: registers
+      // allow it).
+      const half8 vf[2] = {read_v(0), read_v(1)};
+      uint64_t redo[kF2Tiles];
+#pragma unroll
+      for (int t = 0; t < kF2Tiles; t++) redo[t] = fast(t);
+      if (first || (redo[0] | redo[1])) {
+#pragma unroll
+        for (int t = 0; t < kF2Tiles; t++) {
+          if (first || redo[t]) exact(t, sc[t], first, false, 0, pf[t]);
+          else run_sum[t] += bs[t];
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < kF2Tiles; t++) run_sum[t] += bs[t];
+      }
+#pragma unroll
+      for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int t = 0; t < kF2Tiles; t++) o[t] = mfma_f16(vf[s], pf[t][s], o[t]);
+    } else {
+      // One tile at a time, V^T after: fewer registers, for four waves a SIMD.
+#pragma unroll
+      for (int t = 0; t < kF2Tiles; t++) {
+        const bool last = j + 1 == nblk;
+        bool slow = first || last;
+        if (!slow) {
+          slow = fast(t) != 0;
+          if (!slow) run_sum[t] += bs[t];
+        }
+        if (slow) exact(t, sc[t], first, last, 32 * j, pf[t]);
+      }
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        const half8 vf = read_v(s);
+#pragma unroll
+        for (int t = 0; t < kF2Tiles; t++) o[t] = mfma_f16(vf, pf[t][s], o[t]);
+      }
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int t = 0; t < kF2Tiles; t++) {
+    const float rs = run_sum[t] + __shfl_xor(run_sum[t], 32);
+    const int myq = qbase + 32 * (2 * qi + t) + col;
+    if (myq >= Q) continue;
+    const float inv = 1.0f / rs;
+    const half_t* gr = base + (row0 + myq) * ld4 + 3 * C + 32 * h;
+    const int64_t src = a.transpose ? (int64_t)myq * a.B + b : row0 + myq;
+    half_t* out = reinterpret_cast<half_t*>(a.weighted) + src * C + 32 * h;
+    half4 gv[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) gv[g] = *reinterpret_cast<const half4*>(gr + 8 * g + 4 * hi);
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      half4 r;
+#pragma unroll
+      for (int i = 0; i < 4; i++) r[i] = (half_t)(o[t][4 * g + i] * inv * (float)gv[g][i]);
+      *reinterpret_cast<half4*>(out + 8 * g + 4 * hi) = r;
+    }
+  }
+}
+
+// Whether a call can take the head-dimension-32 kernel: its 32-bit buffer
+// offsets cover an entry's rows, a head's bias plane and the read-ahead.
+bool flash2_eligible(const afhip_attention_desc& d, int stride) {
+  const int64_t Q = d.queries;
+  return fast_path(d) && d.channels / d.heads == 32 && (Q + 32) * 8 * (int64_t)d.channels < ((int64_t)1 << 31) &&
+         (Q + kF2Queries) * (int64_t)stride * 4 < ((int64_t)1 << 31);
+}
+
 // out += y over f16 tensors (f32 sum, one rounding): the residual step of
 // an output projection the streaming kernel computed without it.
 __global__ __launch_bounds__(256) void attention_residual_kernel(half_t* __restrict__ out,
@@ -882,6 +1207,7 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
       r.bias = bias;
     }
     r.stride = ws.stride;
+    r.code_stride = ws.code_stride;
     if ((s = launch_rows(r, d.in_dtype, ct, "attention.norm", st))) return s;
   }
   // 2. A separate pair source: its own LayerNorm, projected to the heads.
@@ -936,8 +1262,22 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
     fa.d = C / H;
     fa.transpose = d.transpose;
     fa.stride = ws.stride;
+    fa.code_stride = ws.code_stride;
     fa.clamp = 1e8f;
-    if (fast) {
+    if (flash2_eligible(d, ws.stride)) {
+      const int64_t groups = ceil_div(B, kF2Entries) * H * ceil_div(Q, kF2Queries);
+      AFHIP_REQUIRE(groups < ((int64_t)1 << 31), "attention grid too large");
+      if (bias) {
+        auto k = attention_flash2_kernel<true>;
+        if ((s = allow_lds((const void*)k, kF2Buffers * kF2BufBias))) return s;
+        s = launch("attention.flash", k, dim3((unsigned)groups), dim3(kF2Threads), kF2Buffers * kF2BufBias, st, fa);
+      } else {
+        auto k = attention_flash2_kernel<false>;
+        if ((s = allow_lds((const void*)k, kF2Buffers * kF2BufNoBias))) return s;
+        s = launch("attention.flash", k, dim3((unsigned)groups), dim3(kF2Threads), kF2Buffers * kF2BufNoBias, st,
+                   fa);
+      }
+    } else if (fast) {
       const int64_t groups = ceil_div(B, kFlashBatch) * H * ceil_div(Q, 32 * kFlashQueryWaves);
       AFHIP_REQUIRE(groups < ((int64_t)1 << 31), "attention grid too large");
       s = bias ? launch("attention.flash", attention_flash_f16_kernel<true>, dim3((unsigned)groups),

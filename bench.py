@@ -488,7 +488,9 @@ def measure_attention(steps: int, warmup: int) -> dict:
     kernel), synthetic inputs: triangle attention around the starting node at
     N_res=384 (c_z 128, 4 heads, normalized-input pair bias) and MSA row
     attention at N_seq=512, N_res=256 (c_m 256, 8 heads, pair bias from a
-    [256, 256, 128] pair). Flash FLOPs: 4 d per (batch, head, query, key)."""
+    [256, 256, 128] pair), and MSA column attention at the same shape
+    (transposed: 256 batch entries of 512 queries, no pair bias). Flash FLOPs:
+    4 d per (batch, head, query, key)."""
     import numpy as np
     import torch
 
@@ -498,19 +500,20 @@ def measure_attention(steps: int, warmup: int) -> dict:
     dev = device.device()
     out = {}
     for name, B, Q, C, H, pair, Cp, s in (("triangle_start_l384", 384, 384, 128, 4, "normalized-input", 0, SEED + 5),
-                                          ("msa_row_s512_l256", 512, 256, 256, 8, "separate", 128, SEED + 6)):
+                                          ("msa_row_s512_l256", 512, 256, 256, 8, "separate", 128, SEED + 6),
+                                          ("msa_column_s512_l256", 256, 512, 256, 8, None, 0, SEED + 7)):
         w = {"queryNormScale": ref.normal(s, (C,), 0.01, 1.0), "queryNormOffset": ref.normal(s + 1, (C,), 0.01),
              "queryWeight": ref.normal(s + 2, (C, C), 1 / C), "keyWeight": ref.normal(s + 3, (C, C), 1 / C),
              "valueWeight": ref.normal(s + 4, (C, C), 1 / C), "gatingWeight": ref.normal(s + 5, (C, C), 1 / C),
              "gatingBias": ref.normal(s + 6, (C,), 0.1, 1.0), "outputWeight": ref.normal(s + 7, (C, C), 1 / C),
              "outputBias": ref.normal(s + 8, (C,), 0.01)}
         pc = Cp or C
-        pb = {"source": pair, "projectionWeight": ref.normal(s + 9, (pc, H), 1 / pc)}
+        pb = None if pair is None else {"source": pair, "projectionWeight": ref.normal(s + 9, (pc, H), 1 / pc)}
         if pair == "separate":
             pb.update(channels=Cp, layerNormScale=ref.normal(s + 10, (Cp,), 0.01, 1.0),
                       layerNormOffset=ref.normal(s + 11, (Cp,), 0.01))
-        op = attention.Attention(B, Q, C, H, pair_bias=pair, pair_channels=Cp, precision="f16", in_dtype="f16",
-                                 out_dtype="f16", residual=True)
+        op = attention.Attention(B, Q, C, H, transpose=pair is None, pair_bias=pair, pair_channels=Cp,
+                                 precision="f16", in_dtype="f16", out_dtype="f16", residual=True)
         op.prepare(attention.pack_weights(w, pb))
         x = torch.from_numpy(ref.round_f16(ref.normal(s + 12, (B * Q, C)))).half().to(dev)
         mask = torch.ones(B * Q, dtype=torch.float32, device=dev)
@@ -521,7 +524,7 @@ def measure_attention(steps: int, warmup: int) -> dict:
         ms, k = timed(lambda: op(x, mask, p, out=y), max(5, steps // 5), warmup)
         d = C // H
         flash = 4 * B * H * Q * Q * d
-        total = flash + 2 * B * Q * C * 4 * C + 2 * B * Q * C * C + 2 * Q * Q * pc * H
+        total = flash + 2 * B * Q * C * 4 * C + 2 * B * Q * C * C + (2 * Q * Q * pc * H if pair else 0)
         entry = {"ms": round(ms, 4), "tflops": round(total / (ms * 1e-3) / 1e12, 2),
                  "kernel_ms": {kk: round(v, 5) for kk, v in k.items()}}
         if "attention.flash" in k:

@@ -165,6 +165,31 @@ def test_f16_long_keys_and_residual(dev):
     assert np.abs(got - expect).max() <= 1e-2 * np.abs(expect).max()
 
 
+@pytest.mark.parametrize("name", ["triangle_start", "msa_column", "msa_row"])
+def test_f16_sharp_logits_move_the_offset(dev, name):
+    # Logits spread over tens of units, so a row's running offset moves in
+    # middle key blocks and the fast probability check fails there (the exact
+    # step redoes the block). The spread comes from the pair bias scaled by
+    # 20 (f32 all the way, so the f16 operands add no error beyond the usual),
+    # and for column attention, which has no pair bias, from the queries
+    # scaled by 4. 200 keys (150 for MSA row attention): seven key blocks, the
+    # last ragged, with masked keys and a fully masked stretch.
+    msa = name.startswith("msa")
+    C, H = (256, 8) if msa else (128, 4)
+    x, mask, B, Q, tr, w, pb = case(name, S=200 if msa else 0, L=150 if msa else 200, C=C, H=H, Cp=64,
+                                    seed=0xA7E00)
+    if pb is not None:
+        pb["projectionWeight"] = pb["projectionWeight"] * 20.0
+    else:
+        w["queryWeight"] = w["queryWeight"] * 4.0
+    x = ref.round_f16(x)
+    if pb is not None and pb["source"] == "separate":
+        pb["activations"] = ref.round_f16(pb["activations"])
+    expect = ref.attention(x, mask, w, B, Q, C, H, transpose=tr, pair_bias=pb)
+    got = run_case(dev, x, mask, B, Q, C, H, tr, w, pb, precision="f16", in_dtype="f16", out_dtype="f16")
+    assert np.abs(got - expect).max() <= 1e-2 * np.abs(expect).max()
+
+
 def test_single_query_and_fully_masked(dev):
     # One query: softmax over one key; a fully masked batch entry averages
     # its values (every logit clamps to -1e8).
