@@ -1306,17 +1306,20 @@ int afhip_attention_run(const afhip_attention_desc* desc, const void* activation
     g.ldc = C;
     g.flags = AFHIP_EPILOGUE_BIAS | (d.residual ? AFHIP_EPILOGUE_RESIDUAL : 0u);
     GemmTypes t{d.precision, ct, ct, d.out_dtype};
-    // The streaming kernel has no residual epilogue: with a residual it
-    // writes the projection to the (by now unused) normalised rows, and a
-    // vectorised pass adds them in.
+    // With the residual, the streaming kernel adds the f16 projection into
+    // the output itself (f32 sum, one rounding) at C <= 128, reading the old
+    // values a tile ahead of its stores. At C = 256 its registers are full:
+    // it writes the projection to the (by now unused) normalised rows, and a
+    // vectorised pass adds them in, to the same result.
     GemmArgs gs = g;
     gs.flags &= ~AFHIP_EPILOGUE_RESIDUAL;
     gs.residual = nullptr;
-    if (d.residual) gs.c = wsb + ws.normalized;
+    const bool fused = C <= 128;
+    if (d.residual && !fused) gs.c = wsb + ws.normalized;
     const bool aligned = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
     if (stream_eligible(gs, t) && (!d.residual || aligned)) {
-      if ((s = run_gemm_stream(gs, t, "attention.output", st))) return s;
-      if (d.residual) {
+      if ((s = run_gemm_stream(gs, t, "attention.output", st, d.residual && fused))) return s;
+      if (d.residual && !fused) {
         const int64_t n = rows * C;
         if ((s = launch("attention.residual", attention_residual_kernel, dim3((unsigned)ceil_div(n, 2048)),
                         dim3(256), 0, st, (half_t*)out, (const half_t*)(wsb + ws.normalized), n)))

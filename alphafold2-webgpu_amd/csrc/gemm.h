@@ -93,7 +93,10 @@ __host__ __device__ inline int64_t opm_fused_weight_index(int k, int z) {
 // int8 weights held in registers, K in {64, 128, 256}, N % 64 == 0.
 bool stream_shape_ok(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);
 bool stream_eligible(const GemmArgs& args, const GemmTypes& types);
-int run_gemm_stream(const GemmArgs& args, const GemmTypes& types, const char* label, hipStream_t stream);
+// add_f16: out += f16(result) in f32 with one more rounding (the attention
+// output's residual), after a plain bias epilogue, at K <= 128.
+int run_gemm_stream(const GemmArgs& args, const GemmTypes& types, const char* label, hipStream_t stream,
+                    bool add_f16 = false);
 
 // The variant plans of this shape should use (pinned, calibrated or heuristic).
 afhip_variant select_variant(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);

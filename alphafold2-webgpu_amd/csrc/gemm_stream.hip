@@ -38,6 +38,13 @@
 //  - The epilogue applies the register-staged kernel's operations in its
 //    order (scale, bias, attention q-scaling or gate, ReLU) with the same
 //    roundings, so the two families give bit-identical outputs.
+//  - Adding into the output (out += f16(result), for the attention output's
+//    residual), the storer waves read the old values of a tile one pass
+//    before they store it, so the read's latency hides under a pass of
+//    MFMAs, and add them to the staged f16 result in f32 with one rounding:
+//    the result of writing the product and adding it in a second pass, in
+//    one. (The register-staged kernel's RESIDUAL epilogue rounds once, so
+//    this is not that epilogue.)
 #include <algorithm>
 #include <type_traits>
 
@@ -136,7 +143,7 @@ __device__ __forceinline__ void scale_row(floatx16& x, float s, float b, int& to
   }
 }
 
-template <int K, typename TW, bool BIAS, bool RELU>
+template <int K, typename TW, bool BIAS, bool RELU, bool RESID>
 __global__ __launch_bounds__(kThreads, 2) void gemm_stream_kernel(StreamArgs g) {
   using Lay = StreamLayout<K>;
   constexpr int KS = K / 16;  // MFMA k-steps
@@ -229,13 +236,27 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_stream_kernel(StreamArgs g) 
                                              0x00020000);
   };
   const int scol = 64 * ((3 - ((lane & 31) >> 3)) * g.slices + slice) + 8 * (lane & 7);
-  auto store_part = [&](__amdgpu_buffer_rsrc_t rc, int buf, int i, bool on) {
+  auto part_offset = [&](int i, bool on) {
+    const int r = 2 * ((wave - kLoaders) * kPer + i) + (lane >> 5);
+    return on && scol < g.N ? (uint32_t)(r * g.ldc * 2 + 2 * scol) : kOutOfRange;
+  };
+  auto store_part = [&](__amdgpu_buffer_rsrc_t rc, int buf, int i, bool on, const u32x4& old) {
     const int c = lane & 31;
     const int r = 2 * ((wave - kLoaders) * kPer + i) + (lane >> 5);
     u32x4 v = *reinterpret_cast<const u32x4*>(ost + buf * Lay::OBUF + r * Lay::OROW + 16 * (c ^ (r & 7)));
-    const uint32_t off = on && scol < g.N ? (uint32_t)(r * g.ldc * 2 + 2 * scol) : kOutOfRange;
-    __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
+    if constexpr (RESID) {
+      half8 h = __builtin_bit_cast(half8, v);
+      const half8 o = __builtin_bit_cast(half8, old);
+#pragma unroll
+      for (int e = 0; e < 8; e++) h[e] = (half_t)((float)o[e] + (float)h[e]);
+      v = __builtin_bit_cast(u32x4, h);
+    }
+    __builtin_amdgcn_raw_buffer_store_b128(v, rc, part_offset(i, on), 0, 0);
     stores_read(v);
+  };
+  // The old values under a storer's part of a tile (zeros past the resource).
+  auto load_part = [&](__amdgpu_buffer_rsrc_t rc, int i, bool on) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rc, part_offset(i, on), 0, 0);
   };
 
   // The persistent loop, software-pipelined: tile t's MFMAs, tile t-1's
@@ -279,6 +300,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_stream_kernel(StreamArgs g) 
     for (int cb = 0; cb < 2; cb++)
 #pragma unroll
       for (int v = 0; v < 16; v++) prev[cb][v] = 0.0f;
+    // A storer's old values (adding into the output): part i holds the tile
+    // it stores this pass until that store is formed, then is read again for
+    // the tile whose epilogue runs this pass.
+    u32x4 rcur[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; i++) rcur[i] = u32x4{0u, 0u, 0u, 0u};
     int tile = group;
     if constexpr (LOADER) {
       issue(tile, 0);
@@ -305,6 +332,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_stream_kernel(StreamArgs g) 
       const uint32_t ln = lds0 + ((it + 2) % kStages) * Lay::STAGE + wave * 1024;
       const bool drain = it >= 2;
       const __amdgpu_buffer_rsrc_t rc = store_rsrc(drain ? tile - 2 * g.groups : tile);
+      const bool ahead = it >= 1;
+      const __amdgpu_buffer_rsrc_t rp = store_rsrc(ahead ? tile - g.groups : tile);
       const int sbuf = (it - 1) & 1;
 
       floatx16 cur[2];
@@ -320,7 +349,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_stream_kernel(StreamArgs g) 
             dma16_if(rn, ln + kLoaders * (s / 2) * 1024, load_offset(s / 2), fill);
           } else {
 #pragma unroll
-            for (int j = 0; j < kPer / (KS / 2); j++) store_part(rc, sbuf, (s / 2) * (kPer / (KS / 2)) + j, drain);
+            for (int j = 0; j < kPer / (KS / 2); j++) {
+              const int i = (s / 2) * (kPer / (KS / 2)) + j;
+              store_part(rc, sbuf, i, drain, rcur[i]);
+              if constexpr (RESID) rcur[i] = load_part(rp, i, ahead);
+            }
           }
         }
         const half8 xf = *reinterpret_cast<const half8*>(st + ((32 * (s & 3)) ^ xswz) + 128 * (s >> 2));
@@ -337,15 +370,19 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_stream_kernel(StreamArgs g) 
       if (it >= 2) {
         const __amdgpu_buffer_rsrc_t rc = store_rsrc(tile - 2 * g.groups);
 #pragma unroll
-        for (int i = 0; i < kPer; i++) store_part(rc, (it - 1) & 1, i, true);
+        for (int i = 0; i < kPer; i++) store_part(rc, (it - 1) & 1, i, true, rcur[i]);
       }
     }
     epilogue(prev, it & 1);
     block_barrier();
     if constexpr (!LOADER) {
       const __amdgpu_buffer_rsrc_t rc = store_rsrc(tile - g.groups);
+      if constexpr (RESID) {
 #pragma unroll
-      for (int i = 0; i < kPer; i++) store_part(rc, it & 1, i, true);
+        for (int i = 0; i < kPer; i++) rcur[i] = load_part(rc, i, true);
+      }
+#pragma unroll
+      for (int i = 0; i < kPer; i++) store_part(rc, it & 1, i, true, rcur[i]);
     }
   };
 
@@ -363,30 +400,39 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_stream_kernel(StreamArgs g) 
   }
 }
 
-template <int K, typename TW, bool BIAS, bool RELU>
+template <int K, typename TW, bool BIAS, bool RELU, bool RESID>
 int launch_k(const StreamArgs& a, const char* label, hipStream_t s) {
-  auto kernel = gemm_stream_kernel<K, TW, BIAS, RELU>;
+  auto kernel = gemm_stream_kernel<K, TW, BIAS, RELU, RESID>;
   constexpr size_t shared = StreamLayout<K>::BYTES;
   if (int st = allow_lds((const void*)kernel, shared)) return st;
   return launch(label, kernel, dim3((unsigned)(a.groups * a.slices)), dim3(kThreads), shared, s, a);
 }
 
 template <int K, typename TW>
-int dispatch_epi(const StreamArgs& a, bool bias, bool relu, const char* label, hipStream_t s) {
-  if (bias) return relu ? launch_k<K, TW, true, true>(a, label, s) : launch_k<K, TW, true, false>(a, label, s);
-  return relu ? launch_k<K, TW, false, true>(a, label, s) : launch_k<K, TW, false, false>(a, label, s);
+int dispatch_epi(const StreamArgs& a, bool bias, bool relu, bool resid, const char* label, hipStream_t s) {
+  // Adding into the output comes only with a bias and no ReLU (the attention
+  // output), at K <= 128: at K = 256 the weights leave no registers for the
+  // old values.
+  if constexpr (K <= 128) {
+    if (resid) return launch_k<K, TW, true, false, true>(a, label, s);
+  }
+  if (bias)
+    return relu ? launch_k<K, TW, true, true, false>(a, label, s) : launch_k<K, TW, true, false, false>(a, label, s);
+  return relu ? launch_k<K, TW, false, true, false>(a, label, s) : launch_k<K, TW, false, false, false>(a, label, s);
 }
 
-int dispatch_k(const StreamArgs& a, int K, bool q8, bool bias, bool relu, const char* label, hipStream_t s) {
+int dispatch_k(const StreamArgs& a, int K, bool q8, bool bias, bool relu, bool resid, const char* label,
+               hipStream_t s) {
   switch (K) {
     case 64:
-      return q8 ? dispatch_epi<64, int8_t>(a, bias, relu, label, s) : dispatch_epi<64, half_t>(a, bias, relu, label, s);
+      return q8 ? dispatch_epi<64, int8_t>(a, bias, relu, resid, label, s)
+                : dispatch_epi<64, half_t>(a, bias, relu, resid, label, s);
     case 128:
-      return q8 ? dispatch_epi<128, int8_t>(a, bias, relu, label, s)
-                : dispatch_epi<128, half_t>(a, bias, relu, label, s);
+      return q8 ? dispatch_epi<128, int8_t>(a, bias, relu, resid, label, s)
+                : dispatch_epi<128, half_t>(a, bias, relu, resid, label, s);
     default:
-      return q8 ? dispatch_epi<256, int8_t>(a, bias, relu, label, s)
-                : dispatch_epi<256, half_t>(a, bias, relu, label, s);
+      return q8 ? dispatch_epi<256, int8_t>(a, bias, relu, resid, label, s)
+                : dispatch_epi<256, half_t>(a, bias, relu, resid, label, s);
   }
 }
 
@@ -412,8 +458,11 @@ bool stream_eligible(const GemmArgs& g, const GemmTypes& t) {
   return (int64_t)kBM * std::max(g.lda, g.ldc) * 2 < (int64_t)kOutOfRange;
 }
 
-int run_gemm_stream(const GemmArgs& g, const GemmTypes& t, const char* label, hipStream_t s) {
+int run_gemm_stream(const GemmArgs& g, const GemmTypes& t, const char* label, hipStream_t s, bool add_f16) {
   AFHIP_REQUIRE(stream_eligible(g, t), "operands the STREAM kernel cannot take");
+  AFHIP_REQUIRE(!add_f16 || ((g.flags & AFHIP_EPILOGUE_BIAS) && !(g.flags & (AFHIP_EPILOGUE_RELU | AFHIP_EPILOGUE_ATTENTION)) &&
+                              g.K <= 128),
+                "the STREAM kernel adds into its output only after a plain bias epilogue, at K <= 128");
   StreamArgs a;
   a.a = reinterpret_cast<const half_t*>(g.a);
   a.w = g.b;
@@ -438,7 +487,7 @@ int run_gemm_stream(const GemmArgs& g, const GemmTypes& t, const char* label, hi
   a.groups = groups;
   const bool q8 = t.b_dtype == AFHIP_I8;
   const bool bias = g.flags & AFHIP_EPILOGUE_BIAS, relu = g.flags & AFHIP_EPILOGUE_RELU;
-  return dispatch_k(a, g.K, q8, bias, relu, label, s);
+  return dispatch_k(a, g.K, q8, bias, relu, add_f16, label, s);
 }
 
 }  // namespace afhip

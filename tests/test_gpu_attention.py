@@ -276,6 +276,39 @@ def test_full_size_msa_row_attention_commutes_with_sequence_order(dev):
     assert torch.isfinite(a.float()).all()
 
 
+@pytest.mark.parametrize("name,B,Q,C,H,Cp", [("triangle_start", 384, 384, 128, 4, 0), ("msa_row", 512, 256, 256, 8, 128),
+                                              ("triangle_start", 77, 77, 128, 4, 0)])
+def test_f16_residual_adds_the_rounded_output(dev, name, B, Q, C, H, Cp):
+    # With the residual, out = f16(old + f16(attention)), f32 sum: at c = 128
+    # the output projection's streaming kernel adds into the output itself
+    # (reading the old values a tile ahead of its stores; full size gives
+    # each workgroup nine passes, 77 x 77 a ragged last tile), at c = 256 a
+    # second pass does. Either way bit for bit the two steps done apart.
+    import torch
+
+    from afhip import attention
+
+    pair = "normalized-input" if name.startswith("triangle") else "separate"
+    w, pb = weights(0xA7F00, C, H, pair, Cp)
+    x = torch.from_numpy(ref.round_f16(ref.normal(0xA7F10, (B * Q, C)))).half().to(dev)
+    mask = torch.from_numpy((ref.uniform(0xA7F11, (B * Q,), 0, 1) > 0.1).astype(np.float32)).to(dev)
+    p = None
+    if pair == "separate":
+        p = torch.from_numpy(ref.round_f16(ref.normal(0xA7F12, (Q * Q * Cp,)))).half().to(dev)
+    packed = attention.pack_weights(w, pb)
+    kw = dict(pair_bias=pair, pair_channels=Cp, precision="f16", in_dtype="f16", out_dtype="f16")
+    plain = attention.Attention(B, Q, C, H, **kw)
+    plain.prepare(packed)
+    y = plain(x, mask, p).clone()
+    old = torch.from_numpy(ref.round_f16(ref.normal(0xA7F13, (B * Q, C)))).half().to(dev)
+    res = attention.Attention(B, Q, C, H, residual=True, **kw)
+    res.prepare(packed)
+    out = old.clone()
+    res(x, mask, p, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, (old.float() + y.float()).half())
+
+
 @pytest.mark.parametrize("name", ["msa_row", "msa_column", "triangle_start", "triangle_end"])
 @pytest.mark.parametrize("C,H", [(64, 8), (64, 4), (96, 4)])
 def test_f16_mfma_narrow_heads(dev, name, C, H):
