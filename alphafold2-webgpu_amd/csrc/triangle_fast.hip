@@ -313,13 +313,23 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
         accp[sub][v] = bp;
         accg[sub][v] = bg;
       }
-    auto mfma_sub = [&](int sub) {
+    // Both sub-tiles' x_hat fragments are read first. The next tile's
+    // LayerNorm writes the other x_hat buffer, and the compiler cannot tell
+    // the buffers apart: reads issued after those writes waited for them,
+    // which left sub-tile 1's MFMAs bunched behind their reads with no vector
+    // work between them.
+    half8 zf[2][8];
+#pragma unroll
+    for (int sub = 0; sub < 2; sub++) {
       const half_t* zrow = zn + (sub * 32 + (lane & 31)) * kPitch + 8 * (lane >> 5);
 #pragma unroll
+      for (int s = 0; s < 8; s++) zf[sub][s] = *reinterpret_cast<const half8*>(zrow + 16 * s);
+    }
+    auto mfma_sub = [&](int sub) {
+#pragma unroll
       for (int s = 0; s < 8; s++) {
-        const half8 zf = *reinterpret_cast<const half8*>(zrow + 16 * s);
-        accp[sub] = mfma_f16(zf, fp[s], accp[sub]);
-        accg[sub] = mfma_f16(zf, fg[s], accg[sub]);
+        accp[sub] = mfma_f16(zf[sub][s], fp[s], accp[sub]);
+        accg[sub] = mfma_f16(zf[sub][s], fg[s], accg[sub]);
       }
     };
     auto epilogue_sub = [&](int sub) {
@@ -354,7 +364,7 @@ __global__ __launch_bounds__(kThreads, 1) void tri_project_f16_kernel(FastProjec
 #pragma unroll
     for (int i = 0; i < 32; i++) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then four VALU (five measured 3% slower)
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // then six VALU (four and nine measured 2-3% slower)
     }
     // The wave's own rows go out as soon as it has written them (LDS
     // accesses of one wave complete in order), so no barrier waits for the
