@@ -787,7 +787,9 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
 // LDS buffer: K [entry][16-byte channel granule][key]; V [entry][key][channel]
 // (64-byte rows for the transposing reads); mask codes, a 256-byte slot a
 // wave (its first 32 bytes loaded); pair bias [query][key] f32, the eight
-// 16-byte granules of row q stored at granule ^ (q mod 8).
+// 16-byte granules of row q stored at granule ^ ((q / 2) mod 8): a fragment
+// read's 16 consecutive rows then fall on 16 different granules of the LDS's
+// 256-byte bank width (with ^ (q mod 8), rows q and q + 8 collided).
 constexpr int kF2Entries = 2;
 constexpr int kF2QueryWaves = 2;
 constexpr int kF2Tiles = 2;
@@ -836,7 +838,10 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 2 : 4) void attention_flash2_ker
   const uint32_t k_off = (uint32_t)(2 * (C + 32 * h) + 16 * (2 * qi + hi));
   const uint32_t v_off = (uint32_t)(2 * (2 * C + 32 * h) + 16 * (lane & 3));
   const int v_key = 16 * qi + (lane >> 2);
-  const uint32_t b_gran = (uint32_t)(16 * ((lane & 7) ^ (lane >> 3)));
+  // Bias load n (rows 8 n + lane / 8) puts granule g of its row at slot
+  // g ^ ((row / 2) mod 8) = g ^ (4 (n mod 2) + lane / 16): the lane at slot
+  // lane % 8 fetches that granule.
+  auto b_gran = [&](int n) { return (uint32_t)(16 * ((lane & 7) ^ (4 * (n & 1) + (lane >> 4)))); };
   auto issue = [&](int j) {
     const uint32_t buf = lds0 + (uint32_t)((j % kF2Buffers) * BUF);
     const int k0 = 32 * j;
@@ -848,7 +853,7 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 2 : 4) void attention_flash2_ker
       for (int i = 0; i < 4; i++) {
         const int n = 4 * wave + i;  // bias rows 8 n .. 8 n + 7 of the workgroup's 128
         dma16(bias_rsrc, buf + kF2Bias + 1024 * n,
-              4u * ((uint32_t)(qbase + 8 * n + (lane >> 3)) * (uint32_t)a.stride + (uint32_t)k0) + b_gran);
+              4u * ((uint32_t)(qbase + 8 * n + (lane >> 3)) * (uint32_t)a.stride + (uint32_t)k0) + b_gran(n));
       }
     }
   };
@@ -968,7 +973,7 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 2 : 4) void attention_flash2_ker
         const unsigned char* brow = bp + kF2Bias + 128 * (32 * (2 * qi + t) + col);
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-          const float4 v = *reinterpret_cast<const float4*>(brow + 16 * ((2 * g + hi) ^ (col & 7)));
+          const float4 v = *reinterpret_cast<const float4*>(brow + 16 * ((2 * g + hi) ^ ((col >> 1) & 7)));
           sc[t][4 * g] = v.x, sc[t][4 * g + 1] = v.y, sc[t][4 * g + 2] = v.z, sc[t][4 * g + 3] = v.w;
         }
       }
