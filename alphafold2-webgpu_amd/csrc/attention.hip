@@ -770,13 +770,16 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
 // more independent work a wave and no staging registers:
 //  - a wave takes 64 queries of one (b, h), as two 32-query tiles against
 //    each key block, so the K and V^T fragments it reads from LDS feed two
-//    MFMAs each and the two tiles' softmax and MFMAs interleave;
+//    MFMAs each;
 //  - a workgroup is two batch entries by two such waves (128 queries of one
 //    head per entry), four waves meeting at one barrier a key block;
 //  - K, V, the pair-bias tile and the mask codes of a key block arrive by
-//    DMA (buffer_load ... lds) in a ring of three LDS buffers, two blocks
-//    ahead. A resource per batch entry ends at the entry's last row, so keys
-//    past the end load as zeros; their logits are then set to -inf.
+//    DMA (buffer_load ... lds) in two LDS buffers, one block ahead. That
+//    leaves room for three workgroups a CU with a pair bias (four without):
+//    the latency-bound block chain gains more from the third wave a SIMD
+//    than it loses to the shorter lead. A resource per batch entry ends at
+//    the entry's last row, so keys past the end load as zeros; their logits
+//    are then -inf (their mask codes).
 //  - a block's softmax first takes the probabilities at the current offset
 //    m. When the tile's clamp bounds are far from m and every lane's 16
 //    probabilities sum below 2^7 (so each is below 2^7), the exact path
@@ -795,17 +798,16 @@ constexpr int kF2QueryWaves = 2;
 constexpr int kF2Tiles = 2;
 constexpr int kF2Threads = 64 * kF2Entries * kF2QueryWaves;
 constexpr int kF2Queries = 32 * kF2Tiles * kF2QueryWaves;  // of each entry
-constexpr int kF2Buffers = 3;
+constexpr int kF2Buffers = 2;
 constexpr int kF2K = 0, kF2V = 4096, kF2Code = 8192, kF2Bias = 9216;
 constexpr int kF2BufBias = kF2Bias + kF2Queries * 128;
 constexpr int kF2BufNoBias = kF2Bias;
 constexpr float kF2FastSum = 128.0f;
 
 template <bool BIAS>
-__global__ __launch_bounds__(kF2Threads, BIAS ? 2 : 4) void attention_flash2_kernel(FlashArgs a) {
+__global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_kernel(FlashArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
   constexpr int BUF = BIAS ? kF2BufBias : kF2BufNoBias;
-  constexpr int kIssue = BIAS ? 7 : 3;  // DMA instructions a wave issues a block
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, hi = lane >> 5;
@@ -859,7 +861,6 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 2 : 4) void attention_flash2_ker
   };
   const int nblk = (Q + 31) >> 5;
   issue(0);
-  if (nblk > 1) issue(1);
 
   // This wave's queries: tile t holds qbase + 32 (2 qi + t) + col.
   const bool active = b < a.B && qbase + 64 * qi < Q;  // idle waves still load and meet every barrier
@@ -950,13 +951,12 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 2 : 4) void attention_flash2_ker
   };
 
   for (int j = 0; j < nblk; j++) {
-    // Block j has landed once at most block j + 1's loads are outstanding;
-    // the barrier publishes it and retires buffer (j + 2) % 3, whose block
-    // j - 1 every wave has finished.
-    if (j + 1 < nblk) wait_vmcnt<kIssue>();
-    else wait_vmcnt<0>();
+    // Block j is the only one in flight; once it has landed the barrier
+    // publishes it and retires buffer (j + 1) % 2, whose block j - 1 every
+    // wave has finished.
+    wait_vmcnt<0>();
     block_barrier<false>();
-    if (j + 2 < nblk) issue(j + 2);
+    if (j + 1 < nblk) issue(j + 1);
     if (!active) continue;
     const unsigned char* bp = smem + (j % kF2Buffers) * BUF;
     const bool first = j == 0;
@@ -1003,30 +1003,9 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 2 : 4) void attention_flash2_ker
       }
       return __builtin_amdgcn_ballot_w64(!(bs[t] < kF2FastSum) || margin[t] < 0.0f);
     };
-    if constexpr (BIAS) {
-      // Both tiles in one straight-line block, the V^T fragments read first
-      // so their latency overlaps the softmax (two waves a SIMD: registers
-      // allow it).
-      const half8 vf[2] = {read_v(0), read_v(1)};
-      uint64_t redo[kF2Tiles];
-#pragma unroll
-      for (int t = 0; t < kF2Tiles; t++) redo[t] = fast(t);
-      if (first || (redo[0] | redo[1])) {
-#pragma unroll
-        for (int t = 0; t < kF2Tiles; t++) {
-          if (first || redo[t]) exact(t, sc[t], first, false, 0, pf[t]);
-          else run_sum[t] += bs[t];
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < kF2Tiles; t++) run_sum[t] += bs[t];
-      }
-#pragma unroll
-      for (int s = 0; s < 2; s++)
-#pragma unroll
-        for (int t = 0; t < kF2Tiles; t++) o[t] = mfma_f16(vf[s], pf[t][s], o[t]);
-    } else {
-      // One tile at a time, V^T after: fewer registers, for four waves a SIMD.
+    {
+      // One tile at a time, V^T after: fewer live registers, for three waves a
+      // SIMD with a pair bias, four without.
 #pragma unroll
       for (int t = 0; t < kF2Tiles; t++) {
         const bool last = j + 1 == nblk;
