@@ -799,6 +799,7 @@ constexpr int kF2Tiles = 2;
 constexpr int kF2Threads = 64 * kF2Entries * kF2QueryWaves;
 constexpr int kF2Queries = 32 * kF2Tiles * kF2QueryWaves;  // of each entry
 constexpr int kF2Buffers = 2;
+constexpr int kF2HeadGroup = 4;  // heads an XCD's workgroups share (grid order)
 constexpr int kF2K = 0, kF2V = 4096, kF2Code = 8192, kF2Bias = 9216;
 constexpr int kF2BufBias = kF2Bias + kF2Queries * 128;
 constexpr int kF2BufNoBias = kF2Bias;
@@ -815,13 +816,22 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_ker
   const int Q = a.Q, C = a.C;
   const int qblocks = (Q + kF2Queries - 1) / kF2Queries;
   // Workgroups run on the XCDs in turn; renumbered so that each XCD takes a
-  // contiguous range: the workgroups of one batch pair (its query blocks and
-  // heads) then share that XCD's L2.
+  // contiguous range. Within it the order is (head group, batch pair, head,
+  // query block), four heads a group: the workgroups of one batch pair and
+  // head group run together and share that XCD's L2 (the group's heads read
+  // every byte of the 128-byte lines of K and V they touch), and those an
+  // XCD runs at once need the pair bias of four heads, not of all eight of
+  // the MSA attentions. Groups of 2 and 8 heads measured slower. (With a
+  // head count that 4 does not divide: (batch pair, head, query block).)
   const unsigned G = gridDim.x;
   const unsigned vid = (G % 8 == 0) ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
-  const int qb = (int)(vid % qblocks);
-  const int h = (int)((vid / qblocks) % a.H);
-  const int64_t b0 = (int64_t)(vid / qblocks / a.H) * kF2Entries;
+  const int hp = a.H % kF2HeadGroup == 0 ? kF2HeadGroup : a.H;
+  const unsigned per_pair = (unsigned)(hp * qblocks);
+  const unsigned pairs = (unsigned)((a.B + kF2Entries - 1) / kF2Entries);
+  const unsigned hg = vid / (pairs * per_pair), rr = vid % (pairs * per_pair);
+  const int qb = (int)(rr % qblocks);
+  const int h = (int)(hg * hp + (rr % per_pair) / qblocks);
+  const int64_t b0 = (int64_t)(rr / per_pair) * kF2Entries;
   const int qbase = qb * kF2Queries;
   const half_t* base = reinterpret_cast<const half_t*>(a.qkvg);
   const int64_t ld4 = 4 * (int64_t)C;
@@ -902,14 +912,18 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_ker
   // can matter, m moved, then the probabilities. Keys past the end come with
   // -inf logits (their mask codes), which the clamp leaves alone. (The
   // variant without a pair bias sets them again in the last block, as the
-  // kernel above does: its registers then fit four waves a SIMD.)
+  // kernel above does: its registers then fit four waves a SIMD. The
+  // threshold passes through an empty asm so that the compares stay in the
+  // last block instead of being computed ahead in every block.)
   auto exact = [&](int t, floatx16& x, bool first, bool last, int k0, half8 (&pf)[2]) {
     auto drop_past_end = [&]() {
+      int rem = Q - k0 - 4 * hi;  // element 4 g + i is key k0 + 8 g + 4 hi + i
+      asm volatile("" : "+v"(rem));
 #pragma unroll
       for (int g = 0; g < 4; g++)
 #pragma unroll
         for (int i = 0; i < 4; i++)
-          if (k0 + 8 * g + 4 * hi + i >= Q) x[4 * g + i] = -INFINITY;
+          if (8 * g + i >= rem) x[4 * g + i] = -INFINITY;
     };
     if (!BIAS && last) drop_past_end();
     float bm = x[0];
