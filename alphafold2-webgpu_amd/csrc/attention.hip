@@ -787,8 +787,12 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
 //    move m, and would compute the same probabilities: they are kept. The
 //    first block, the last and any other block run the exact path of the
 //    kernel above.
-// LDS buffer: K [entry][16-byte channel granule][key]; V [entry][key][channel]
-// (64-byte rows for the transposing reads); mask codes, a 256-byte slot a
+// LDS buffer: K [entry][key][channel], the four 16-byte granules of key r
+// stored at granule ^ ((r / 4) mod 4), so a fragment read's 16 keys fall on
+// 16 different granules of the bank width, while each DMA instruction reads
+// 16 keys' whole 64-byte pieces (32 keys' half pieces touched twice as many
+// lines); V [entry][key][channel] (64-byte rows for the transposing reads);
+// mask codes, a 256-byte slot a
 // wave (its first 32 bytes loaded); pair bias [query][key] f32, the eight
 // 16-byte granules of row q stored at granule ^ ((q / 2) mod 8): a fragment
 // read's 16 consecutive rows then fall on 16 different granules of the LDS's
@@ -847,7 +851,8 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_ker
   if (BIAS) bias_rsrc = make_rsrc(a.bias + (int64_t)h * Q * a.stride, 4u * (uint32_t)Q * (uint32_t)a.stride);
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
   // Per-lane parts of the block's DMA offsets (block k0 adds k0 rows or keys).
-  const uint32_t k_off = (uint32_t)(2 * (C + 32 * h) + 16 * (2 * qi + hi));
+  const int k_key = 16 * qi + (lane >> 2);
+  const uint32_t k_off = (uint32_t)(2 * (C + 32 * h) + 16 * ((lane & 3) ^ ((k_key >> 2) & 3)));
   const uint32_t v_off = (uint32_t)(2 * (2 * C + 32 * h) + 16 * (lane & 3));
   const int v_key = 16 * qi + (lane >> 2);
   // Bias load n (rows 8 n + lane / 8) puts granule g of its row at slot
@@ -857,7 +862,7 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_ker
   auto issue = [&](int j) {
     const uint32_t buf = lds0 + (uint32_t)((j % kF2Buffers) * BUF);
     const int k0 = 32 * j;
-    dma16(kv_rsrc, buf + kF2K + 2048 * bi + 1024 * qi, (uint32_t)(k0 + col) * row_bytes + k_off);
+    dma16(kv_rsrc, buf + kF2K + 2048 * bi + 1024 * qi, (uint32_t)(k0 + k_key) * row_bytes + k_off);
     dma16(kv_rsrc, buf + kF2V + 2048 * bi + 1024 * qi, (uint32_t)(k0 + v_key) * row_bytes + v_off);
     dma4(code_rsrc, buf + kF2Code + 256 * wave, lane < 8 ? 2u * (uint32_t)(k0 + 16 * qi + 2 * lane) : kOutOfRange);
     if (BIAS) {
@@ -974,9 +979,10 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_ker
     if (!active) continue;
     const unsigned char* bp = smem + (j % kF2Buffers) * BUF;
     const bool first = j == 0;
-    const unsigned char* kp = bp + kF2K + 2048 * bi + 16 * col;
-    const half8 kf0 = *reinterpret_cast<const half8*>(kp + 512 * hi);
-    const half8 kf1 = *reinterpret_cast<const half8*>(kp + 512 * (2 + hi));
+    const unsigned char* kp = bp + kF2K + 2048 * bi + 64 * col;
+    const int ksw = (col >> 2) & 3;
+    const half8 kf0 = *reinterpret_cast<const half8*>(kp + 16 * (hi ^ ksw));
+    const half8 kf1 = *reinterpret_cast<const half8*>(kp + 16 * ((2 + hi) ^ ksw));
     const half_t code = *reinterpret_cast<const half_t*>(bp + kF2Code + 256 * (2 * bi + (col >> 4)) + 2 * (col & 15));
     const half4 am = hi ? half4{} : half4{code, one, (half_t)0.0f, (half_t)0.0f};
     floatx16 sc[kF2Tiles];
