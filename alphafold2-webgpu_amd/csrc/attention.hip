@@ -792,8 +792,9 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
 // 16 different granules of the bank width, while each DMA instruction reads
 // 16 keys' whole 64-byte pieces (32 keys' half pieces touched twice as many
 // lines); V [entry][key][channel] (64-byte rows for the transposing reads);
-// mask codes, a 256-byte slot a
-// wave (its first 32 bytes loaded); pair bias [query][key] f32, the eight
+// mask codes, 64 bytes an entry, both entries' brought by one DMA
+// instruction of wave 0 (one resource over the pair's two code rows; a
+// missing second entry reads zeros); pair bias [query][key] f32, the eight
 // 16-byte granules of row q stored at granule ^ ((q / 2) mod 8): a fragment
 // read's 16 consecutive rows then fall on 16 different granules of the LDS's
 // 256-byte bank width (with ^ (q mod 8), rows q and q + 8 collided).
@@ -846,7 +847,8 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_ker
   const int64_t b = b0 + bi;
   const int64_t be = b < a.B ? b : a.B - 1;
   const int32x4_t kv_rsrc = make_rsrc(base + be * Q * ld4, (uint32_t)Q * row_bytes);
-  const int32x4_t code_rsrc = make_rsrc(a.key_mask + be * a.code_stride, 2u * (uint32_t)a.code_stride);
+  const int32x4_t code_rsrc =
+      make_rsrc(a.key_mask + b0 * a.code_stride, 2u * (uint32_t)a.code_stride * (uint32_t)min<int64_t>(2, a.B - b0));
   int32x4_t bias_rsrc{};
   if (BIAS) bias_rsrc = make_rsrc(a.bias + (int64_t)h * Q * a.stride, 4u * (uint32_t)Q * (uint32_t)a.stride);
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
@@ -864,7 +866,10 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_ker
     const int k0 = 32 * j;
     dma16(kv_rsrc, buf + kF2K + 2048 * bi + 1024 * qi, (uint32_t)(k0 + k_key) * row_bytes + k_off);
     dma16(kv_rsrc, buf + kF2V + 2048 * bi + 1024 * qi, (uint32_t)(k0 + v_key) * row_bytes + v_off);
-    dma4(code_rsrc, buf + kF2Code + 256 * wave, lane < 8 ? 2u * (uint32_t)(k0 + 16 * qi + 2 * lane) : kOutOfRange);
+    if (wave == 0)
+      dma4(code_rsrc, buf + kF2Code,
+           lane < 32 ? 2u * ((uint32_t)(lane >> 4) * (uint32_t)a.code_stride + (uint32_t)(k0 + 2 * (lane & 15)))
+                     : kOutOfRange);
     if (BIAS) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -983,7 +988,7 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_ker
     const int ksw = (col >> 2) & 3;
     const half8 kf0 = *reinterpret_cast<const half8*>(kp + 16 * (hi ^ ksw));
     const half8 kf1 = *reinterpret_cast<const half8*>(kp + 16 * ((2 + hi) ^ ksw));
-    const half_t code = *reinterpret_cast<const half_t*>(bp + kF2Code + 256 * (2 * bi + (col >> 4)) + 2 * (col & 15));
+    const half_t code = *reinterpret_cast<const half_t*>(bp + kF2Code + 64 * bi + 2 * col);
     const half4 am = hi ? half4{} : half4{code, one, (half_t)0.0f, (half_t)0.0f};
     floatx16 sc[kF2Tiles];
 #pragma unroll
