@@ -1033,8 +1033,12 @@ __global__ __launch_bounds__(kF2Threads, BIAS ? 3 : 4) void attention_flash2_ker
       // SIMD with a pair bias, four without.
 #pragma unroll
       for (int t = 0; t < kF2Tiles; t++) {
+        // The fast check holds in the last block too (keys past the end
+        // have -inf logits); the variant without a bias uses it there, the
+        // one with a bias keeps the exact step, which its registers favour
+        // (three waves a SIMD measured faster that way).
         const bool last = j + 1 == nblk;
-        bool slow = first || last;
+        bool slow = first || (BIAS && last);
         if (!slow) {
           slow = fast(t) != 0;
           if (!slow) run_sum[t] += bs[t];
