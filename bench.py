@@ -474,10 +474,17 @@ def measure_block(steps: int, warmup: int) -> dict:
         pair.copy_(z0)
         blk(msa, msa_mask, pair, pair_mask)
 
+    def resets():
+        msa.copy_(m0)
+        pair.copy_(z0)
+
     ms, k = timed(step, max(5, steps // 10), warmup)
+    copies_ms, _ = timed(resets, max(5, steps // 10), warmup)
     entry = {"ms": round(ms, 4), "workload": f"Evoformer block, N_seq={S}, N_res={L}, c_m={cm}, c_z={cz}, f16",
+             "copies_ms": round(copies_ms, 4), "ms_without_copies": round(ms - copies_ms, 4),
              "kernel_avg_ms": {kk: round(v, 5) for kk, v in sorted(k.items(), key=lambda kv: -kv[1])}}
     entry["note"] = ("ms includes two device copies that reset the MSA and the pair before each block; "
+                     "copies_ms times those copies alone and ms_without_copies is the difference; "
                      "kernel_avg_ms averages every launch under a label, whichever step made it")
     ex.release()
     return entry
