@@ -785,8 +785,8 @@ __global__ __launch_bounds__(kFlashThreads) void attention_flash_f16_kernel(Flas
 //    probabilities sum below 2^7 (so each is below 2^7), the exact path
 //    would neither clamp (its clamped logits underflow to 0 either way) nor
 //    move m, and would compute the same probabilities: they are kept. The
-//    first block, the last and any other block run the exact path of the
-//    kernel above.
+//    first block (and, with a pair bias, the last) and any block whose
+//    check fails run the exact path of the kernel above.
 // LDS buffer: K [entry][key][channel], the four 16-byte granules of key r
 // stored at granule ^ ((r / 4) mod 4), so a fragment read's 16 keys fall on
 // 16 different granules of the bank width, while each DMA instruction reads
