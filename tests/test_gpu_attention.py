@@ -276,6 +276,23 @@ def test_full_size_msa_row_attention_commutes_with_sequence_order(dev):
     assert torch.isfinite(a.float()).all()
 
 
+@pytest.mark.parametrize("name,S,L,C,H", [("msa_row", 11, 70, 192, 6), ("msa_column", 11, 37, 192, 6),
+                                          ("msa_row", 13, 45, 256, 8), ("msa_column", 12, 37, 256, 8)])
+def test_f16_head_groups_and_odd_batches(dev, name, S, L, C, H):
+    # The head-dimension-32 kernel orders its workgroups in groups of four
+    # heads when the head count allows (8 here) and batch pair by batch pair
+    # otherwise (6); an odd number of batch entries leaves the last
+    # workgroup's second entry empty, whose mask-code row lies past the
+    # codes (column attention: 37 batch entries).
+    x, mask, B, Q, tr, w, pb = case(name, S=S, L=L, C=C, H=H, Cp=32, seed=0xA8100)
+    x = ref.round_f16(x)
+    if pb is not None and pb["source"] == "separate":
+        pb["activations"] = ref.round_f16(pb["activations"])
+    expect = ref.attention(x, mask, w, B, Q, C, H, transpose=tr, pair_bias=pb)
+    got = run_case(dev, x, mask, B, Q, C, H, tr, w, pb, precision="f16", in_dtype="f16", out_dtype="f16")
+    assert np.abs(got - expect).max() <= 1e-2 * np.abs(expect).max()
+
+
 @pytest.mark.parametrize("name,B,Q,C,H,Cp", [("triangle_start", 384, 384, 128, 4, 0), ("msa_row", 512, 256, 256, 8, 128),
                                               ("triangle_start", 77, 77, 128, 4, 0)])
 def test_f16_residual_adds_the_rounded_output(dev, name, B, Q, C, H, Cp):
