@@ -435,7 +435,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     return;
   }
   if constexpr (sizeof(TC) == 2) {
-    if (g.flags == 0 && (g.ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(g.c) & 15) == 0 && (g.sc & 7) == 0) {
+    if (g.flags == 0 && !g.c_column_major && (g.ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(g.c) & 15) == 0 &&
+        (g.sc & 7) == 0) {
       // Plain f16 store (the contraction's case), staged through the stage
       // memory (BM x BN halves fit in it) so that every wave-level store
       // writes whole 128-byte lines. Row r keeps 16-byte chunk c at slot
@@ -486,7 +487,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     }
   }
   if constexpr (sizeof(TC) == 2) {
-    if (g.flags == EPILOGUE_OPM_CONTRACT && g.opm_outer == 32 && (reinterpret_cast<uintptr_t>(g.c) & 15) == 0) {
+    if (g.flags == EPILOGUE_OPM_CONTRACT && !g.c_column_major && g.opm_outer == 32 &&
+        (reinterpret_cast<uintptr_t>(g.c) & 15) == 0) {
       // Outer-product-mean contraction with c_outer = 32: row = i_local * 32
       // + a, col = j * 32 + b, so each 32 x 32 MFMA tile is one pair (i, j)
       // and lands as the contiguous 2 KiB block outer[i_local][j][a][b],
@@ -542,7 +544,7 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
       return;
     }
   }
-  if ((g.flags & ~gemm_detail::kRowwiseEpilogue) == 0) {
+  if ((g.flags & ~gemm_detail::kRowwiseEpilogue) == 0 && !g.c_column_major) {
     // Row-wise epilogues (plain, scale, bias, ReLU, residual, the
     // outer-product-mean output's bias / (eps + count)) straight from the
     // accumulators: lane holds row m0 + wm + 32 i + lane % 32 and, per group
@@ -631,6 +633,45 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
           float y[4] = {acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3]};
           gemm_detail::epilogue_row4<TC>(g, bt, row, col, y, min(4, g.N - col), vec4);
         }
+    }
+    return;
+  }
+  if (g.c_column_major && (g.flags & ~(AFHIP_EPILOGUE_SCALE | AFHIP_EPILOGUE_BIAS | AFHIP_EPILOGUE_RELU |
+                                       AFHIP_EPILOGUE_RESIDUAL)) == 0) {
+    // A column-major output with the row-wise epilogues, straight from the
+    // accumulators: for element v a lane holds row m0 + wm + 32 i + lane % 32
+    // of column n0 + wn + 32 j + mfma_row(v, lane), so each half-wave's 32
+    // lanes write 32 consecutive elements of one output column. The steps
+    // and roundings are epilogue_store's.
+#pragma clang fp contract(off)
+    const uint32_t flags = g.flags;
+    TC* const C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
+    const TC* const R = reinterpret_cast<const TC*>(g.residual) + (int64_t)bt * g.sc;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int row = m0 + wm + 32 * i + (lane & 31);
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+#pragma unroll 1
+        for (int g4 = 0; g4 < 4; g4++) {
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) y[e] = acc[i][j][4 * g4 + e];
+          const int col0 = n0 + wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int col = col0 + e;
+            if (row >= g.M || col >= g.N) continue;
+            float t = y[e];
+            if (flags & AFHIP_EPILOGUE_SCALE) t *= g.scale[col];
+            if (flags & AFHIP_EPILOGUE_BIAS) t += g.bias[col];
+            if (flags & AFHIP_EPILOGUE_RELU) t = fmaxf(t, 0.0f);
+            const int64_t at = (int64_t)col * g.ldc + row;
+            if (flags & AFHIP_EPILOGUE_RESIDUAL) t += (float)R[at];
+            C[at] = (TC)t;
+          }
+        }
+      }
     }
     return;
   }
@@ -726,7 +767,7 @@ bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
   auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
   if (t.precision != AFHIP_PRECISION_F16 || t.a_dtype != AFHIP_F16 || t.b_dtype != AFHIP_F16) return false;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return false;
-  if (g.a_row_contiguous || g.c_column_major) return false;
+  if (g.a_row_contiguous) return false;
   // 16-byte loads (dma_wide) or, for rows that are only 4-byte aligned,
   // 4-byte loads, which need K and the strides even.
   if (!al4(g.a) || !al4(g.b)) return false;

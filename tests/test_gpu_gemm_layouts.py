@@ -104,6 +104,73 @@ def test_row_contiguous_source_column_major_output_epilogue(dev, out_dtype):
     assert rel_max(got, expect) <= (4e-3 if out_dtype == "f32" else 1e-2)
 
 
+LDS_DMA_TILES = [(128, 128), (192, 192), (128, 256), (256, 256)]
+
+
+@pytest.mark.parametrize("out_dtype", ["f32", "f16"])
+@pytest.mark.parametrize("K,epilogue", [(104, ()), (104, ("bias", "relu", "residual")), (98, ("bias", "residual"))])
+def test_column_major_output_on_lds_dma_matches_register_kernel(dev, out_dtype, K, epilogue):
+    # A column-major output (C stored [N][M], the reference's column-major
+    # matrixEpilogue) on the LDS_DMA family: its tiles leave through each
+    # wave's LDS square with the lanes along m, applying the register-staged
+    # kernel's epilogue steps: the same bits on every tile, a batch of two with
+    # ragged M and N, and rows only 4-byte aligned at K = 98.
+    import torch
+
+    from afhip import gemm
+
+    B, M, N = 2, 333, 200
+    a = ref.round_f16(ref.normal(131, (B, M, K)))
+    w = ref.round_f16(ref.normal(132, (B, N, K), 1 / K))
+    bias = to_dev(ref.normal(133, (N,), 0.1), dev)
+    tdt = torch.float16 if out_dtype == "f16" else torch.float32
+    start = to_dev(ref.round_f16(ref.normal(134, (B, N, M))), dev).to(tdt)
+    ad, wd = to_dev(a, dev, half=True), to_dev(w, dev, half=True)
+    results = {}
+    for kernel, tiles in (("register", [(128, 128)]), ("lds_dma", LDS_DMA_TILES)):
+        for tr, tc in tiles:
+            gemm.force_variant(gemm.GemmVariant("f16", tr, tc, source="pinned", kernel=kernel))
+            try:
+                plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
+                                      out_dtype=out_dtype, epilogue=epilogue, batch=B, batch_stride_a=M * K,
+                                      batch_stride_w=N * K, batch_stride_c=N * M, c_layout="column")
+                assert plan.variant().kernel == kernel
+                out = start.clone()
+                kw = {}
+                if "bias" in epilogue:
+                    kw["bias"] = bias
+                if "residual" in epilogue:
+                    kw["residual"] = out
+                results[(kernel, tr, tc)] = plan.run(ad, wd, out=out, **kw).float().cpu().numpy()
+            finally:
+                gemm.force_variant(None)
+    base = results[("register", 128, 128)]
+    for key, got in results.items():
+        assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), key
+    expect = np.einsum("bmk,bnk->bnm", a.astype(np.float64), w.astype(np.float64))
+    if "bias" in epilogue:
+        expect = expect + ref.normal(133, (N,), 0.1)[None, :, None]
+    if "relu" in epilogue:
+        expect = np.maximum(expect, 0)
+    if "residual" in epilogue:
+        expect = expect + start.float().cpu().numpy().astype(np.float64)
+    assert rel_max(base, expect) <= (4e-3 if out_dtype == "f32" else 1e-2)
+
+
+def test_column_major_output_selects_lds_dma(dev):
+    # Without a pin, an f16 plan with a column-major output takes the tile
+    # heuristic's family (LDS_DMA here); a row-contiguous source still takes
+    # the register-staged family.
+    from afhip import gemm
+
+    plan = gemm.TiledGemm(4096, 256, 4096, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
+                          out_dtype="f16", c_layout="column")
+    assert plan.variant().kernel == "lds_dma"
+    plan = gemm.TiledGemm(4096, 256, 4096, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
+                          out_dtype="f16", a_layout="row", c_layout="column")
+    assert plan.variant().kernel == "register"
+
+
 def test_opm_contraction_as_a_plan(dev):
     # outer[i a][j b] = sum_s left[s][i a] right[s][j b]: the outer-product
     # mean's contraction with both operands accumulated over sequences, as
