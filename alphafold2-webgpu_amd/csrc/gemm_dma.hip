@@ -646,7 +646,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 #pragma clang fp contract(off)
     const uint32_t flags = g.flags;
     TC* const C = reinterpret_cast<TC*>(g.c) + (int64_t)bt * g.sc;
-    const TC* const R = reinterpret_cast<const TC*>(g.residual) + (int64_t)bt * g.sc;
+    const TC* const R =
+        (flags & AFHIP_EPILOGUE_RESIDUAL) ? reinterpret_cast<const TC*>(g.residual) + (int64_t)bt * g.sc : nullptr;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int row = m0 + wm + 32 * i + (lane & 31);
