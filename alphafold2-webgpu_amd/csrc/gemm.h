@@ -21,7 +21,7 @@ struct GemmArgs {
   int64_t lda = 0, ldb = 0, ldc = 0;
   int64_t sa = 0, sb = 0, sc = 0;
   int batch = 1;
-  bool a_row_contiguous = false;  // only the REGISTER_STAGED kernel takes it
+  bool a_row_contiguous = false;  // the REGISTER_STAGED and LDS_DMA kernels take it
   bool c_column_major = false;    // the REGISTER_STAGED and LDS_DMA kernels take it
   uint32_t flags = 0;
   int head_cols = 0;  // heads * head_dim, ATTENTION only

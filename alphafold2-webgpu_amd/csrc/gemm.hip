@@ -347,19 +347,14 @@ void pin_variant(const afhip_variant* v) {
   if (v) g_pin = *v;
 }
 
-// The variant a description runs with. A row-contiguous source is staged by
-// the REGISTER_STAGED family only, so such a plan takes that family's variant
-// whatever the selection for its shape class says. A column-major output is
-// stored by the REGISTER_STAGED and LDS_DMA families, not by STREAM: a STREAM
-// selection becomes the tile heuristic's variant.
+// The variant a description runs with. A row-contiguous source and a
+// column-major output are taken by the REGISTER_STAGED and LDS_DMA families,
+// not by STREAM: a STREAM selection becomes the tile heuristic's variant.
 afhip_variant select_plan_variant(const afhip_gemm_desc& d, const GemmTypes& kt) {
   afhip_variant v = select_variant(kt, d.rows, d.columns, d.inner, d.batch);
   const int source = v.source;
-  if (d.a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS && v.kernel != AFHIP_KERNEL_REGISTER_STAGED) {
-    v = heuristic_variant(GemmTypes{kt.precision, AFHIP_F32, AFHIP_F32, kt.c_dtype}, d.rows, d.columns, d.inner,
-                          d.batch);
-    v.source = source;
-  } else if (d.c_layout == AFHIP_OUTPUT_COLUMN_MAJOR && v.kernel == AFHIP_KERNEL_STREAM) {
+  if ((d.a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS || d.c_layout == AFHIP_OUTPUT_COLUMN_MAJOR) &&
+      v.kernel == AFHIP_KERNEL_STREAM) {
     v = tile_variant(kt, d.rows, d.columns, d.inner, d.batch);
     v.source = source;
   }

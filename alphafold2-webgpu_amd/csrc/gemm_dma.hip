@@ -59,12 +59,17 @@ constexpr int kTileGroup = 8;
 
 __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
 
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef short short8v __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
 // Epilogue families: GENERIC applies g.flags; OPM_FUSED is the outer-product
 // mean's output projection run on the finished contraction tile.
 constexpr int kEpiGeneric = 0;
 constexpr int kEpiOpmFused = 1;
 
-template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int EPI = kEpiGeneric, int LW = 16>
+template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int EPI = kEpiGeneric, int LW = 16,
+          bool AK = false>
 __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_kernel(gemm_detail::KernelArgs ka) {
   constexpr int WAVES = WM * WN;
   constexpr int kThreads = 64 * WAVES;
@@ -81,6 +86,12 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   static_assert(BM % RPL == 0, "a load instruction fills rows of one operand");
   static_assert((STAGES - 2) * LPW < 64, "vmcnt holds at most 63 outstanding loads");
   static_assert(!PIPE || STAGES >= 4, "the pipelined schedule keeps STAGES - 2 steps in flight");
+  // A k-major A ([K][M], a row-contiguous source) keeps the stage's A part as
+  // 32 k rows of BM halves: an A load instruction fills KRPL whole k rows.
+  static_assert(!AK || (LW == 16 && (BM == 128 || BM == 256) && EPI == kEpiGeneric), "k-major A tiles");
+  constexpr int AROWB = BM * 2;          // bytes of a k row of a k-major A stage
+  constexpr int KRPL = 1024 / AROWB;     // k rows an A load instruction fills
+  constexpr int CPK = BM / 8;            // 16-byte chunks of such a k row
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
 
   const GemmArgs& g = ka.g;
@@ -103,11 +114,15 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   const int wm = (wave / WN) * WTM;
   const int wn = (wave % WN) * WTN;
 
-  const half_t* A = reinterpret_cast<const half_t*>(g.a) + (int64_t)bt * g.sa + (int64_t)m0 * g.lda;
+  const half_t* A = reinterpret_cast<const half_t*>(g.a) + (int64_t)bt * g.sa + (AK ? (int64_t)m0 : (int64_t)m0 * g.lda);
   const half_t* B = reinterpret_cast<const half_t*>(g.b) + (int64_t)bt * g.sb + (int64_t)n0 * g.ldb;
   const int rows_a = min(BM, g.M - m0);
   const int rows_b = min(BN, g.N - n0);
-  const int32x4_t ra = make_rsrc(A, (uint32_t)((int64_t)rows_a * g.lda * 2));
+  // k-major: from column m0 of k row 0 to column M of k row K - 1. A k row's
+  // columns past M (whole chunks: M % 8 == 0) read the next row's first
+  // columns or zeros, which reach only output rows >= M.
+  const int32x4_t ra = AK ? make_rsrc(A, (uint32_t)(((int64_t)(g.K - 1) * g.lda + g.M - m0) * 2))
+                          : make_rsrc(A, (uint32_t)((int64_t)rows_a * g.lda * 2));
   const int32x4_t rb = make_rsrc(B, (uint32_t)((int64_t)rows_b * g.ldb * 2));
 
   // This lane's part of each of the wave's load instructions: instruction
@@ -120,6 +135,15 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 #pragma unroll
   for (int i = 0; i < LPW; i++) {
     const int q = wave + WAVES * i;
+    if (AK && RPL * q < BM) {
+      // k-major A: k row kr of the stage, 16-byte slot lane % CPK, which
+      // holds chunk (columns m / 8) slot ^ 4 (kr mod 4), so that the four k
+      // rows a transposing read spans sit in different banks.
+      const int kr = KRPL * q + lane / CPK;
+      chunk_k[i] = kr;
+      base_off[i] = (uint32_t)((int64_t)kr * g.lda * 2 + 16 * ((lane % CPK) ^ (4 * (kr & 3))));
+      continue;
+    }
     const int row = RPL * q + lane / LPR;
     const int byte = LW * (lane % LPR);
     const int chunk = (byte >> 4) ^ swizzle(row);
@@ -135,7 +159,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
       const int q = wave + WAVES * i;
-      const uint32_t off = k0 + chunk_k[i] < g.K ? base_off[i] + 2u * k0 : kOutOfRange;
+      const uint32_t step = AK && RPL * q < BM ? (uint32_t)k0 * (uint32_t)g.lda * 2u : 2u * k0;
+      const uint32_t off = k0 + chunk_k[i] < g.K ? base_off[i] + step : kOutOfRange;
       if constexpr (LW == 16) dma16(RPL * q < BM ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
       else dma4(RPL * q < BM ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
     }
@@ -194,8 +219,29 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     const int chunk = 2 * kk + (lane >> 5);
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-      const int row = wm + 32 * i + frag_row;
-      af[i] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
+      if constexpr (AK) {
+        // Two transposing reads (ds_read_b64_tr_b16: in a 16-lane group, lane
+        // x gets as element j element x % 4 of the 8 bytes lane 4 j + x / 4
+        // addressed): lane 16 g + p addresses k row 16 kk + 8 hi + 4 r + p / 4
+        // (hi = lane / 32)
+        // at columns m = wm + 32 i + 16 (g % 2) + 4 (p % 4) .., so lane l ends
+        // with k 16 kk + 8 hi + [0, 8) of row wm + 32 i + l % 32, the
+        // fragment a k-contiguous A gives.
+        const int p = lane & 15;
+        const int m = wm + 32 * i + 16 * ((lane >> 4) & 1) + 4 * (p & 3);
+        short4v part[2];
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+          const int k = 16 * kk + 8 * (lane >> 5) + 4 * r + (p >> 2);
+          part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_short4v*)(st + k * AROWB + 16 * ((m >> 3) ^ (4 * (k & 3))) + 2 * (m & 7)));
+        }
+        af[i] = __builtin_bit_cast(half8, short8v{part[0][0], part[0][1], part[0][2], part[0][3], part[1][0],
+                                                  part[1][1], part[1][2], part[1][3]});
+      } else {
+        const int row = wm + 32 * i + frag_row;
+        af[i] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
+      }
     }
 #pragma unroll
     for (int j = 0; j < TN; j++) {
@@ -702,7 +748,7 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     }
 }
 
-template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int LW = 16>
+template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int LW = 16, bool AK = false>
 int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   gemm_detail::KernelArgs ka;
   ka.g = g;
@@ -713,7 +759,7 @@ int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   ka.total_tiles = (int)total;
   ka.per_xcd = (int)ceil_div(total, 8);
   const size_t shared = (size_t)STAGES * (BM + BN) * kRowBytes;
-  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC, kEpiGeneric, LW>;
+  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC, kEpiGeneric, LW, AK>;
   if (int st = allow_lds((const void*)kernel, shared)) return st;
   return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(64 * WM * WN), shared, s, ka);
 }
@@ -747,6 +793,17 @@ bool dma_wide(const GemmArgs& g) {
 }
 
 template <typename TC> int launch_typed(const GemmArgs& g, int tm, int tn, const char* label, hipStream_t s) {
+  // A k-major A (dma_eligible: 16-byte rows) on the tiles whose k rows fill
+  // whole load instructions. 192 x 192 runs as 128 x 256 where that still
+  // gives every CU two tiles, else as 128 x 128 (8192 x 512 x 8192 on
+  // MI355X: 87.0 us against 96.2 us).
+  if (g.a_row_contiguous) {
+    const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    if (tm == 192 && ceil_div(g.M, 128) * ceil_div(g.N, 256) * g.batch >= 2 * cus) tn = 256, tm = 128;
+    if (tm == 128 && tn == 256) return launch_tile<128, 256, 3, 2, 2, false, TC, 16, true>(g, label, s);
+    if (tm == 256 && tn == 256) return launch_tile<256, 256, 5, 2, 4, true, TC, 16, true>(g, label, s);
+    return launch_tile<128, 128, 4, 2, 2, false, TC, 16, true>(g, label, s);
+  }
   // 4-byte loads take four times the instructions; the 128 x 128 tile (five
   // stages of 16 loads a wave, three in flight) keeps them within vmcnt's
   // range.
@@ -768,7 +825,10 @@ bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
   auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
   if (t.precision != AFHIP_PRECISION_F16 || t.a_dtype != AFHIP_F16 || t.b_dtype != AFHIP_F16) return false;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return false;
-  if (g.a_row_contiguous) return false;
+  // A k-major A loads whole 16-byte chunks of its k rows.
+  if (g.a_row_contiguous)
+    return dma_wide(g) && g.M % 8 == 0 && g.lda >= g.M && g.ldb >= g.K &&
+           (int64_t)g.K * g.lda * 2 < (int64_t)kOutOfRange && (int64_t)256 * g.ldb * 2 < (int64_t)kOutOfRange;
   // 16-byte loads (dma_wide) or, for rows that are only 4-byte aligned,
   // 4-byte loads, which need K and the strides even.
   if (!al4(g.a) || !al4(g.b)) return false;

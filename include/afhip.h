@@ -136,9 +136,8 @@ AFHIP_API int afhip_synchronize(void* stream);
  * (src/runtime/gemm.ts:230-339) with its WGSL fragments replaced by an
  * enumerated description. C[b][m][n] = epilogue(sum_k A[b][m][k] W[b][k][n]).
  * lda, ldw and ldc are the strides between the operands' outer index
- * (rows of A[m][k], or k of A[k][m]; and so on). A row-contiguous source runs
- * on the REGISTER_STAGED family; a column-major output on REGISTER_STAGED or
- * LDS_DMA (not STREAM). */
+ * (rows of A[m][k], or k of A[k][m]; and so on). A row-contiguous source and
+ * a column-major output run on REGISTER_STAGED or LDS_DMA (not STREAM). */
 typedef struct afhip_gemm_desc {
   int32_t rows;          /* M */
   int32_t inner;         /* K */

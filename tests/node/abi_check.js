@@ -37,16 +37,18 @@ async function main() {
   assert.deepStrictEqual(afhip.gemmGrid(100, 300, 64, 128), [5, 1]);
   assert.throws(function () { afhip.gemmGrid(0, 4); }, RangeError);
 
-  // Selection without a device: f16 operands take the LDS_DMA family; a
-  // row-contiguous source (the reference's sourceContiguous "row") the
-  // register-staged one.
+  // Selection without a device: f16 operands take the LDS_DMA family, also
+  // with a row-contiguous source (the reference's sourceContiguous "row");
+  // f32 operands the register-staged one.
   var desc = { rows: 384, inner: 384, columns: 384, batch: 128, precision: 1, aDtype: 1, wDtype: 1, wLayout: 1,
     outDtype: 1 };
   var v = afhip.gemmSelect(desc);
   assert.strictEqual(v.kernel, afhip.KERNEL.lds_dma);
   assert.strictEqual(v.tileRows, 192);
   assert.strictEqual(afhip.gemmSelect(Object.assign({ aLayout: afhip.SOURCE.row }, desc)).kernel,
-    afhip.KERNEL.register);
+    afhip.KERNEL.lds_dma);
+  assert.strictEqual(afhip.gemmSelect(Object.assign({}, desc, { aLayout: afhip.SOURCE.row, precision: 0, aDtype: 0,
+    wDtype: 0, outDtype: 0 })).kernel, afhip.KERNEL.register);
 
   // Input validation rejects the run's promise before any device work
   // (RangeError, src/triangle/types.ts:42-52, attention.ts:102-141).

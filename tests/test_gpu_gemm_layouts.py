@@ -80,7 +80,9 @@ def test_reference_layout_cases(dev, precision, tol, source, weight):
 def test_row_contiguous_source_column_major_output_epilogue(dev, out_dtype):
     # A batched plan with A stored [K][M] (ragged M whose rows are padded to
     # 136, so the 16-byte loads run and the last chunk of each k-row is
-    # guarded) and C stored [N][M], through bias, ReLU and residual.
+    # guarded) and C stored [N][M], through bias, ReLU and residual. The plan
+    # takes the tile heuristic's family; an M that is not a multiple of 8
+    # leaves LDS_DMA's whole-chunk k rows, so the run is register-staged.
     import torch
 
     from afhip import gemm
@@ -96,7 +98,7 @@ def test_row_contiguous_source_column_major_output_epilogue(dev, out_dtype):
     plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k", out_dtype=out_dtype,
                           epilogue=("bias", "relu", "residual"), batch=B, lda=lda, batch_stride_a=K * lda,
                           batch_stride_w=N * K, batch_stride_c=N * M, a_layout="row", c_layout="column")
-    assert plan.variant().kernel == "register"
+    assert plan.variant().kernel == "lds_dma"
     res = to_dev(residual, dev).to(torch.float32 if out_dtype == "f32" else torch.float16)
     out = plan.run(to_dev(a_stored, dev, half=True), to_dev(w, dev, half=True), bias=to_dev(bias, dev),
                    residual=res, out=res.clone())
@@ -157,10 +159,74 @@ def test_column_major_output_on_lds_dma_matches_register_kernel(dev, out_dtype, 
     assert rel_max(base, expect) <= (4e-3 if out_dtype == "f32" else 1e-2)
 
 
+@pytest.mark.parametrize("c_layout", ["row", "column"])
+@pytest.mark.parametrize("K,epilogue", [(104, ()), (72, ("bias", "relu", "residual")), (40, ("scale", "bias"))])
+def test_row_contiguous_source_on_lds_dma_matches_register_kernel(dev, c_layout, K, epilogue):
+    # A stored [K][M] (the outer-product mean's and the incoming triangle
+    # contraction's sequence- and k-major operands) on the LDS_DMA family,
+    # whose stages keep k rows and hand the MFMAs k-contiguous fragments
+    # through transposing LDS reads: the same bits as the register-staged
+    # kernel on every tile, in a batch of two with M and N ragged against
+    # every tile and K not a multiple of the 32-deep k-step. The rows' padding
+    # past M holds NaN, which must reach no stored output.
+    import torch
+
+    from afhip import gemm
+
+    B, M, N, lda = 2, 200, 300, 216
+    sa = K * lda + 64
+    rows = np.full((B, K, lda), np.nan, np.float32)
+    rows[:, :, :M] = ref.round_f16(ref.normal(141, (B, K, M)))
+    a_stored = np.full((B, sa), np.nan, np.float32)
+    a_stored[:, :K * lda] = rows.reshape(B, K * lda)
+    a = np.transpose(rows[:, :, :M], (0, 2, 1))
+    w = ref.round_f16(ref.normal(142, (B, N, K), 1 / K))
+    scale = ref.normal(143, (N,), 0.5)
+    bias = ref.normal(144, (N,), 0.1)
+    cshape = (B, N, M) if c_layout == "column" else (B, M, N)
+    start = to_dev(ref.round_f16(ref.normal(145, cshape)), dev)
+    ad, wd = to_dev(a_stored, dev, half=True), to_dev(w, dev, half=True)
+    results = {}
+    for kernel, tiles in (("register", [(128, 128)]), ("lds_dma", LDS_DMA_TILES)):
+        for tr, tc in tiles:
+            gemm.force_variant(gemm.GemmVariant("f16", tr, tc, source="pinned", kernel=kernel))
+            try:
+                plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
+                                      out_dtype="f32", epilogue=epilogue, batch=B, lda=lda, batch_stride_a=sa,
+                                      batch_stride_w=N * K, batch_stride_c=M * N, a_layout="row", c_layout=c_layout)
+                assert plan.variant().kernel == kernel
+                out = start.clone()
+                kw = {}
+                if "scale" in epilogue:
+                    kw["scale"] = to_dev(scale, dev)
+                if "bias" in epilogue:
+                    kw["bias"] = to_dev(bias, dev)
+                if "residual" in epilogue:
+                    kw["residual"] = out
+                results[(kernel, tr, tc)] = plan.run(ad, wd, out=out, **kw).cpu().numpy()
+            finally:
+                gemm.force_variant(None)
+    base = results[("register", 128, 128)]
+    assert np.isfinite(base).all()
+    for key, got in results.items():
+        assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), key
+    expect = np.einsum("bmk,bnk->bmn", a.astype(np.float64), w.astype(np.float64))
+    if "scale" in epilogue:
+        expect = expect * scale
+    if "bias" in epilogue:
+        expect = expect + bias
+    if "relu" in epilogue:
+        expect = np.maximum(expect, 0)
+    if c_layout == "column":
+        expect = np.transpose(expect, (0, 2, 1))
+    if "residual" in epilogue:
+        expect = expect + start.cpu().numpy().astype(np.float64)
+    assert rel_max(base, expect) <= 4e-3
+
+
 def test_column_major_output_selects_lds_dma(dev):
-    # Without a pin, an f16 plan with a column-major output takes the tile
-    # heuristic's family (LDS_DMA here); a row-contiguous source still takes
-    # the register-staged family.
+    # Without a pin, an f16 plan with a column-major output or a
+    # row-contiguous source takes the tile heuristic's family (LDS_DMA here).
     from afhip import gemm
 
     plan = gemm.TiledGemm(4096, 256, 4096, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
@@ -168,7 +234,7 @@ def test_column_major_output_selects_lds_dma(dev):
     assert plan.variant().kernel == "lds_dma"
     plan = gemm.TiledGemm(4096, 256, 4096, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
                           out_dtype="f16", a_layout="row", c_layout="column")
-    assert plan.variant().kernel == "register"
+    assert plan.variant().kernel == "lds_dma"
 
 
 def test_opm_contraction_as_a_plan(dev):
