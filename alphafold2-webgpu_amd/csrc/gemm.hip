@@ -55,7 +55,7 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
   }
   if (v.kernel == AFHIP_KERNEL_LDS_DMA) {
     if (dma_eligible(g, t) && dma_tile_supported(v.tile_rows, v.tile_columns))
-      return run_gemm_dma(g, t.c_dtype, v.tile_rows, v.tile_columns, label, stream);
+      return run_gemm_dma(g, t.a_dtype, t.c_dtype, v.tile_rows, v.tile_columns, label, stream);
     // Operands the LDS_DMA family cannot take (alignment, K % 8, dtypes) run
     // on the register-staged kernel with its heuristic tile.
     afhip_variant r = heuristic_variant(GemmTypes{t.precision, AFHIP_F32, AFHIP_F32, t.c_dtype}, g.M, g.N, g.K, g.batch);
@@ -84,10 +84,11 @@ static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int6
   v.vectorized = 1;
   v.source = 0;
   // LDS_DMA takes f16 operands with an even K (16-byte loads when K is a
-  // multiple of 8, 4-byte loads otherwise), and int8 weights that a plan
+  // multiple of 8, 4-byte loads otherwise), an f32 A with K a multiple of 8
+  // (rounded to f16 as its fragments are read), and int8 weights that a plan
   // widens to f16 first (exact); anything else is staged through registers.
-  if (t.precision == AFHIP_PRECISION_F16 && t.a_dtype == AFHIP_F16 &&
-      (t.b_dtype == AFHIP_F16 || t.b_dtype == AFHIP_I8) && K % 2 == 0) {
+  if (t.precision == AFHIP_PRECISION_F16 && ((t.a_dtype == AFHIP_F16 && K % 2 == 0) || (t.a_dtype == AFHIP_F32 && K % 8 == 0)) &&
+      (t.b_dtype == AFHIP_F16 || t.b_dtype == AFHIP_I8)) {
     v.kernel = AFHIP_KERNEL_LDS_DMA;
     dma_heuristic_tile(M, N, K, batch, &v.tile_rows, &v.tile_columns);
     return v;
@@ -305,7 +306,8 @@ afhip_variant select_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K
     // A pinned LDS_DMA or STREAM variant only applies where that family runs.
     if (v.kernel == AFHIP_KERNEL_STREAM) {
       if (stream_shape_ok(t, M, N, K, batch)) return v;
-    } else if (v.kernel != AFHIP_KERNEL_LDS_DMA || (t.a_dtype == AFHIP_F16 && t.b_dtype == AFHIP_F16)) {
+    } else if (v.kernel != AFHIP_KERNEL_LDS_DMA ||
+               ((t.a_dtype == AFHIP_F16 || t.a_dtype == AFHIP_F32) && t.b_dtype == AFHIP_F16)) {
       return v;
     }
   }

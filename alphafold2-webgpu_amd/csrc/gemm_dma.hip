@@ -39,6 +39,7 @@
 //  - The epilogue is the register-staged kernel's (gemm_kernel.h), so both
 //    families give the same epilogue arithmetic.
 #include <algorithm>
+#include <type_traits>
 
 #include "dma.h"
 #include "gemm_kernel.h"
@@ -58,10 +59,18 @@ constexpr int kRowBytes = 64;  // one row of a k-step stage
 constexpr int kTileGroup = 8;
 
 __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
+// The slot of a 128-byte f32 A row's 16-byte chunk: chunk ^ swizzle_f32(row)
+// puts the rows of 8 (and of 16) consecutive lanes on distinct banks.
+__device__ __forceinline__ int swizzle_f32(int row) { return ((row >> 1) & 7) ^ ((row & 1) << 2); }
+
+// Bytes of one k-step stage: A's part (BM rows of 32 k, 4-byte elements for
+// an f32 A) then B's (BN rows of 32 halves).
+constexpr int dma_stage_bytes(int bm, int bn, bool a_f32) { return bm * (a_f32 ? 2 * kRowBytes : kRowBytes) + bn * kRowBytes; }
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef short short8v __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) short4v lds_short4v;
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 // Epilogue families: GENERIC applies g.flags; OPM_FUSED is the outer-product
 // mean's output projection run on the finished contraction tile.
@@ -69,21 +78,26 @@ constexpr int kEpiGeneric = 0;
 constexpr int kEpiOpmFused = 1;
 
 template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int EPI = kEpiGeneric, int LW = 16,
-          bool AK = false>
+          bool AK = false, bool AF = false>
 __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_kernel(gemm_detail::KernelArgs ka) {
   constexpr int WAVES = WM * WN;
   constexpr int kThreads = 64 * WAVES;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int ROWS = BM + BN;
-  constexpr int STAGE_BYTES = ROWS * kRowBytes;
   static_assert(LW == 16 || LW == 4, "16- or 4-byte loads");
-  constexpr int RPL = LW;             // stage rows a wave-level load fills (64 lanes x LW bytes)
-  constexpr int LPR = 64 / LW;        // lanes a row
-  constexpr int LOADS = ROWS / RPL;   // wave-level load instructions per stage
-  constexpr int LPW = LOADS / WAVES;  // per wave
+  // An f32 A (f16 arithmetic) keeps 128-byte rows of 32 k in its part of a
+  // stage and is rounded to f16 as the fragments are read.
+  static_assert(!AF || (LW == 16 && !AK && EPI == kEpiGeneric), "f32 A tiles");
+  constexpr int AROW = AF ? 2 * kRowBytes : kRowBytes;  // bytes of a k-contiguous A row
+  constexpr int A_BYTES = BM * AROW;
+  constexpr int STAGE_BYTES = dma_stage_bytes(BM, BN, AF);
+  constexpr int RPL = LW;                     // stage rows of 64 bytes a wave-level load fills
+  constexpr int LPR = 64 / LW;                // lanes a row
+  constexpr int A_LOADS = A_BYTES / (64 * LW);  // wave-level load instructions per stage: A's
+  constexpr int LOADS = A_LOADS + BN / RPL;   // and all
+  constexpr int LPW = LOADS / WAVES;          // per wave
   static_assert(WTM % 32 == 0 && WTN % 32 == 0 && LOADS % WAVES == 0, "tile shape");
-  static_assert(BM % RPL == 0, "a load instruction fills rows of one operand");
+  static_assert(BM % RPL == 0 && A_BYTES % (64 * LW) == 0, "a load instruction fills rows of one operand");
   static_assert((STAGES - 2) * LPW < 64, "vmcnt holds at most 63 outstanding loads");
   static_assert(!PIPE || STAGES >= 4, "the pipelined schedule keeps STAGES - 2 steps in flight");
   // A k-major A ([K][M], a row-contiguous source) keeps the stage's A part as
@@ -114,7 +128,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   const int wm = (wave / WN) * WTM;
   const int wn = (wave % WN) * WTN;
 
-  const half_t* A = reinterpret_cast<const half_t*>(g.a) + (int64_t)bt * g.sa + (AK ? (int64_t)m0 : (int64_t)m0 * g.lda);
+  using TA = typename std::conditional<AF, float, half_t>::type;
+  const TA* A = reinterpret_cast<const TA*>(g.a) + (int64_t)bt * g.sa + (AK ? (int64_t)m0 : (int64_t)m0 * g.lda);
   const half_t* B = reinterpret_cast<const half_t*>(g.b) + (int64_t)bt * g.sb + (int64_t)n0 * g.ldb;
   const int rows_a = min(BM, g.M - m0);
   const int rows_b = min(BN, g.N - n0);
@@ -122,20 +137,30 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   // columns past M (whole chunks: M % 8 == 0) read the next row's first
   // columns or zeros, which reach only output rows >= M.
   const int32x4_t ra = AK ? make_rsrc(A, (uint32_t)(((int64_t)(g.K - 1) * g.lda + g.M - m0) * 2))
-                          : make_rsrc(A, (uint32_t)((int64_t)rows_a * g.lda * 2));
+                          : make_rsrc(A, (uint32_t)((int64_t)rows_a * g.lda * sizeof(TA)));
   const int32x4_t rb = make_rsrc(B, (uint32_t)((int64_t)rows_b * g.ldb * 2));
 
   // This lane's part of each of the wave's load instructions: instruction
-  // q = wave + WAVES i fills stage rows [RPL q, RPL q + RPL); the lane fills
-  // bytes [LW s, LW s + LW) of row RPL q + lane / LPR, s = lane % LPR, which
-  // lie in 16-byte slot LW s / 16: it loads the same bytes of global chunk
+  // q = wave + WAVES i fills stage bytes [64 LW q, 64 LW (q + 1)), A's rows
+  // for q < A_LOADS, then B's. For 64-byte rows the lane fills bytes
+  // [LW s, LW s + LW) of row RPL q + lane / LPR, s = lane % LPR, which lie in
+  // 16-byte slot LW s / 16: it loads the same bytes of global chunk
   // slot ^ swizzle(row).
   uint32_t base_off[LPW];
   int chunk_k[LPW];  // the first k the lane's bytes hold
 #pragma unroll
   for (int i = 0; i < LPW; i++) {
     const int q = wave + WAVES * i;
-    if (AK && RPL * q < BM) {
+    if (AF && q < A_LOADS) {
+      // f32 A: row 8 q + lane / 8, slot lane % 8, which holds the row's
+      // chunk (4 k) slot ^ swizzle_f32(row).
+      const int row = 8 * q + lane / 8;
+      const int chunk = (lane % 8) ^ swizzle_f32(row);
+      chunk_k[i] = 4 * chunk;
+      base_off[i] = (uint32_t)((int64_t)row * g.lda * 4 + 16 * chunk);
+      continue;
+    }
+    if (AK && q < A_LOADS) {
       // k-major A: k row kr of the stage, 16-byte slot lane % CPK, which
       // holds chunk (columns m / 8) slot ^ 4 (kr mod 4), so that the four k
       // rows a transposing read spans sit in different banks.
@@ -144,13 +169,13 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
       base_off[i] = (uint32_t)((int64_t)kr * g.lda * 2 + 16 * ((lane % CPK) ^ (4 * (kr & 3))));
       continue;
     }
-    const int row = RPL * q + lane / LPR;
+    const bool is_a = q < A_LOADS;
+    const int row = RPL * (is_a ? q : q - A_LOADS) + lane / LPR;  // of the operand's tile
     const int byte = LW * (lane % LPR);
     const int chunk = (byte >> 4) ^ swizzle(row);
     const int inner = 16 * chunk + (byte & 15);
     chunk_k[i] = inner / 2;
-    if (RPL * q < BM) base_off[i] = (uint32_t)((int64_t)row * g.lda * 2 + inner);
-    else base_off[i] = (uint32_t)((int64_t)(row - BM) * g.ldb * 2 + inner);
+    base_off[i] = (uint32_t)((int64_t)row * (is_a ? g.lda : g.ldb) * 2 + inner);
   }
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
 
@@ -159,10 +184,11 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
       const int q = wave + WAVES * i;
-      const uint32_t step = AK && RPL * q < BM ? (uint32_t)k0 * (uint32_t)g.lda * 2u : 2u * k0;
+      const bool is_a = q < A_LOADS;
+      const uint32_t step = AK && is_a ? (uint32_t)k0 * (uint32_t)g.lda * 2u : (AF && is_a ? 4u : 2u) * k0;
       const uint32_t off = k0 + chunk_k[i] < g.K ? base_off[i] + step : kOutOfRange;
-      if constexpr (LW == 16) dma16(RPL * q < BM ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
-      else dma4(RPL * q < BM ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
+      if constexpr (LW == 16) dma16(is_a ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
+      else dma4(is_a ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
     }
   };
 
@@ -238,6 +264,16 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
         }
         af[i] = __builtin_bit_cast(half8, short8v{part[0][0], part[0][1], part[0][2], part[0][3], part[1][0],
                                                   part[1][1], part[1][2], part[1][3]});
+      } else if constexpr (AF) {
+        // The lane's 8 k are f32 chunks 2 chunk and 2 chunk + 1 of its row,
+        // rounded to f16 (to nearest even, as the register-staged kernels'
+        // loaders round).
+        const int row = wm + 32 * i + frag_row;
+        const unsigned char* rp = st + row * AROW;
+        const int sw = swizzle_f32(row);
+        const f32x4v lo = *reinterpret_cast<const f32x4v*>(rp + 16 * ((2 * chunk) ^ sw));
+        const f32x4v hi = *reinterpret_cast<const f32x4v*>(rp + 16 * ((2 * chunk + 1) ^ sw));
+        af[i] = __builtin_convertvector(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), half8);
       } else {
         const int row = wm + 32 * i + frag_row;
         af[i] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
@@ -245,8 +281,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     }
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-      const int row = BM + wn + 32 * j + frag_row;
-      bf[j] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
+      const int row = wn + 32 * j + frag_row;
+      bf[j] = *reinterpret_cast<const half8*>(st + A_BYTES + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
     }
   };
   // Issued as B x A^T: the accumulator's rows are output columns, so a lane
@@ -748,7 +784,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     }
 }
 
-template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int LW = 16, bool AK = false>
+template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int LW = 16, bool AK = false,
+          bool AF = false>
 int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   gemm_detail::KernelArgs ka;
   ka.g = g;
@@ -758,8 +795,8 @@ int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   if (total > ((int64_t)1 << 30)) return set_error(AFHIP_ERR_INVALID_ARGUMENT, "GEMM has too many tiles");
   ka.total_tiles = (int)total;
   ka.per_xcd = (int)ceil_div(total, 8);
-  const size_t shared = (size_t)STAGES * (BM + BN) * kRowBytes;
-  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC, kEpiGeneric, LW, AK>;
+  const size_t shared = (size_t)STAGES * dma_stage_bytes(BM, BN, AF);
+  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC, kEpiGeneric, LW, AK, AF>;
   if (int st = allow_lds((const void*)kernel, shared)) return st;
   return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(64 * WM * WN), shared, s, ka);
 }
@@ -772,7 +809,7 @@ int launch_opm_fused(const GemmArgs& g, const char* label, hipStream_t s) {
   ka.tiles_n = (int)ceil_div(g.N, BN);
   ka.total_tiles = ka.tiles_m * ka.tiles_n;
   ka.per_xcd = (int)ceil_div(ka.total_tiles, 8);
-  const size_t shared = (size_t)STAGES * (BM + BN) * kRowBytes;
+  const size_t shared = (size_t)STAGES * dma_stage_bytes(BM, BN, false);
   auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC, kEpiOpmFused>;
   if (int st = allow_lds((const void*)kernel, shared)) return st;
   return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(64 * WM * WN), shared, s, ka);
@@ -792,7 +829,14 @@ bool dma_wide(const GemmArgs& g) {
   return al16(g.a) && al16(g.b) && g.K % 8 == 0 && g.lda % 8 == 0 && g.ldb % 8 == 0 && g.sa % 8 == 0 && g.sb % 8 == 0;
 }
 
-template <typename TC> int launch_typed(const GemmArgs& g, int tm, int tn, const char* label, hipStream_t s) {
+template <typename TC>
+int launch_typed(const GemmArgs& g, bool a_f32, int tm, int tn, const char* label, hipStream_t s) {
+  // An f32 A (dma_eligible: 16-byte rows) on 128 x 128 tiles whatever the
+  // selection: three stages of 24 KiB keep two workgroups a CU, where
+  // 128 x 256 (32 KiB stages) keeps one. Measured on MI355X, f16 out
+  // (128 x 128 / 128 x 256): 29972 x 1024 x 256 31.4 / 36.5 us,
+  // 29972 x 256 x 1024 36.5 / 40.5, 4096 x 1024 x 4096 58.0 / 63.7.
+  if (a_f32) return launch_tile<128, 128, 3, 2, 2, false, TC, 16, false, true>(g, label, s);
   // A k-major A (dma_eligible: 16-byte rows) on the tiles whose k rows fill
   // whole load instructions. 192 x 192 runs as 128 x 256 where that still
   // gives every CU two tiles, else as 128 x 128 (8192 x 512 x 8192 on
@@ -823,8 +867,16 @@ bool dma_tile_supported(int tm, int tn) {
 
 bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
   auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
-  if (t.precision != AFHIP_PRECISION_F16 || t.a_dtype != AFHIP_F16 || t.b_dtype != AFHIP_F16) return false;
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (t.precision != AFHIP_PRECISION_F16 || t.b_dtype != AFHIP_F16) return false;
+  if (t.a_dtype != AFHIP_F16 && t.a_dtype != AFHIP_F32) return false;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return false;
+  // An f32 A loads 16-byte chunks of 4 k (k-contiguous rows), B 16-byte
+  // chunks of 8: K a multiple of 8, so no chunk runs past K.
+  if (t.a_dtype == AFHIP_F32)
+    return !g.a_row_contiguous && al16(g.a) && al16(g.b) && g.K % 8 == 0 && g.lda % 4 == 0 && g.sa % 4 == 0 &&
+           g.ldb % 8 == 0 && g.sb % 8 == 0 && g.lda >= g.K && g.ldb >= g.K &&
+           (int64_t)256 * g.lda * 4 < (int64_t)kOutOfRange && (int64_t)256 * g.ldb * 2 < (int64_t)kOutOfRange;
   // A k-major A loads whole 16-byte chunks of its k rows.
   if (g.a_row_contiguous)
     return dma_wide(g) && g.M % 8 == 0 && g.lda >= g.M && g.ldb >= g.K &&
@@ -883,9 +935,10 @@ int run_opm_fused(const GemmArgs& g, int c_dtype, const char* label, hipStream_t
   return launch_opm_fused_tile<float>(g, label, s);
 }
 
-int run_gemm_dma(const GemmArgs& g, int c_dtype, int tm, int tn, const char* label, hipStream_t s) {
-  if (c_dtype == AFHIP_F16) return launch_typed<half_t>(g, tm, tn, label, s);
-  return launch_typed<float>(g, tm, tn, label, s);
+int run_gemm_dma(const GemmArgs& g, int a_dtype, int c_dtype, int tm, int tn, const char* label, hipStream_t s) {
+  const bool a_f32 = a_dtype == AFHIP_F32;
+  if (c_dtype == AFHIP_F16) return launch_typed<half_t>(g, a_f32, tm, tn, label, s);
+  return launch_typed<float>(g, a_f32, tm, tn, label, s);
 }
 
 }  // namespace afhip

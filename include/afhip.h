@@ -209,8 +209,13 @@ typedef struct afhip_variant {
  *   k-steps in flight; f16 operands (an int8 weight is widened to f16 by the
  *   plan first, exactly) with an even K: 16-byte loads when K and the leading
  *   dimensions are multiples of 8, 4-byte loads (128x128 tiles) otherwise;
- *   tiles 128x128, 192x192, 128x256 or 256x256. The counterpart of the
- *   reference's matrix kernel with deeper k-staging (src/runtime/gemm.ts:470-479).
+ *   tiles 128x128, 192x192, 128x256 or 256x256. An f32 source under f16
+ *   precision (K a multiple of 8, 16-byte aligned rows) is staged as f32 and
+ *   rounded to f16 as the MFMA fragments are read, on 128x128 tiles; a
+ *   row-contiguous source (M a multiple of 8, 16-byte aligned k rows) is
+ *   staged as k rows and read through transposing LDS loads. The
+ *   counterpart of the reference's matrix kernel with deeper k-staging
+ *   (src/runtime/gemm.ts:470-479).
  * STREAM: weight-stationary: the weight stays in registers and 64-row tiles of
  *   the activations stream past it, each byte read and written once; f16
  *   activations and output, f16 or int8 weights, K of 64, 128 or 256, columns

@@ -224,9 +224,75 @@ def test_row_contiguous_source_on_lds_dma_matches_register_kernel(dev, c_layout,
     assert rel_max(base, expect) <= 4e-3
 
 
+@pytest.mark.parametrize("c_layout", ["row", "column"])
+@pytest.mark.parametrize("K,epilogue,pad", [(104, (), 8), (64, ("bias", "relu", "residual"), 4), (40, ("scale",), 2)])
+def test_f32_source_on_lds_dma_matches_register_kernel(dev, c_layout, K, epilogue, pad):
+    # An f32 A under f16 precision (the reference's f32 activations into its
+    # f16 matrix units) on the LDS_DMA family, which stages the f32 rows and
+    # rounds them to f16 as the MFMA fragments are read: the same bits as the
+    # register-staged kernel, which rounds in its loader, on every tile, with
+    # NaN in the rows' padding past K. lda = K + 2 leaves the rows 8-byte
+    # aligned, which LDS_DMA does not take: that plan runs register-staged.
+    import torch
+
+    from afhip import gemm
+
+    B, M, N = 2, 333, 200
+    lda = K + pad
+    sa = M * lda + 4
+    rows = np.full((B, M, lda), np.nan, np.float32)
+    rows[:, :, :K] = ref.normal(151, (B, M, K))
+    a_stored = np.full((B, sa), np.nan, np.float32)
+    a_stored[:, :M * lda] = rows.reshape(B, M * lda)
+    a = rows[:, :, :K]
+    w = ref.round_f16(ref.normal(152, (B, N, K), 1 / K))
+    scale = ref.normal(153, (N,), 0.5)
+    bias = ref.normal(154, (N,), 0.1)
+    cshape = (B, N, M) if c_layout == "column" else (B, M, N)
+    start = to_dev(ref.round_f16(ref.normal(155, cshape)), dev)
+    ad, wd = to_dev(a_stored, dev), to_dev(w, dev, half=True)
+    results = {}
+    for kernel, tiles in (("register", [(128, 128)]), ("lds_dma", LDS_DMA_TILES)):
+        for tr, tc in tiles:
+            gemm.force_variant(gemm.GemmVariant("f16", tr, tc, source="pinned", kernel=kernel))
+            try:
+                plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f32", w_dtype="f16", w_layout="k",
+                                      out_dtype="f32", epilogue=epilogue, batch=B, lda=lda, batch_stride_a=sa,
+                                      batch_stride_w=N * K, batch_stride_c=M * N, c_layout=c_layout)
+                assert plan.variant().kernel == kernel
+                out = start.clone()
+                kw = {}
+                if "scale" in epilogue:
+                    kw["scale"] = to_dev(scale, dev)
+                if "bias" in epilogue:
+                    kw["bias"] = to_dev(bias, dev)
+                if "residual" in epilogue:
+                    kw["residual"] = out
+                results[(kernel, tr, tc)] = plan.run(ad, wd, out=out, **kw).cpu().numpy()
+            finally:
+                gemm.force_variant(None)
+    base = results[("register", 128, 128)]
+    assert np.isfinite(base).all()
+    for key, got in results.items():
+        assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), key
+    expect = np.einsum("bmk,bnk->bmn", ref.round_f16(a).astype(np.float64), w.astype(np.float64))
+    if "scale" in epilogue:
+        expect = expect * scale
+    if "bias" in epilogue:
+        expect = expect + bias
+    if "relu" in epilogue:
+        expect = np.maximum(expect, 0)
+    if c_layout == "column":
+        expect = np.transpose(expect, (0, 2, 1))
+    if "residual" in epilogue:
+        expect = expect + start.cpu().numpy().astype(np.float64)
+    assert rel_max(base, expect) <= 4e-3
+
+
 def test_column_major_output_selects_lds_dma(dev):
-    # Without a pin, an f16 plan with a column-major output or a
-    # row-contiguous source takes the tile heuristic's family (LDS_DMA here).
+    # Without a pin, an f16-precision plan with a column-major output, a
+    # row-contiguous source or an f32 source takes the tile heuristic's
+    # family (LDS_DMA here).
     from afhip import gemm
 
     plan = gemm.TiledGemm(4096, 256, 4096, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
@@ -234,6 +300,9 @@ def test_column_major_output_selects_lds_dma(dev):
     assert plan.variant().kernel == "lds_dma"
     plan = gemm.TiledGemm(4096, 256, 4096, precision="f16", a_dtype="f16", w_dtype="f16", w_layout="k",
                           out_dtype="f16", a_layout="row", c_layout="column")
+    assert plan.variant().kernel == "lds_dma"
+    plan = gemm.TiledGemm(4096, 256, 4096, precision="f16", a_dtype="f32", w_dtype="f16", w_layout="k",
+                          out_dtype="f16")
     assert plan.variant().kernel == "lds_dma"
 
 
