@@ -166,6 +166,12 @@ GEMM_SHAPES = [
     # trans2 with the bundle's mixed-q8 weight: int8 [N][K], per-column f32 scales
     # (tools/quantize-web-model.ts:98-119 quantises every weight of the bundle).
     ("trans2-q8", 29972, 1024, 256, "i8"),
+    # f32 activations into the f16 units (the reference's f32 storage,
+    # src/runtime/gemm.ts:308-321 sourceFormat) and the outer-product mean's
+    # sequence-major operand as a row-contiguous source [K][M]
+    # (src/evoformer/outer-product-mean.ts:376-389).
+    ("project-f32a", 29972, 256, 1024, "f16", "f32"), ("trans2-f32a", 29972, 1024, 256, "f16", "f32"),
+    ("opmcon32-rowA", 128, 512, 32000, "f16", "f16", "row"),
 ]
 GEMM_CANDIDATES = [("register", 64, 64), ("register", 64, 128), ("register", 128, 64), ("register", 128, 128),
                    ("lds_dma", 128, 128), ("lds_dma", 192, 192), ("lds_dma", 128, 256), ("lds_dma", 256, 256),
@@ -178,11 +184,13 @@ def gemm_shapes(launches: int = 20) -> dict:
     f16 GEMM (f16 operands, f32 accumulation, f16 output, weight [N][K]) on
     every shape of SHAPES, beside the variant the heuristic picks; a shape
     marked i8 has an int8 weight with per-column scales (the plan widens it
-    to f16 for LDS_DMA, inside the timed run). A candidate is timed only
-    where its family takes the operands (LDS_DMA: K even; STREAM: K of 64,
-    128 or 256 and N a multiple of 64), as the library would otherwise run it
-    on another family. ms is the average of `launches` back-to-back launches
-    between two events after three warm-up launches."""
+    to f16 for LDS_DMA, inside the timed run); one marked with an f32 source
+    or a row-contiguous ([K][M]) source says so. A candidate is timed only
+    where its family takes the operands (LDS_DMA: K even, a multiple of 8 for
+    an f32 or row-contiguous source; STREAM: an f16 k-contiguous source, K of
+    64, 128 or 256 and N a multiple of 64), as the library would otherwise
+    run it on another family. ms is the average of `launches` back-to-back
+    launches between two events after three warm-up launches."""
     import torch
 
     from afhip import device, gemm
@@ -191,8 +199,9 @@ def gemm_shapes(launches: int = 20) -> dict:
     dev = device.device()
     out = {"unit": "ms", "launches": launches, "shapes": []}
     for name, M, K, N, *kind in GEMM_SHAPES:
-        wdt = kind[0] if kind else "f16"
-        a = torch.randn(M, K, device=dev).half()
+        wdt, adt, a_layout = (list(kind) + ["f16", "f16", "k"][len(kind):])[:3]
+        a = torch.randn(*((K, M) if a_layout == "row" else (M, K)), device=dev)
+        a = a if adt == "f32" else a.half()
         if wdt == "i8":
             w = torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8)
             scale = torch.rand(N, device=dev) * 9e-3 + 1e-3
@@ -204,8 +213,9 @@ def gemm_shapes(launches: int = 20) -> dict:
         def run(pin):
             gemm.force_variant(pin)
             try:
-                plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype="f16", w_dtype=wdt, w_layout="k",
-                                      out_dtype="f16", epilogue=("scale",) if scale is not None else ())
+                plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype=adt, w_dtype=wdt, w_layout="k",
+                                      out_dtype="f16", epilogue=("scale",) if scale is not None else (),
+                                      a_layout=a_layout)
                 chosen = plan.variant()
                 for _ in range(3):
                     plan.run(a, w, scale=scale, out=c)
@@ -221,14 +231,14 @@ def gemm_shapes(launches: int = 20) -> dict:
 
         flops = 2.0 * M * K * N
         chosen, heuristic_ms = run(None)
-        entry = {"shape": name, "M": M, "K": K, "N": N, "weight": wdt,
+        entry = {"shape": name, "M": M, "K": K, "N": N, "weight": wdt, "source": adt, "source_layout": a_layout,
                  "heuristic": {"variant": chosen.name, "ms": round(heuristic_ms, 5),
                                "tflops": round(flops / heuristic_ms / 1e9, 1)},
                  "candidates": {}}
         for kernel, tr, tc in GEMM_CANDIDATES:
-            if kernel == "lds_dma" and K % 2:
+            if kernel == "lds_dma" and K % (2 if adt == "f16" and a_layout == "k" else 8):
                 continue
-            if kernel == "stream" and (K not in (64, 128, 256) or N % 64):
+            if kernel == "stream" and (K not in (64, 128, 256) or N % 64 or adt != "f16" or a_layout != "k"):
                 continue
             v = gemm.GemmVariant("f16", tr, tc, source="pinned", kernel=kernel)
             _, ms = run(v)
