@@ -49,6 +49,10 @@ async function main() {
     afhip.KERNEL.lds_dma);
   assert.strictEqual(afhip.gemmSelect(Object.assign({}, desc, { aLayout: afhip.SOURCE.row, precision: 0, aDtype: 0,
     wDtype: 0, outDtype: 0 })).kernel, afhip.KERNEL.register);
+  // An f32 source under f16 precision: LDS_DMA when K is a multiple of 8.
+  assert.strictEqual(afhip.gemmSelect(Object.assign({}, desc, { aDtype: 0 })).kernel, afhip.KERNEL.lds_dma);
+  assert.strictEqual(afhip.gemmSelect(Object.assign({}, desc, { aDtype: 0, inner: 388 })).kernel,
+    afhip.KERNEL.register);
 
   // Input validation rejects the run's promise before any device work
   // (RangeError, src/triangle/types.ts:42-52, attention.ts:102-141).
