@@ -102,9 +102,10 @@ int run_gemm_stream(const GemmArgs& args, const GemmTypes& types, const char* la
 
 // The variant plans of this shape should use (pinned, calibrated or heuristic).
 afhip_variant select_variant(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);
-// select_variant for a whole description (its layouts included), with the
-// weight dtype the kernels read.
-afhip_variant select_plan_variant(const afhip_gemm_desc& desc, const GemmTypes& kernel_types);
+// select_variant for a whole description: its layouts, strides and the
+// weight dtype the kernels read included (types as the description gives
+// them).
+afhip_variant select_plan_variant(const afhip_gemm_desc& desc, const GemmTypes& types);
 
 // W[k][n] (src) -> W[n][k] (dst), with dtype conversion.
 int pack_transpose(const void* src, int src_dtype, int rows_k, int cols_n, int64_t ld_src, void* dst,

@@ -349,17 +349,60 @@ void pin_variant(const afhip_variant* v) {
   if (v) g_pin = *v;
 }
 
-// The variant a description runs with. A row-contiguous source and a
-// column-major output are taken by the REGISTER_STAGED and LDS_DMA families,
-// not by STREAM: a STREAM selection becomes the tile heuristic's variant.
-afhip_variant select_plan_variant(const afhip_gemm_desc& d, const GemmTypes& kt) {
+// The GemmArgs a run of this description passes its kernels (run_gemm_plan),
+// with 256-byte aligned stand-ins for the operand pointers, which nothing
+// dereferences: what the description alone decides of a family's operand
+// rules. `repacked`: the weight goes through the plan's workspace ([N][K],
+// ldb = K).
+static GemmArgs desc_args(const afhip_gemm_desc& d, bool repacked) {
+  const char* const aligned = reinterpret_cast<const char*>(uintptr_t{256});
+  GemmArgs g;
+  g.a = g.b = g.residual = aligned;
+  g.c = const_cast<char*>(aligned);
+  g.M = d.rows;
+  g.N = d.columns;
+  g.K = d.inner;
+  g.batch = d.batch;
+  g.lda = d.lda ? d.lda : (d.a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS ? d.rows : d.inner);
+  g.ldb = repacked ? d.inner : (d.ldw ? d.ldw : (d.w_layout == AFHIP_WEIGHT_K_CONTIGUOUS ? d.inner : d.columns));
+  g.ldc = d.ldc ? d.ldc : (d.c_layout == AFHIP_OUTPUT_COLUMN_MAJOR ? d.rows : d.columns);
+  g.sa = d.batch_stride_a;
+  g.sb = repacked ? (d.batch_stride_w == 0 ? 0 : (int64_t)d.inner * d.columns) : d.batch_stride_w;
+  g.sc = d.batch_stride_c;
+  g.a_row_contiguous = d.a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS;
+  g.c_column_major = d.c_layout == AFHIP_OUTPUT_COLUMN_MAJOR;
+  g.flags = d.epilogue;
+  if (d.epilogue & AFHIP_EPILOGUE_ATTENTION) g.head_cols = d.heads * d.head_dim;
+  return g;
+}
+
+// The variant a description runs with: the selection for its shape class,
+// except where the description itself rules that family out (a layout, a
+// stride, K or M that STREAM or LDS_DMA does not take), where it is the
+// variant the run would fall back to. So the variant names the family that
+// runs, unless the operands' own addresses are misaligned, which only the
+// run sees (and falls back the same way).
+afhip_variant select_plan_variant(const afhip_gemm_desc& d, const GemmTypes& types) {
+  // The weight dtype the kernels read: f16 under f16 arithmetic (a
+  // column-contiguous weight is converted on its way into the workspace)
+  // unless it is int8.
+  GemmTypes kt = types;
+  if (d.precision == AFHIP_PRECISION_F16 && d.w_dtype != AFHIP_I8) kt.b_dtype = AFHIP_F16;
   afhip_variant v = select_variant(kt, d.rows, d.columns, d.inner, d.batch);
   const int source = v.source;
-  if ((d.a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS || d.c_layout == AFHIP_OUTPUT_COLUMN_MAJOR) &&
-      v.kernel == AFHIP_KERNEL_STREAM) {
+  const bool column_w = d.w_layout == AFHIP_WEIGHT_COLUMN_CONTIGUOUS;
+  if (v.kernel == AFHIP_KERNEL_STREAM && !stream_eligible(desc_args(d, column_w), kt))
     v = tile_variant(kt, d.rows, d.columns, d.inner, d.batch);
-    v.source = source;
+  if (v.kernel == AFHIP_KERNEL_LDS_DMA) {
+    // LDS_DMA reads an int8 weight widened to f16 in the workspace.
+    GemmTypes dt = kt;
+    if (dt.b_dtype == AFHIP_I8) dt.b_dtype = AFHIP_F16;
+    if (!dma_eligible(desc_args(d, column_w || d.w_dtype == AFHIP_I8), dt) ||
+        !dma_tile_supported(v.tile_rows, v.tile_columns))
+      v = heuristic_variant(GemmTypes{kt.precision, AFHIP_F32, AFHIP_F32, kt.c_dtype}, d.rows, d.columns, d.inner,
+                            d.batch);
   }
+  v.source = source;
   return v;
 }
 
@@ -446,11 +489,7 @@ int afhip_gemm_plan_create(const afhip_gemm_desc* desc, afhip_gemm_plan** out) {
   p->lda = desc->lda ? desc->lda : (desc->a_layout == AFHIP_SOURCE_ROW_CONTIGUOUS ? desc->rows : desc->inner);
   p->ldw = desc->ldw ? desc->ldw : (desc->w_layout == AFHIP_WEIGHT_K_CONTIGUOUS ? desc->inner : desc->columns);
   p->ldc = desc->ldc ? desc->ldc : (desc->c_layout == AFHIP_OUTPUT_COLUMN_MAJOR ? desc->rows : desc->columns);
-  // Selected with the weight dtype the kernels will read (a column-contiguous
-  // f32 weight is converted on its way into the workspace).
-  GemmTypes kt = p->types;
-  if (desc->precision == AFHIP_PRECISION_F16 && desc->w_dtype != AFHIP_I8) kt.b_dtype = AFHIP_F16;
-  p->variant = select_plan_variant(*desc, kt);
+  p->variant = select_plan_variant(*desc, p->types);
   *out = p;
   return AFHIP_OK;
 }

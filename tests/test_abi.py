@@ -193,6 +193,42 @@ def test_variant_selection_without_device():
     assert v.kernel == "lds_dma"
 
 
+def test_plan_variant_names_the_family_that_runs():
+    # afhip_gemm_select on a whole description (no device): where its
+    # layouts, strides, K or M rule the selected family out, the variant is
+    # the one the run falls back to, so it names the kernel family that runs.
+    import ctypes
+
+    from afhip import _lib, gemm
+
+    def select(rows, inner, columns, a_dtype=1, w_layout=_lib.WEIGHT_K_CONTIGUOUS, w_dtype=1, out_dtype=1,
+               epilogue=0, lda=0, sa=0, batch=1, a_layout=_lib.SOURCE_K_CONTIGUOUS, c_layout=_lib.OUTPUT_ROW_MAJOR):
+        desc = _lib.GemmDesc(rows, inner, columns, batch, 1, a_dtype, w_dtype, w_layout, out_dtype, epilogue, 0, 0,
+                             lda, 0, 0, sa, 0, rows * columns, a_layout, c_layout)
+        v = _lib.Variant()
+        _lib.call("afhip_gemm_select", ctypes.byref(desc), ctypes.byref(v))
+        return gemm.GemmVariant._from_c(v).kernel
+
+    row = dict(a_layout=_lib.SOURCE_ROW_CONTIGUOUS)
+    # A row-contiguous source on LDS_DMA needs whole 16-byte chunks of m.
+    assert select(4096, 256, 4096, **row) == "lds_dma"
+    assert select(4090, 256, 4096, lda=4096, **row) == "register"
+    assert select(4096, 256, 4096, lda=4100, **row) == "register"
+    # An f32 source needs 16-byte rows (lda a multiple of 4) and K % 8 == 0.
+    assert select(4096, 256, 4096, a_dtype=0) == "lds_dma"
+    assert select(4096, 256, 4096, a_dtype=0, lda=258) == "register"
+    assert select(4096, 252, 4096, a_dtype=0) == "register"
+    # An f32 [K][N] weight under f16 precision is converted into the
+    # workspace and takes the f16 families.
+    assert select(4096, 256, 4096, w_dtype=0, w_layout=_lib.WEIGHT_COLUMN_CONTIGUOUS) == "lds_dma"
+    # STREAM shapes with what STREAM does not take: a residual, a
+    # column-major output, a row-contiguous source.
+    assert select(29972, 256, 1024) == "stream"
+    assert select(29972, 256, 1024, epilogue=_lib.EPILOGUE_RESIDUAL) == "lds_dma"
+    assert select(29972, 256, 1024, c_layout=_lib.OUTPUT_COLUMN_MAJOR) == "lds_dma"
+    assert select(29976, 256, 1024, **row) == "lds_dma"
+
+
 def test_calibration_document_round_trip(tmp_path):
     from afhip import gemm
 
