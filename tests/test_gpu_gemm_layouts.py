@@ -290,6 +290,45 @@ def test_f32_source_on_lds_dma_matches_register_kernel(dev, c_layout, K, epilogu
     assert rel_max(base, expect) <= 4e-3
 
 
+@pytest.mark.parametrize("case", ["trans2-f32a", "opmcon32-rowA"])
+def test_new_lds_dma_sources_at_model_size(dev, case):
+    # The f32 source (trans2, 29,972 x 1024 x 256) and the row-contiguous
+    # source (the outer-product mean's contraction, 128 x 512 x 32,000 with A
+    # given [K][M]) at the model's sizes, where every workgroup runs its
+    # steady state: bit-identical to the register-staged kernel over the whole
+    # output, and within f16 rounding of float64 on 512 seeded rows.
+    import torch
+
+    from afhip import gemm
+
+    if case == "trans2-f32a":
+        M, K, N, a_dtype, a_layout = 29972, 1024, 256, "f32", "k"
+    else:
+        M, K, N, a_dtype, a_layout = 128, 512, 32000, "f16", "row"
+    g = torch.Generator(device="cpu").manual_seed(0xAF3001 + M)
+    a = torch.randn(K, M, generator=g) if a_layout == "row" else torch.randn(M, K, generator=g)
+    a = a if a_dtype == "f32" else a.half()
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).half()
+    ad, wd = a.to(dev), w.to(dev)
+    results = {}
+    for kernel in ("register", "lds_dma"):
+        gemm.force_variant(gemm.GemmVariant("f16", 128, 128, source="pinned", kernel=kernel))
+        try:
+            plan = gemm.TiledGemm(M, K, N, precision="f16", a_dtype=a_dtype, w_dtype="f16", w_layout="k",
+                                  out_dtype="f32", a_layout=a_layout)
+            assert plan.variant().kernel == kernel
+            results[kernel] = plan.run(ad, wd)
+            torch.cuda.synchronize()
+        finally:
+            gemm.force_variant(None)
+    assert torch.equal(results["lds_dma"].view(torch.int32), results["register"].view(torch.int32))
+    rows = np.sort(np.random.default_rng(M).choice(M, size=min(M, 512), replace=False))
+    a_mk = (a.T if a_layout == "row" else a).half().double().numpy()
+    expect = a_mk[rows] @ w.double().numpy().T
+    got = results["lds_dma"].cpu().double().numpy()[rows]
+    assert rel_max(got, expect) <= 4e-3
+
+
 def test_column_major_output_selects_lds_dma(dev):
     # Without a pin, an f16-precision plan with a column-major output, a
     # row-contiguous source or an f32 source takes the tile heuristic's
