@@ -59,13 +59,15 @@ int run_gemm(const GemmArgs& args, const GemmTypes& types, const afhip_variant& 
 
 // Heuristic kernel and tile choice for a problem of these types and size.
 afhip_variant heuristic_variant(const GemmTypes& types, int64_t M, int64_t N, int64_t K, int batch);
+// The REGISTER_STAGED variant for a shape: what takes every operand form.
+afhip_variant register_variant(int precision, int64_t M, int64_t N, int64_t K, int batch);
 
 // The LDS_DMA kernel family (gemm_dma.hip): f16 arithmetic on an f16 or f32
-// A and an f16 B (k-contiguous).
+// A and an f16 B (k-contiguous), or f32 arithmetic on f32 operands.
 bool dma_tile_supported(int tile_m, int tile_n);
 bool dma_eligible(const GemmArgs& args, const GemmTypes& types);
 void dma_heuristic_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int* tile_m, int* tile_n);
-int run_gemm_dma(const GemmArgs& args, int a_dtype, int c_dtype, int tile_m, int tile_n, const char* label,
+int run_gemm_dma(const GemmArgs& args, const GemmTypes& types, int tile_m, int tile_n, const char* label,
                  hipStream_t stream);
 
 // The outer-product mean's contraction and output projection in one launch

@@ -55,11 +55,10 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
   }
   if (v.kernel == AFHIP_KERNEL_LDS_DMA) {
     if (dma_eligible(g, t) && dma_tile_supported(v.tile_rows, v.tile_columns))
-      return run_gemm_dma(g, t.a_dtype, t.c_dtype, v.tile_rows, v.tile_columns, label, stream);
+      return run_gemm_dma(g, t, v.tile_rows, v.tile_columns, label, stream);
     // Operands the LDS_DMA family cannot take (alignment, K % 8, dtypes) run
     // on the register-staged kernel with its heuristic tile.
-    afhip_variant r = heuristic_variant(GemmTypes{t.precision, AFHIP_F32, AFHIP_F32, t.c_dtype}, g.M, g.N, g.K, g.batch);
-    return run_gemm(g, t, r, label, stream);
+    return run_gemm(g, t, register_variant(t.precision, g.M, g.N, g.K, g.batch), label, stream);
   }
   AFHIP_REQUIRE(v.kernel == AFHIP_KERNEL_REGISTER_STAGED, "unknown kernel family %d", v.kernel);
   const int va = 16 / (int)dtype_size(t.a_dtype), vb = 16 / (int)dtype_size(t.b_dtype);
@@ -76,13 +75,34 @@ int run_gemm(const GemmArgs& g, const GemmTypes& t, const afhip_variant& v, cons
   return gemm_dispatch_f32(g, t, v, vec, label, stream);
 }
 
-// The heuristic among the tiled families (LDS_DMA, REGISTER_STAGED).
-static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K, int batch) {
+// The REGISTER_STAGED family's variant, the one every operand form runs on
+// (and what a run falls back to when a faster family refuses its operands).
+// Prefer the largest tile that still gives every CU two workgroups, or one
+// when K is long enough for a tile's own k-loop to hide its latency
+// (measured on the reference's opm-contract shape, 128 x 508 x 32000:
+// 128 x 64 at 0.053 ms against 64 x 64 at 0.065 ms).
+afhip_variant register_variant(int precision, int64_t M, int64_t N, int64_t K, int batch) {
   afhip_variant v{};
-  v.precision = t.precision;
+  v.precision = precision;
   v.tile_inner = gemm_detail::kBK;
   v.vectorized = 1;
   v.source = 0;
+  v.kernel = AFHIP_KERNEL_REGISTER_STAGED;
+  const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const int64_t target = K >= 384 ? cus : 2 * cus;
+  const int shapes[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
+  for (auto& s : shapes) {
+    int64_t tiles = ceil_div(M, s[0]) * ceil_div(N, s[1]) * batch;
+    v.tile_rows = s[0];
+    v.tile_columns = s[1];
+    if (tiles >= target) return v;
+  }
+  return v;
+}
+
+// The heuristic among the tiled families (LDS_DMA, REGISTER_STAGED).
+static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K, int batch) {
+  afhip_variant v = register_variant(t.precision, M, N, K, batch);
   // LDS_DMA takes f16 operands with an even K (16-byte loads when K is a
   // multiple of 8, 4-byte loads otherwise), an f32 A with K a multiple of 8
   // (rounded to f16 as its fragments are read), and int8 weights that a plan
@@ -93,19 +113,16 @@ static afhip_variant tile_variant(const GemmTypes& t, int64_t M, int64_t N, int6
     dma_heuristic_tile(M, N, K, batch, &v.tile_rows, &v.tile_columns);
     return v;
   }
-  v.kernel = AFHIP_KERNEL_REGISTER_STAGED;
-  // Prefer the largest tile that still gives every CU two workgroups, or one
-  // when K is long enough for a tile's own k-loop to hide its latency
-  // (measured on the reference's opm-contract shape, 128 x 508 x 32000:
-  // 128 x 64 at 0.053 ms against 64 x 64 at 0.065 ms).
-  const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  const int64_t target = K >= 384 ? cus : 2 * cus;
-  const int shapes[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
-  for (auto& s : shapes) {
-    int64_t tiles = ceil_div(M, s[0]) * ceil_div(N, s[1]) * batch;
-    v.tile_rows = s[0];
-    v.tile_columns = s[1];
-    if (tiles >= target) return v;
+  // f32 arithmetic with K a multiple of 4 takes LDS_DMA too, which runs it
+  // on 64 x 64 tiles whatever the variant's tile (its nominal 128 x 128).
+  // Measured on MI355X against the register-staged kernel's best tile (f32
+  // out, bias + ReLU): 4096 x 128 x 512 10.6 / 12.5 us, 1024^3 26.3 / 32.9,
+  // 128 x 384^3 142 / 158, 4096 x 1024 x 4096 317 / 331, 65536 x 128 x 512
+  // 111 / 109.
+  if (t.precision == AFHIP_PRECISION_F32 && t.a_dtype == AFHIP_F32 && t.b_dtype == AFHIP_F32 && K % 4 == 0) {
+    v.kernel = AFHIP_KERNEL_LDS_DMA;
+    v.tile_rows = v.tile_columns = 128;
+    return v;
   }
   return v;
 }
@@ -307,7 +324,8 @@ afhip_variant select_variant(const GemmTypes& t, int64_t M, int64_t N, int64_t K
     if (v.kernel == AFHIP_KERNEL_STREAM) {
       if (stream_shape_ok(t, M, N, K, batch)) return v;
     } else if (v.kernel != AFHIP_KERNEL_LDS_DMA ||
-               ((t.a_dtype == AFHIP_F16 || t.a_dtype == AFHIP_F32) && t.b_dtype == AFHIP_F16)) {
+               ((t.a_dtype == AFHIP_F16 || t.a_dtype == AFHIP_F32) && t.b_dtype == AFHIP_F16) ||
+               (t.precision == AFHIP_PRECISION_F32 && t.a_dtype == AFHIP_F32 && t.b_dtype == AFHIP_F32)) {
       return v;
     }
   }
@@ -335,8 +353,7 @@ void replace_calibrated(const std::map<std::string, afhip_variant>& m) {
 
 bool valid_variant(const afhip_variant& v) {
   if (v.tile_inner != gemm_detail::kBK || !valid_precision(v.precision)) return false;
-  if (v.kernel == AFHIP_KERNEL_LDS_DMA)
-    return v.precision == AFHIP_PRECISION_F16 && dma_tile_supported(v.tile_rows, v.tile_columns);
+  if (v.kernel == AFHIP_KERNEL_LDS_DMA) return dma_tile_supported(v.tile_rows, v.tile_columns);
   if (v.kernel == AFHIP_KERNEL_STREAM)
     return v.precision == AFHIP_PRECISION_F16 && v.tile_rows == 64 && v.tile_columns == 512;
   return v.kernel == AFHIP_KERNEL_REGISTER_STAGED && (v.tile_rows == 64 || v.tile_rows == 128) &&
@@ -399,8 +416,7 @@ afhip_variant select_plan_variant(const afhip_gemm_desc& d, const GemmTypes& typ
     if (dt.b_dtype == AFHIP_I8) dt.b_dtype = AFHIP_F16;
     if (!dma_eligible(desc_args(d, column_w || d.w_dtype == AFHIP_I8), dt) ||
         !dma_tile_supported(v.tile_rows, v.tile_columns))
-      v = heuristic_variant(GemmTypes{kt.precision, AFHIP_F32, AFHIP_F32, kt.c_dtype}, d.rows, d.columns, d.inner,
-                            d.batch);
+      v = register_variant(kt.precision, d.rows, d.columns, d.inner, d.batch);
   }
   v.source = source;
   return v;

@@ -64,13 +64,16 @@ __device__ __forceinline__ int swizzle(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int swizzle_f32(int row) { return ((row >> 1) & 7) ^ ((row & 1) << 2); }
 
 // Bytes of one k-step stage: A's part (BM rows of 32 k, 4-byte elements for
-// an f32 A) then B's (BN rows of 32 halves).
-constexpr int dma_stage_bytes(int bm, int bn, bool a_f32) { return bm * (a_f32 ? 2 * kRowBytes : kRowBytes) + bn * kRowBytes; }
+// an f32 A) then B's (BN rows of 32 k, likewise).
+constexpr int dma_stage_bytes(int bm, int bn, bool a_f32, bool b_f32 = false) {
+  return bm * (a_f32 ? 2 * kRowBytes : kRowBytes) + bn * (b_f32 ? 2 * kRowBytes : kRowBytes);
+}
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef short short8v __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) short4v lds_short4v;
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef float f32x8v __attribute__((ext_vector_type(8)));
 
 // Epilogue families: GENERIC applies g.flags; OPM_FUSED is the outer-product
 // mean's output projection run on the finished contraction tile.
@@ -78,7 +81,7 @@ constexpr int kEpiGeneric = 0;
 constexpr int kEpiOpmFused = 1;
 
 template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int EPI = kEpiGeneric, int LW = 16,
-          bool AK = false, bool AF = false>
+          bool AK = false, bool AF = false, bool FP32 = false>
 __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_kernel(gemm_detail::KernelArgs ka) {
   constexpr int WAVES = WM * WN;
   constexpr int kThreads = 64 * WAVES;
@@ -87,14 +90,19 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   static_assert(LW == 16 || LW == 4, "16- or 4-byte loads");
   // An f32 A (f16 arithmetic) keeps 128-byte rows of 32 k in its part of a
   // stage and is rounded to f16 as the fragments are read.
+  // f32 arithmetic (FP32): A and B both f32 in 128-byte rows, on the f32
+  // MFMA (32 x 32 x 2), with the register-staged kernel's k pairing.
   static_assert(!AF || (LW == 16 && !AK && EPI == kEpiGeneric), "f32 A tiles");
-  constexpr int AROW = AF ? 2 * kRowBytes : kRowBytes;  // bytes of a k-contiguous A row
+  static_assert(!FP32 || (LW == 16 && !AK && !AF && EPI == kEpiGeneric), "f32 tiles");
+  constexpr bool A4 = AF || FP32;  // A rows of 4-byte elements
+  constexpr int AROW = A4 ? 2 * kRowBytes : kRowBytes;    // bytes of a k-contiguous A row
+  constexpr int BROW = FP32 ? 2 * kRowBytes : kRowBytes;  // and of a B row
   constexpr int A_BYTES = BM * AROW;
-  constexpr int STAGE_BYTES = dma_stage_bytes(BM, BN, AF);
+  constexpr int STAGE_BYTES = dma_stage_bytes(BM, BN, A4, FP32);
   constexpr int RPL = LW;                     // stage rows of 64 bytes a wave-level load fills
   constexpr int LPR = 64 / LW;                // lanes a row
   constexpr int A_LOADS = A_BYTES / (64 * LW);  // wave-level load instructions per stage: A's
-  constexpr int LOADS = A_LOADS + BN / RPL;   // and all
+  constexpr int LOADS = (STAGE_BYTES) / (64 * LW);  // and all
   constexpr int LPW = LOADS / WAVES;          // per wave
   static_assert(WTM % 32 == 0 && WTN % 32 == 0 && LOADS % WAVES == 0, "tile shape");
   static_assert(BM % RPL == 0 && A_BYTES % (64 * LW) == 0, "a load instruction fills rows of one operand");
@@ -128,9 +136,12 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   const int wm = (wave / WN) * WTM;
   const int wn = (wave % WN) * WTN;
 
-  using TA = typename std::conditional<AF, float, half_t>::type;
+  using TA = typename std::conditional<A4, float, half_t>::type;
+  using TB = typename std::conditional<FP32, float, half_t>::type;
+  // A lane's MFMA operand for one 32-row block and half-step: 8 k.
+  using Frag = typename std::conditional<FP32, f32x8v, half8>::type;
   const TA* A = reinterpret_cast<const TA*>(g.a) + (int64_t)bt * g.sa + (AK ? (int64_t)m0 : (int64_t)m0 * g.lda);
-  const half_t* B = reinterpret_cast<const half_t*>(g.b) + (int64_t)bt * g.sb + (int64_t)n0 * g.ldb;
+  const TB* B = reinterpret_cast<const TB*>(g.b) + (int64_t)bt * g.sb + (int64_t)n0 * g.ldb;
   const int rows_a = min(BM, g.M - m0);
   const int rows_b = min(BN, g.N - n0);
   // k-major: from column m0 of k row 0 to column M of k row K - 1. A k row's
@@ -138,7 +149,7 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
   // columns or zeros, which reach only output rows >= M.
   const int32x4_t ra = AK ? make_rsrc(A, (uint32_t)(((int64_t)(g.K - 1) * g.lda + g.M - m0) * 2))
                           : make_rsrc(A, (uint32_t)((int64_t)rows_a * g.lda * sizeof(TA)));
-  const int32x4_t rb = make_rsrc(B, (uint32_t)((int64_t)rows_b * g.ldb * 2));
+  const int32x4_t rb = make_rsrc(B, (uint32_t)((int64_t)rows_b * g.ldb * sizeof(TB)));
 
   // This lane's part of each of the wave's load instructions: instruction
   // q = wave + WAVES i fills stage bytes [64 LW q, 64 LW (q + 1)), A's rows
@@ -151,13 +162,15 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 #pragma unroll
   for (int i = 0; i < LPW; i++) {
     const int q = wave + WAVES * i;
-    if (AF && q < A_LOADS) {
-      // f32 A: row 8 q + lane / 8, slot lane % 8, which holds the row's
-      // chunk (4 k) slot ^ swizzle_f32(row).
-      const int row = 8 * q + lane / 8;
+    if ((A4 && q < A_LOADS) || (FP32 && q >= A_LOADS)) {
+      // 128-byte f32 rows: row 8 q' + lane / 8 of the operand (q' = q, or
+      // q - A_LOADS for B), slot lane % 8, which holds the row's chunk (4 k)
+      // slot ^ swizzle_f32(row).
+      const bool is_a = q < A_LOADS;
+      const int row = 8 * (is_a ? q : q - A_LOADS) + lane / 8;
       const int chunk = (lane % 8) ^ swizzle_f32(row);
       chunk_k[i] = 4 * chunk;
-      base_off[i] = (uint32_t)((int64_t)row * g.lda * 4 + 16 * chunk);
+      base_off[i] = (uint32_t)((int64_t)row * (is_a ? g.lda : g.ldb) * 4 + 16 * chunk);
       continue;
     }
     if (AK && q < A_LOADS) {
@@ -185,7 +198,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     for (int i = 0; i < LPW; i++) {
       const int q = wave + WAVES * i;
       const bool is_a = q < A_LOADS;
-      const uint32_t step = AK && is_a ? (uint32_t)k0 * (uint32_t)g.lda * 2u : (AF && is_a ? 4u : 2u) * k0;
+      const uint32_t step = AK && is_a ? (uint32_t)k0 * (uint32_t)g.lda * 2u
+                                       : ((A4 && is_a) || (FP32 && !is_a) ? 4u : 2u) * k0;
       const uint32_t off = k0 + chunk_k[i] < g.K ? base_off[i] + step : kOutOfRange;
       if constexpr (LW == 16) dma16(is_a ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
       else dma4(is_a ? ra : rb, lds0 + stage * STAGE_BYTES + q * 64 * LW, off);
@@ -241,7 +255,7 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 
   const int frag_row = lane & 31;
   // Fragments of half kk (16 halves of k) of a stage: chunk 2 kk + lane / 32.
-  auto read_frags = [&](const unsigned char* st, int kk, half8* af, half8* bf) {
+  auto read_frags = [&](const unsigned char* st, int kk, Frag* af, Frag* bf) {
     const int chunk = 2 * kk + (lane >> 5);
 #pragma unroll
     for (int i = 0; i < TM; i++) {
@@ -264,16 +278,17 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
         }
         af[i] = __builtin_bit_cast(half8, short8v{part[0][0], part[0][1], part[0][2], part[0][3], part[1][0],
                                                   part[1][1], part[1][2], part[1][3]});
-      } else if constexpr (AF) {
-        // The lane's 8 k are f32 chunks 2 chunk and 2 chunk + 1 of its row,
-        // rounded to f16 (to nearest even, as the register-staged kernels'
-        // loaders round).
+      } else if constexpr (A4) {
+        // The lane's 8 k are f32 chunks 2 chunk and 2 chunk + 1 of its row;
+        // under f16 arithmetic rounded to f16 (to nearest even, as the
+        // register-staged kernels' loaders round).
         const int row = wm + 32 * i + frag_row;
         const unsigned char* rp = st + row * AROW;
         const int sw = swizzle_f32(row);
         const f32x4v lo = *reinterpret_cast<const f32x4v*>(rp + 16 * ((2 * chunk) ^ sw));
         const f32x4v hi = *reinterpret_cast<const f32x4v*>(rp + 16 * ((2 * chunk + 1) ^ sw));
-        af[i] = __builtin_convertvector(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), half8);
+        if constexpr (FP32) af[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        else af[i] = __builtin_convertvector(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), half8);
       } else {
         const int row = wm + 32 * i + frag_row;
         af[i] = *reinterpret_cast<const half8*>(st + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
@@ -282,17 +297,35 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       const int row = wn + 32 * j + frag_row;
-      bf[j] = *reinterpret_cast<const half8*>(st + A_BYTES + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
+      if constexpr (FP32) {
+        const unsigned char* rp = st + A_BYTES + row * BROW;
+        const int sw = swizzle_f32(row);
+        const f32x4v lo = *reinterpret_cast<const f32x4v*>(rp + 16 * ((2 * chunk) ^ sw));
+        const f32x4v hi = *reinterpret_cast<const f32x4v*>(rp + 16 * ((2 * chunk + 1) ^ sw));
+        bf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      } else {
+        bf[j] = *reinterpret_cast<const half8*>(st + A_BYTES + row * kRowBytes + ((chunk ^ swizzle(row)) << 4));
+      }
     }
   };
   // Issued as B x A^T: the accumulator's rows are output columns, so a lane
   // ends with four consecutive columns of one output row per group (the same
   // products summed in the same k order as A x B^T).
-  auto mfmas = [&](const half8* af, const half8* bf) {
+  auto mfmas = [&](const Frag* af, const Frag* bf) {
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int j = 0; j < TN; j++) acc[i][j] = mfma_f16(bf[j], af[i], acc[i][j]);
+      for (int j = 0; j < TN; j++) {
+        if constexpr (FP32) {
+          // The f32 MFMA takes k = 16 kk + e from lanes 0-31 and + 8 from
+          // lanes 32-63, e = 0 .. 7 in order: the register-staged kernel's
+          // pairs and order.
+#pragma unroll
+          for (int e = 0; e < 8; e++) acc[i][j] = mfma_f32(bf[j][e], af[i][e], acc[i][j]);
+        } else {
+          acc[i][j] = mfma_f16(bf[j], af[i], acc[i][j]);
+        }
+      }
   };
   if constexpr (PIPE) {
     // The rest of the prologue: stages nk .. STAGES - 2 are issued too (their
@@ -307,7 +340,7 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     // Stage 0 has landed once at most stages 1 .. STAGES - 2 are pending.
     wait_vmcnt<(STAGES - 2) * LPW>();
     block_barrier<false>();
-    half8 a0[TM], b0[TN], a1[TM], b1[TN];
+    Frag a0[TM], b0[TN], a1[TM], b1[TN];
     read_frags(smem, 0, a0, b0);
     // sched_barrier(0) keeps the compiler from moving instructions across
     // the phase boundaries: left free, it reuses one set of fragment
@@ -344,7 +377,7 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
     const unsigned char* st = smem + (ks % STAGES) * STAGE_BYTES;
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) {
-      half8 af[TM], bf[TN];
+      Frag af[TM], bf[TN];
       read_frags(st, kk, af, bf);
       mfmas(af, bf);
     }
@@ -785,7 +818,7 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN == 4 ? 2 : 1) void gemm_dma_k
 }
 
 template <int BM, int BN, int STAGES, int WM, int WN, bool PIPE, typename TC, int LW = 16, bool AK = false,
-          bool AF = false>
+          bool AF = false, bool FP32 = false>
 int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   gemm_detail::KernelArgs ka;
   ka.g = g;
@@ -795,8 +828,8 @@ int launch_tile(const GemmArgs& g, const char* label, hipStream_t s) {
   if (total > ((int64_t)1 << 30)) return set_error(AFHIP_ERR_INVALID_ARGUMENT, "GEMM has too many tiles");
   ka.total_tiles = (int)total;
   ka.per_xcd = (int)ceil_div(total, 8);
-  const size_t shared = (size_t)STAGES * dma_stage_bytes(BM, BN, AF);
-  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC, kEpiGeneric, LW, AK, AF>;
+  const size_t shared = (size_t)STAGES * dma_stage_bytes(BM, BN, AF || FP32, FP32);
+  auto kernel = gemm_dma_kernel<BM, BN, STAGES, WM, WN, PIPE, TC, kEpiGeneric, LW, AK, AF, FP32>;
   if (int st = allow_lds((const void*)kernel, shared)) return st;
   return launch(label, kernel, dim3((unsigned)(ka.per_xcd * 8)), dim3(64 * WM * WN), shared, s, ka);
 }
@@ -830,7 +863,14 @@ bool dma_wide(const GemmArgs& g) {
 }
 
 template <typename TC>
-int launch_typed(const GemmArgs& g, bool a_f32, int tm, int tn, const char* label, hipStream_t s) {
+int launch_typed(const GemmArgs& g, const GemmTypes& t, int tm, int tn, const char* label, hipStream_t s) {
+  // f32 arithmetic (dma_eligible: f32 operands in 16-byte rows) on 64 x 64
+  // tiles whatever the selection: four 16 KiB stages, three in flight, two
+  // workgroups a CU; the f32 MFMA's rate makes the small tile's operand
+  // traffic no limit.
+  if (t.precision == AFHIP_PRECISION_F32)
+    return launch_tile<64, 64, 4, 2, 2, false, TC, 16, false, false, true>(g, label, s);
+  const bool a_f32 = t.a_dtype == AFHIP_F32;
   // An f32 A (dma_eligible: 16-byte rows) on 128 x 128 tiles whatever the
   // selection: three stages of 24 KiB keep two workgroups a CU, where
   // 128 x 256 (32 KiB stages) keeps one. Measured on MI355X, f16 out
@@ -868,9 +908,15 @@ bool dma_tile_supported(int tm, int tn) {
 bool dma_eligible(const GemmArgs& g, const GemmTypes& t) {
   auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return false;
+  // f32 arithmetic: f32 operands, both k-contiguous, in 16-byte chunks of
+  // 4 k (K a multiple of 4, so no chunk runs past K).
+  if (t.precision == AFHIP_PRECISION_F32)
+    return t.a_dtype == AFHIP_F32 && t.b_dtype == AFHIP_F32 && !g.a_row_contiguous && al16(g.a) && al16(g.b) &&
+           g.K % 4 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && g.sa % 4 == 0 && g.sb % 4 == 0 && g.lda >= g.K &&
+           g.ldb >= g.K && (int64_t)256 * std::max(g.lda, g.ldb) * 4 < (int64_t)kOutOfRange;
   if (t.precision != AFHIP_PRECISION_F16 || t.b_dtype != AFHIP_F16) return false;
   if (t.a_dtype != AFHIP_F16 && t.a_dtype != AFHIP_F32) return false;
-  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) return false;
   // An f32 A loads 16-byte chunks of 4 k (k-contiguous rows), B 16-byte
   // chunks of 8: K a multiple of 8, so no chunk runs past K.
   if (t.a_dtype == AFHIP_F32)
@@ -935,10 +981,9 @@ int run_opm_fused(const GemmArgs& g, int c_dtype, const char* label, hipStream_t
   return launch_opm_fused_tile<float>(g, label, s);
 }
 
-int run_gemm_dma(const GemmArgs& g, int a_dtype, int c_dtype, int tm, int tn, const char* label, hipStream_t s) {
-  const bool a_f32 = a_dtype == AFHIP_F32;
-  if (c_dtype == AFHIP_F16) return launch_typed<half_t>(g, a_f32, tm, tn, label, s);
-  return launch_typed<float>(g, a_f32, tm, tn, label, s);
+int run_gemm_dma(const GemmArgs& g, const GemmTypes& t, int tm, int tn, const char* label, hipStream_t s) {
+  if (t.c_dtype == AFHIP_F16) return launch_typed<half_t>(g, t, tm, tn, label, s);
+  return launch_typed<float>(g, t, tm, tn, label, s);
 }
 
 }  // namespace afhip

@@ -332,8 +332,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(KernelArgs ka) {
     } else {
 #pragma unroll
       for (int kk = 0; kk < kBK / 2; kk++) {
+        // MFMA kk of a step takes k = 16 (kk / 8) + kk % 8 from lanes 0-31
+        // and that + 8 from lanes 32-63, so each lane's 8 consecutive k of a
+        // half-step are one contiguous run, the order the LDS_DMA kernel's f32
+        // stages read them in (the two families give the same bits).
         float af[TM], bf[TN];
-        const int koff = kk * 2 + (lane >> 5);
+        const int koff = 16 * (kk >> 3) + 8 * (lane >> 5) + (kk & 7);
 #pragma unroll
         for (int i = 0; i < TM; i++) af[i] = as[(wm + 32 * i + (lane & 31)) * pitch + koff];
 #pragma unroll

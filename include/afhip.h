@@ -213,9 +213,11 @@ typedef struct afhip_variant {
  *   precision (K a multiple of 8, 16-byte aligned rows) is staged as f32 and
  *   rounded to f16 as the MFMA fragments are read, on 128x128 tiles; a
  *   row-contiguous source (M a multiple of 8, 16-byte aligned k rows) is
- *   staged as k rows and read through transposing LDS loads. The
- *   counterpart of the reference's matrix kernel with deeper k-staging
- *   (src/runtime/gemm.ts:470-479).
+ *   staged as k rows and read through transposing LDS loads. f32 precision
+ *   (f32 operands, K a multiple of 4, 16-byte aligned rows) runs the f32
+ *   MFMA on 64x64 tiles whatever the variant's tile, with the
+ *   REGISTER_STAGED kernel's bits. The counterpart of the reference's
+ *   matrix kernel with deeper k-staging (src/runtime/gemm.ts:470-479).
  * STREAM: weight-stationary: the weight stays in registers and 64-row tiles of
  *   the activations stream past it, each byte read and written once; f16
  *   activations and output, f16 or int8 weights, K of 64, 128 or 256, columns

@@ -227,6 +227,20 @@ def test_plan_variant_names_the_family_that_runs():
     assert select(29972, 256, 1024, epilogue=_lib.EPILOGUE_RESIDUAL) == "lds_dma"
     assert select(29972, 256, 1024, c_layout=_lib.OUTPUT_COLUMN_MAJOR) == "lds_dma"
     assert select(29976, 256, 1024, **row) == "lds_dma"
+    # f32 arithmetic (precision 0): LDS_DMA for k-contiguous f32 operands
+    # with K and lda multiples of 4; otherwise register-staged (and the
+    # variant a refused LDS_DMA selection falls back to is register-staged).
+    def select32(rows, inner, columns, **kw):
+        desc = _lib.GemmDesc(rows, inner, columns, 1, 0, 0, 0, _lib.WEIGHT_K_CONTIGUOUS, 0, 0, 0, 0,
+                             kw.get("lda", 0), 0, 0, 0, 0, rows * columns, kw.get("a_layout", 0), 0)
+        v = _lib.Variant()
+        _lib.call("afhip_gemm_select", ctypes.byref(desc), ctypes.byref(v))
+        return gemm.GemmVariant._from_c(v).kernel
+
+    assert select32(4096, 128, 512) == "lds_dma"
+    assert select32(4096, 98, 512) == "register"
+    assert select32(4096, 128, 512, lda=130) == "register"
+    assert select32(4096, 128, 512, a_layout=_lib.SOURCE_ROW_CONTIGUOUS) == "register"
 
 
 def test_calibration_document_round_trip(tmp_path):

@@ -290,6 +290,80 @@ def test_f32_source_on_lds_dma_matches_register_kernel(dev, c_layout, K, epilogu
     assert rel_max(base, expect) <= 4e-3
 
 
+@pytest.mark.parametrize("shape", [(2, 333, 200, 104, 0), (1, 4096, 512, 128, 0), (3, 130, 70, 36, 44),
+                                   (1, 200, 96, 98, 0)])
+@pytest.mark.parametrize("epilogue", [(), ("bias", "relu"), ("bias", "residual")])
+def test_f32_precision_on_lds_dma_matches_register_kernel(dev, shape, epilogue):
+    # f32 arithmetic on the LDS_DMA family (f32 operands staged as 128-byte
+    # rows, the f32 MFMA with the register-staged kernel's k pairs and order):
+    # the register-staged kernel's bits, ragged M, N and K tails, padded rows
+    # holding NaN past K, and config 1's shape (4096 x 128 x 512). K = 98 is
+    # not a multiple of 4: that plan names, and runs, the register-staged
+    # kernel even with LDS_DMA pinned; so does a run whose source is only
+    # 4-byte aligned. Against float64 within config 1's 1e-5.
+    import torch
+
+    from afhip import gemm
+
+    B, M, N, K, lda = shape
+    lda = lda or K
+    rows = np.full((B, M, lda), np.nan, np.float32)
+    rows[:, :, :K] = ref.normal(161 + M, (B, M, K))
+    w = ref.normal(162 + N, (B, N, K), 1 / K)
+    bias = ref.normal(163, (N,), 0.02)
+    start = to_dev(ref.normal(164, (B, M, N)), dev)
+    ad, wd = to_dev(rows, dev), to_dev(w, dev)
+    eligible = K % 4 == 0 and lda % 4 == 0
+    results = {}
+    for kernel, tiles in (("register", [(64, 64), (128, 128)]), ("lds_dma", [(128, 128), (256, 256)])):
+        for tr, tc in tiles:
+            gemm.force_variant(gemm.GemmVariant("f32", tr, tc, source="pinned", kernel=kernel))
+            try:
+                plan = gemm.TiledGemm(M, K, N, precision="f32", a_dtype="f32", w_dtype="f32", w_layout="k",
+                                      out_dtype="f32", epilogue=epilogue, batch=B, lda=lda,
+                                      batch_stride_a=M * lda, batch_stride_w=N * K, batch_stride_c=M * N)
+                assert plan.variant().kernel == (kernel if eligible else "register")
+                out = start.clone()
+                kw = {}
+                if "bias" in epilogue:
+                    kw["bias"] = to_dev(bias, dev)
+                if "residual" in epilogue:
+                    kw["residual"] = out
+                results[(kernel, tr, tc)] = plan.run(ad, wd, out=out, **kw).cpu().numpy()
+            finally:
+                gemm.force_variant(None)
+    # A source only 4-byte aligned (one float into its buffer): the LDS_DMA
+    # plan refuses it at run time and runs the register-staged kernel.
+    shifted = torch.empty(ad.numel() + 1, dtype=torch.float32, device=dev)
+    shifted[1:] = ad.reshape(-1)
+    gemm.force_variant(gemm.GemmVariant("f32", 128, 128, source="pinned", kernel="lds_dma"))
+    try:
+        plan = gemm.TiledGemm(M, K, N, precision="f32", a_dtype="f32", w_dtype="f32", w_layout="k",
+                              out_dtype="f32", epilogue=epilogue, batch=B, lda=lda,
+                              batch_stride_a=M * lda, batch_stride_w=N * K, batch_stride_c=M * N)
+        out = start.clone()
+        kw = {}
+        if "bias" in epilogue:
+            kw["bias"] = to_dev(bias, dev)
+        if "residual" in epilogue:
+            kw["residual"] = out
+        results["shifted"] = plan.run(shifted[1:], wd, out=out, **kw).cpu().numpy()
+    finally:
+        gemm.force_variant(None)
+    base = results[("register", 64, 64)]
+    assert np.isfinite(base).all()
+    for key, got in results.items():
+        assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), key
+    expect = np.einsum("bmk,bnk->bmn", rows[:, :, :K].astype(np.float64), w.astype(np.float64))
+    if "bias" in epilogue:
+        expect = expect + bias
+    if "relu" in epilogue:
+        expect = np.maximum(expect, 0)
+    if "residual" in epilogue:
+        expect = expect + start.cpu().numpy().astype(np.float64)
+    assert rel_max(base, expect) <= 1e-5
+
+
 @pytest.mark.parametrize("case", ["trans2-f32a", "opmcon32-rowA"])
 def test_new_lds_dma_sources_at_model_size(dev, case):
     # The f32 source (trans2, 29,972 x 1024 x 256) and the row-contiguous
