@@ -1,5 +1,9 @@
 // The LDS_DMA GEMM kernel family for gfx950: C[b] = epilogue(A[b] B[b]^T)
-// with A [M][K] and B [N][K] f16 (k-contiguous), f32 accumulation.
+// with A [M][K] and B [N][K] f16 (k-contiguous), f32 accumulation. Three
+// template variants widen the operand forms: a row-contiguous A [K][M]
+// (AK: k rows in LDS, transposing fragment reads), an f32 A under f16
+// arithmetic (AF: f32 rows in LDS, rounded to f16 as fragments are read) and
+// f32 arithmetic on f32 operands (FP32: f32 rows, the f32 MFMA).
 //
 // It carries the triangle multiplication's O(L^3) contraction (per hidden
 // channel b, out[b][i][j] = sum_k R[b][i][k] C[b][j][k]; the reference
