@@ -364,6 +364,41 @@ def test_f32_precision_on_lds_dma_matches_register_kernel(dev, shape, epilogue):
     assert rel_max(base, expect) <= 1e-5
 
 
+@pytest.mark.parametrize("epilogue", [(), ("bias", "relu", "residual")])
+def test_f32_precision_column_major_output_on_lds_dma(dev, epilogue):
+    # f32 arithmetic on LDS_DMA with a column-major output (C stored [N][M]),
+    # which leaves straight from the f32 MFMA's accumulators: the
+    # register-staged kernel's bits, a batch of two, ragged M and N.
+    import torch
+
+    from afhip import gemm
+
+    B, M, N, K = 2, 333, 200, 104
+    a = ref.normal(171, (B, M, K))
+    w = ref.normal(172, (B, N, K), 1 / K)
+    bias = to_dev(ref.normal(173, (N,), 0.02), dev)
+    start = to_dev(ref.normal(174, (B, N, M)), dev)
+    ad, wd = to_dev(a, dev), to_dev(w, dev)
+    results = {}
+    for kernel in ("register", "lds_dma"):
+        gemm.force_variant(gemm.GemmVariant("f32", 128, 128, source="pinned", kernel=kernel))
+        try:
+            plan = gemm.TiledGemm(M, K, N, precision="f32", a_dtype="f32", w_dtype="f32", w_layout="k",
+                                  out_dtype="f32", epilogue=epilogue, batch=B, batch_stride_a=M * K,
+                                  batch_stride_w=N * K, batch_stride_c=N * M, c_layout="column")
+            assert plan.variant().kernel == kernel
+            out = start.clone()
+            kw = {"bias": bias, "residual": out} if epilogue else {}
+            results[kernel] = plan.run(ad, wd, out=out, **kw).cpu().numpy()
+        finally:
+            gemm.force_variant(None)
+    assert np.array_equal(results["lds_dma"].view(np.uint32), results["register"].view(np.uint32))
+    expect = np.einsum("bmk,bnk->bnm", a.astype(np.float64), w.astype(np.float64))
+    if epilogue:
+        expect = np.maximum(expect + bias.cpu().numpy()[None, :, None], 0) + start.cpu().numpy()
+    assert rel_max(results["lds_dma"], expect) <= 1e-5
+
+
 @pytest.mark.parametrize("case", ["trans2-f32a", "opmcon32-rowA"])
 def test_new_lds_dma_sources_at_model_size(dev, case):
     # The f32 source (trans2, 29,972 x 1024 x 256) and the row-contiguous
